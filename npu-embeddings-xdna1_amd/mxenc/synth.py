@@ -1,0 +1,158 @@
+"""Seeded synthetic encoders and inputs for the five workload geometries.
+
+The weights follow the reference packer's conventions
+(tools/pack/pack_npue.py:2630,2747; common/host_b.hpp:68-73):
+  * GEMM operands are [K, N] row-major, fused QKV along N as Q|K|V, head h at
+    columns h*head_dim of each block;
+  * 1/sqrt(head_dim) is folded into Q's weight columns and Q's bias before the
+    weight is rounded to bf16 (round-to-nearest-even), so attention runs at
+    scale 1;
+  * biases, LayerNorm parameters and embedding tables stay fp32.
+Weights are N(0, 0.02). LayerNorm gamma = 1, beta = 0 unless `ln_random`
+(the tests randomise them so a dropped gamma or beta is visible).
+"""
+import math
+
+import numpy as np
+
+SEED = 20260926
+
+CONFIGS = {
+    # all-MiniLM-L6-v2 geometry, mean pooling.
+    "minilm": dict(kind="bert", layers=6, hidden=384, heads=12, head_dim=32, ffn=1536,
+                   vocab=30522, max_pos=512, batch=32, seq=128, len_lo=16, len_hi=128,
+                   cls_pool=False, sep=True),
+    # bge-base geometry, CLS pooling.
+    "bge_base": dict(kind="bert", layers=12, hidden=768, heads=12, head_dim=64, ffn=3072,
+                     vocab=30522, max_pos=512, batch=64, seq=512, len_lo=64, len_hi=512,
+                     cls_pool=True, sep=False),
+    # bge-large geometry, CLS pooling, every sequence full length.
+    "bge_large": dict(kind="bert", layers=24, hidden=1024, heads=16, head_dim=64, ffn=4096,
+                      vocab=30522, max_pos=512, batch=128, seq=512, len_lo=512, len_hi=512,
+                      cls_pool=True, sep=False),
+    # ViT-base/16 at 224x224: 196 patches + CLS = 197 tokens, pre-LN.
+    "vit_base": dict(kind="vit", layers=12, hidden=768, heads=12, head_dim=64, ffn=3072,
+                     batch=256, image=224, patch=16, labels=1000, eps=1e-12),
+    # Whisper-large-v3 encoder: 128 mels x 3000 frames -> 1500 positions, pre-LN.
+    "whisper_enc": dict(kind="whisper", layers=32, hidden=1280, heads=20, head_dim=64,
+                        ffn=5120, batch=8, mels=128, frames=3000, eps=1e-5),
+}
+
+
+def _bf16(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    r = (((u.astype(np.uint64) + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32)
+    return r.view(np.float32)
+
+
+def _normal(rng, shape, std=0.02):
+    return (rng.standard_normal(size=shape, dtype=np.float32) * np.float32(std))
+
+
+def make_layers(rng, L, d, heads, hd, f, ln_random=False):
+    """Per-layer tensors, contiguous over layers."""
+    m = {}
+    scale = np.float32(1.0 / math.sqrt(hd))
+    w_qkv = _normal(rng, (L, d, 3 * d))
+    b_qkv = _normal(rng, (L, 3 * d))
+    w_qkv[:, :, :d] *= scale
+    b_qkv[:, :d] *= scale
+    m["w_qkv"] = _bf16(w_qkv)
+    m["b_qkv"] = b_qkv
+    m["w_ao"] = _bf16(_normal(rng, (L, d, d)))
+    m["b_ao"] = _normal(rng, (L, d))
+    m["w_up"] = _bf16(_normal(rng, (L, d, f)))
+    m["b_up"] = _normal(rng, (L, f))
+    m["w_down"] = _bf16(_normal(rng, (L, f, d)))
+    m["b_down"] = _normal(rng, (L, d))
+    for n in ("ln1", "ln2"):
+        if ln_random:
+            m[n + "_g"] = (1.0 + _normal(rng, (L, d), 0.1)).astype(np.float32)
+            m[n + "_b"] = _normal(rng, (L, d), 0.05)
+        else:
+            m[n + "_g"] = np.ones((L, d), np.float32)
+            m[n + "_b"] = np.zeros((L, d), np.float32)
+    return m
+
+
+def make_model(name, seed=SEED, layers=None, ln_random=False, **over):
+    """A synthetic model of configuration `name`, optionally with fewer layers
+    or other overrides (hidden, heads, ...) for small tests."""
+    cfg = dict(CONFIGS[name])
+    cfg.update(over)
+    if layers is not None:
+        cfg["layers"] = layers
+    rng = np.random.default_rng(seed)
+    L, d, H, hd, f = cfg["layers"], cfg["hidden"], cfg["heads"], cfg["head_dim"], cfg["ffn"]
+    assert H * hd == d
+    m = dict(cfg)
+    m.update(make_layers(rng, L, d, H, hd, f, ln_random))
+    ln = (lambda n: (1.0 + _normal(rng, (n,), 0.1)).astype(np.float32)) if ln_random else \
+        (lambda n: np.ones((n,), np.float32))
+    lb = (lambda n: _normal(rng, (n,), 0.05)) if ln_random else \
+        (lambda n: np.zeros((n,), np.float32))
+    if cfg["kind"] == "bert":
+        m["word"] = _normal(rng, (cfg["vocab"], d))
+        m["pos"] = _normal(rng, (cfg["max_pos"], d))
+        m["type"] = _normal(rng, (2, d))
+        m["emb_ln_g"], m["emb_ln_b"] = ln(d), lb(d)
+    else:
+        m["fin_ln_g"], m["fin_ln_b"] = ln(d), lb(d)
+    if cfg["kind"] == "vit":
+        pd = 3 * cfg["patch"] ** 2
+        n_pos = (cfg["image"] // cfg["patch"]) ** 2 + 1
+        m["patch_w"] = _bf16(_normal(rng, (pd, d)))
+        m["patch_b"] = _normal(rng, (d,))
+        m["cls_token"] = _normal(rng, (d,))
+        m["pos"] = _normal(rng, (n_pos, d))
+        m["head_w"] = _normal(rng, (d, cfg["labels"]))
+        m["head_b"] = _normal(rng, (cfg["labels"],))
+        m["seq"] = n_pos
+    if cfg["kind"] == "whisper":
+        m["conv1_w"] = _normal(rng, (d, cfg["mels"], 3))
+        m["conv1_b"] = _normal(rng, (d,))
+        m["conv2_w"] = _normal(rng, (d, d, 3))
+        m["conv2_b"] = _normal(rng, (d,))
+        m["seq"] = cfg["frames"] // 2
+        m["pos"] = sinusoids(m["seq"], d)
+    return m
+
+
+def sinusoids(length, channels, max_timescale=10000.0):
+    """Whisper's fixed encoder position table: [sin | cos] halves."""
+    inc = math.log(max_timescale) / (channels // 2 - 1)
+    inv = np.exp(-inc * np.arange(channels // 2, dtype=np.float64))
+    t = np.arange(length, dtype=np.float64)[:, None] * inv[None, :]
+    return np.concatenate([np.sin(t), np.cos(t)], axis=1).astype(np.float32)
+
+
+def make_text_inputs(cfg, seed=SEED + 1, batch=None, seq=None):
+    """Token ids and the 1/0 attention mask for a BERT configuration:
+    ids U[1000, 30521], [CLS]=101 at 0, [SEP]=102 at len-1 when cfg['sep'],
+    valid length U[len_lo, len_hi], id 0 and mask 0 past it."""
+    rng = np.random.default_rng(seed)
+    B = batch or cfg["batch"]
+    S = seq or cfg["seq"]
+    lo, hi = min(cfg["len_lo"], S), min(cfg["len_hi"], S)
+    lens = rng.integers(lo, hi + 1, size=B)
+    ids = rng.integers(1000, 30522, size=(B, S)).astype(np.int32)
+    mask = np.zeros((B, S), np.float32)
+    for b, n in enumerate(lens):
+        ids[b, n:] = 0
+        mask[b, :n] = 1.0
+        ids[b, 0] = 101
+        if cfg.get("sep"):
+            ids[b, n - 1] = 102
+    return ids, mask, lens
+
+
+def make_pixels(cfg, seed=SEED + 2, batch=None):
+    rng = np.random.default_rng(seed)
+    B = batch or cfg["batch"]
+    return rng.uniform(-1.0, 1.0, size=(B, 3, cfg["image"], cfg["image"])).astype(np.float32)
+
+
+def make_mel(cfg, seed=SEED + 3, batch=None):
+    rng = np.random.default_rng(seed)
+    B = batch or cfg["batch"]
+    return rng.standard_normal(size=(B, cfg["mels"], cfg["frames"]), dtype=np.float32)

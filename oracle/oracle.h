@@ -1,0 +1,228 @@
+/*
+ * oracle.h -- CPU restatement of the reference's host (CPU-fallback) encoder
+ * path. TEST INFRASTRUCTURE ONLY.
+ *
+ * This library is the checker: tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product path (libmx_encoder.so) never links
+ * or calls it, and there is no CPU fallback in the product.
+ *
+ * Written in plain C from the reference's algorithms (the reference's C++ does
+ * not build here: it needs XRT, and common/json_min.hpp does not compile
+ * against this GCC's libstdc++). Each function names the reference file:line
+ * it restates. Compiled with the reference's own host flags
+ * (-O2 -march=x86-64-v3, runtime/CMakeLists.txt:302) so the AVX2 branches are
+ * the ones restated and timed.
+ *
+ * Parity pins (what checks each function against something other than itself)
+ * are listed per function below; tests/test_oracle_*.py hold the checks.
+ *
+ * Every weight operand is fp32 [K, N] row-major holding bf16-exact values (the
+ * reference widens its bf16 container operands exactly, common/host_b.hpp:
+ * 74-224). Every tensor argument is a plain host pointer.
+ */
+#ifndef MX_ORACLE_H
+#define MX_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- threads -------------------------------------------------------------
+ * One persistent pool, like app::Pool (runtime/src/pool.cpp:28-110). Rows are
+ * independent in every op below, so the partition never changes a bit. */
+void orc_set_threads(int n);
+int orc_threads(void);
+
+/* ---- bf16 -----------------------------------------------------------------
+ * to_bf16: (u + 0x7FFF + ((u >> 16) & 1)) >> 16 on the fp32 bits
+ * (runtime/include/common/host_kernels.hpp:157-161). Pinned bit-exact against
+ * oracle/_ref (the reference header compiled as-is) over all 2^32 inputs. */
+uint16_t orc_to_bf16(float x);
+float orc_from_bf16(uint16_t h);
+void orc_bf16_fill(uint16_t *dst, const float *src, size_t n);
+void orc_bf16_read(float *dst, const uint16_t *src, size_t n);
+/* Round every element to the nearest bf16 value, kept as fp32. */
+void orc_round_bf16_inplace(float *x, size_t n);
+
+/* ---- GELU -----------------------------------------------------------------
+ * gelu8: max(x,0) + p(min(|x|,4)), degree-8 Horner in fp32 FMA
+ * (host_kernels.hpp:325-352; bert_encoder.cpp:532-580 gelu_cpu).
+ * Pinned bit-exact against oracle/_ref's gelu8 (scalar and AVX2 forms), and
+ * against 0.5x(1+erf(x/sqrt2)) to the fit's stated accuracy.
+ * gelu_erf_exact: 0.5 x (1 + erf(x / sqrt 2)) in double, rounded once
+ * (runtime/include/common/app_state.hpp:116-120); pinned against Python's
+ * math.erf. */
+float orc_gelu8(float x);
+void orc_gelu_poly_inplace(float *x, size_t n);   /* gelu_cpu            */
+float orc_gelu_erf_exact(float x);
+void orc_gelu_erf_inplace(float *x, size_t n);    /* npu_ops.cpp:470-476 */
+
+/* ---- exp2 polynomial (exp2_avx2, host_kernels.hpp:358-379) ----------------
+ * 2^x = 2^k * p(f), k = trunc(x), f = x - k, degree-7 Horner. Pinned
+ * bit-exact against oracle/_ref's exp2_avx2. */
+void orc_exp2_poly(const float *x, float *y, size_t n);
+
+/* ---- softmax --------------------------------------------------------------
+ * softmax_cpu (bert_encoder.cpp:481-530): per row r of `cols` scores, add
+ * mask row add_mask[(r / rows_per_mask_row) * cols ...], then
+ * e_j = exp2_poly(max((x_j - max) * log2e, -120)), out = e_j * (1/sum).
+ * rows_per_mask_row = heads * seq for BERT. add_mask may be NULL.
+ * Pinned against an fp64 softmax (closed form) to 1e-6 and, per element,
+ * against oracle/_ref's exp2_avx2. */
+void orc_softmax_rows_poly(float *x, int64_t rows, int64_t cols,
+                           const float *add_mask, int64_t rows_per_mask_row);
+/* whisper::attention's softmax_row (npu_ops.cpp:591-599): max-subtracted
+ * std::exp, sum in fp32, scaled by 1/sum (0 if sum is 0). Pinned against
+ * an fp64 softmax. */
+void orc_softmax_rows_exact(float *x, int64_t rows, int64_t cols,
+                            const float *add_mask, int64_t rows_per_mask_row);
+
+/* ---- LayerNorm ------------------------------------------------------------
+ * layer_norm_cpu (bert_encoder.cpp:416-463), AVX2 branch: 8-lane fp32 mean and
+ * variance partials, hsum256, biased variance, 1/sqrt(var + eps), then
+ * fma(d*is, gamma, beta). `cols` must be a multiple of 8 (the reference
+ * enforces hidden % 8 == 0, app_state.hpp:380-631). Pinned against a two-pass
+ * fp64 LayerNorm. The reference hard-codes eps = 1e-12 for BERT. */
+void orc_layer_norm_rows(float *x, int64_t rows, int64_t cols,
+                         const float *gamma, const float *beta, float eps);
+/* layernorm_rows (npu_ops.cpp:449-468): double sum and variance, fp32
+ * normalise. Used by the ViT and Whisper encoders. */
+void orc_layernorm_rows_f64(float *x, int64_t rows, int64_t cols,
+                            const float *gamma, const float *beta, double eps);
+/* x <- y + residual, elementwise (add_into, bert_encoder.cpp:1183-1194). */
+void orc_add_into(float *x, const float *y, const float *residual, size_t n);
+
+/* ---- GEMM -----------------------------------------------------------------
+ * hostconv::gemm_nt (runtime/include/common/conv_host.hpp:148-181):
+ * C[M,N] = A[M,K] @ B[K,N] + bias[N]; per element a sequential k-ordered FMA
+ * chain from 0, bias added last. bias may be NULL (zero). Pinned bit-exact
+ * against oracle/_ref's gemm_nt and against an fp64 product. */
+void orc_gemm_nt(const float *A, int64_t M, const float *B, int64_t K,
+                 int64_t N, const float *bias, float *C);
+
+/* ---- host attention (BERT) ------------------------------------------------
+ * qk_impl (bert_encoder.cpp:995-1052): scores[((b*H+h)*S + i)*S + j] =
+ * q_i . k_j over head_dim, no scale (folded into Q), AVX2 8-wide FMA + hsum.
+ * av_impl (bert_encoder.cpp:1062-1126): ctx[b*S+i, h*hd..] = sum_j p_ij v_j.
+ * qkv is [B*S, 3*hidden] as Q|K|V. head_dim must be a multiple of 8. Pinned
+ * against an fp64 brute-force attention on small shapes. */
+void orc_qk(const float *qkv, int64_t B, int64_t S, int64_t H, int64_t hd,
+            float *scores);
+void orc_av(const float *scores, const float *qkv, int64_t B, int64_t S,
+            int64_t H, int64_t hd, float *ctx);
+
+/* whisper::attention (npu_ops.cpp:478-644), the no-softmax-design branch:
+ * per query row and head, scores = (q.k) * scale, exact max-subtracted
+ * softmax, ctx = sum p v. q row stride q_stride, K|V rows at kv (K at 0,
+ * V at d_model) with stride kv_stride. No mask. Pinned against fp64. */
+void orc_whisper_attention(const float *q, int64_t q_stride, const float *kv,
+                           int64_t kv_stride, int64_t n_q, int64_t n_kv,
+                           int64_t d_model, int64_t heads, int64_t head_dim,
+                           float scale, float *out);
+
+/* ---- embedding sum, mask, pooling -----------------------------------------
+ * EmbedService::chunk / BertEncoder::encode (embed_service.cpp:29-64;
+ * bert_encoder.cpp:1367-1417): emb[b*S+s] = word[id] + pos[s] + type[0]
+ * (summed left to right in fp32); cam = mask (1/0); cmask = m > 0 ? 0 : -1e30.
+ * Pinned by exact indexing invariants (tests). */
+void orc_embed_sum(const int32_t *ids, const float *attn_mask, int64_t B,
+                   int64_t S, int64_t hidden, const float *word,
+                   const float *pos, const float *type0, float *emb,
+                   float *add_mask);
+/* app::pool_rows (runtime/include/common/app_state.hpp:335-374): CLS (row 0;
+ * returns -1 if position 0 is masked) or mean (in-order double accumulation of
+ * h*m, denominator max(sum m, 1e-9f)); optional L2 (double, clamp 1e-24 on the
+ * squared norm). Pinned against the reference's own goldens: HF
+ * last_hidden_state -> hf.pool.mean / hf.out.embedding / st.embedding
+ * (the reference/goldens boundary .npz files). Returns 0 on success. */
+int orc_pool_rows(const float *h, const float *attn_mask, int64_t B, int64_t S,
+                  int64_t hidden, int cls_pool, int l2_normalize, float *out);
+
+/* ---- AIE kernel restatements (bf16 in/out; the accelerator ops the GPU
+ * kernels replace). bf16 narrowing here is RNE (the *_rne.cc variants and
+ * narrow_*.cc all set conv_even). ---------------------------------------- */
+/* softmax.cc:76-160 (softmax_rne.cc:42-52): per row of `cols`: x = max(x,
+ * -1e30) (in bf16); m = max; d = max(x - m, -100); arg = max(d*log2e, -120);
+ * e = bf16(exp2_poly(arg)); sum over e in fp32; inv = 1/sum; out =
+ * bf16(e*inv). */
+void orc_aie_softmax_bf16(const uint16_t *in, uint16_t *out, int64_t rows,
+                          int64_t cols);
+/* layernorm.cc:85-142 (layernorm_rne.cc): fp32 two-pass stats of the bf16 row,
+ * inv_std = fast_invsqrt(var + eps) (bit-trick seed + 2 Newton steps,
+ * layernorm.cc:65-75), out = bf16((x-mean)*inv_std*gamma + beta). */
+void orc_aie_layernorm_bf16(const uint16_t *in, uint16_t *out, int64_t rows,
+                            int64_t cols, const float *gamma,
+                            const float *beta, float eps);
+/* gelu_erf.cc:79-145: 0.5x + 0.5|x| * (1 - t*P(t)*2^max(-u^2 log2e, -125)),
+ * u = x/sqrt2, t = 1/(1+p|u|), A&S 7.1.26; bf16 RNE out. */
+void orc_aie_gelu_erf_bf16(const uint16_t *in, uint16_t *out, int64_t n);
+/* gelu_poly_rne.cc / gelu_poly.cc:77-176: gelu8 on the widened bf16 value,
+ * bf16 RNE out. */
+void orc_aie_gelu_poly_bf16(const uint16_t *in, uint16_t *out, int64_t n);
+/* narrow_f32_bf16.cc:51-90: fp32 -> bf16, round to nearest even. The GPU
+ * kernel is pinned to the host's to_bf16 integer formula. */
+void orc_narrow_f32_bf16(const float *in, uint16_t *out, int64_t n);
+/* narrow_i32_bf16.cc:66-95: int32 -> bf16 in ONE rounding (RNE on the
+ * integer). Note the reference's host stand-in (--sim-c-bf16,
+ * host_kernels.hpp:583-610) rounds twice (int32 -> fp32 -> bf16); the two
+ * differ only for |v| > 2^24. This function is the single rounding; pinned
+ * against exact integer arithmetic. */
+void orc_narrow_i32_bf16(const int32_t *in, uint16_t *out, int64_t n);
+/* The two-rounding host form, for the tests that state the difference. */
+void orc_narrow_i32_bf16_twice(const int32_t *in, uint16_t *out, int64_t n);
+
+/* ---- whole encoders --------------------------------------------------------
+ * Every per-layer tensor is contiguous over layers: w_qkv is [L, d, 3d],
+ * b_qkv [L, 3d], w_ao [L, d, d], w_up [L, d, f], w_down [L, f, d], LN
+ * gamma/beta [L, d]. Q's block of w_qkv/b_qkv already carries 1/sqrt(hd)
+ * (tools/pack/pack_npue.py:2630,2747), so attention uses scale 1. */
+typedef struct {
+  int64_t layers, hidden, heads, head_dim, ffn;
+  const float *w_qkv, *b_qkv, *w_ao, *b_ao, *w_up, *b_up, *w_down, *b_down;
+  const float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
+  const float *emb_ln_g, *emb_ln_b; /* BERT only: the embedding LayerNorm   */
+  const float *fin_ln_g, *fin_ln_b; /* pre-LN only: the final LayerNorm     */
+} orc_encoder;
+
+/* BertEncoder::run, host branch (bert_encoder.cpp:1419-1598): embedding LN,
+ * then per layer QKV GEMM -> qk -> softmax_cpu (mask) -> av -> attn-out GEMM
+ * -> add_into + layer_norm_cpu -> FFN-up GEMM -> gelu_cpu -> FFN-down GEMM ->
+ * add_into + layer_norm_cpu. eps 1e-12 (hard-coded, :438/:456). x_io is
+ * [B*S, hidden] fp32, updated in place (emb_in -> final hidden). add_mask is
+ * [B, S] (0 / -1e30). layers_to_run < 0 means all. */
+void orc_bert_run(const orc_encoder *m, float *x_io, const float *add_mask,
+                  int64_t B, int64_t S, int64_t layers_to_run);
+
+/* VitEncoder::run / WhisperEncoder::run layer body (vit/encoder.cpp:222-431;
+ * whisper/encoder.cpp:114-213): pre-LN, layernorm_rows (double stats, eps),
+ * whisper::attention per sequence (scale as given; 1 when folded into Q),
+ * gelu_erf_exact, residual adds, final LayerNorm. x_io is [B*S, hidden]. */
+void orc_preln_run(const orc_encoder *m, float *x_io, int64_t B, int64_t S,
+                   double eps, float scale, int64_t layers_to_run);
+
+/* Whisper's conv front end (whisper/features.cpp:390-469): conv1 (k3, p1) +
+ * gelu_erf_exact, conv2 (k3, s2, p1) + gelu_erf_exact, permuted to
+ * [T/2, hidden]. mel is [n_mels, T] channel-major; w1 [hidden, n_mels, 3],
+ * w2 [hidden, hidden, 3] (PyTorch Conv1d layout). out is [T/2, hidden]. */
+void orc_conv_front_end(const float *mel, int64_t n_mels, int64_t T,
+                        const float *w1, const float *b1, const float *w2,
+                        const float *b2, int64_t hidden, float *out);
+
+/* ViT patch embedding input (vit/encoder.cpp:288-332 consumes it): im2col of
+ * [3, H, W] pixels into [n_patches, 3*p*p] rows in (c, ky, kx) order, the
+ * PyTorch Conv2d weight order. */
+void orc_vit_patches(const float *pixels, int64_t img, int64_t patch,
+                     float *rows);
+
+/* head_matvec (runtime/src/vit/head.cpp:16-49): logits[j] = bias[j] +
+ * sum_t cls[t] * head[t*num_labels + j], double accumulation. */
+void orc_head_matvec(const float *head, const float *bias, const float *cls_row,
+                     int64_t d_model, int64_t num_labels, float *logits);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,137 @@
+/*
+ * orc_encoders.c -- whole encoder stacks on the host, restated from the
+ * reference's host branches. TEST INFRASTRUCTURE (the oracle); see oracle.h.
+ */
+#include "orc_internal.h"
+
+#include <stdlib.h>
+
+static float *falloc(size_t n) { return (float *)malloc(n * sizeof(float)); }
+
+/* BertEncoder::run, every op on the host (bert_encoder.cpp:1419-1598 with
+ * gemm_on_array() false, host_ln/host_sm/host_gelu true, attn_ null). */
+void orc_bert_run(const orc_encoder *m, float *x, const float *add_mask,
+                  int64_t B, int64_t S, int64_t layers_to_run) {
+  const int64_t d = m->hidden, f = m->ffn, H = m->heads, hd = m->head_dim;
+  const int64_t rows = B * S;
+  const int64_t L = layers_to_run < 0 || layers_to_run > m->layers ? m->layers
+                                                                   : layers_to_run;
+  const float eps = 1e-12f; /* hard-coded in layer_norm_cpu (:438) */
+  float *qkv = falloc((size_t)(rows * 3 * d));
+  float *scores = falloc((size_t)(B * H * S * S));
+  float *ctx = falloc((size_t)(rows * d));
+  float *proj = falloc((size_t)(rows * d));
+  float *up = falloc((size_t)(rows * f));
+  float *residual = falloc((size_t)(rows * d));
+
+  orc_layer_norm_rows(x, rows, d, m->emb_ln_g, m->emb_ln_b, eps);
+  for (int64_t l = 0; l < L; ++l) {
+    memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
+    orc_gemm_nt(x, rows, m->w_qkv + l * d * 3 * d, d, 3 * d, m->b_qkv + l * 3 * d, qkv);
+    orc_qk(qkv, B, S, H, hd, scores);
+    orc_softmax_rows_poly(scores, B * H * S, S, add_mask, H * S);
+    orc_av(scores, qkv, B, S, H, hd, ctx);
+    orc_gemm_nt(ctx, rows, m->w_ao + l * d * d, d, d, m->b_ao + l * d, proj);
+    orc_add_into(x, proj, residual, (size_t)(rows * d));
+    orc_layer_norm_rows(x, rows, d, m->ln1_g + l * d, m->ln1_b + l * d, eps);
+    memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
+    orc_gemm_nt(x, rows, m->w_up + l * d * f, d, f, m->b_up + l * f, up);
+    orc_gelu_poly_inplace(up, (size_t)(rows * f));
+    orc_gemm_nt(up, rows, m->w_down + l * f * d, f, d, m->b_down + l * d, proj);
+    orc_add_into(x, proj, residual, (size_t)(rows * d));
+    orc_layer_norm_rows(x, rows, d, m->ln2_g + l * d, m->ln2_b + l * d, eps);
+  }
+  free(qkv);
+  free(scores);
+  free(ctx);
+  free(proj);
+  free(up);
+  free(residual);
+}
+
+/* VitEncoder::run (vit/encoder.cpp:347-431) / WhisperEncoder::run
+ * (whisper/encoder.cpp:156-213) body, host branch: pre-LN, the whole
+ * sequence in one chunk (chunking by the design's rows does not change a
+ * row's arithmetic: every op is row-wise except attention, which always sees
+ * the whole sequence). */
+void orc_preln_run(const orc_encoder *m, float *x, int64_t B, int64_t S,
+                   double eps, float scale, int64_t layers_to_run) {
+  const int64_t d = m->hidden, f = m->ffn;
+  const int64_t rows = B * S;
+  const int64_t L = layers_to_run < 0 || layers_to_run > m->layers ? m->layers
+                                                                   : layers_to_run;
+  float *norm = falloc((size_t)(rows * d));
+  float *qkv = falloc((size_t)(rows * 3 * d));
+  float *ctx = falloc((size_t)(rows * d));
+  float *proj = falloc((size_t)(rows * d));
+  float *up = falloc((size_t)(rows * f));
+  for (int64_t l = 0; l < L; ++l) {
+    memcpy(norm, x, (size_t)(rows * d) * sizeof(float));
+    orc_layernorm_rows_f64(norm, rows, d, m->ln1_g + l * d, m->ln1_b + l * d, eps);
+    orc_gemm_nt(norm, rows, m->w_qkv + l * d * 3 * d, d, 3 * d, m->b_qkv + l * 3 * d, qkv);
+    for (int64_t b = 0; b < B; ++b) {
+      const float *base = qkv + b * S * 3 * d;
+      orc_whisper_attention(base, 3 * d, base + d, 3 * d, S, S, d, m->heads,
+                            m->head_dim, scale, ctx + b * S * d);
+    }
+    orc_gemm_nt(ctx, rows, m->w_ao + l * d * d, d, d, m->b_ao + l * d, proj);
+    for (int64_t i = 0; i < rows * d; ++i) x[i] += proj[i];
+    memcpy(norm, x, (size_t)(rows * d) * sizeof(float));
+    orc_layernorm_rows_f64(norm, rows, d, m->ln2_g + l * d, m->ln2_b + l * d, eps);
+    orc_gemm_nt(norm, rows, m->w_up + l * d * f, d, f, m->b_up + l * f, up);
+    orc_gelu_erf_inplace(up, (size_t)(rows * f));
+    orc_gemm_nt(up, rows, m->w_down + l * f * d, f, d, m->b_down + l * d, proj);
+    for (int64_t i = 0; i < rows * d; ++i) x[i] += proj[i];
+  }
+  if (m->fin_ln_g) orc_layernorm_rows_f64(x, rows, d, m->fin_ln_g, m->fin_ln_b, eps);
+  free(norm);
+  free(qkv);
+  free(ctx);
+  free(proj);
+  free(up);
+}
+
+/* whisper/features.cpp:390-469 */
+typedef struct {
+  const float *in, *w, *bias;
+  float *out;
+  int64_t cin, T_in, T_out, stride, hidden;
+} conv_task;
+
+static void conv_worker(void *p, int w, int nw) {
+  const conv_task *t = (const conv_task *)p;
+  int64_t lo, hi;
+  orc_range(t->hidden, w, nw, &lo, &hi);
+  for (int64_t o = lo; o < hi; ++o) {
+    const float *wo = t->w + o * t->cin * 3;
+    for (int64_t tt = 0; tt < t->T_out; ++tt) {
+      const int64_t centre = tt * t->stride;
+      float acc = t->bias[o];
+      for (int64_t c = 0; c < t->cin; ++c) {
+        const float *wc = wo + c * 3;
+        for (int64_t k = 0; k < 3; ++k) {
+          const int64_t ti = centre + k - 1;
+          if (ti < 0 || ti >= t->T_in) continue;
+          acc = fmaf(wc[k], t->in[c * t->T_in + ti], acc);
+        }
+      }
+      t->out[o * t->T_out + tt] = orc_gelu_erf_exact(acc);
+    }
+  }
+}
+
+void orc_conv_front_end(const float *mel, int64_t n_mels, int64_t T,
+                        const float *w1, const float *b1, const float *w2,
+                        const float *b2, int64_t hidden, float *out) {
+  const int64_t T2 = T / 2;
+  float *h1 = falloc((size_t)(hidden * T));
+  float *h2 = falloc((size_t)(hidden * T2));
+  conv_task c1 = {mel, w1, b1, h1, n_mels, T, T, 1, hidden};
+  orc_run(conv_worker, &c1);
+  conv_task c2 = {h1, w2, b2, h2, hidden, T, T2, 2, hidden};
+  orc_run(conv_worker, &c2);
+  for (int64_t o = 0; o < hidden; ++o)
+    for (int64_t t = 0; t < T2; ++t) out[t * hidden + o] = h2[o * T2 + t];
+  free(h1);
+  free(h2);
+}
