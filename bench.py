@@ -1,0 +1,174 @@
+"""Throughput of the encoder hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config bge_base]
+                    [--no-cpu-baseline]
+
+A step is one pass of the hot path over one batch: token ids and the
+attention mask (already in HBM) -> embedding sum -> the whole encoder stack ->
+pooling + L2 normalisation (EmbedService::chunk minus the tokenizer), on the
+bge-base geometry at batch 64 x seq 512 by default. Weights are random-init
+(N(0, 0.02), Q scale folded, bf16), inputs synthetic; see mxenc/synth.py.
+
+Prints one JSON line: sequences/s, the GEMM family's MFMA roofline (HIP event
+time of every GEMM launch in the timed steps, on the stream they run on), and
+the oracle's host path timed on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "npu-embeddings-xdna1_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+HBM_PEAK_GBS = 8000.0
+
+
+def cpu_baseline(name, sample_batch, threads):
+    """The oracle's host path (the reference CPU fallback restated) over
+    `sample_batch` sequences of the same workload, all layers."""
+    import numpy as np
+
+    import orc as orc_mod
+    from mxenc import synth
+
+    orc = orc_mod.load()
+    orc.orc_set_threads(threads)
+    m = synth.make_model(name)
+    ids, am, _ = synth.make_text_inputs(m)
+    ids = np.ascontiguousarray(ids[:sample_batch])
+    am = np.ascontiguousarray(am[:sample_batch])
+    B, S = ids.shape
+    d = m["hidden"]
+    P = orc_mod.P
+    keep = []
+    enc = orc_mod.encoder_struct(m, keep)
+    emb = np.empty((B * S, d), np.float32)
+    cm = np.empty((B, S), np.float32)
+    out = np.empty((B, d), np.float32)
+    t0 = time.perf_counter()
+    orc.orc_embed_sum(P(ids), P(am), B, S, d, P(m["word"]), P(m["pos"]), P(m["type"]), P(emb),
+                      P(cm))
+    orc.orc_bert_run(enc, P(emb), P(cm), B, S, -1)
+    orc.orc_pool_rows(P(emb), P(am), B, S, d, int(m["cls_pool"]), 1, P(out))
+    dt = time.perf_counter() - t0
+    return {"value": B / dt, "unit": "sequences/s", "cores": threads, "kind": "port",
+            "sample": f"{B} of the {m['batch']} sequences (seq {S}, {m['layers']} layers, "
+                      f"embed+run+pool) through the oracle's host path, {dt:.1f} s wall"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="bge_base")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=4)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this backend runs on one GPU; multi-GPU sharding of the "
+                                   "encoder path is a design note, not a code path here",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import numpy as np
+
+    import mxenc
+    from mxenc import synth
+
+    m = synth.make_model(args.config)
+    assert m["kind"] == "bert"
+    ids, am, lens = synth.make_text_inputs(m)
+    B, S = ids.shape
+    ctx = mxenc.Context(0)
+    enc = mxenc.Encoder(ctx, m)
+    d_ids, d_am = ctx.put(ids), ctx.put(am)
+    out = ctx.empty((B, m["hidden"]), np.float32)
+    print(f"bench: {args.config} B={B} S={S} L={m['layers']} on {ctx.props.arch.decode()} "
+          f"({ctx.props.compute_units} CUs)", file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        enc.embed(d_ids, d_am, B, S, out)
+    ctx.sync()
+
+    # Timed region: throughput without per-launch events.
+    enc.set_timing(False)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        enc.embed(d_ids, d_am, B, S, out)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+    seq_s = args.steps * B / dt
+    print(f"bench: {args.steps} steps in {dt*1e3:.1f} ms -> {seq_s:.1f} seq/s",
+          file=sys.stderr, flush=True)
+
+    # The same steps again with a HIP event pair around every launch, on the
+    # stream the kernels run on: per-kernel-family durations for the roofline.
+    enc.set_timing(True)
+    g_ms = a_ms = ln_ms = o_ms = 0.0
+    g_n = a_n = 0
+    g_flop = a_flop = 0.0
+    for _ in range(args.steps):
+        enc.embed(d_ids, d_am, B, S, out)
+        t = enc.timings()
+        g_ms += t.gemm_ms
+        a_ms += t.attn_ms
+        ln_ms += t.ln_ms
+        o_ms += t.other_ms
+        g_n += t.gemm_launches
+        a_n += t.attn_launches
+        g_flop += t.gemm_flop
+        a_flop += t.attn_flop
+    enc.set_timing(False)
+    gemm_tflops = g_flop / (g_ms * 1e-3) / 1e12
+    attn_tflops = a_flop / (a_ms * 1e-3) / 1e12
+    print(f"bench: GEMM {g_ms/args.steps:.2f} ms/step ({gemm_tflops:.0f} TFLOP/s, "
+          f"{g_n // args.steps} launches), attention {a_ms/args.steps:.2f} ms/step "
+          f"({attn_tflops:.0f} TFLOP/s), LN {ln_ms/args.steps:.2f} ms, other "
+          f"{o_ms/args.steps:.2f} ms", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(args.config, args.cpu_sample, threads)
+        print(f"bench: cpu baseline {cpu['value']:.3f} seq/s ({cpu['sample']})",
+              file=sys.stderr, flush=True)
+
+    line = {
+        "metric": "sequences/sec (bge-base, seq 512, b64) + GEMM MFMA util % of bf16 peak",
+        "value": seq_s,
+        "unit": "sequences/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dt / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded token ids and valid lengths; random-init N(0,0.02) weights)",
+        "config": {"workload": f"{args.config} encoder embed: ids -> {m['layers']}-layer "
+                               f"BERT (d {m['hidden']}, {m['heads']} heads, FFN {m['ffn']}) -> "
+                               f"{'CLS' if m['cls_pool'] else 'mean'} pool + L2",
+                   "batch": B, "seq_len": S, "layers": m["layers"]},
+        "gemm_mfma_util_pct": 100.0 * gemm_tflops / BF16_PEAK_TFLOPS,
+        "roofline": {"bound": "mfma", "kernel": "gemm_bf16_k (all encoder GEMMs)",
+                     "achieved": gemm_tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": gemm_tflops / BF16_PEAK_TFLOPS, "traffic": None,
+                     "flop_per_launch": g_flop / max(g_n, 1),
+                     "avg_launch_ms": g_ms / max(g_n, 1)},
+        "attention": {"achieved_tflops": attn_tflops, "frac": attn_tflops / BF16_PEAK_TFLOPS},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    enc.close()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,290 @@
+/*
+ * mx_encoder.h -- C ABI of the MI355X (gfx950) encoder backend.
+ *
+ * The drop-in boundary for the reference runtime's encoder-layer hot path: the
+ * per-op placement layer (--npu-ops codes gemm, attn, softm, layn, gelu) gains
+ * a GPU backend, and every op the reference dispatches to its accelerator
+ * through npu::Design (runtime/include/runtime/design.hpp:199-263) has an
+ * entry point here. Each declaration names the reference interface it
+ * replaces.
+ *
+ * Conventions
+ *   - Every function returns an int status: MX_OK (0) or a negative MX_E_*.
+ *     Nothing throws across the ABI. mx_last_error() returns the calling
+ *     thread's message for its last failure, naming what was refused (the
+ *     reference's refusals are std::runtime_error with a named reason,
+ *     runtime/src/entry.cpp:74-77).
+ *   - Tensor arguments are DEVICE pointers (from mx_alloc, or any device
+ *     allocation on the context's GPU) unless the name ends in _host.
+ *   - Operations on one mx_stream run in order; distinct streams may run
+ *     concurrently (one per --pipeline lane, runtime/include/runtime/
+ *     run_setup.hpp:778-874). Op calls are asynchronous; mx_sync() waits.
+ *   - Weights staged with mx_stage_weight belong to the context; activations
+ *     belong to the caller.
+ *   - bf16 tensors are uint16_t bit patterns. Every fp32 -> bf16 narrowing is
+ *     round-to-nearest-even by the reference's integer formula
+ *     (u + 0x7FFF + ((u >> 16) & 1)) >> 16 (common/host_kernels.hpp:157-161),
+ *     bit for bit, NaN behaviour included.
+ */
+#ifndef MX_ENCODER_H
+#define MX_ENCODER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MX_OK 0
+#define MX_E_INVALID (-1)     /* an argument was refused (shape, pointer, code) */
+#define MX_E_DEVICE (-2)      /* a HIP call failed                             */
+#define MX_E_UNSUPPORTED (-3) /* valid request this backend does not implement */
+#define MX_E_STATE (-4)       /* object not ready (e.g. missing weights)       */
+#define MX_E_DATA (-5)        /* the data itself was refused (e.g. CLS masked) */
+
+typedef enum { MX_F32 = 0, MX_BF16 = 1, MX_I32 = 2 } mx_dtype;
+
+/* GEMM epilogues: applied to acc + bias in fp32 before narrowing. */
+typedef enum {
+  MX_EPI_NONE = 0,
+  MX_EPI_GELU_POLY = 1, /* gelu8 / gelu_cpu (bert_encoder.cpp:532-580)        */
+  MX_EPI_GELU_ERF = 2   /* 0.5x(1+erf(x/sqrt2)) (app_state.hpp:116-120)       */
+} mx_epilogue;
+
+typedef enum {
+  MX_GELU_POLY = 0,   /* gelu_cpu / gelu_poly_rne.cc: degree-8 fit            */
+  MX_GELU_ERF = 1,    /* exact-erf GELU (gelu_erf_exact)                      */
+  MX_GELU_ERF_AS = 2  /* gelu_erf.cc: A&S 7.1.26 erf with exp2_poly           */
+} mx_gelu_variant;
+
+typedef enum {
+  MX_SOFTMAX_POLY = 0,  /* softmax_cpu: exp2 poly, -120 argument floor       */
+  MX_SOFTMAX_EXACT = 1, /* whisper::attention softmax_row: max-subtracted exp */
+  MX_SOFTMAX_AIE = 2    /* softmax_rne.cc: bf16 in/out, three clamps, exps
+                           narrowed to bf16 before the sum                    */
+} mx_softmax_variant;
+
+typedef struct mx_ctx mx_ctx;
+typedef struct mx_stream mx_stream;
+typedef struct mx_encoder mx_encoder;
+
+typedef struct {
+  int device;
+  int compute_units;
+  int clock_mhz;          /* peak engine clock                               */
+  int64_t hbm_bytes;
+  char arch[32];          /* "gfx950"                                        */
+  double bf16_dense_tflops; /* compute_units * 4096 FLOP/clk * clock         */
+} mx_device_props;
+
+/* ---- library, device, streams, memory ------------------------------------ */
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char *mx_last_error(void);
+int mx_version(void);
+
+/* Replaces npu::Device (runtime/include/runtime/device.hpp:28-39): opens GPU
+ * `device`. Refuses a device that is not gfx950. */
+int mx_create(int device, mx_ctx **out);
+void mx_destroy(mx_ctx *ctx);
+int mx_device_props_get(mx_ctx *ctx, mx_device_props *out);
+
+/* One stream per --pipeline lane (run_setup.hpp:778-874; the reference's
+ * lanes share one device under npu_mu, GPU lanes are independent streams). */
+int mx_stream_create(mx_ctx *ctx, mx_stream **out);
+void mx_stream_destroy(mx_stream *s);
+/* Wait for every op issued on s. The reference's dispatch is synchronous
+ * (Design::dispatch_only, runtime/src/design.cpp:502-532); a caller wanting
+ * those semantics calls mx_sync after each op. */
+int mx_sync(mx_stream *s);
+/* The stream's hipStream_t, for callers that interleave their own work. */
+void *mx_stream_handle(mx_stream *s);
+
+/* Device buffers (Design::stage_alloc / slot_ptr, design.hpp:236-240, without
+ * the host mapping: the GPU path keeps activations resident). */
+int mx_alloc(mx_ctx *ctx, size_t bytes, void **dev);
+int mx_free(mx_ctx *ctx, void *dev);
+int mx_copy_h2d(mx_stream *s, void *dev_dst, const void *host_src, size_t bytes);
+int mx_copy_d2h(mx_stream *s, void *host_dst, const void *dev_src, size_t bytes);
+
+/* Replaces Design::stage (design.hpp:236) of a GEMM B operand: the [K, N]
+ * row-major weight (host memory, fp32 holding any value -- it is rounded to
+ * bf16 here by to_bf16 -- or bf16 bits) is copied once into a
+ * context-owned, MFMA-ready [N, K] bf16 panel. *slot >= 1 on success. */
+int mx_stage_weight(mx_ctx *ctx, const void *kn_host, int dtype, int64_t K,
+                    int64_t N, int *slot);
+int mx_release_weight(mx_ctx *ctx, int slot);
+
+/* ---- per-op entry points (the accelerator ops of --npu-ops) --------------- */
+
+/* gemm: replaces BertEncoder::gemm's array branch (bert_encoder.cpp:741-924)
+ * and NpuGemm::run (runtime/src/whisper/npu_ops.cpp:200-288).
+ * C[M, N] = epilogue(A[M, K] @ W + bias) (+ residual), W = slot `wslot`
+ * ([K, N] as staged), bf16 A with row stride lda (elements), fp32 accumulate,
+ * fp32 bias (nullable), optional fp32 residual [M, N] with stride ldc (may
+ * alias C when c_dtype is MX_F32; the pre-LN encoders' x += proj), C fp32 or
+ * bf16 (RNE) with row stride ldc. K % 8 == 0, lda % 8 == 0, 16-byte aligned A. */
+int mx_gemm(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t lda,
+            int wslot, const float *bias, int epilogue, const float *residual,
+            void *C, int c_dtype, int64_t ldc);
+/* The same with the weight panel given directly: Wt is [N, K] bf16 on the
+ * device (row stride K). */
+int mx_gemm_wt(mx_stream *s, const uint16_t *A, int64_t M, int64_t K,
+               int64_t lda, const uint16_t *Wt, int64_t N, const float *bias,
+               int epilogue, const float *residual, void *C, int c_dtype,
+               int64_t ldc);
+
+/* attn (+softm fused): replaces the host qk/softmax_cpu/av triple
+ * (bert_encoder.cpp:995-1135, :481-530), BertEncoder::attention_npu /
+ * NpuAttention::run (runtime/src/whisper/attention_npu.cpp:177) and
+ * whisper::attention (npu_ops.cpp:478-644). One pass per (sequence, head,
+ * 128-query tile), scores never leave the chip.
+ * qkv: bf16 [B*S, >=3*H*hd] rows of Q|K|V (head h at h*hd of each block), row
+ * stride ld_qkv. scale multiplies q.k (1 when folded into Q). add_mask:
+ * fp32 [B, S] additive (0 / -1e30), nullable. kv_len: int32 [B], keys at or
+ * past kv_len[b] are skipped (must be masked anyway; nullable = S).
+ * ctx: bf16 [B*S, H*hd], row stride ld_ctx. hd in {32, 64}. */
+int mx_attention(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B,
+                 int64_t S, int64_t H, int64_t hd, float scale,
+                 const float *add_mask, const int32_t *kv_len, uint16_t *ctx,
+                 int64_t ld_ctx);
+
+/* softm: replaces add_additive_mask + eltwise(softmax) (bert_encoder.cpp:
+ * 465-475, :322-368) and NpuEltwise::softmax (whisper/eltwise.cpp:110-138):
+ * in-place row softmax of `rows` rows of `cols`, row stride row_stride;
+ * mask row add_mask[(r / rows_per_mask_row) * cols] added first (nullable).
+ * dtype MX_F32 or MX_BF16 (MX_SOFTMAX_AIE needs MX_BF16). cols <= 4096. */
+int mx_softmax_rows(mx_stream *s, void *x, int dtype, int64_t rows,
+                    int64_t cols, int64_t row_stride, const float *add_mask,
+                    int64_t rows_per_mask_row, int variant);
+
+/* layn: replaces layer_norm / layer_norm_cpu / add_norm_bf16
+ * (bert_encoder.cpp:370-463, :1304-1361) and layernorm_rows (npu_ops.cpp:
+ * 449-468). z = x (+ y); out = (z - mean) / sqrt(var + eps) * gamma + beta,
+ * biased variance, fp32 statistics. x, y: fp32 or bf16 (y nullable); outputs
+ * out_f32 (nullable, may alias x when x is fp32) and/or out_bf16 (nullable).
+ * Row stride = cols for every tensor. */
+int mx_layernorm(mx_stream *s, const void *x, int x_dtype, const void *y,
+                 int y_dtype, const float *gamma, const float *beta, float eps,
+                 int64_t rows, int64_t cols, float *out_f32, uint16_t *out_bf16);
+
+/* gelu: replaces gelu_cpu / eltwise(gelu) (bert_encoder.cpp:532-580),
+ * gelu_erf_inplace (npu_ops.cpp:470-476) and NpuEltwise::gelu. Elementwise,
+ * in place allowed (x == y with equal dtypes). */
+int mx_gelu(mx_stream *s, const void *x, int x_dtype, void *y, int y_dtype,
+            int64_t n, int variant);
+
+/* The GEMM output epilogues of kernels/narrow_f32_bf16.cc:51-123 and
+ * kernels/narrow_i32_bf16.cc:66-126 as standalone passes: fp32 -> bf16 by the
+ * to_bf16 formula; int32 -> bf16 in ONE round-to-nearest-even rounding. */
+int mx_narrow_f32_bf16(mx_stream *s, const float *in, uint16_t *out, int64_t n);
+int mx_narrow_i32_bf16(mx_stream *s, const int32_t *in, uint16_t *out, int64_t n);
+
+/* The callers either side of the encoder: EmbedService::chunk's embedding
+ * sum and mask (runtime/src/server/embed_service.cpp:29-64) and
+ * app::pool_rows (common/app_state.hpp:335-374).
+ * embed_sum: emb[b*S+s] = word[ids] + pos[s] + type0 (fp32, left to right);
+ * add_mask = m > 0 ? 0 : -1e30; kv_len[b] = 1 + last s with m > 0 (S when the
+ * whole row is masked, which attends uniformly like the reference). Every
+ * output nullable except emb. Ids outside [0, vocab) are refused by the
+ * kernel (MX_E_DATA after the stream drains). */
+int mx_embed_sum(mx_stream *s, const int32_t *ids, const float *attn_mask,
+                 int64_t B, int64_t S, int64_t hidden, const float *word,
+                 int64_t vocab, const float *pos, const float *type0,
+                 float *emb, float *add_mask, int32_t *kv_len);
+/* pool_rows: CLS (row 0; MX_E_DATA if position 0 is masked) or mean (in-order
+ * double accumulation, denominator max(sum m, 1e-9f)), then optional L2
+ * (double, clamp 1e-24). Bit-exact with the host form. Synchronises s. */
+int mx_pool_rows(mx_stream *s, const float *h, const float *attn_mask,
+                 int64_t B, int64_t S, int64_t hidden, int cls_pool,
+                 int l2_normalize, float *out);
+
+/* ---- placement registry (common/npu_ops_flag.hpp:75-214) ------------------ */
+
+/* parse_npu_ops: comma list of codes (spaces ignored, empty items skipped);
+ * an unknown code is refused by name with the list of valid ones, and the
+ * set is replaced only on success. The codes and their meaning are the
+ * reference's; "on the accelerator" means on this GPU. */
+int mx_ops_parse(const char *list);
+/* op_on_array(code): 1 if listed, 0 if not. */
+int mx_op_on_gpu(const char *code);
+/* The codes this build knows, comma-joined in table order. */
+const char *mx_op_codes(void);
+/* refuse_removed_op_flags (npu_ops_flag.hpp:238-268): MX_E_INVALID naming the
+ * replacement when `flag` is one of the removed flags, else MX_OK. */
+int mx_ops_check_flag(const char *flag);
+
+/* ---- the encoder stack ----------------------------------------------------- */
+
+typedef enum {
+  MX_ARCH_BERT = 0,  /* post-LN (BertEncoder::run, bert_encoder.cpp:1419-1598) */
+  MX_ARCH_PRELN = 1  /* pre-LN + final LN (VitEncoder::run, vit/encoder.cpp:
+                        222-431; WhisperEncoder::run, whisper/encoder.cpp:
+                        114-213)                                             */
+} mx_arch;
+
+typedef struct {
+  int arch;           /* mx_arch                                             */
+  int64_t layers, hidden, heads, head_dim, ffn;
+  float ln_eps;       /* BERT: 1e-12 (hard-coded in the reference); ViT 1e-12;
+                         Whisper 1e-5                                         */
+  float attn_scale;   /* 1 when 1/sqrt(hd) is folded into Q (the packer's
+                         convention)                                          */
+  int gelu;           /* MX_GELU_POLY (BERT host path) or MX_GELU_ERF         */
+  int cls_pool;       /* embed(): 1 = CLS, 0 = mean                           */
+  int l2_normalize;   /* embed(): L2-normalise the pooled vector              */
+  int64_t vocab, max_pos; /* embed(): word and position table rows (BERT)     */
+} mx_encoder_desc;
+
+/* Replaces the BertEncoder + Design set wiring of setup_encoder
+ * (run_setup.hpp:483-877). Tensors are then given by name with
+ * mx_encoder_set, using the container's names (runtime/src/model.cpp:
+ * 214-380): "layer.{i}.qkv", "layer.{i}.qkv.bias", "layer.{i}.attn_out",
+ * "layer.{i}.attn_out.bias", "layer.{i}.ffn_up", "layer.{i}.ffn_up.bias",
+ * "layer.{i}.ffn_down", "layer.{i}.ffn_down.bias", "layer.{i}.ln1.weight",
+ * "layer.{i}.ln1.bias", "layer.{i}.ln2.weight", "layer.{i}.ln2.bias",
+ * "embeddings.ln.weight", "embeddings.ln.bias", "embeddings.word",
+ * "embeddings.position", "embeddings.token_type" (BERT), "final_ln.weight",
+ * "final_ln.bias" (pre-LN). GEMM operands are [K, N] (fp32 values rounded
+ * to bf16 by to_bf16, or bf16 bits); everything else fp32. */
+int mx_encoder_create(mx_ctx *ctx, const mx_encoder_desc *desc,
+                      mx_encoder **out);
+void mx_encoder_destroy(mx_encoder *enc);
+int mx_encoder_set(mx_encoder *enc, const char *name, const void *host,
+                   int dtype, int64_t count);
+/* Every tensor the architecture needs has been set: MX_OK, else MX_E_STATE
+ * naming the first missing one. */
+int mx_encoder_ready(mx_encoder *enc);
+
+/* BertEncoder::run (bert_encoder.cpp:1419-1598) with every op on the GPU,
+ * activations resident: x_io fp32 [B*S, hidden] (device) goes in as the
+ * embedding sum (BERT) or the front end's output (pre-LN) and comes out as
+ * the final hidden state. add_mask fp32 [B, S] (nullable: no mask); kv_len
+ * int32 [B] (nullable). Requires every code of the path (gemm, attn, softm,
+ * layn, gelu) to be placed on the GPU, or no code at all (then the whole
+ * stack is the GPU's by construction); a partial placement is refused by
+ * name -- the per-op entry points above serve it. */
+int mx_encoder_run(mx_encoder *enc, mx_stream *s, float *x_io,
+                   const float *add_mask, const int32_t *kv_len, int64_t B,
+                   int64_t S);
+/* EmbedService::chunk minus the tokenizer (embed_service.cpp:29-64): ids and
+ * the 1/0 attention mask (device, [B, S]) -> embedding sum -> run -> pool ->
+ * out [B, hidden] (device). BERT only. Synchronises s. */
+int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids,
+                     const float *attn_mask, int64_t B, int64_t S, float *out);
+
+/* BertEncoder::Timings (runtime/include/encoders/bert_encoder.hpp:72-87) as
+ * hipEvent times of the last run, in milliseconds, when timing is on. */
+typedef struct {
+  double gemm_ms, attn_ms, ln_ms, other_ms, total_ms;
+  int64_t gemm_launches, attn_launches, ln_launches, other_launches;
+  double gemm_flop, attn_flop; /* algorithmic FLOPs of the last run           */
+} mx_timings;
+int mx_encoder_set_timing(mx_encoder *enc, int on);
+int mx_encoder_timings(mx_encoder *enc, mx_timings *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,245 @@
+// k_attn.hip -- fused masked attention on gfx950 MFMA: QK^T, additive-mask
+// softmax and PV in one pass per (sequence, head, 128-query tile); the score
+// matrix never reaches HBM.
+//
+// Each of the 4 waves owns 32 queries and computes the TRANSPOSED score tile
+// S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (keys on rows, queries on
+// columns), so every lane holds 16 scores of ONE query: the row max and sum of
+// the online softmax are lane-local plus one exchange with lane^32, and the
+// rescale of the running output is a per-lane scalar. The output is kept as
+// O^T = V^T P^T: the probabilities go straight from the score accumulator into
+// the B operand (converted to bf16) -- the keys a lane holds are a fixed
+// permutation of the MFMA's k index, and the A operand (V^T, from LDS) is read
+// in that same permutation, so no shuffle is needed.
+//
+// K is staged row-major in LDS, V transposed (Vt[hd][key], via a 4x4 register
+// transpose on the way in), both double-buffered with the mask tile; the next
+// 64-key tile is fetched into registers while the current one is consumed.
+// Softmax runs in the log2 domain (scores * scale * log2e, mask * log2e) with
+// the hardware exp2. Keys at or past kv_len[b] are skipped (whole tiles) or
+// given -inf (inside the last tile); -1e30 mask entries stay finite, so a row
+// whose keys are all masked attends uniformly, as the host softmax does.
+#include "mx_common.hpp"
+#include "mx_kernels.hpp"
+
+using namespace mxd;
+
+namespace {
+
+constexpr int BQ = 128, BKV = 64;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_fwd_k(const uint16_t *__restrict__ qkv, int64_t ldq,
+                                                  int S, int H, float scale_log2e,
+                                                  const float *__restrict__ add_mask,
+                                                  const int32_t *__restrict__ kv_len,
+                                                  uint16_t *__restrict__ ctx, int64_t ldo,
+                                                  int n_qblk) {
+  constexpr int KS = HD + 8;   // K row stride in LDS (elements)
+  constexpr int VS = BKV + 4;  // Vt row stride in LDS (elements)
+  constexpr int KCH = BKV * HD / 8 / 256;  // 16-byte K chunks per thread (1 or 2)
+  constexpr int VBLK = (BKV / 4) * (HD / 4);  // 4x4 V blocks per tile (128 or 256)
+  constexpr int NKK = HD / 16;
+  constexpr int NHT = HD / 32;
+  static_assert(KCH >= 1, "tile too small");
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][BKV * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][HD * VS];
+  __shared__ float sM[2][BKV];
+
+  const int blk = blockIdx.x;
+  const int qb = blk % n_qblk;
+  const int bh = blk / n_qblk;
+  const int h = bh % H, b = bh / H;
+  const int d = H * HD;
+  const uint16_t *base = qkv + (int64_t)b * S * ldq;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, li = lane & 31;
+  int kvl = kv_len ? kv_len[b] : S;
+  kvl = kvl < 1 ? 1 : (kvl > S ? S : kvl);
+
+  // Q fragments: B operand of S^T = K Q^T (column = query, k = head dim).
+  const int q = qb * BQ + wave * 32 + li;
+  bf16x8 qf[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (q < S) v = *(const uint4 *)(base + (int64_t)q * ldq + h * HD + kk * 16 + g * 8);
+    qf[kk] = __builtin_bit_cast(bf16x8, v);
+  }
+
+  // Register staging of one K/V/mask tile.
+  uint4 rk[KCH];
+  uint2 rv[4];
+  float rm = 0.0f;
+  const int vkb = tid & 15, vhb = tid >> 4;  // 4x4 block: keys vkb*4.., dims vhb*4..
+  auto gload = [&](int t) {
+    const int k0 = t * BKV;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + i * 256, key = c / (HD / 8), c8 = (c % (HD / 8)) * 8;
+      rk[i] = (k0 + key < S)
+                  ? *(const uint4 *)(base + (int64_t)(k0 + key) * ldq + d + h * HD + c8)
+                  : make_uint4(0, 0, 0, 0);
+    }
+    if (tid < VBLK) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + vkb * 4 + r;
+        rv[r] = key < S ? *(const uint2 *)(base + (int64_t)key * ldq + 2 * d + h * HD + vhb * 4)
+                        : make_uint2(0, 0);
+      }
+    }
+    if (tid < BKV) {
+      const int key = k0 + tid;
+      rm = key < kvl ? (add_mask ? add_mask[(int64_t)b * S + key] * 1.4426950408889634f : 0.0f)
+                     : -INFINITY;
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + i * 256, key = c / (HD / 8), c8 = (c % (HD / 8)) * 8;
+      *(uint4 *)&sK[buf][key * KS + c8] = rk[i];
+    }
+    if (tid < VBLK) {
+      // rows r (keys) x 4 dims -> 4 dims x 4 keys
+      const uint32_t r0l = rv[0].x, r0h = rv[0].y, r1l = rv[1].x, r1h = rv[1].y;
+      const uint32_t r2l = rv[2].x, r2h = rv[2].y, r3l = rv[3].x, r3h = rv[3].y;
+      uint2 c0, c1, c2, c3;
+      c0.x = (r0l & 0xFFFFu) | (r1l << 16);
+      c0.y = (r2l & 0xFFFFu) | (r3l << 16);
+      c1.x = (r0l >> 16) | (r1l & 0xFFFF0000u);
+      c1.y = (r2l >> 16) | (r3l & 0xFFFF0000u);
+      c2.x = (r0h & 0xFFFFu) | (r1h << 16);
+      c2.y = (r2h & 0xFFFFu) | (r3h << 16);
+      c3.x = (r0h >> 16) | (r1h & 0xFFFF0000u);
+      c3.y = (r2h >> 16) | (r3h & 0xFFFF0000u);
+      uint16_t *vt = &sV[buf][(vhb * 4) * VS + vkb * 4];
+      *(uint2 *)(vt) = c0;
+      *(uint2 *)(vt + VS) = c1;
+      *(uint2 *)(vt + 2 * VS) = c2;
+      *(uint2 *)(vt + 3 * VS) = c3;
+    }
+    if (tid < BKV) sM[buf][tid] = rm;
+  };
+
+  f32x16 o[NHT];
+#pragma unroll
+  for (int t = 0; t < NHT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  const int ntile = (kvl + BKV - 1) / BKV;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int t = 0; t < ntile; ++t) {
+    const int cur = t & 1;
+    if (t + 1 < ntile) gload(t + 1);
+
+    // S^T for the two 32-key halves of the tile.
+    f32x16 sc[2];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[sub][r] = 0.0f;
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk) {
+        const bf16x8 kf = *(const bf16x8 *)&sK[cur][(sub * 32 + li) * KS + kk * 16 + g * 8];
+        sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sc[sub], 0, 0, 0);
+      }
+    }
+    // Logits (log2 units) and the tile max of this lane's query.
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = sub * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+        const float v = sc[sub][r] * scale_log2e + sM[cur][key];
+        sc[sub][r] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int ht = 0; ht < NHT; ++ht)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[ht][r] *= alpha;
+
+    // Probabilities -> bf16 B operands, one per 16-key chunk.
+    bf16x8 pk[4];
+    float ps = 0.0f;
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) {
+      const int sub = ch >> 1, c = ch & 1;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const float p = __builtin_amdgcn_exp2f(sc[sub][c * 8 + jj] - m_new);
+        ps += p;
+        pk[ch][jj] = (__bf16)p;
+      }
+    }
+    l_run += ps;
+
+    // O^T += V^T P^T over the tile's 4 chunks of 16 keys.
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) {
+      const int sub = ch >> 1, c = ch & 1;
+      const int kb = sub * 32 + c * 16 + g * 4;
+#pragma unroll
+      for (int ht = 0; ht < NHT; ++ht) {
+        const uint16_t *vr = &sV[cur][(ht * 32 + li) * VS];
+        const uint2 lo = *(const uint2 *)(vr + kb);
+        const uint2 hi = *(const uint2 *)(vr + kb + 8);
+        const uint4 vv = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        o[ht] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vv), pk[ch],
+                                                        o[ht], 0, 0, 0);
+      }
+    }
+
+    if (t + 1 < ntile) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  const float l = l_run + __shfl_xor(l_run, 32);
+  const float inv = 1.0f / l;
+  if (q < S) {
+    uint16_t *dst = ctx + ((int64_t)b * S + q) * ldo + h * HD;
+#pragma unroll
+    for (int ht = 0; ht < NHT; ++ht)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int hd0 = ht * 32 + r4 * 8 + g * 4;
+        uint2 w;
+        w.x = pack_bf2(o[ht][r4 * 4 + 0] * inv, o[ht][r4 * 4 + 1] * inv);
+        w.y = pack_bf2(o[ht][r4 * 4 + 2] * inv, o[ht][r4 * 4 + 3] * inv);
+        *(uint2 *)(dst + hd0) = w;
+      }
+  }
+}
+
+}  // namespace
+
+namespace mxk {
+
+hipError_t attention(const AttnArgs &a, hipStream_t s) {
+  const int n_qblk = (int)((a.S + BQ - 1) / BQ);
+  const int64_t blocks = a.B * a.H * n_qblk;
+  const float sl2e = a.scale * 1.4426950408889634f;
+  if (a.hd == 64)
+    attn_fwd_k<64><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
+                                                   a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk);
+  else if (a.hd == 32)
+    attn_fwd_k<32><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
+                                                   a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace mxk

@@ -1,0 +1,517 @@
+// k_elem.hip -- the HBM-bound kernels of the encoder path on gfx950:
+// narrowing (fp32/int32 -> bf16), GELU, row LayerNorm with the residual add
+// fused, row softmax, the embedding sum + mask, and pooling.
+//
+// Every kernel is a coalesced streaming pass: one wave per row for the row ops
+// (rows of <= 2048 values live in registers, reductions by wave shuffles), 16-
+// or 8-byte accesses for the elementwise ops, grid-stride loops sized to fill
+// the 256 CUs.
+#include "mx_common.hpp"
+#include "mx_kernels.hpp"
+
+using namespace mxd;
+
+namespace {
+
+constexpr int kElemThreads = 256;
+
+inline int grid_for(int64_t work_items, int per_block) {
+  int64_t g = (work_items + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > 65536) g = 65536;
+  return (int)g;
+}
+
+// ---- narrowing --------------------------------------------------------------
+
+__global__ void narrow_f32_vec_k(const float4 *__restrict__ in, uint4 *__restrict__ out,
+                                 int64_t n8) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float4 a = in[2 * i], b = in[2 * i + 1];
+    uint4 o;
+    o.x = pack_bf2(a.x, a.y);
+    o.y = pack_bf2(a.z, a.w);
+    o.z = pack_bf2(b.x, b.y);
+    o.w = pack_bf2(b.z, b.w);
+    out[i] = o;
+  }
+}
+
+__global__ void narrow_f32_scalar_k(const float *__restrict__ in, uint16_t *__restrict__ out,
+                                    int64_t lo, int64_t n) {
+  for (int64_t i = lo + blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = f2bf(in[i]);
+}
+
+// int32 -> bf16 in one nearest-even rounding of the integer itself: keep the
+// top 8 significant bits of |v|, round on the dropped bits.
+__device__ __forceinline__ uint16_t i32_to_bf16(int32_t v) {
+  if (v == 0) return 0;
+  const uint32_t sign = v < 0 ? 0x8000u : 0u;
+  const uint32_t a = v < 0 ? (uint32_t)(-(int64_t)v) : (uint32_t)v;
+  int e = 31 - __clz(a);
+  uint32_t mant;
+  if (e <= 7) {
+    mant = a << (7 - e);
+  } else {
+    const int sh = e - 7;
+    mant = a >> sh;
+    const uint32_t rem = a & ((1u << sh) - 1u);
+    const uint32_t half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (mant & 1u))) ++mant;
+    if (mant == 256u) {
+      mant = 128u;
+      ++e;
+    }
+  }
+  return (uint16_t)(sign | ((uint32_t)(e + 127) << 7) | (mant & 0x7Fu));
+}
+
+__global__ void narrow_i32_vec_k(const int4 *__restrict__ in, uint4 *__restrict__ out,
+                                 int64_t n8) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int4 a = in[2 * i], b = in[2 * i + 1];
+    uint4 o;
+    o.x = (uint32_t)i32_to_bf16(a.x) | ((uint32_t)i32_to_bf16(a.y) << 16);
+    o.y = (uint32_t)i32_to_bf16(a.z) | ((uint32_t)i32_to_bf16(a.w) << 16);
+    o.z = (uint32_t)i32_to_bf16(b.x) | ((uint32_t)i32_to_bf16(b.y) << 16);
+    o.w = (uint32_t)i32_to_bf16(b.z) | ((uint32_t)i32_to_bf16(b.w) << 16);
+    out[i] = o;
+  }
+}
+
+__global__ void narrow_i32_scalar_k(const int32_t *__restrict__ in, uint16_t *__restrict__ out,
+                                    int64_t lo, int64_t n) {
+  for (int64_t i = lo + blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = i32_to_bf16(in[i]);
+}
+
+// ---- GELU -------------------------------------------------------------------
+
+// gelu_erf.cc:79-145: A&S 7.1.26 erf with the AIE exp2, unfused steps.
+__device__ __forceinline__ float gelu_erf_as(float x) {
+  const float u = __fmul_rn(x, 0.70710678118654752440f);
+  const float au = fabsf(u);
+  const float t = __fdiv_rn(1.0f, __fadd_rn(1.0f, __fmul_rn(0.3275911f, au)));
+  float p = 1.061405429f;
+  p = __fadd_rn(__fmul_rn(p, t), -1.453152027f);
+  p = __fadd_rn(__fmul_rn(p, t), 1.421413741f);
+  p = __fadd_rn(__fmul_rn(p, t), -0.284496736f);
+  p = __fadd_rn(__fmul_rn(p, t), 0.254829592f);
+  float z = __fmul_rn(__fsub_rn(0.0f, __fmul_rn(u, u)), 1.4426950408889634f);
+  z = z > -125.0f ? z : -125.0f;
+  const float ex = exp2_poly_aie(z);
+  const float eabs = __fsub_rn(1.0f, __fmul_rn(__fmul_rn(t, p), ex));
+  return __fadd_rn(__fmul_rn(x, 0.5f), __fmul_rn(__fmul_rn(fabsf(x), 0.5f), eabs));
+}
+
+__device__ __forceinline__ float gelu_variant(float v, int variant) {
+  if (variant == 0) return gelu_poly(v);
+  if (variant == 1) return gelu_erf(v);
+  return gelu_erf_as(v);
+}
+
+template <bool IN_BF, bool OUT_BF>
+__global__ void gelu_k(const void *__restrict__ x, void *__restrict__ y, int64_t n,
+                       int variant) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = IN_BF ? bf2f(((const uint16_t *)x)[i]) : ((const float *)x)[i];
+    const float r = gelu_variant(v, variant);
+    if (OUT_BF)
+      ((uint16_t *)y)[i] = f2bf(r);
+    else
+      ((float *)y)[i] = r;
+  }
+}
+
+// ---- LayerNorm: one wave per row, NP pairs of columns per lane --------------
+
+template <int NP>
+__global__ __launch_bounds__(256) void layernorm_wave_k(
+    const void *__restrict__ x, int x_bf, const void *__restrict__ y, int y_bf,
+    const float *__restrict__ gamma, const float *__restrict__ beta, float eps,
+    int64_t rows, float *out_f32, uint16_t *out_bf16) {
+  constexpr int cols = NP * 128;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float v[2 * NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int64_t off = row * cols + i * 128 + lane * 2;
+    float a0, a1;
+    if (x_bf) {
+      const uint32_t p = *(const uint32_t *)((const uint16_t *)x + off);
+      a0 = bf2f(p & 0xFFFFu);
+      a1 = bf2f(p >> 16);
+    } else {
+      const float2 p = *(const float2 *)((const float *)x + off);
+      a0 = p.x;
+      a1 = p.y;
+    }
+    if (y) {
+      if (y_bf) {
+        const uint32_t p = *(const uint32_t *)((const uint16_t *)y + off);
+        a0 += bf2f(p & 0xFFFFu);
+        a1 += bf2f(p >> 16);
+      } else {
+        const float2 p = *(const float2 *)((const float *)y + off);
+        a0 += p.x;
+        a1 += p.y;
+      }
+    }
+    v[2 * i] = a0;
+    v[2 * i + 1] = a1;
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2 * NP; ++i) s += v[i];
+  const float mean = wave_sum(s) / (float)cols;
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2 * NP; ++i) {
+    const float d = v[i] - mean;
+    q = __builtin_fmaf(d, d, q);
+  }
+  const float var = wave_sum(q) / (float)cols;
+  const float is = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int c = i * 128 + lane * 2;
+    const float2 g = *(const float2 *)(gamma + c);
+    const float2 b = *(const float2 *)(beta + c);
+    const float r0 = __builtin_fmaf((v[2 * i] - mean) * is, g.x, b.x);
+    const float r1 = __builtin_fmaf((v[2 * i + 1] - mean) * is, g.y, b.y);
+    const int64_t off = row * cols + c;
+    if (out_f32) *(float2 *)(out_f32 + off) = make_float2(r0, r1);
+    if (out_bf16) *(uint32_t *)(out_bf16 + off) = pack_bf2(r0, r1);
+  }
+}
+
+// Any width: one 256-thread block per row, two passes through global memory.
+__global__ __launch_bounds__(256) void layernorm_any_k(
+    const void *__restrict__ x, int x_bf, const void *__restrict__ y, int y_bf,
+    const float *__restrict__ gamma, const float *__restrict__ beta, float eps,
+    int64_t rows, int64_t cols, float *out_f32, uint16_t *out_bf16) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  auto load = [&](int64_t c) {
+    const int64_t off = row * cols + c;
+    float a = x_bf ? bf2f(((const uint16_t *)x)[off]) : ((const float *)x)[off];
+    if (y) a += y_bf ? bf2f(((const uint16_t *)y)[off]) : ((const float *)y)[off];
+    return a;
+  };
+  auto block_sum = [&](float s) {
+    s = wave_sum(s);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+  };
+  float s = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) s += load(c);
+  const float mean = block_sum(s) / (float)cols;
+  float q = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float d = load(c) - mean;
+    q = __builtin_fmaf(d, d, q);
+  }
+  const float var = block_sum(q) / (float)cols;
+  const float is = 1.0f / sqrtf(var + eps);
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float r = __builtin_fmaf((load(c) - mean) * is, gamma[c], beta[c]);
+    if (out_f32) out_f32[row * cols + c] = r;
+    if (out_bf16) out_bf16[row * cols + c] = f2bf(r);
+  }
+}
+
+// ---- softmax: one wave per row, NV values per lane (cols <= 64 * NV) --------
+
+template <int NV>
+__global__ __launch_bounds__(256) void softmax_wave_k(void *x, int bf, int64_t rows,
+                                                      int64_t cols, int64_t stride,
+                                                      const float *__restrict__ mask,
+                                                      int64_t rpm, int variant) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float *mk = mask ? mask + (row / rpm) * cols : nullptr;
+  float v[NV];
+  float m = -INFINITY;
+  const float lo_aie = bf2f(f2bf(-1.0e30f));
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = lane + 64 * i;
+    float a = -INFINITY;
+    if (c < cols) {
+      a = bf ? bf2f(((const uint16_t *)x)[row * stride + c]) : ((const float *)x)[row * stride + c];
+      if (variant == 2) {
+        a = a > lo_aie ? a : lo_aie;  // softmax.cc clamp 1, in bf16
+      } else if (mk) {
+        a += mk[c];
+      }
+      m = fmaxf(m, a);
+    }
+    v[i] = a;
+  }
+  m = wave_max(m);
+  if (variant == 2) m = fmaxf(m, -1.0e30f);  // softmax.cc's running max starts at -1e30
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = lane + 64 * i;
+    float e = 0.0f;
+    if (c < cols) {
+      if (variant == 0) {
+        float a = (v[i] - m) * 1.4426950408889634f;
+        a = a > -120.0f ? a : -120.0f;
+        e = exp2_poly(a);
+      } else if (variant == 1) {
+        e = expf(v[i] - m);
+      } else {
+        float d = v[i] - m;
+        d = d > -100.0f ? d : -100.0f;
+        float a = __fmul_rn(d, 1.4426950408889634f);
+        a = a > -120.0f ? a : -120.0f;
+        e = bf2f(f2bf(exp2_poly_aie(a)));
+      }
+      s += e;
+    }
+    v[i] = e;
+  }
+  s = wave_sum(s);
+  const float inv = variant == 1 ? (s > 0.0f ? 1.0f / s : 0.0f) : 1.0f / s;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = lane + 64 * i;
+    if (c < cols) {
+      const float r = v[i] * inv;
+      if (bf)
+        ((uint16_t *)x)[row * stride + c] = f2bf(r);
+      else
+        ((float *)x)[row * stride + c] = r;
+    }
+  }
+}
+
+// ---- embedding sum + mask ---------------------------------------------------
+
+__global__ __launch_bounds__(256) void embed_sum_k(const int32_t *__restrict__ ids, int64_t rows,
+                                                   int64_t S, int64_t d,
+                                                   const float *__restrict__ word, int64_t vocab,
+                                                   const float *__restrict__ pos,
+                                                   const float *__restrict__ type0,
+                                                   float *__restrict__ emb, int *err) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int32_t id = ids[r];
+  const int64_t s = r % S;
+  if (id < 0 || id >= vocab) {
+    if (lane == 0) atomicOr(err, 1);
+    for (int64_t c = lane; c < d; c += 64) emb[r * d + c] = 0.0f;
+    return;
+  }
+  const float *wv = word + (int64_t)id * d;
+  const float *pv = pos + s * d;
+  for (int64_t c = lane; c < d; c += 64) emb[r * d + c] = (wv[c] + pv[c]) + type0[c];
+}
+
+__global__ __launch_bounds__(256) void mask_k(const float *__restrict__ am, int64_t S,
+                                              float *add_mask, int32_t *kv_len) {
+  __shared__ int last;
+  if (threadIdx.x == 0) last = 0;
+  __syncthreads();
+  const int64_t b = blockIdx.x;
+  int mine = 0;
+  for (int64_t s = threadIdx.x; s < S; s += blockDim.x) {
+    const float m = am[b * S + s];
+    if (add_mask) add_mask[b * S + s] = m > 0.0f ? 0.0f : -1.0e30f;
+    if (m > 0.0f) mine = (int)s + 1;
+  }
+  atomicMax(&last, mine);
+  __syncthreads();
+  if (threadIdx.x == 0 && kv_len) kv_len[b] = last > 0 ? last : (int32_t)S;
+}
+
+// ---- pooling (app_state.hpp:335-374), bit-exact with the host form ----------
+
+__global__ __launch_bounds__(256) void pool_k(const float *__restrict__ h,
+                                              const float *__restrict__ am, int64_t S,
+                                              int64_t d, int cls, int l2, float *out,
+                                              int *err) {
+  extern __shared__ double acc[];
+  __shared__ double nrm_s;
+  __shared__ float denom_s;
+  const int64_t b = blockIdx.x;
+  const float *amb = am + b * S;
+  const float *hb = h + b * S * d;
+  if (cls) {
+    if (amb[0] == 0.0f) {
+      if (threadIdx.x == 0) atomicOr(err, 2);
+      for (int64_t c = threadIdx.x; c < d; c += blockDim.x) out[b * d + c] = 0.0f;
+      return;
+    }
+    for (int64_t c = threadIdx.x; c < d; c += blockDim.x) acc[c] = (double)hb[c];
+  } else {
+    if (threadIdx.x == 0) {
+      float den = 0.0f;
+      for (int64_t s = 0; s < S; ++s) den += amb[s];
+      denom_s = den > 1e-9f ? den : 1e-9f;
+    }
+    __syncthreads();
+    for (int64_t c = threadIdx.x; c < d; c += blockDim.x) {
+      double a = 0.0;
+      for (int64_t s = 0; s < S; ++s) {
+        const float m = amb[s];
+        if (m == 0.0f) continue;
+        a += (double)(__fmul_rn(hb[s * d + c], m));
+      }
+      acc[c] = a / (double)denom_s;
+    }
+  }
+  __syncthreads();
+  if (l2) {
+    if (threadIdx.x == 0) {
+      double n = 0.0;
+      for (int64_t c = 0; c < d; ++c) n = __builtin_fma(acc[c], acc[c], n);
+      nrm_s = sqrt(n > 1e-24 ? n : 1e-24);
+    }
+    __syncthreads();
+    const double nrm = nrm_s;
+    for (int64_t c = threadIdx.x; c < d; c += blockDim.x) out[b * d + c] = (float)(acc[c] / nrm);
+  } else {
+    for (int64_t c = threadIdx.x; c < d; c += blockDim.x) out[b * d + c] = (float)acc[c];
+  }
+}
+
+}  // namespace
+
+namespace mxk {
+
+hipError_t narrow_f32_bf16(const float *in, uint16_t *out, int64_t n, hipStream_t s) {
+  int64_t done = 0;
+  if (((uintptr_t)in % 16 == 0) && ((uintptr_t)out % 16 == 0) && n >= 8) {
+    const int64_t n8 = n / 8;
+    narrow_f32_vec_k<<<grid_for(n8, kElemThreads), kElemThreads, 0, s>>>(
+        (const float4 *)in, (uint4 *)out, n8);
+    done = n8 * 8;
+  }
+  if (done < n)
+    narrow_f32_scalar_k<<<grid_for(n - done, kElemThreads), kElemThreads, 0, s>>>(in, out, done,
+                                                                                  n);
+  return hipGetLastError();
+}
+
+hipError_t narrow_i32_bf16(const int32_t *in, uint16_t *out, int64_t n, hipStream_t s) {
+  int64_t done = 0;
+  if (((uintptr_t)in % 16 == 0) && ((uintptr_t)out % 16 == 0) && n >= 8) {
+    const int64_t n8 = n / 8;
+    narrow_i32_vec_k<<<grid_for(n8, kElemThreads), kElemThreads, 0, s>>>((const int4 *)in,
+                                                                        (uint4 *)out, n8);
+    done = n8 * 8;
+  }
+  if (done < n)
+    narrow_i32_scalar_k<<<grid_for(n - done, kElemThreads), kElemThreads, 0, s>>>(in, out, done,
+                                                                                  n);
+  return hipGetLastError();
+}
+
+hipError_t gelu(const void *x, int x_bf, void *y, int y_bf, int64_t n, int variant,
+                hipStream_t s) {
+  const int g = grid_for(n, kElemThreads);
+  if (x_bf && y_bf)
+    gelu_k<true, true><<<g, kElemThreads, 0, s>>>(x, y, n, variant);
+  else if (x_bf)
+    gelu_k<true, false><<<g, kElemThreads, 0, s>>>(x, y, n, variant);
+  else if (y_bf)
+    gelu_k<false, true><<<g, kElemThreads, 0, s>>>(x, y, n, variant);
+  else
+    gelu_k<false, false><<<g, kElemThreads, 0, s>>>(x, y, n, variant);
+  return hipGetLastError();
+}
+
+hipError_t layernorm(const void *x, int x_bf, const void *y, int y_bf, const float *gamma,
+                     const float *beta, float eps, int64_t rows, int64_t cols, float *out_f32,
+                     uint16_t *out_bf16, hipStream_t s) {
+  const int rpb = 4;  // rows (waves) per block
+  const int g = (int)((rows + rpb - 1) / rpb);
+  bool aligned = ((uintptr_t)x % 8 == 0) && (!y || (uintptr_t)y % 8 == 0) &&
+                 ((uintptr_t)gamma % 8 == 0) && ((uintptr_t)beta % 8 == 0) &&
+                 (!out_f32 || (uintptr_t)out_f32 % 8 == 0) &&
+                 (!out_bf16 || (uintptr_t)out_bf16 % 4 == 0);
+  if (aligned && cols % 128 == 0 && rows <= (int64_t)1 << 36) {
+#define MX_LN_CASE(np)                                                                     \
+  case np:                                                                                 \
+    layernorm_wave_k<np><<<g, 256, 0, s>>>(x, x_bf, y, y_bf, gamma, beta, eps, rows,      \
+                                           out_f32, out_bf16);                            \
+    return hipGetLastError();
+    switch (cols / 128) {
+      MX_LN_CASE(1)
+      MX_LN_CASE(2)
+      MX_LN_CASE(3)
+      MX_LN_CASE(4)
+      MX_LN_CASE(5)
+      MX_LN_CASE(6)
+      MX_LN_CASE(7)
+      MX_LN_CASE(8)
+      MX_LN_CASE(10)
+      MX_LN_CASE(12)
+      MX_LN_CASE(16)
+      default:
+        break;
+    }
+#undef MX_LN_CASE
+  }
+  layernorm_any_k<<<(unsigned)rows, 256, 0, s>>>(x, x_bf, y, y_bf, gamma, beta, eps, rows, cols,
+                                                 out_f32, out_bf16);
+  return hipGetLastError();
+}
+
+hipError_t softmax_rows(void *x, int bf, int64_t rows, int64_t cols, int64_t stride,
+                        const float *mask, int64_t rpm, int variant, hipStream_t s) {
+  const int g = (int)((rows + 3) / 4);
+  const int64_t nv = (cols + 63) / 64;
+#define MX_SM_CASE(NV)                                                                      \
+  if (nv <= NV) {                                                                           \
+    softmax_wave_k<NV><<<g, 256, 0, s>>>(x, bf, rows, cols, stride, mask, rpm, variant);   \
+    return hipGetLastError();                                                               \
+  }
+  MX_SM_CASE(2)
+  MX_SM_CASE(4)
+  MX_SM_CASE(8)
+  MX_SM_CASE(16)
+  MX_SM_CASE(32)
+  MX_SM_CASE(64)
+#undef MX_SM_CASE
+  return hipErrorInvalidValue;
+}
+
+hipError_t embed_sum(const int32_t *ids, int64_t B, int64_t S, int64_t d, const float *word,
+                     int64_t vocab, const float *pos, const float *type0, float *emb, int *err,
+                     hipStream_t s) {
+  const int64_t rows = B * S;
+  embed_sum_k<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(ids, rows, S, d, word, vocab, pos,
+                                                         type0, emb, err);
+  return hipGetLastError();
+}
+
+hipError_t mask_build(const float *am, int64_t B, int64_t S, float *add_mask, int32_t *kv_len,
+                      hipStream_t s) {
+  mask_k<<<(unsigned)B, 256, 0, s>>>(am, S, add_mask, kv_len);
+  return hipGetLastError();
+}
+
+hipError_t pool_rows(const float *h, const float *am, int64_t B, int64_t S, int64_t d, int cls,
+                     int l2, float *out, int *err, hipStream_t s) {
+  pool_k<<<(unsigned)B, 256, (size_t)d * sizeof(double), s>>>(h, am, S, d, cls, l2, out, err);
+  return hipGetLastError();
+}
+
+}  // namespace mxk

@@ -1,0 +1,185 @@
+// k_gemm.hip -- the unified bf16 GEMM of the encoder path on gfx950 MFMA.
+//
+// C[M, N] = epilogue(A[M, K] @ W[K, N] + bias) (+ residual), A bf16 row-major,
+// W held as its transpose Wt[N, K] (K contiguous, the layout mx_stage_weight
+// writes once) so both operands are read the same way. fp32 accumulation in
+// v_mfma_f32_32x32x16_bf16; one rounding to bf16 (the host's to_bf16
+// formula) at the very end when C is bf16 -- the single-narrowing contract of
+// kernels/narrow_f32_bf16.cc, here fused into the store.
+//
+// Tiling: a BM x BN block tile over (BM/WM) x (BN/WN) waves, each wave owning
+// a WM x WN sub-tile of (WM/32) x (WN/32) MFMA tiles. K advances BK at a time
+// through two LDS buffers: the next K-slab is fetched from HBM into registers
+// while the MFMAs consume the current one, then written to the other buffer,
+// so there is one barrier per slab. LDS rows are padded by 16 bytes, which
+// makes the 16-byte fragment reads of 8 consecutive rows hit distinct banks.
+//
+// Blocks are numbered so that each XCD (workgroups go round-robin over the 8
+// XCDs) owns a contiguous run of tiles in row-major (m, n) order: the blocks
+// resident on one XCD share A row-panels and the whole of W in its L2.
+#include "mx_common.hpp"
+#include "mx_kernels.hpp"
+
+using namespace mxd;
+
+namespace {
+
+template <int BM, int BN, int BK, int WM, int WN>
+struct GemmCfg {
+  static constexpr int NWM = BM / WM, NWN = BN / WN;
+  static constexpr int NT = NWM * NWN * 64;
+  static constexpr int LDK = BK + 8;  // padded LDS row, elements
+  static constexpr int TM = WM / 32, TN = WN / 32;
+  static constexpr int CPR = BK / 8;  // 16-byte chunks per row
+  static constexpr int A_PER_T = BM * CPR / NT;
+  static constexpr int B_PER_T = BN * CPR / NT;
+  static constexpr int LDS_BYTES = 2 * (BM + BN) * LDK * 2;
+  static_assert(BM * CPR % NT == 0 && BN * CPR % NT == 0, "chunks must divide threads");
+  static_assert(WM % 32 == 0 && WN % 32 == 0 && BK % 16 == 0, "MFMA tile shape");
+};
+
+__device__ __forceinline__ float apply_epi(float v, int epi) {
+  if (epi == 1) return gelu_poly(v);
+  if (epi == 2) return gelu_erf(v);
+  return v;
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_bf16_k(
+    const uint16_t *__restrict__ A, int64_t lda, const uint16_t *__restrict__ Wt, int M, int N,
+    int K, const float *__restrict__ bias, int epi, const float *residual, void *C, int c_bf16,
+    int64_t ldc, int tiles_m, int tiles_n) {
+  using Cfg = GemmCfg<BM, BN, BK, WM, WN>;
+  constexpr int LDK = Cfg::LDK, NT = Cfg::NT, CPR = Cfg::CPR;
+  constexpr int TM = Cfg::TM, TN = Cfg::TN;
+  __shared__ __attribute__((aligned(16))) uint16_t smA[2][BM * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t smB[2][BN * LDK];
+
+  // XCD-aware tile order.
+  const int total = tiles_m * tiles_n;
+  int tile = blockIdx.x;
+  if ((total & 7) == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+  const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / Cfg::NWN, wn = wave - wm * Cfg::NWN;
+
+  uint4 ra[Cfg::A_PER_T], rb[Cfg::B_PER_T];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < Cfg::A_PER_T; ++i) {
+      const int c = tid + i * NT, r = c / CPR, kc = (c - r * CPR) * 8;
+      const int gr = m0 + r, gk = k0 + kc;
+      ra[i] = (gr < M && gk < K) ? *(const uint4 *)(A + (int64_t)gr * lda + gk)
+                                 : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < Cfg::B_PER_T; ++i) {
+      const int c = tid + i * NT, r = c / CPR, kc = (c - r * CPR) * 8;
+      const int gr = n0 + r, gk = k0 + kc;
+      rb[i] = (gr < N && gk < K) ? *(const uint4 *)(Wt + (int64_t)gr * K + gk)
+                                 : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < Cfg::A_PER_T; ++i) {
+      const int c = tid + i * NT, r = c / CPR, kc = (c - r * CPR) * 8;
+      *(uint4 *)&smA[buf][r * LDK + kc] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < Cfg::B_PER_T; ++i) {
+      const int c = tid + i * NT, r = c / CPR, kc = (c - r * CPR) * 8;
+      *(uint4 *)&smB[buf][r * LDK + kc] = rb[i];
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int nk = (K + BK - 1) / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int frow = lane & 31, fk = (lane >> 5) * 8;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      bf16x8 af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *(const bf16x8 *)&smA[cur][(wm * WM + i * 32 + frow) * LDK + kk * 16 + fk];
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bfr[j] = *(const bf16x8 *)&smB[cur][(wn * WN + j * 32 + frow) * LDK + kk * 16 + fk];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue. 32x32 accumulator layout: lane holds column (lane & 31) and rows
+  // 8*(r/4) + 4*(lane/32) + (r%4), r = 0..15.
+  const int rbase = (lane >> 5) * 4;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int col = n0 + wn * WN + j * 32 + (lane & 31);
+    if (col >= N) continue;
+    const float bj = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + rbase + (r & 3);
+        if (row >= M) continue;
+        float v = apply_epi(acc[i][j][r] + bj, epi);
+        const int64_t off = (int64_t)row * ldc + col;
+        if (residual) v += residual[off];
+        if (c_bf16)
+          ((uint16_t *)C)[off] = f2bf(v);
+        else
+          ((float *)C)[off] = v;
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+hipError_t launch(const mxk::GemmArgs &a, hipStream_t s) {
+  using Cfg = GemmCfg<BM, BN, BK, WM, WN>;
+  const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
+  const int blocks = tiles_m * tiles_n;
+  gemm_bf16_k<BM, BN, BK, WM, WN><<<blocks, Cfg::NT, 0, s>>>(
+      a.A, a.lda, a.Wt, (int)a.M, (int)a.N, (int)a.K, a.bias, a.epilogue, a.residual, a.C,
+      a.c_bf16, a.ldc, tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+namespace mxk {
+
+const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
+  (void)M;
+  (void)N;
+  (void)K;
+  return "128x128x64_w64x64";
+}
+
+hipError_t gemm(const GemmArgs &a, hipStream_t s) {
+  return launch<128, 128, 64, 64, 64>(a, s);
+}
+
+}  // namespace mxk

@@ -1,0 +1,547 @@
+// mx_abi.cpp -- the C ABI: device, streams, memory, weight staging, the
+// per-op entry points (validated, refused by name) and the placement registry.
+#include "mx_internal.hpp"
+#include "mx_kernels.hpp"
+
+#include <algorithm>
+#include <cctype>
+#include <cmath>
+#include <cstring>
+#include <set>
+#include <sstream>
+
+namespace mx {
+
+static thread_local std::string t_err;
+
+void set_error(const std::string &msg) { t_err = msg; }
+void clear_error() { t_err.clear(); }
+
+int fail(int code, const std::string &msg) {
+  set_error(msg);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(MX_E_DEVICE, std::string(what) + ": " + hipGetErrorName(e) + " (" +
+                               hipGetErrorString(e) + ")");
+}
+
+int use_device(const mx_ctx *ctx) {
+  if (!ctx) return fail(MX_E_INVALID, "null context");
+  const hipError_t e = hipSetDevice(ctx->device);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "hipSetDevice");
+}
+
+static inline uint16_t to_bf16(float x) {
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  return static_cast<uint16_t>((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+int stage_panel(mx_ctx *ctx, const void *kn_host, int dtype, int64_t K, int64_t N,
+                uint16_t **out) {
+  if (!kn_host) return fail(MX_E_INVALID, "stage_weight: null host operand");
+  if (K <= 0 || N <= 0) return fail(MX_E_INVALID, "stage_weight: zero dimension");
+  if (K % 8) {
+    return fail(MX_E_INVALID, "stage_weight: K = " + std::to_string(K) +
+                                  " is not a multiple of 8 (the GEMM reads K in 16-byte "
+                                  "chunks; the reference enforces hidden % 8 == 0 too)");
+  }
+  if (dtype != MX_F32 && dtype != MX_BF16)
+    return fail(MX_E_INVALID, "stage_weight: dtype must be MX_F32 or MX_BF16");
+  std::vector<uint16_t> panel(static_cast<size_t>(K) * N);
+  for (int64_t k = 0; k < K; ++k)
+    for (int64_t n = 0; n < N; ++n) {
+      const size_t src = static_cast<size_t>(k) * N + n;
+      panel[static_cast<size_t>(n) * K + k] =
+          dtype == MX_F32 ? to_bf16(static_cast<const float *>(kn_host)[src])
+                          : static_cast<const uint16_t *>(kn_host)[src];
+    }
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, panel.size() * 2);
+  if (e != hipSuccess) return hip_fail(e, "stage_weight: hipMalloc");
+  e = hipMemcpy(p, panel.data(), panel.size() * 2, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(e, "stage_weight: hipMemcpy");
+  }
+  *out = static_cast<uint16_t *>(p);
+  return MX_OK;
+}
+
+static bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t lda,
+                 const uint16_t *Wt, int64_t N, const float *bias, int epilogue,
+                 const float *residual, void *C, int c_dtype, int64_t ldc) {
+  if (!s) return fail(MX_E_INVALID, "gemm: null stream");
+  if (!A || !Wt || !C) return fail(MX_E_INVALID, "gemm: null A, weight or C");
+  if (M <= 0 || N <= 0 || K <= 0) return fail(MX_E_INVALID, "gemm: zero dimension");
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2)
+    return fail(MX_E_INVALID, "gemm: dimension beyond 2^30");
+  if (K % 8 || lda % 8)
+    return fail(MX_E_INVALID, "gemm: K (" + std::to_string(K) + ") and lda (" +
+                                  std::to_string(lda) + ") must be multiples of 8");
+  if (lda < K) return fail(MX_E_INVALID, "gemm: lda < K");
+  if (ldc < N) return fail(MX_E_INVALID, "gemm: ldc < N");
+  if (!aligned(A, 16) || !aligned(Wt, 16))
+    return fail(MX_E_INVALID, "gemm: A and the weight panel must be 16-byte aligned");
+  if (epilogue < MX_EPI_NONE || epilogue > MX_EPI_GELU_ERF)
+    return fail(MX_E_INVALID, "gemm: unknown epilogue " + std::to_string(epilogue));
+  if (c_dtype != MX_F32 && c_dtype != MX_BF16)
+    return fail(MX_E_INVALID, "gemm: C dtype must be MX_F32 or MX_BF16");
+  mxk::GemmArgs a{A, lda, Wt, M, N, K, bias, epilogue, residual, C, c_dtype == MX_BF16 ? 1 : 0,
+                  ldc};
+  const hipError_t e = mxk::gemm(a, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "gemm launch");
+}
+
+int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
+                      int64_t H, int64_t hd, float scale, const float *add_mask,
+                      const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx) {
+  if (!s) return fail(MX_E_INVALID, "attention: null stream");
+  if (!qkv || !ctx) return fail(MX_E_INVALID, "attention: null qkv or ctx");
+  if (B <= 0 || S <= 0 || H <= 0) return fail(MX_E_INVALID, "attention: zero dimension");
+  if (hd != 32 && hd != 64)
+    return fail(MX_E_UNSUPPORTED, "attention: head_dim " + std::to_string(hd) +
+                                      " (this kernel is built for 32 and 64)");
+  if (ld_qkv < 3 * H * hd || ld_qkv % 8)
+    return fail(MX_E_INVALID, "attention: qkv row stride " + std::to_string(ld_qkv) +
+                                  " cannot hold Q|K|V of " + std::to_string(H * hd) +
+                                  " each, or is not a multiple of 8");
+  if (ld_ctx < H * hd || ld_ctx % 4)
+    return fail(MX_E_INVALID, "attention: ctx row stride too small or not a multiple of 4");
+  if (!aligned(qkv, 16) || !aligned(ctx, 8))
+    return fail(MX_E_INVALID, "attention: qkv must be 16-byte and ctx 8-byte aligned");
+  if (B * H * ((S + 127) / 128) > INT32_MAX || S > INT32_MAX / 4)
+    return fail(MX_E_INVALID, "attention: grid too large");
+  if (!std::isfinite(scale)) return fail(MX_E_INVALID, "attention: non-finite scale");
+  mxk::AttnArgs a{qkv, ld_qkv, B, S, H, hd, scale, add_mask, kv_len, ctx, ld_ctx};
+  const hipError_t e = mxk::attention(a, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "attention launch");
+}
+
+int take_data_error(mx_stream *s, int *flags) {
+  int h = 0;
+  hipError_t e = hipMemcpyAsync(&h, s->err_dev, sizeof(int), hipMemcpyDeviceToHost, s->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+  if (e != hipSuccess) return hip_fail(e, "reading the refusal flag");
+  *flags = h;
+  if (h) {
+    e = hipMemsetAsync(s->err_dev, 0, sizeof(int), s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(e, "clearing the refusal flag");
+  }
+  return MX_OK;
+}
+
+// ---- placement registry ---------------------------------------------------
+
+struct OpCode {
+  const char *code;
+  const char *long_name;
+};
+
+// The reference's codes, in its table order (npu_ops_flag.hpp:105-142).
+static const OpCode kOps[] = {
+    {"gemm", "the per-layer GEMMs"},
+    {"gelu", "GELU"},
+    {"layn", "LayerNorm"},
+    {"softm", "softmax"},
+    {"conv", "conv1d (Whisper's audio front end)"},
+    {"attn", "attention (QK^T, softmax, softmax.V fused)"},
+    {"mproj", "Whisper's mel filter bank, as a GEMM"},
+    {"fft", "Whisper's 400-point transform, as a GEMM"},
+    {"logit", "the vocabulary projection, as a GEMM"},
+};
+
+static std::mutex g_ops_mu;
+static std::set<std::string> g_ops;
+
+static std::string codes_joined() {
+  std::string s;
+  for (const auto &o : kOps) {
+    if (!s.empty()) s += ", ";
+    s += o.code;
+  }
+  return s;
+}
+
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" {
+
+const char *mx_last_error(void) { return t_err.c_str(); }
+
+int mx_version(void) { return 1; }
+
+int mx_create(int device, mx_ctx **out) {
+  clear_error();
+  if (!out) return fail(MX_E_INVALID, "mx_create: null out");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  if (device < 0 || device >= n)
+    return fail(MX_E_INVALID, "mx_create: device " + std::to_string(device) + " of " +
+                                  std::to_string(n) + " visible");
+  hipDeviceProp_t p;
+  e = hipGetDeviceProperties(&p, device);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+    return fail(MX_E_UNSUPPORTED, std::string("mx_create: device is ") + p.gcnArchName +
+                                      "; this backend is built for gfx950 (MI355X) only");
+  auto *c = new mx_ctx();
+  c->device = device;
+  c->props.device = device;
+  c->props.compute_units = p.multiProcessorCount;
+  c->props.clock_mhz = p.clockRate / 1000;
+  c->props.hbm_bytes = static_cast<int64_t>(p.totalGlobalMem);
+  std::snprintf(c->props.arch, sizeof c->props.arch, "%s", p.gcnArchName);
+  c->props.bf16_dense_tflops =
+      static_cast<double>(p.multiProcessorCount) * 4096.0 * (p.clockRate * 1e3) / 1e12;
+  *out = c;
+  return MX_OK;
+}
+
+void mx_destroy(mx_ctx *ctx) {
+  if (!ctx) return;
+  if (use_device(ctx) == MX_OK)
+    for (auto &w : ctx->slots)
+      if (w.wt) (void)hipFree(w.wt);
+  delete ctx;
+}
+
+int mx_device_props_get(mx_ctx *ctx, mx_device_props *out) {
+  if (!ctx || !out) return fail(MX_E_INVALID, "mx_device_props_get: null argument");
+  *out = ctx->props;
+  return MX_OK;
+}
+
+int mx_stream_create(mx_ctx *ctx, mx_stream **out) {
+  clear_error();
+  if (!out) return fail(MX_E_INVALID, "mx_stream_create: null out");
+  *out = nullptr;
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  auto *s = new mx_stream();
+  s->ctx = ctx;
+  hipError_t e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete s;
+    return hip_fail(e, "hipStreamCreate");
+  }
+  e = hipMalloc(&s->err_dev, sizeof(int));
+  if (e == hipSuccess) e = hipMemset(s->err_dev, 0, sizeof(int));
+  if (e != hipSuccess) {
+    (void)hipStreamDestroy(s->stream);
+    delete s;
+    return hip_fail(e, "stream refusal flag");
+  }
+  *out = s;
+  return MX_OK;
+}
+
+void mx_stream_destroy(mx_stream *s) {
+  if (!s) return;
+  if (use_device(s->ctx) == MX_OK) {
+    (void)hipStreamSynchronize(s->stream);
+    (void)hipFree(s->err_dev);
+    (void)hipStreamDestroy(s->stream);
+  }
+  delete s;
+}
+
+int mx_sync(mx_stream *s) {
+  if (!s) return fail(MX_E_INVALID, "mx_sync: null stream");
+  const hipError_t e = hipStreamSynchronize(s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+void *mx_stream_handle(mx_stream *s) { return s ? static_cast<void *>(s->stream) : nullptr; }
+
+int mx_alloc(mx_ctx *ctx, size_t bytes, void **dev) {
+  if (!dev) return fail(MX_E_INVALID, "mx_alloc: null out");
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  const hipError_t e = hipMalloc(dev, bytes ? bytes : 1);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "hipMalloc");
+}
+
+int mx_free(mx_ctx *ctx, void *dev) {
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  const hipError_t e = hipFree(dev);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "hipFree");
+}
+
+int mx_copy_h2d(mx_stream *s, void *dst, const void *src, size_t bytes) {
+  if (!s || (!dst && bytes) || (!src && bytes)) return fail(MX_E_INVALID, "mx_copy_h2d: null");
+  const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "hipMemcpyAsync H2D");
+}
+
+int mx_copy_d2h(mx_stream *s, void *dst, const void *src, size_t bytes) {
+  if (!s || (!dst && bytes) || (!src && bytes)) return fail(MX_E_INVALID, "mx_copy_d2h: null");
+  const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "hipMemcpyAsync D2H");
+}
+
+int mx_stage_weight(mx_ctx *ctx, const void *kn_host, int dtype, int64_t K, int64_t N,
+                    int *slot) {
+  clear_error();
+  if (!ctx || !slot) return fail(MX_E_INVALID, "mx_stage_weight: null argument");
+  uint16_t *p = nullptr;
+  const int rc = stage_panel(ctx, kn_host, dtype, K, N, &p);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  ctx->slots.push_back(WeightSlot{p, K, N});
+  *slot = static_cast<int>(ctx->slots.size());
+  return MX_OK;
+}
+
+int mx_release_weight(mx_ctx *ctx, int slot) {
+  if (!ctx) return fail(MX_E_INVALID, "mx_release_weight: null context");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  if (slot < 1 || slot > static_cast<int>(ctx->slots.size()) || !ctx->slots[slot - 1].wt)
+    return fail(MX_E_INVALID, "mx_release_weight: no weight in slot " + std::to_string(slot));
+  int rc = use_device(ctx);
+  if (rc) return rc;
+  (void)hipFree(ctx->slots[slot - 1].wt);
+  ctx->slots[slot - 1] = WeightSlot{};
+  return MX_OK;
+}
+
+int mx_gemm(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t lda, int wslot,
+            const float *bias, int epilogue, const float *residual, void *C, int c_dtype,
+            int64_t ldc) {
+  clear_error();
+  if (!s) return fail(MX_E_INVALID, "gemm: null stream");
+  WeightSlot w;
+  {
+    std::lock_guard<std::mutex> lk(s->ctx->mu);
+    if (wslot < 1 || wslot > static_cast<int>(s->ctx->slots.size()) ||
+        !s->ctx->slots[wslot - 1].wt)
+      return fail(MX_E_INVALID, "gemm: no weight staged in slot " + std::to_string(wslot));
+    w = s->ctx->slots[wslot - 1];
+  }
+  if (w.K != K)
+    return fail(MX_E_INVALID, "gemm: A has K = " + std::to_string(K) + " but slot " +
+                                  std::to_string(wslot) + " holds a [" + std::to_string(w.K) +
+                                  ", " + std::to_string(w.N) + "] operand");
+  return gemm_checked(s, A, M, K, lda, w.wt, w.N, bias, epilogue, residual, C, c_dtype, ldc);
+}
+
+int mx_gemm_wt(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t lda,
+               const uint16_t *Wt, int64_t N, const float *bias, int epilogue,
+               const float *residual, void *C, int c_dtype, int64_t ldc) {
+  clear_error();
+  return gemm_checked(s, A, M, K, lda, Wt, N, bias, epilogue, residual, C, c_dtype, ldc);
+}
+
+int mx_attention(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
+                 int64_t H, int64_t hd, float scale, const float *add_mask,
+                 const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx) {
+  clear_error();
+  return attention_checked(s, qkv, ld_qkv, B, S, H, hd, scale, add_mask, kv_len, ctx, ld_ctx);
+}
+
+int mx_softmax_rows(mx_stream *s, void *x, int dtype, int64_t rows, int64_t cols,
+                    int64_t row_stride, const float *add_mask, int64_t rows_per_mask_row,
+                    int variant) {
+  clear_error();
+  if (!s || !x) return fail(MX_E_INVALID, "softmax: null stream or tensor");
+  if (rows <= 0 || cols <= 0) return fail(MX_E_INVALID, "softmax: zero dimension");
+  if (cols > 4096)
+    return fail(MX_E_UNSUPPORTED, "softmax: rows of " + std::to_string(cols) +
+                                      " (this kernel holds a row in one wave, <= 4096)");
+  if (row_stride < cols) return fail(MX_E_INVALID, "softmax: row stride narrower than a row");
+  if (dtype != MX_F32 && dtype != MX_BF16)
+    return fail(MX_E_INVALID, "softmax: dtype must be MX_F32 or MX_BF16");
+  if (variant < MX_SOFTMAX_POLY || variant > MX_SOFTMAX_AIE)
+    return fail(MX_E_INVALID, "softmax: unknown variant " + std::to_string(variant));
+  if (variant == MX_SOFTMAX_AIE && dtype != MX_BF16)
+    return fail(MX_E_INVALID, "softmax: the AIE variant is bf16 in and out");
+  if (variant == MX_SOFTMAX_AIE && add_mask)
+    return fail(MX_E_INVALID,
+                "softmax: the AIE variant takes scores with the mask already added "
+                "(add_additive_mask runs before it, in fp32)");
+  if (add_mask && rows_per_mask_row <= 0)
+    return fail(MX_E_INVALID, "softmax: rows_per_mask_row must be positive with a mask");
+  const hipError_t e =
+      mxk::softmax_rows(x, dtype == MX_BF16, rows, cols, row_stride, add_mask,
+                        rows_per_mask_row > 0 ? rows_per_mask_row : 1, variant, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "softmax launch");
+}
+
+int mx_layernorm(mx_stream *s, const void *x, int x_dtype, const void *y, int y_dtype,
+                 const float *gamma, const float *beta, float eps, int64_t rows, int64_t cols,
+                 float *out_f32, uint16_t *out_bf16) {
+  clear_error();
+  if (!s || !x || !gamma || !beta) return fail(MX_E_INVALID, "layernorm: null argument");
+  if (!out_f32 && !out_bf16) return fail(MX_E_INVALID, "layernorm: no output given");
+  if (rows <= 0 || cols <= 0) return fail(MX_E_INVALID, "layernorm: zero dimension");
+  if (rows > INT32_MAX) return fail(MX_E_INVALID, "layernorm: more than 2^31 rows");
+  if ((x_dtype != MX_F32 && x_dtype != MX_BF16) || (y && y_dtype != MX_F32 && y_dtype != MX_BF16))
+    return fail(MX_E_INVALID, "layernorm: dtypes must be MX_F32 or MX_BF16");
+  if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(MX_E_INVALID, "layernorm: bad eps");
+  if (out_f32 && static_cast<const void *>(out_f32) == x && x_dtype != MX_F32)
+    return fail(MX_E_INVALID, "layernorm: out_f32 aliases a bf16 input");
+  const hipError_t e = mxk::layernorm(x, x_dtype == MX_BF16, y, y_dtype == MX_BF16, gamma, beta,
+                                      eps, rows, cols, out_f32, out_bf16, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "layernorm launch");
+}
+
+int mx_gelu(mx_stream *s, const void *x, int x_dtype, void *y, int y_dtype, int64_t n,
+            int variant) {
+  clear_error();
+  if (!s || !x || !y) return fail(MX_E_INVALID, "gelu: null argument");
+  if (n <= 0) return fail(MX_E_INVALID, "gelu: empty tensor");
+  if ((x_dtype != MX_F32 && x_dtype != MX_BF16) || (y_dtype != MX_F32 && y_dtype != MX_BF16))
+    return fail(MX_E_INVALID, "gelu: dtypes must be MX_F32 or MX_BF16");
+  if (x == y && x_dtype != y_dtype)
+    return fail(MX_E_INVALID, "gelu: in place needs equal dtypes");
+  if (variant < MX_GELU_POLY || variant > MX_GELU_ERF_AS)
+    return fail(MX_E_INVALID, "gelu: unknown variant " + std::to_string(variant));
+  const hipError_t e =
+      mxk::gelu(x, x_dtype == MX_BF16, y, y_dtype == MX_BF16, n, variant, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "gelu launch");
+}
+
+int mx_narrow_f32_bf16(mx_stream *s, const float *in, uint16_t *out, int64_t n) {
+  clear_error();
+  if (!s || !in || !out) return fail(MX_E_INVALID, "narrow_f32_bf16: null argument");
+  if (n < 0) return fail(MX_E_INVALID, "narrow_f32_bf16: negative count");
+  if (n == 0) return MX_OK;
+  const hipError_t e = mxk::narrow_f32_bf16(in, out, n, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "narrow_f32_bf16 launch");
+}
+
+int mx_narrow_i32_bf16(mx_stream *s, const int32_t *in, uint16_t *out, int64_t n) {
+  clear_error();
+  if (!s || !in || !out) return fail(MX_E_INVALID, "narrow_i32_bf16: null argument");
+  if (n < 0) return fail(MX_E_INVALID, "narrow_i32_bf16: negative count");
+  if (n == 0) return MX_OK;
+  const hipError_t e = mxk::narrow_i32_bf16(in, out, n, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "narrow_i32_bf16 launch");
+}
+
+int mx_embed_sum(mx_stream *s, const int32_t *ids, const float *attn_mask, int64_t B, int64_t S,
+                 int64_t hidden, const float *word, int64_t vocab, const float *pos,
+                 const float *type0, float *emb, float *add_mask, int32_t *kv_len) {
+  clear_error();
+  if (!s || !ids || !attn_mask || !word || !pos || !type0 || !emb)
+    return fail(MX_E_INVALID, "embed_sum: null argument");
+  if (B <= 0 || S <= 0 || hidden <= 0 || vocab <= 0)
+    return fail(MX_E_INVALID, "embed_sum: zero dimension");
+  hipError_t e = mxk::embed_sum(ids, B, S, hidden, word, vocab, pos, type0, emb, s->err_dev,
+                                s->stream);
+  if (e == hipSuccess && (add_mask || kv_len))
+    e = mxk::mask_build(attn_mask, B, S, add_mask, kv_len, s->stream);
+  if (e != hipSuccess) return hip_fail(e, "embed_sum launch");
+  int flags = 0;
+  const int rc = take_data_error(s, &flags);
+  if (rc) return rc;
+  if (flags & 1)
+    return fail(MX_E_DATA, "embed_sum: a token id is outside [0, " + std::to_string(vocab) +
+                               ") (its row was written as zeros)");
+  return MX_OK;
+}
+
+int mx_pool_rows(mx_stream *s, const float *h, const float *attn_mask, int64_t B, int64_t S,
+                 int64_t hidden, int cls_pool, int l2_normalize, float *out) {
+  clear_error();
+  if (!s || !h || !attn_mask || !out) return fail(MX_E_INVALID, "pool_rows: null argument");
+  if (B <= 0 || S <= 0 || hidden <= 0) return fail(MX_E_INVALID, "pool_rows: zero dimension");
+  if (hidden > 4096) return fail(MX_E_UNSUPPORTED, "pool_rows: hidden > 4096");
+  const hipError_t e =
+      mxk::pool_rows(h, attn_mask, B, S, hidden, cls_pool, l2_normalize, out, s->err_dev,
+                     s->stream);
+  if (e != hipSuccess) return hip_fail(e, "pool_rows launch");
+  int flags = 0;
+  const int rc = take_data_error(s, &flags);
+  if (rc) return rc;
+  if (flags & 2)
+    return fail(MX_E_DATA, "CLS pooling on a sequence whose first token is masked");
+  return MX_OK;
+}
+
+int mx_ops_parse(const char *list) {
+  clear_error();
+  if (!list) return fail(MX_E_INVALID, "--npu-ops: null list");
+  std::set<std::string> out;
+  std::string item;
+  auto commit = [&]() -> bool {
+    std::string code;
+    for (char c : item)
+      if (!std::isspace(static_cast<unsigned char>(c))) code.push_back(c);
+    item.clear();
+    if (code.empty()) return true;
+    bool known = false;
+    for (const auto &o : kOps) known = known || code == o.code;
+    if (!known) {
+      set_error("--npu-ops: '" + code + "' is not an op this build knows. Valid codes: [" +
+                codes_joined() +
+                "]. Nothing listed means no op is placed on the accelerator.");
+      return false;
+    }
+    out.insert(code);
+    return true;
+  };
+  for (const char *p = list; *p; ++p) {
+    if (*p == ',') {
+      if (!commit()) return MX_E_INVALID;
+      continue;
+    }
+    item.push_back(*p);
+  }
+  if (!commit()) return MX_E_INVALID;
+  std::lock_guard<std::mutex> lk(g_ops_mu);
+  g_ops = out;
+  return MX_OK;
+}
+
+int mx_op_on_gpu(const char *code) {
+  if (!code) return 0;
+  std::lock_guard<std::mutex> lk(g_ops_mu);
+  return g_ops.count(code) ? 1 : 0;
+}
+
+const char *mx_op_codes(void) {
+  static const std::string s = codes_joined();
+  return s.c_str();
+}
+
+int mx_ops_check_flag(const char *flag) {
+  clear_error();
+  if (!flag) return MX_OK;
+  static const std::pair<const char *, const char *> removed[] = {
+      {"--npu-eltwise", "--npu-ops gelu,layn,softm"},
+      {"--host-gelu", "--npu-ops without gelu"},
+      {"--host-ln", "--npu-ops without layn"},
+      {"--host-sm", "--npu-ops without softm"},
+      {"--npu-extra-ops", "--npu-ops"},
+  };
+  for (const auto &r : removed)
+    if (std::strcmp(flag, r.first) == 0)
+      return fail(MX_E_INVALID, std::string(r.first) +
+                                    " is gone: one flag now says which ops go on the "
+                                    "accelerator, and an op is on the host when it is NOT "
+                                    "listed. Use " +
+                                    r.second + ".");
+  return MX_OK;
+}
+
+}  // extern "C"
+
+namespace mx {
+std::set<std::string> placed_ops() {
+  std::lock_guard<std::mutex> lk(g_ops_mu);
+  return g_ops;
+}
+}  // namespace mx

@@ -1,0 +1,94 @@
+// mx_common.hpp -- device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mxd {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// fp32 -> bf16 by the reference's integer formula (host_kernels.hpp:157-161):
+// round to nearest even on the bit pattern, NaN behaviour included (a NaN
+// whose payload carries into the exponent becomes Inf or 0, as on the host).
+__device__ __forceinline__ uint16_t f2bf(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// gelu8 with the lane semantics of the reference's AVX2 branch
+// (bert_encoder.cpp:547-570): u = min(|v|, 4), degree-8 Horner by FMA, plus
+// max(v, 0); a NaN input gives the polynomial at 4 (min_ps/max_ps return the
+// second operand on NaN).
+__device__ __forceinline__ float gelu_poly(float v) {
+  const float av = fabsf(v);
+  const float u = av < 4.0f ? av : 4.0f;
+  float p = __builtin_fmaf(-7.2340282171e-05f, u, 1.8179518005e-03f);
+  p = __builtin_fmaf(p, u, -1.7707383379e-02f);
+  p = __builtin_fmaf(p, u, 8.4577147641e-02f);
+  p = __builtin_fmaf(p, u, -1.9228671834e-01f);
+  p = __builtin_fmaf(p, u, 9.8431124458e-02f);
+  p = __builtin_fmaf(p, u, 3.6137852062e-01f);
+  p = __builtin_fmaf(p, u, -4.9454128936e-01f);
+  p = __builtin_fmaf(p, u, -1.3007010117e-04f);
+  return (v > 0.0f ? v : 0.0f) + p;
+}
+
+// Exact-erf GELU, in fp32 (the host form rounds a double result once).
+__device__ __forceinline__ float gelu_erf(float v) {
+  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+}
+
+// exp2_avx2 (host_kernels.hpp:358-379): k = trunc(x), f = x - k, degree-7
+// Horner by FMA, times 2^k written into the exponent field. Bit-identical to
+// the host lane for x in [-126, 127].
+__device__ __forceinline__ float exp2_poly(float x) {
+  const int k = (int)x;
+  const float f = x - (float)k;
+  float p = __builtin_fmaf(1.5483275463e-05f, f, 1.5669833174e-04f);
+  p = __builtin_fmaf(p, f, 1.3331825236e-03f);
+  p = __builtin_fmaf(p, f, 9.6164605538e-03f);
+  p = __builtin_fmaf(p, f, 5.5504156855e-02f);
+  p = __builtin_fmaf(p, f, 2.4022684109e-01f);
+  p = __builtin_fmaf(p, f, 6.9314717694e-01f);
+  p = __builtin_fmaf(p, f, 9.9999998955e-01f);
+  return p * __uint_as_float((uint32_t)(k + 127) << 23);
+}
+
+// The AIE exp2_poly (kernels/exp2_poly.h:35-65): the same table, each Horner
+// step a rounded multiply then a rounded add (no FMA).
+__device__ __forceinline__ float exp2_poly_aie(float x) {
+  const int k = (int)x;
+  const float f = __fsub_rn(x, (float)k);
+  float p = 1.5483275463e-05f;
+  p = __fadd_rn(__fmul_rn(p, f), 1.5669833174e-04f);
+  p = __fadd_rn(__fmul_rn(p, f), 1.3331825236e-03f);
+  p = __fadd_rn(__fmul_rn(p, f), 9.6164605538e-03f);
+  p = __fadd_rn(__fmul_rn(p, f), 5.5504156855e-02f);
+  p = __fadd_rn(__fmul_rn(p, f), 2.4022684109e-01f);
+  p = __fadd_rn(__fmul_rn(p, f), 6.9314717694e-01f);
+  p = __fadd_rn(__fmul_rn(p, f), 9.9999998955e-01f);
+  return __fmul_rn(p, __uint_as_float((uint32_t)(k + 127) << 23));
+}
+
+}  // namespace mxd

@@ -1,0 +1,59 @@
+// mx_internal.hpp -- host-side objects behind the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/mx_encoder.h"
+
+namespace mx {
+
+// Thread-local last error, set by every failing entry point.
+void set_error(const std::string &msg);
+void clear_error();
+int fail(int code, const std::string &msg);
+int hip_fail(hipError_t e, const char *what);
+
+struct WeightSlot {
+  uint16_t *wt = nullptr;  // [N, K] bf16
+  int64_t K = 0, N = 0;
+};
+
+}  // namespace mx
+
+struct mx_ctx {
+  int device = 0;
+  mx_device_props props{};
+  std::mutex mu;
+  std::vector<mx::WeightSlot> slots;  // index = slot - 1
+};
+
+struct mx_stream {
+  mx_ctx *ctx = nullptr;
+  hipStream_t stream = nullptr;
+  int *err_dev = nullptr;  // device flag for kernels that refuse data
+};
+
+namespace mx {
+
+// Make ctx's device current for the calling thread.
+int use_device(const mx_ctx *ctx);
+// Copy a [K, N] host weight (fp32 values or bf16 bits) into a new [N, K] bf16
+// device panel.
+int stage_panel(mx_ctx *ctx, const void *kn_host, int dtype, int64_t K, int64_t N,
+                uint16_t **out);
+// Validated launches shared by the per-op entry points and the encoder.
+int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t lda,
+                 const uint16_t *Wt, int64_t N, const float *bias, int epilogue,
+                 const float *residual, void *C, int c_dtype, int64_t ldc);
+int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
+                      int64_t H, int64_t hd, float scale, const float *add_mask,
+                      const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx);
+// Read and clear the stream's data-refusal flag (synchronises the stream).
+int take_data_error(mx_stream *s, int *flags);
+
+}  // namespace mx

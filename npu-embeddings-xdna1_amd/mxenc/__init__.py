@@ -1,0 +1,331 @@
+"""Python binding of libmx_encoder.so (the gfx950 encoder backend's C ABI).
+
+Everything here goes through the C ABI declared in include/mx_encoder.h:
+device buffers come from mx_alloc and move with mx_copy_*; there is no
+fallback -- if the library is not built, or no gfx950 device is present,
+the calls fail loudly with the library's own message.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(HERE), "_build", "libmx_encoder.so")
+
+MX_OK = 0
+MX_F32, MX_BF16, MX_I32 = 0, 1, 2
+MX_EPI_NONE, MX_EPI_GELU_POLY, MX_EPI_GELU_ERF = 0, 1, 2
+MX_GELU_POLY, MX_GELU_ERF, MX_GELU_ERF_AS = 0, 1, 2
+MX_SOFTMAX_POLY, MX_SOFTMAX_EXACT, MX_SOFTMAX_AIE = 0, 1, 2
+MX_ARCH_BERT, MX_ARCH_PRELN = 0, 1
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+
+
+class MxError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class DeviceProps(ctypes.Structure):
+    _fields_ = [("device", _int), ("compute_units", _int), ("clock_mhz", _int),
+                ("hbm_bytes", _i64), ("arch", ctypes.c_char * 32),
+                ("bf16_dense_tflops", ctypes.c_double)]
+
+
+class EncoderDesc(ctypes.Structure):
+    _fields_ = [("arch", _int), ("layers", _i64), ("hidden", _i64), ("heads", _i64),
+                ("head_dim", _i64), ("ffn", _i64), ("ln_eps", ctypes.c_float),
+                ("attn_scale", ctypes.c_float), ("gelu", _int), ("cls_pool", _int),
+                ("l2_normalize", _int), ("vocab", _i64), ("max_pos", _i64)]
+
+
+class Timings(ctypes.Structure):
+    _fields_ = [("gemm_ms", ctypes.c_double), ("attn_ms", ctypes.c_double),
+                ("ln_ms", ctypes.c_double), ("other_ms", ctypes.c_double),
+                ("total_ms", ctypes.c_double), ("gemm_launches", _i64),
+                ("attn_launches", _i64), ("ln_launches", _i64), ("other_launches", _i64),
+                ("gemm_flop", ctypes.c_double), ("attn_flop", ctypes.c_double)]
+
+
+# name -> (restype, argtypes); the complete exported surface of mx_encoder.h
+SIGNATURES = {
+    "mx_last_error": (ctypes.c_char_p, []),
+    "mx_version": (_int, []),
+    "mx_create": (_int, [_int, ctypes.POINTER(_vp)]),
+    "mx_destroy": (None, [_vp]),
+    "mx_device_props_get": (_int, [_vp, ctypes.POINTER(DeviceProps)]),
+    "mx_stream_create": (_int, [_vp, ctypes.POINTER(_vp)]),
+    "mx_stream_destroy": (None, [_vp]),
+    "mx_sync": (_int, [_vp]),
+    "mx_stream_handle": (_vp, [_vp]),
+    "mx_alloc": (_int, [_vp, ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "mx_free": (_int, [_vp, _vp]),
+    "mx_copy_h2d": (_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+    "mx_copy_d2h": (_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+    "mx_stage_weight": (_int, [_vp, _vp, _int, _i64, _i64, ctypes.POINTER(_int)]),
+    "mx_release_weight": (_int, [_vp, _int]),
+    "mx_gemm": (_int, [_vp, _vp, _i64, _i64, _i64, _int, _vp, _int, _vp, _vp, _int, _i64]),
+    "mx_gemm_wt": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp, _int,
+                          _i64]),
+    "mx_attention": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp,
+                            _vp, _i64]),
+    "mx_softmax_rows": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _i64, _int]),
+    "mx_layernorm": (_int, [_vp, _vp, _int, _vp, _int, _vp, _vp, ctypes.c_float, _i64, _i64,
+                            _vp, _vp]),
+    "mx_gelu": (_int, [_vp, _vp, _int, _vp, _int, _i64, _int]),
+    "mx_narrow_f32_bf16": (_int, [_vp, _vp, _vp, _i64]),
+    "mx_narrow_i32_bf16": (_int, [_vp, _vp, _vp, _i64]),
+    "mx_embed_sum": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _vp,
+                            _vp]),
+    "mx_pool_rows": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp]),
+    "mx_ops_parse": (_int, [ctypes.c_char_p]),
+    "mx_op_on_gpu": (_int, [ctypes.c_char_p]),
+    "mx_op_codes": (ctypes.c_char_p, []),
+    "mx_ops_check_flag": (_int, [ctypes.c_char_p]),
+    "mx_encoder_create": (_int, [_vp, ctypes.POINTER(EncoderDesc), ctypes.POINTER(_vp)]),
+    "mx_encoder_destroy": (None, [_vp]),
+    "mx_encoder_set": (_int, [_vp, ctypes.c_char_p, _vp, _int, _i64]),
+    "mx_encoder_ready": (_int, [_vp]),
+    "mx_encoder_run": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64]),
+    "mx_encoder_embed": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "mx_encoder_set_timing": (_int, [_vp, _int]),
+    "mx_encoder_timings": (_int, [_vp, ctypes.POINTER(Timings)]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MxError(-3, f"{LIB_PATH} is not built: run "
+                              "python npu-embeddings-xdna1_amd/build.py")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != MX_OK:
+        raise MxError(rc, lib().mx_last_error().decode())
+    return rc
+
+
+def _np_dtype_code(a):
+    if a.dtype == np.float32:
+        return MX_F32
+    if a.dtype == np.uint16:
+        return MX_BF16
+    if a.dtype == np.int32:
+        return MX_I32
+    raise TypeError(a.dtype)
+
+
+class DevBuf:
+    """A device allocation from mx_alloc, with its shape and numpy dtype."""
+
+    def __init__(self, ctx, shape, dtype):
+        self.ctx = ctx
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = _vp()
+        check(lib().mx_alloc(ctx.handle, max(self.nbytes, 1), ctypes.byref(p)))
+        self.ptr = p.value
+
+    def offset(self, elements):
+        return _vp(self.ptr + int(elements) * self.dtype.itemsize)
+
+    @property
+    def p(self):
+        return _vp(self.ptr)
+
+    def host(self):
+        out = np.empty(self.shape, self.dtype)
+        self.ctx.sync()
+        check(lib().mx_copy_d2h(self.ctx.stream, out.ctypes.data, self.ptr, self.nbytes))
+        self.ctx.sync()
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().mx_free(self.ctx.handle, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    """One device and one stream."""
+
+    def __init__(self, device=0):
+        h = _vp()
+        check(lib().mx_create(device, ctypes.byref(h)))
+        self.handle = h.value
+        s = _vp()
+        check(lib().mx_stream_create(self.handle, ctypes.byref(s)))
+        self.stream = s.value
+        self.props = DeviceProps()
+        check(lib().mx_device_props_get(self.handle, ctypes.byref(self.props)))
+
+    def sync(self):
+        check(lib().mx_sync(self.stream))
+
+    def empty(self, shape, dtype):
+        return DevBuf(self, shape, dtype)
+
+    def put(self, a):
+        a = np.ascontiguousarray(a)
+        b = DevBuf(self, a.shape, a.dtype)
+        check(lib().mx_copy_h2d(self.stream, b.ptr, a.ctypes.data, b.nbytes))
+        self.sync()
+        return b
+
+    def close(self):
+        if self.stream:
+            lib().mx_stream_destroy(self.stream)
+            self.stream = None
+        if self.handle:
+            lib().mx_destroy(self.handle)
+            self.handle = None
+
+
+def _p(b):
+    return None if b is None else (b if isinstance(b, ctypes.c_void_p) else b.p)
+
+
+# ---- per-op wrappers (device buffers in and out) ------------------------------
+
+def narrow_f32_bf16(ctx, x, out):
+    check(lib().mx_narrow_f32_bf16(ctx.stream, x.p, out.p, int(np.prod(x.shape))))
+
+
+def narrow_i32_bf16(ctx, x, out):
+    check(lib().mx_narrow_i32_bf16(ctx.stream, x.p, out.p, int(np.prod(x.shape))))
+
+
+def gelu(ctx, x, y, variant):
+    check(lib().mx_gelu(ctx.stream, x.p, _np_dtype_code(np.empty(0, x.dtype)), y.p,
+                        _np_dtype_code(np.empty(0, y.dtype)), int(np.prod(x.shape)), variant))
+
+
+def layernorm(ctx, x, y, gamma, beta, eps, rows, cols, out_f32=None, out_bf16=None):
+    xd = _np_dtype_code(np.empty(0, x.dtype))
+    yd = _np_dtype_code(np.empty(0, y.dtype)) if y is not None else MX_F32
+    check(lib().mx_layernorm(ctx.stream, x.p, xd, _p(y), yd, gamma.p, beta.p, eps, rows, cols,
+                             _p(out_f32), _p(out_bf16)))
+
+
+def softmax_rows(ctx, x, rows, cols, stride, mask=None, rows_per_mask_row=1,
+                 variant=MX_SOFTMAX_POLY):
+    check(lib().mx_softmax_rows(ctx.stream, x.p, _np_dtype_code(np.empty(0, x.dtype)), rows,
+                                cols, stride, _p(mask), rows_per_mask_row, variant))
+
+
+def gemm_wt(ctx, A, M, K, lda, Wt, N, bias, epilogue, residual, C, ldc):
+    cd = _np_dtype_code(np.empty(0, C.dtype))
+    check(lib().mx_gemm_wt(ctx.stream, _p(A), M, K, lda, _p(Wt), N, _p(bias), epilogue,
+                           _p(residual), _p(C), cd, ldc))
+
+
+def attention(ctx, qkv, ld_qkv, B, S, H, hd, scale, mask, kv_len, out, ld_out):
+    check(lib().mx_attention(ctx.stream, _p(qkv), ld_qkv, B, S, H, hd, scale, _p(mask),
+                             _p(kv_len), _p(out), ld_out))
+
+
+def to_bf16_bits(x):
+    """fp32 -> bf16 bit patterns by the reference's to_bf16 formula."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def from_bf16_bits(h):
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ---- the encoder ---------------------------------------------------------------
+
+class Encoder:
+    """An mx_encoder loaded from a synthetic model dict (mxenc.synth)."""
+
+    def __init__(self, ctx, m, gelu=None, ln_eps=None, attn_scale=1.0, cls_pool=None,
+                 l2_normalize=True):
+        self.ctx = ctx
+        self.m = m
+        bert = m["kind"] == "bert"
+        d = EncoderDesc()
+        d.arch = MX_ARCH_BERT if bert else MX_ARCH_PRELN
+        d.layers, d.hidden, d.heads = m["layers"], m["hidden"], m["heads"]
+        d.head_dim, d.ffn = m["head_dim"], m["ffn"]
+        d.ln_eps = ln_eps if ln_eps is not None else (1e-12 if bert else m["eps"])
+        d.attn_scale = attn_scale
+        d.gelu = gelu if gelu is not None else (MX_GELU_POLY if bert else MX_GELU_ERF)
+        d.cls_pool = int(m.get("cls_pool", False) if cls_pool is None else cls_pool)
+        d.l2_normalize = int(l2_normalize)
+        d.vocab = m.get("vocab", 0) if bert else 0
+        d.max_pos = m.get("max_pos", 0) if bert else 0
+        self.desc = d
+        h = _vp()
+        check(lib().mx_encoder_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)))
+        self.handle = h.value
+        names = [("qkv", "w_qkv", "b_qkv"), ("attn_out", "w_ao", "b_ao"),
+                 ("ffn_up", "w_up", "b_up"), ("ffn_down", "w_down", "b_down")]
+        for l in range(m["layers"]):
+            for n, w, b in names:
+                self.set(f"layer.{l}.{n}", m[w][l])
+                self.set(f"layer.{l}.{n}.bias", m[b][l])
+            self.set(f"layer.{l}.ln1.weight", m["ln1_g"][l])
+            self.set(f"layer.{l}.ln1.bias", m["ln1_b"][l])
+            self.set(f"layer.{l}.ln2.weight", m["ln2_g"][l])
+            self.set(f"layer.{l}.ln2.bias", m["ln2_b"][l])
+        if bert:
+            self.set("embeddings.ln.weight", m["emb_ln_g"])
+            self.set("embeddings.ln.bias", m["emb_ln_b"])
+            self.set("embeddings.word", m["word"])
+            self.set("embeddings.position", m["pos"])
+            self.set("embeddings.token_type", m["type"])
+        else:
+            self.set("final_ln.weight", m["fin_ln_g"])
+            self.set("final_ln.bias", m["fin_ln_b"])
+        check(lib().mx_encoder_ready(self.handle))
+
+    def set(self, name, arr):
+        a = np.ascontiguousarray(arr)
+        check(lib().mx_encoder_set(self.handle, name.encode(), a.ctypes.data,
+                                   _np_dtype_code(a), a.size))
+
+    def run(self, x, mask, kv_len, B, S):
+        check(lib().mx_encoder_run(self.handle, self.ctx.stream, _p(x), _p(mask), _p(kv_len),
+                                   B, S))
+
+    def embed(self, ids, attn_mask, B, S, out):
+        check(lib().mx_encoder_embed(self.handle, self.ctx.stream, _p(ids), _p(attn_mask), B,
+                                     S, _p(out)))
+
+    def set_timing(self, on):
+        check(lib().mx_encoder_set_timing(self.handle, int(on)))
+
+    def timings(self):
+        t = Timings()
+        check(lib().mx_encoder_timings(self.handle, ctypes.byref(t)))
+        return t
+
+    def close(self):
+        if self.handle:
+            lib().mx_encoder_destroy(self.handle)
+            self.handle = None

@@ -1,0 +1,142 @@
+"""The whole encoder stack on the GPU against the oracle's host path, through
+the C ABI: pooled, L2-normalised embeddings must reach cosine >= 0.9999 per
+sequence. Sequences are independent (test_oracle_encoder pins that on the
+host), so at full batch the oracle checks a subset of the batch's sequences
+exactly."""
+import numpy as np
+import pytest
+
+import mxenc
+from mxenc import synth
+from orc import P, encoder_struct
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.9999
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = mxenc.Context(0)
+    yield c
+    c.close()
+
+
+def cosines(a, b):
+    a = a.astype(np.float64)
+    b = b.astype(np.float64)
+    return np.sum(a * b, -1) / (np.linalg.norm(a, axis=-1) * np.linalg.norm(b, axis=-1))
+
+
+def oracle_embed(orc, m, ids, am):
+    """EmbedService::chunk on the host: embedding sum, mask, run, pool."""
+    B, S = ids.shape
+    d = m["hidden"]
+    emb = np.empty((B * S, d), np.float32)
+    cm = np.empty((B, S), np.float32)
+    orc.orc_embed_sum(P(ids), P(am), B, S, d, P(m["word"]), P(m["pos"]), P(m["type"]), P(emb),
+                      P(cm))
+    keep = []
+    orc.orc_bert_run(encoder_struct(m, keep), P(emb), P(cm), B, S, -1)
+    out = np.empty((B, d), np.float32)
+    assert orc.orc_pool_rows(P(emb), P(am), B, S, d, int(m["cls_pool"]), 1, P(out)) == 0
+    return out, emb
+
+
+def gpu_embed(ctx, enc, ids, am):
+    B, S = ids.shape
+    d_ids, d_am = ctx.put(ids), ctx.put(am)
+    out = ctx.empty((B, enc.desc.hidden), np.float32)
+    enc.embed(d_ids, d_am, B, S, out)
+    return out.host()
+
+
+def test_minilm_full_config(ctx, orc):
+    """all-MiniLM-L6-v2 geometry, batch 32 x seq 128, mean pooling, whole batch
+    checked against the host path."""
+    m = synth.make_model("minilm", ln_random=True)
+    ids, am, lens = synth.make_text_inputs(m)
+    want, _ = oracle_embed(orc, m, ids, am)
+    enc = mxenc.Encoder(ctx, m)
+    got = gpu_embed(ctx, enc, ids, am)
+    cos = cosines(got, want)
+    assert np.min(cos) >= COS_MIN, np.min(cos)
+    # every output row is unit length (L2 in double on both sides)
+    assert np.max(np.abs(np.linalg.norm(got, axis=1) - 1)) < 1e-6
+    enc.close()
+
+
+def test_bge_base_full_batch_subset_checked(ctx, orc):
+    """bge-base geometry at its full shape (batch 64 x seq 512, 12 layers, CLS
+    pooling) on the GPU; three of its sequences (the longest, the shortest and
+    one more) rerun on the host path."""
+    m = synth.make_model("bge_base")
+    ids, am, lens = synth.make_text_inputs(m)
+    enc = mxenc.Encoder(ctx, m)
+    got = gpu_embed(ctx, enc, ids, am)
+    pick = [int(np.argmax(lens)), int(np.argmin(lens)), 5]
+    want, _ = oracle_embed(orc, m, np.ascontiguousarray(ids[pick]), np.ascontiguousarray(am[pick]))
+    cos = cosines(got[pick], want)
+    assert np.min(cos) >= COS_MIN, cos
+    enc.close()
+
+
+def test_streams_agree_bitwise(ctx):
+    """Two lanes (streams) given the same batch produce identical bits, the
+    reference's --pipeline lane agreement (run_execute.hpp:547-565)."""
+    m = synth.make_model("minilm", layers=2)
+    ids, am, _ = synth.make_text_inputs(m, batch=8)
+    enc = mxenc.Encoder(ctx, m)
+    a = gpu_embed(ctx, enc, ids, am)
+    ctx2 = mxenc.Context(0)
+    enc2 = mxenc.Encoder(ctx2, m)
+    b = gpu_embed(ctx2, enc2, ids, am)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    enc2.close()
+    ctx2.close()
+    enc.close()
+
+
+def _preln_case(ctx, orc, name, B, layers, eps):
+    m = synth.make_model(name, layers=layers, ln_random=True)
+    S, d = m["seq"], m["hidden"]
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((B * S, d)).astype(np.float32)
+    want = x.copy()
+    keep = []
+    orc.orc_preln_run(encoder_struct(m, keep), P(want), B, S, eps, 1.0, -1)
+    enc = mxenc.Encoder(ctx, m)
+    dx = ctx.put(x)
+    enc.run(dx, None, None, B, S)
+    got = dx.host()
+    cos = cosines(got, want)
+    assert np.min(cos) >= COS_MIN, np.min(cos)
+    enc.close()
+
+
+def test_vit_body_197_tokens(ctx, orc):
+    """ViT-base/16 body: 12 pre-LN layers over 197 positions (odd length, no
+    mask), exact-erf GELU, final LayerNorm; 2 images."""
+    _preln_case(ctx, orc, "vit_base", 2, 12, 1e-12)
+
+
+def test_whisper_body_1500_positions(ctx, orc):
+    """Whisper-large-v3 encoder body at its width (d 1280, 20 heads, FFN 5120)
+    over 1500 positions, unmasked, eps 1e-5; 2 of its 32 layers."""
+    _preln_case(ctx, orc, "whisper_enc", 1, 2, 1e-5)
+
+
+def test_partial_placement_refused(ctx):
+    m = synth.make_model("minilm", layers=1)
+    enc = mxenc.Encoder(ctx, m)
+    L = mxenc.lib()
+    try:
+        assert L.mx_ops_parse(b"gemm,attn") == 0
+        x = ctx.empty((128, 384), np.float32)
+        with pytest.raises(mxenc.MxError, match="softm, layn, gelu"):
+            enc.run(x, None, None, 1, 128)
+        assert L.mx_ops_parse(b"gemm,attn,softm,layn,gelu") == 0
+        enc.run(x, None, None, 1, 128)
+    finally:
+        L.mx_ops_parse(b"")
+        enc.close()

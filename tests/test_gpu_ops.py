@@ -1,0 +1,420 @@
+"""GPU parity of every per-op entry point against the oracle, through the
+C ABI, on seeded inputs. Integer/byte work is checked bit-exact; floating
+point to the tolerance stated in each test."""
+import numpy as np
+import pytest
+
+import mxenc
+from mxenc import from_bf16_bits, to_bf16_bits
+from orc import P
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = mxenc.Context(0)
+    yield c
+    c.close()
+
+
+def test_device_is_mi355x(ctx):
+    assert ctx.props.arch.decode().startswith("gfx950")
+    assert ctx.props.compute_units >= 256
+
+
+# ---- narrow_f32_bf16: bit-exact with the host's to_bf16 ----------------------
+
+def test_narrow_f32_bf16_bit_exact(ctx, orc):
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    lows = np.array([0, 1, 0x7FFF, 0x8000, 0x8001, 0xFFFF, 0x4000, 0xC000], np.uint32)
+    rng = np.random.default_rng(0)
+    bits = np.concatenate([(hi[:, None] | lows[None, :]).reshape(-1),
+                           rng.integers(0, 1 << 32, 1 << 22, dtype=np.uint64).astype(np.uint32)])
+    x = bits.view(np.float32)
+    want = np.empty(x.size, np.uint16)
+    orc.orc_bf16_fill(P(want), P(bits), x.size)
+    dx = ctx.put(bits)
+    out = ctx.empty(x.shape, np.uint16)
+    mxenc.narrow_f32_bf16(ctx, dx, out)
+    got = out.host()
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"bits {bits[bad[0]]:#x}: {got[bad[0]]:#x} != {want[bad[0]]:#x}"
+
+
+def test_narrow_f32_bf16_tails_and_misaligned(ctx, orc):
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 1 << 32, 1031, dtype=np.uint64).astype(np.uint32)
+    want = np.empty(bits.size, np.uint16)
+    orc.orc_bf16_fill(P(want), P(bits), bits.size)
+    dx = ctx.put(bits)
+    out = ctx.empty((bits.size,), np.uint16)
+    # odd length: vector body + scalar tail
+    mxenc.check(mxenc.lib().mx_narrow_f32_bf16(ctx.stream, dx.p, out.p, bits.size))
+    assert np.array_equal(out.host(), want)
+    # one element in: misaligned pointers take the scalar kernel
+    mxenc.check(mxenc.lib().mx_narrow_f32_bf16(ctx.stream, dx.offset(1), out.offset(1),
+                                               bits.size - 1))
+    assert np.array_equal(out.host()[1:], want[1:])
+
+
+def test_narrow_i32_bf16_single_rounding(ctx, orc):
+    rng = np.random.default_rng(2)
+    v = np.concatenate([rng.integers(-2**31, 2**31, 1 << 20, dtype=np.int64),
+                        rng.integers(-5000, 5000, 4096),
+                        [0, 1, -1, 255, 256, 257, 2**24 + 1, 2**24 + 2**16 + 2**15 + 1,
+                         2**31 - 1, -2**31]]).astype(np.int32)
+    want = np.empty(v.size, np.uint16)
+    orc.orc_narrow_i32_bf16(P(v), P(want), v.size)
+    dv = ctx.put(v)
+    out = ctx.empty(v.shape, np.uint16)
+    mxenc.narrow_i32_bf16(ctx, dv, out)
+    assert np.array_equal(out.host(), want)
+
+
+# ---- GELU ----------------------------------------------------------------------
+
+def test_gelu_poly_fp32_bit_exact(ctx, orc):
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(1 << 20).astype(np.float32) * 3,
+                        np.array([0, -0.0, 4, -4, 3.9999, 1e30, -1e30, np.inf], np.float32)])
+    want = x.copy()
+    orc.orc_gelu_poly_inplace(P(want), want.size)
+    dx = ctx.put(x)
+    mxenc.gelu(ctx, dx, dx, mxenc.MX_GELU_POLY)  # in place
+    assert np.array_equal(dx.host().view(np.uint32), want.view(np.uint32))
+
+
+def test_gelu_erf_fp32(ctx, orc):
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal(1 << 18) * 4).astype(np.float32)
+    want = x.copy()
+    orc.orc_gelu_erf_inplace(P(want), want.size)
+    dx = ctx.put(x)
+    dy = ctx.empty(x.shape, np.float32)
+    mxenc.gelu(ctx, dx, dy, mxenc.MX_GELU_ERF)
+    got = dy.host()
+    # fp32 erff against the host's double erf rounded once: a few ulp
+    assert np.max(np.abs(got - want) / (np.abs(want) + 1e-30)) < 1e-5 or \
+        np.max(np.abs(got - want)) < 1e-6
+
+
+def test_gelu_erf_as_bf16_matches_aie_restatement(ctx, orc):
+    x = np.linspace(-12, 12, 1 << 16, dtype=np.float32)
+    xb = to_bf16_bits(x)
+    want = np.empty_like(xb)
+    orc.orc_aie_gelu_erf_bf16(P(xb), P(want), xb.size)
+    dx = ctx.put(xb)
+    dy = ctx.empty(xb.shape, np.uint16)
+    mxenc.gelu(ctx, dx, dy, mxenc.MX_GELU_ERF_AS)
+    assert np.array_equal(dy.host(), want)
+
+
+def test_gelu_poly_bf16_vs_aie_kernel(ctx, orc):
+    """bf16 in/out: the fused-FMA polynomial against gelu_poly_rne.cc's
+    multiply-then-add: at most one bf16 ulp apart."""
+    x = np.linspace(-9, 9, 1 << 16, dtype=np.float32)
+    xb = to_bf16_bits(x)
+    want = np.empty_like(xb)
+    orc.orc_aie_gelu_poly_bf16(P(xb), P(want), xb.size)
+    dx = ctx.put(xb)
+    dy = ctx.empty(xb.shape, np.uint16)
+    mxenc.gelu(ctx, dx, dy, mxenc.MX_GELU_POLY)
+    got = dy.host()
+    assert np.max(np.abs(got.astype(np.int32) - want.astype(np.int32))) <= 1
+
+
+# ---- LayerNorm -----------------------------------------------------------------
+
+@pytest.mark.parametrize("cols", [384, 768, 1024, 1280, 200])
+def test_layernorm_residual_fused(ctx, orc, cols):
+    rng = np.random.default_rng(cols)
+    rows = 1000
+    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    y = (rng.standard_normal((rows, cols)) * 0.5).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(cols)).astype(np.float32)
+    want = np.empty_like(x)
+    orc.orc_add_into(P(want), P(y), P(x), x.size)
+    if cols % 8 == 0:
+        orc.orc_layer_norm_rows(P(want), rows, cols, P(g), P(b), 1e-12)
+    else:
+        orc.orc_layernorm_rows_f64(P(want), rows, cols, P(g), P(b), 1e-12)
+    dx, dy, dg, db = ctx.put(x), ctx.put(y), ctx.put(g), ctx.put(b)
+    of = ctx.empty(x.shape, np.float32)
+    ob = ctx.empty(x.shape, np.uint16)
+    mxenc.layernorm(ctx, dx, dy, dg, db, 1e-12, rows, cols, out_f32=of, out_bf16=ob)
+    got = of.host()
+    assert np.max(np.abs(got - want)) < 2e-5
+    # the bf16 copy is the fp32 result narrowed by to_bf16, bit for bit
+    assert np.array_equal(ob.host(), to_bf16_bits(got))
+    # in place over the residual stream
+    mxenc.layernorm(ctx, dx, dy, dg, db, 1e-12, rows, cols, out_f32=dx)
+    assert np.array_equal(dx.host(), got)
+
+
+def test_layernorm_bf16_input(ctx, orc):
+    rng = np.random.default_rng(9)
+    rows, cols = 257, 768
+    x = to_bf16_bits(rng.standard_normal((rows, cols)).astype(np.float32))
+    g = np.ones(cols, np.float32)
+    b = np.zeros(cols, np.float32)
+    want = from_bf16_bits(x).copy()
+    orc.orc_layernorm_rows_f64(P(want), rows, cols, P(g), P(b), 1e-5)
+    dx, dg, db = ctx.put(x), ctx.put(g), ctx.put(b)
+    of = ctx.empty((rows, cols), np.float32)
+    mxenc.layernorm(ctx, dx, None, dg, db, 1e-5, rows, cols, out_f32=of)
+    assert np.max(np.abs(of.host() - want)) < 2e-5
+
+
+# ---- softmax -------------------------------------------------------------------
+
+def test_softmax_poly_masked(ctx, orc):
+    rng = np.random.default_rng(10)
+    B, H, S = 3, 4, 128
+    x = (rng.standard_normal((B * H * S, S)) * 3).astype(np.float32)
+    mask = np.zeros((B, S), np.float32)
+    mask[1, 70:] = -1e30
+    mask[2, 5:] = -1e30
+    want = x.copy()
+    orc.orc_softmax_rows_poly(P(want), B * H * S, S, P(mask), H * S)
+    dx, dm = ctx.put(x), ctx.put(mask)
+    mxenc.softmax_rows(ctx, dx, B * H * S, S, S, dm, H * S, mxenc.MX_SOFTMAX_POLY)
+    got = dx.host()
+    assert np.max(np.abs(got - want)) < 1e-6
+    assert np.all(got[H * S:2 * H * S, 70:] < 1e-30)
+
+
+@pytest.mark.parametrize("cols", [197, 1500])
+def test_softmax_exact_wide_rows(ctx, orc, cols):
+    rng = np.random.default_rng(cols)
+    rows = 300
+    x = (rng.standard_normal((rows, cols)) * 4).astype(np.float32)
+    want = x.copy()
+    orc.orc_softmax_rows_exact(P(want), rows, cols, None, 1)
+    dx = ctx.put(x)
+    mxenc.softmax_rows(ctx, dx, rows, cols, cols, None, 1, mxenc.MX_SOFTMAX_EXACT)
+    assert np.max(np.abs(dx.host() - want)) < 1e-6
+
+
+def test_softmax_aie_bf16(ctx, orc):
+    rng = np.random.default_rng(11)
+    rows, cols = 512, 64
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    x[7, 30:] = -1e30
+    xb = to_bf16_bits(x)
+    want = np.empty_like(xb)
+    orc.orc_aie_softmax_bf16(P(xb), P(want), rows, cols)
+    dx = ctx.put(xb)
+    mxenc.softmax_rows(ctx, dx, rows, cols, cols, None, 1, mxenc.MX_SOFTMAX_AIE)
+    got = dx.host()
+    # identical exponentials; the fp32 sum order differs: <= 1 bf16 ulp
+    assert np.max(np.abs(got.astype(np.int32) - want.astype(np.int32))) <= 1
+
+
+# ---- GEMM ------------------------------------------------------------------------
+
+GEMM_SHAPES = [
+    (77, 136, 200),      # every tail: M, N and K not multiples of the tiles
+    (256, 768, 2304),    # bge-base QKV shape at small M
+    (4096, 384, 1152),   # MiniLM QKV
+    (512, 3072, 768),    # bge-base FFN-down
+    (256, 768, 1000),    # ViT head-like N
+    (1000, 1280, 3840),  # Whisper QKV, ragged M
+]
+
+
+@pytest.mark.parametrize("M,K,N", GEMM_SHAPES)
+def test_gemm_vs_oracle(ctx, orc, M, K, N):
+    rng = np.random.default_rng(M * 7 + N)
+    A = to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    W = to_bf16_bits((rng.standard_normal((K, N)) * 0.05).astype(np.float32))
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    Af, Wf = from_bf16_bits(A), from_bf16_bits(W)
+    want = np.empty((M, N), np.float32)
+    orc.orc_gemm_nt(P(np.ascontiguousarray(Af)), M, P(np.ascontiguousarray(Wf)), K, N, P(bias),
+                    P(want))
+    dA = ctx.put(A)
+    dW = ctx.put(np.ascontiguousarray(W.T))  # [N, K] panel
+    db = ctx.put(bias)
+    C = ctx.empty((M, N), np.float32)
+    mxenc.gemm_wt(ctx, dA, M, K, K, dW, N, db, mxenc.MX_EPI_NONE, None, C, N)
+    got = C.host()
+    scale = np.max(np.abs(want))
+    assert np.max(np.abs(got - want)) / scale < 1e-5
+    # bf16 C: the same sums narrowed once
+    Cb = ctx.empty((M, N), np.uint16)
+    mxenc.gemm_wt(ctx, dA, M, K, K, dW, N, db, mxenc.MX_EPI_NONE, None, Cb, N)
+    gb = from_bf16_bits(Cb.host())
+    rel = np.abs(gb - want) / (np.abs(want) + 1e-3 * scale)
+    assert np.max(rel) < 1e-2  # the per-op GEMM bar: max relative error <= 1e-2
+    assert np.array_equal(Cb.host(), to_bf16_bits(got)) or \
+        np.mean(Cb.host() != to_bf16_bits(got)) < 1e-3
+
+
+def test_gemm_epilogues_and_residual(ctx, orc):
+    M, K, N = 300, 384, 1536
+    rng = np.random.default_rng(12)
+    A = to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    W = to_bf16_bits((rng.standard_normal((K, N)) * 0.05).astype(np.float32))
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    base = np.empty((M, N), np.float32)
+    orc.orc_gemm_nt(P(from_bf16_bits(A)), M, P(from_bf16_bits(W)), K, N, P(bias), P(base))
+    dA, dW, db = ctx.put(A), ctx.put(np.ascontiguousarray(W.T)), ctx.put(bias)
+    C = ctx.empty((M, N), np.float32)
+    for epi, fn in ((mxenc.MX_EPI_GELU_POLY, orc.orc_gelu_poly_inplace),
+                    (mxenc.MX_EPI_GELU_ERF, orc.orc_gelu_erf_inplace)):
+        want = base.copy()
+        fn(P(want), want.size)
+        mxenc.gemm_wt(ctx, dA, M, K, K, dW, N, db, epi, None, C, N)
+        assert np.max(np.abs(C.host() - want)) < 1e-4
+    R = (rng.standard_normal((M, N))).astype(np.float32)
+    dR = ctx.put(R)
+    mxenc.gemm_wt(ctx, dA, M, K, K, dW, N, db, mxenc.MX_EPI_NONE, dR, dR, N)  # in place
+    assert np.max(np.abs(dR.host() - (R + base))) < 1e-4
+
+
+def test_gemm_refusals(ctx):
+    A = ctx.empty((8, 12), np.uint16)
+    W = ctx.empty((8, 12), np.uint16)
+    C = ctx.empty((8, 8), np.float32)
+    with pytest.raises(mxenc.MxError, match="multiples of 8"):
+        mxenc.gemm_wt(ctx, A, 8, 12, 12, W, 8, None, 0, None, C, 8)
+
+
+# ---- attention -------------------------------------------------------------------
+
+def _attn_ref(orc, qkv_bits, B, S, H, hd, mask, scale=1.0):
+    d = H * hd
+    q = from_bf16_bits(qkv_bits).reshape(B * S, 3 * d).copy()
+    out = np.empty((B * S, d), np.float32)
+    if mask is None and scale != 1.0 or S % 8:
+        for b in range(B):
+            base = np.ascontiguousarray(q[b * S:(b + 1) * S])
+            import ctypes
+            o = np.empty((S, d), np.float32)
+            orc.orc_whisper_attention(P(base), 3 * d, ctypes.c_void_p(base.ctypes.data + d * 4),
+                                      3 * d, S, S, d, H, hd, scale, P(o))
+            out[b * S:(b + 1) * S] = o
+        return out
+    sc = np.empty((B * H * S, S), np.float32)
+    orc.orc_qk(P(q), B, S, H, hd, P(sc))
+    orc.orc_softmax_rows_poly(P(sc), B * H * S, S, P(mask) if mask is not None else None, H * S)
+    orc.orc_av(P(sc), P(q), B, S, H, hd, P(out))
+    return out
+
+
+@pytest.mark.parametrize("B,S,H,hd", [(4, 128, 3, 32), (3, 512, 2, 64), (2, 64, 12, 64)])
+def test_attention_masked_vs_oracle(ctx, orc, B, S, H, hd):
+    rng = np.random.default_rng(S + hd)
+    d = H * hd
+    qkv = to_bf16_bits((rng.standard_normal((B * S, 3 * d))).astype(np.float32))
+    lens = rng.integers(1, S + 1, size=B)
+    lens[0] = S
+    mask = np.zeros((B, S), np.float32)
+    for b, n in enumerate(lens):
+        mask[b, n:] = -1e30
+    kv = lens.astype(np.int32)
+    want = _attn_ref(orc, qkv, B, S, H, hd, mask)
+    dq, dm, dk = ctx.put(qkv), ctx.put(mask), ctx.put(kv)
+    out = ctx.empty((B * S, d), np.uint16)
+    for kvl in (None, dk):  # skipping masked tiles changes nothing the tolerance sees
+        mxenc.attention(ctx, dq, 3 * d, B, S, H, hd, 1.0, dm, kvl, out, d)
+        got = from_bf16_bits(out.host())
+        err = np.abs(got - want)
+        assert np.max(err) < 2e-2 * np.max(np.abs(want)), np.max(err)
+        assert np.mean(err) < 2e-3
+
+
+@pytest.mark.parametrize("B,S,H,scale", [(2, 197, 3, 0.125), (1, 1500, 2, 1.0)])
+def test_attention_unmasked_odd_lengths(ctx, orc, B, S, H, scale):
+    hd = 64
+    rng = np.random.default_rng(S)
+    d = H * hd
+    qkv = to_bf16_bits(rng.standard_normal((B * S, 3 * d)).astype(np.float32))
+    want = _attn_ref(orc, qkv, B, S, H, hd, None, scale)
+    dq = ctx.put(qkv)
+    out = ctx.empty((B * S, d), np.uint16)
+    mxenc.attention(ctx, dq, 3 * d, B, S, H, hd, scale, None, None, out, d)
+    got = from_bf16_bits(out.host())
+    assert np.max(np.abs(got - want)) < 2e-2 * np.max(np.abs(want))
+
+
+def test_attention_fully_masked_row_is_uniform(ctx):
+    """All keys masked with -1e30: the host softmax gives every key the same
+    weight; so does the kernel (kv_len = S, finite mask)."""
+    B, S, H, hd = 1, 64, 1, 64
+    rng = np.random.default_rng(5)
+    qkv = to_bf16_bits(rng.standard_normal((S, 3 * hd)).astype(np.float32))
+    mask = np.full((B, S), -1e30, np.float32)
+    dq, dm = ctx.put(qkv), ctx.put(mask)
+    out = ctx.empty((S, hd), np.uint16)
+    mxenc.attention(ctx, dq, 3 * hd, B, S, H, hd, 1.0, dm, None, out, hd)
+    v = from_bf16_bits(qkv)[:, 2 * hd:]
+    want = np.repeat(v.mean(0, keepdims=True), S, axis=0)
+    assert np.max(np.abs(from_bf16_bits(out.host()) - want)) < 2e-2
+
+
+# ---- embedding sum, mask, pooling ------------------------------------------------
+
+def test_embed_sum_mask_kvlen_bit_exact(ctx, orc, golden_dir):
+    z = np.load(golden_dir / "minilm_s64_pool.npz")
+    ids = np.ascontiguousarray(z["input_ids"])
+    am = np.ascontiguousarray(z["attention_mask"])
+    B, S = ids.shape
+    d = 384
+    rng = np.random.default_rng(13)
+    word = (rng.standard_normal((30522, d)) * 0.02).astype(np.float32)
+    pos = (rng.standard_normal((512, d)) * 0.02).astype(np.float32)
+    typ = (rng.standard_normal((2, d)) * 0.02).astype(np.float32)
+    want = np.empty((B * S, d), np.float32)
+    wmask = np.empty((B, S), np.float32)
+    orc.orc_embed_sum(P(ids), P(am), B, S, d, P(word), P(pos), P(typ), P(want), P(wmask))
+    L = mxenc.lib()
+    d_ids, d_am, d_w, d_p, d_t = ctx.put(ids), ctx.put(am), ctx.put(word), ctx.put(pos), ctx.put(typ)
+    emb = ctx.empty((B * S, d), np.float32)
+    msk = ctx.empty((B, S), np.float32)
+    kvl = ctx.empty((B,), np.int32)
+    mxenc.check(L.mx_embed_sum(ctx.stream, d_ids.p, d_am.p, B, S, d, d_w.p, 30522, d_p.p, d_t.p,
+                               emb.p, msk.p, kvl.p))
+    assert np.array_equal(emb.host(), want)
+    assert np.array_equal(msk.host(), wmask)
+    assert np.array_equal(kvl.host(), am.sum(1).astype(np.int32))  # prefix masks: 8,22,17,33
+    bad = ids.copy()
+    bad[1, 3] = 30522
+    d_bad = ctx.put(bad)
+    with pytest.raises(mxenc.MxError, match="outside"):
+        mxenc.check(L.mx_embed_sum(ctx.stream, d_bad.p, d_am.p, B, S, d, d_w.p, 30522, d_p.p,
+                                   d_t.p, emb.p, None, None))
+
+
+@pytest.mark.parametrize("cls", [0, 1])
+def test_pool_rows_bit_exact_on_reference_goldens(ctx, orc, golden_dir, cls):
+    if cls:
+        z = np.load(golden_dir / "bge_base_s64_cls.npz")
+        head = z["last_hidden_state_head"]
+        B, _, d = head.shape
+        S = z["attention_mask"].shape[1]
+        h = np.full((B, S, d), np.nan, np.float32)
+        h[:, :4] = head
+    else:
+        z = np.load(golden_dir / "minilm_s64_pool.npz")
+        h = np.ascontiguousarray(z["last_hidden_state"])
+        B, S, d = h.shape
+    am = np.ascontiguousarray(z["attention_mask"])
+    L = mxenc.lib()
+    dh, dam = ctx.put(h), ctx.put(am)
+    out = ctx.empty((B, d), np.float32)
+    for l2 in (0, 1):
+        want = np.empty((B, d), np.float32)
+        assert orc.orc_pool_rows(P(h), P(am), B, S, d, cls, l2, P(want)) == 0
+        mxenc.check(L.mx_pool_rows(ctx.stream, dh.p, dam.p, B, S, d, cls, l2, out.p))
+        assert np.array_equal(out.host().view(np.uint32), want.view(np.uint32))
+    # and against the reference's own golden embedding
+    assert np.max(np.abs(out.host() - z["embedding"])) < 1e-7
+    if cls:
+        am2 = am.copy()
+        am2[1, 0] = 0
+        dam2 = ctx.put(am2)
+        with pytest.raises(mxenc.MxError, match="first token is masked"):
+            mxenc.check(L.mx_pool_rows(ctx.stream, dh.p, dam2.p, B, S, d, 1, 1, out.p))
