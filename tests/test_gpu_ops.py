@@ -112,7 +112,11 @@ def test_gelu_erf_as_bf16_matches_aie_restatement(ctx, orc):
 
 def test_gelu_poly_bf16_vs_aie_kernel(ctx, orc):
     """bf16 in/out: the fused-FMA polynomial against gelu_poly_rne.cc's
-    multiply-then-add: at most one bf16 ulp apart."""
+    multiply-then-add. Where the output is not small they are at most one bf16
+    ulp apart. Near |x| = 4 the polynomial cancels to ~3e-4 from terms of size
+    ~0.5 and each Horner step's rounding is amplified by u^(8-k) ~ 4^7, so the
+    two evaluation orders differ by up to ~4e-6 absolute there (two bf16 ulps
+    of a 3e-4 output); 1e-5 absolute bounds that."""
     x = np.linspace(-9, 9, 1 << 16, dtype=np.float32)
     xb = to_bf16_bits(x)
     want = np.empty_like(xb)
@@ -121,7 +125,14 @@ def test_gelu_poly_bf16_vs_aie_kernel(ctx, orc):
     dy = ctx.empty(xb.shape, np.uint16)
     mxenc.gelu(ctx, dx, dy, mxenc.MX_GELU_POLY)
     got = dy.host()
-    assert np.max(np.abs(got.astype(np.int32) - want.astype(np.int32))) <= 1
+    wf, gf = from_bf16_bits(want), from_bf16_bits(got)
+    big = np.abs(wf) >= 1e-2
+    assert np.max(np.abs(got[big].astype(np.int32) - want[big].astype(np.int32))) <= 1
+    assert np.max(np.abs(gf[~big] - wf[~big])) <= 1e-5
+    # and the fp32-then-narrow result is the host gelu_cpu's, narrowed, bit for bit
+    f = from_bf16_bits(xb).copy()
+    orc.orc_gelu_poly_inplace(P(f), f.size)
+    assert np.array_equal(got, to_bf16_bits(f))
 
 
 # ---- LayerNorm -----------------------------------------------------------------
@@ -194,7 +205,16 @@ def test_softmax_exact_wide_rows(ctx, orc, cols):
     orc.orc_softmax_rows_exact(P(want), rows, cols, None, 1)
     dx = ctx.put(x)
     mxenc.softmax_rows(ctx, dx, rows, cols, cols, None, 1, mxenc.MX_SOFTMAX_EXACT)
-    assert np.max(np.abs(dx.host() - want)) < 1e-6
+    got = dx.host()
+    # The host sums the exponentials left to right, the kernel as a tree, and
+    # the two exps may differ by an ulp: relative gap ~ (cols**0.5) * 2^-24,
+    # bounded here by 1e-5 (1e-12 absolute for the tiny probabilities).
+    assert np.max(np.abs(got - want) / (want + 1e-7)) < 1e-5
+    # and both sit within the same bound of the fp64 closed form
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(1, keepdims=True))
+    exact = e / e.sum(1, keepdims=True)
+    assert np.max(np.abs(got - exact) / (exact + 1e-7)) < 1e-5
 
 
 def test_softmax_aie_bf16(ctx, orc):
@@ -259,7 +279,8 @@ def test_gemm_epilogues_and_residual(ctx, orc):
     W = to_bf16_bits((rng.standard_normal((K, N)) * 0.05).astype(np.float32))
     bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
     base = np.empty((M, N), np.float32)
-    orc.orc_gemm_nt(P(from_bf16_bits(A)), M, P(from_bf16_bits(W)), K, N, P(bias), P(base))
+    Af, Wf = from_bf16_bits(A), from_bf16_bits(W)  # kept alive across the call
+    orc.orc_gemm_nt(P(Af), M, P(Wf), K, N, P(bias), P(base))
     dA, dW, db = ctx.put(A), ctx.put(np.ascontiguousarray(W.T)), ctx.put(bias)
     C = ctx.empty((M, N), np.float32)
     for epi, fn in ((mxenc.MX_EPI_GELU_POLY, orc.orc_gelu_poly_inplace),
