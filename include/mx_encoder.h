@@ -135,6 +135,14 @@ int mx_gemm_wt(mx_stream *s, const uint16_t *A, int64_t M, int64_t K,
                int epilogue, const float *residual, void *C, int c_dtype,
                int64_t ldc);
 
+/* The GEMM kernel configuration mx_gemm / mx_gemm_wt choose for an [M, K] x
+ * [K, N] product with aligned operands (no counterpart in the reference,
+ * whose array GEMM has one fixed tiling per design): "lds_*" names the
+ * direct-to-LDS pipelined kernel and its block tile, "staged_*" the
+ * register-staged kernel used when K % 32 != 0 or an operand is not
+ * vector-aligned. */
+const char *mx_gemm_plan(int64_t M, int64_t N, int64_t K);
+
 /* attn (+softm fused): replaces the host qk/softmax_cpu/av triple
  * (bert_encoder.cpp:995-1135, :481-530), BertEncoder::attention_npu /
  * NpuAttention::run (runtime/src/whisper/attention_npu.cpp:177) and

@@ -23,7 +23,8 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(HERE, "..", "include"),
 ]
-SOURCES = ["k_elem.hip", "k_gemm.hip", "k_attn.hip", "mx_abi.cpp", "mx_encoder.cpp"]
+SOURCES = ["k_elem.hip", "k_gemm.hip", "k_gemm_lds.hip", "k_attn.hip", "mx_abi.cpp",
+           "mx_encoder.cpp"]
 
 
 def _compile(src):

@@ -38,12 +38,6 @@ struct GemmCfg {
   static_assert(WM % 32 == 0 && WN % 32 == 0 && BK % 16 == 0, "MFMA tile shape");
 };
 
-__device__ __forceinline__ float apply_epi(float v, int epi) {
-  if (epi == 1) return gelu_poly(v);
-  if (epi == 2) return gelu_erf(v);
-  return v;
-}
-
 template <int BM, int BN, int BK, int WM, int WN>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_bf16_k(
     const uint16_t *__restrict__ A, int64_t lda, const uint16_t *__restrict__ Wt, int M, int N,
@@ -144,7 +138,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_bf16_k(
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + rbase + (r & 3);
         if (row >= M) continue;
-        float v = apply_epi(acc[i][j][r] + bj, epi);
+        float v = gemm_epilogue(acc[i][j][r] + bj, epi);
         const int64_t off = (int64_t)row * ldc + col;
         if (residual) v += residual[off];
         if (c_bf16)
@@ -171,15 +165,59 @@ hipError_t launch(const mxk::GemmArgs &a, hipStream_t s) {
 
 namespace mxk {
 
+// The LDS-pipelined kernel (k_gemm_lds.hip) serves every call whose K is a
+// multiple of 32 and whose C, bias and residual allow 16-byte (fp32) or 8-byte
+// (bf16) vector access; the register-staged kernel above serves the rest.
+template <int BM, int BN, int WGM, int WGN, int NS>
+hipError_t gemm_lds_launch(const GemmArgs &a, hipStream_t s);
+
+namespace {
+
+enum GemmPath { PATH_STAGED, PATH_LDS_256x256, PATH_LDS_128x256, PATH_LDS_128x128 };
+
+bool lds_path_ok(const GemmArgs &a) {
+  const uintptr_t c = (uintptr_t)a.C;
+  const size_t cvec = a.c_bf16 ? 8 : 16;
+  return a.K % 32 == 0 && a.lda % 8 == 0 && a.ldc % 4 == 0 && c % cvec == 0 &&
+         (!a.bias || (uintptr_t)a.bias % 16 == 0) &&
+         (!a.residual || (uintptr_t)a.residual % 16 == 0);
+}
+
+GemmPath pick(const GemmArgs &a) {
+  if (!lds_path_ok(a)) return PATH_STAGED;
+  const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+  const int64_t t128x256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
+  // 256x256 tiles once there are at least two full waves of them over the
+  // 256 CUs and N is wide; else 128x256; tiny problems take 128x128.
+  if (a.N >= 1536 && t256 >= 512) return PATH_LDS_256x256;
+  if (t128x256 >= 256) return PATH_LDS_128x256;
+  return PATH_LDS_128x128;
+}
+
+}  // namespace
+
 const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
-  (void)M;
-  (void)N;
-  (void)K;
-  return "128x128x64_w64x64";
+  GemmArgs a{};
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.lda = K;
+  a.ldc = N;
+  switch (pick(a)) {
+    case PATH_LDS_256x256: return "lds_256x256x32_w128x64_ns3";
+    case PATH_LDS_128x256: return "lds_128x256x32_w64x64_ns4";
+    case PATH_LDS_128x128: return "lds_128x128x32_w64x64_ns4";
+    default: return "staged_128x128x64_w64x64";
+  }
 }
 
 hipError_t gemm(const GemmArgs &a, hipStream_t s) {
-  return launch<128, 128, 64, 64, 64>(a, s);
+  switch (pick(a)) {
+    case PATH_LDS_256x256: return gemm_lds_launch<256, 256, 2, 4, 3>(a, s);
+    case PATH_LDS_128x256: return gemm_lds_launch<128, 256, 2, 4, 4>(a, s);
+    case PATH_LDS_128x128: return gemm_lds_launch<128, 128, 2, 2, 4>(a, s);
+    default: return launch<128, 128, 64, 64, 64>(a, s);
+  }
 }
 
 }  // namespace mxk

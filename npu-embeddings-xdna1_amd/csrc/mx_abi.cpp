@@ -344,6 +344,10 @@ int mx_gemm_wt(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t ld
   return gemm_checked(s, A, M, K, lda, Wt, N, bias, epilogue, residual, C, c_dtype, ldc);
 }
 
+const char *mx_gemm_plan(int64_t M, int64_t N, int64_t K) {
+  return mxk::gemm_config_name(M, N, K);
+}
+
 int mx_attention(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
                  int64_t H, int64_t hd, float scale, const float *add_mask,
                  const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx) {

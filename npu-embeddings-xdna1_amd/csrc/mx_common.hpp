@@ -59,6 +59,13 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
 }
 
+// The GEMM epilogue activation (mx_epilogue): 0 none, 1 gelu_poly, 2 gelu_erf.
+__device__ __forceinline__ float gemm_epilogue(float v, int epi) {
+  if (epi == 1) return gelu_poly(v);
+  if (epi == 2) return gelu_erf(v);
+  return v;
+}
+
 // exp2_avx2 (host_kernels.hpp:358-379): k = trunc(x), f = x - k, degree-7
 // Horner by FMA, times 2^k written into the exponent field. Bit-identical to
 // the host lane for x in [-126, 127].

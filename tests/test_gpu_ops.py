@@ -295,6 +295,58 @@ def test_gemm_epilogues_and_residual(ctx, orc):
     assert np.max(np.abs(dR.host() - (R + base))) < 1e-4
 
 
+GEMM_PATHS = [
+    # M, K, N, epilogue, C dtype, residual, expected kernel
+    (16384, 768, 2304, mxenc.MX_EPI_NONE, np.uint16, False, "lds_256x256"),     # QKV
+    (16384, 768, 3072, mxenc.MX_EPI_GELU_POLY, np.uint16, False, "lds_256x256"),  # FFN-up
+    (16384, 3072, 768, mxenc.MX_EPI_NONE, np.float32, False, "lds_128x256"),    # FFN-down
+    (16384, 768, 768, mxenc.MX_EPI_NONE, np.float32, True, "lds_128x256"),      # x += proj
+    (1000, 1280, 3840, mxenc.MX_EPI_GELU_ERF, np.float32, True, "lds_128x128"),  # ragged M
+    (777, 512, 1004, mxenc.MX_EPI_GELU_ERF, np.uint16, False, "lds_128x128"),   # ragged M, N
+]
+
+
+@pytest.mark.parametrize("M,K,N,epi,cdt,res,plan", GEMM_PATHS)
+def test_gemm_kernel_paths(ctx, orc, M, K, N, epi, cdt, res, plan):
+    """Each GEMM kernel configuration at a size that selects it, checked on a
+    subset of rows (rows are independent) against the oracle's gemm_nt with
+    the same epilogue: the first and last 128 rows and 128 random ones."""
+    assert mxenc.lib().mx_gemm_plan(M, N, K).decode().startswith(plan)
+    rng = np.random.default_rng(M + K + N)
+    A = to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    W = to_bf16_bits((rng.standard_normal((K, N)) * 0.05).astype(np.float32))
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    R = rng.standard_normal((M, N)).astype(np.float32) if res else None
+    dA, dW, db = ctx.put(A), ctx.put(np.ascontiguousarray(W.T)), ctx.put(bias)
+    if res:
+        dC = ctx.put(R)  # in place: C = epi(A W + b) + C
+        mxenc.gemm_wt(ctx, dA, M, K, K, dW, N, db, epi, dC, dC, N)
+    else:
+        dC = ctx.empty((M, N), cdt)
+        mxenc.gemm_wt(ctx, dA, M, K, K, dW, N, db, epi, None, dC, N)
+    got = dC.host()
+    rows = np.unique(np.concatenate([np.arange(128), np.arange(M - 128, M),
+                                     rng.integers(0, M, 128)]))
+    Af = np.ascontiguousarray(from_bf16_bits(A[rows]))
+    Wf = np.ascontiguousarray(from_bf16_bits(W))
+    want = np.empty((rows.size, N), np.float32)
+    orc.orc_gemm_nt(P(Af), rows.size, P(Wf), K, N, P(bias), P(want))
+    if epi == mxenc.MX_EPI_GELU_POLY:
+        orc.orc_gelu_poly_inplace(P(want), want.size)
+    elif epi == mxenc.MX_EPI_GELU_ERF:
+        orc.orc_gelu_erf_inplace(P(want), want.size)
+    if res:
+        want += R[rows]
+    g = got[rows]
+    scale = np.max(np.abs(want))
+    if cdt == np.uint16:
+        g = from_bf16_bits(g)
+        # one bf16 rounding of an fp32 result: half a bf16 ulp relative
+        assert np.max(np.abs(g - want) / (np.abs(want) + 1e-3 * scale)) < 1e-2
+    else:
+        assert np.max(np.abs(g - want)) / scale < 1e-5
+
+
 def test_gemm_refusals(ctx):
     A = ctx.empty((8, 12), np.uint16)
     W = ctx.empty((8, 12), np.uint16)
