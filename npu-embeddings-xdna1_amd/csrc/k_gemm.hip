@@ -165,11 +165,12 @@ hipError_t launch(const mxk::GemmArgs &a, hipStream_t s) {
 
 namespace mxk {
 
-// The LDS-pipelined kernel (k_gemm_lds.hip) serves every call whose K is a
-// multiple of 32 and whose C, bias and residual allow 16-byte (fp32) or 8-byte
-// (bf16) vector access; the register-staged kernel above serves the rest.
+// The persistent LDS-pipelined kernel (k_gemm_lds.hip) serves every call it
+// can: K a multiple of 32 and at least 128 (four slabs, the deepest ring), N a
+// multiple of 4, a bias, and C, bias and residual aligned for 16-byte vector
+// access; the register-staged kernel above serves the rest.
 template <int BM, int BN, int WGM, int WGN, int NS>
-hipError_t gemm_lds_launch(const GemmArgs &a, hipStream_t s);
+hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s);
 
 namespace {
 
@@ -177,9 +178,8 @@ enum GemmPath { PATH_STAGED, PATH_LDS_256x256, PATH_LDS_128x256, PATH_LDS_128x12
 
 bool lds_path_ok(const GemmArgs &a) {
   const uintptr_t c = (uintptr_t)a.C;
-  const size_t cvec = a.c_bf16 ? 8 : 16;
-  return a.K % 32 == 0 && a.lda % 8 == 0 && a.ldc % 4 == 0 && c % cvec == 0 &&
-         (!a.bias || (uintptr_t)a.bias % 16 == 0) &&
+  return a.K % 32 == 0 && a.K >= 128 && a.N % 4 == 0 && a.lda % 8 == 0 && a.bias &&
+         a.ldc % (a.c_bf16 ? 8 : 4) == 0 && c % 16 == 0 && (uintptr_t)a.bias % 16 == 0 &&
          (!a.residual || (uintptr_t)a.residual % 16 == 0);
 }
 
@@ -187,35 +187,53 @@ GemmPath pick(const GemmArgs &a) {
   if (!lds_path_ok(a)) return PATH_STAGED;
   const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
   const int64_t t128x256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
-  // 256x256 tiles once there are at least two full waves of them over the
-  // 256 CUs and N is wide; else 128x256; tiny problems take 128x128.
+  // 256x256 tiles once there are at least two rounds of them over the 256
+  // CUs and N is wide; else 128x256; small problems take 128x128.
   if (a.N >= 1536 && t256 >= 512) return PATH_LDS_256x256;
   if (t128x256 >= 256) return PATH_LDS_128x256;
   return PATH_LDS_128x128;
 }
 
+// Resident blocks of the persistent kernel: one per CU of the current device.
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 }  // namespace
 
 const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
+  static const float aligned_probe[4] __attribute__((aligned(16))) = {0, 0, 0, 0};
   GemmArgs a{};
   a.M = M;
   a.N = N;
   a.K = K;
   a.lda = K;
   a.ldc = N;
+  a.bias = aligned_probe;
+  a.C = (void *)aligned_probe;
   switch (pick(a)) {
-    case PATH_LDS_256x256: return "lds_256x256x32_w128x64_ns3";
-    case PATH_LDS_128x256: return "lds_128x256x32_w64x64_ns4";
-    case PATH_LDS_128x128: return "lds_128x128x32_w64x64_ns4";
+    case PATH_LDS_256x256: return "lds_256x256x32_w128x64_ns3_persistent";
+    case PATH_LDS_128x256: return "lds_128x256x32_w64x64_ns4_persistent";
+    case PATH_LDS_128x128: return "lds_128x128x32_w64x64_ns4_persistent";
     default: return "staged_128x128x64_w64x64";
   }
 }
 
 hipError_t gemm(const GemmArgs &a, hipStream_t s) {
   switch (pick(a)) {
-    case PATH_LDS_256x256: return gemm_lds_launch<256, 256, 2, 4, 3>(a, s);
-    case PATH_LDS_128x256: return gemm_lds_launch<128, 256, 2, 4, 4>(a, s);
-    case PATH_LDS_128x128: return gemm_lds_launch<128, 128, 2, 2, 4>(a, s);
+    case PATH_LDS_256x256: return gemm_lds_launch<256, 256, 2, 4, 3>(a, cu_count(), s);
+    case PATH_LDS_128x256: return gemm_lds_launch<128, 256, 2, 4, 4>(a, cu_count(), s);
+    case PATH_LDS_128x128: return gemm_lds_launch<128, 128, 2, 2, 4>(a, cu_count(), s);
     default: return launch<128, 128, 64, 64, 64>(a, s);
   }
 }

@@ -1,40 +1,59 @@
-// k_gemm_lds.hip -- the encoder's bf16 GEMM, pipelined through LDS by direct
-// global->LDS loads (gfx950 global_load_lds_dwordx4).
+// k_gemm_lds.hip -- the encoder's bf16 GEMM on gfx950: a persistent kernel
+// whose operand tiles reach LDS by direct global->LDS loads
+// (global_load_lds_dwordx4) through a ring of slabs.
 //
 // C[M, N] = epilogue(A[M, K] @ W[K, N] + bias) (+ residual), A bf16 row-major,
 // W held as Wt[N, K] (K contiguous), fp32 accumulation in
 // v_mfma_f32_32x32x16_bf16, one to_bf16 rounding at the store when C is bf16.
 //
-// Pipeline. The K axis advances BK = 32 at a time through an NS-slot LDS ring.
-// Each slab is fetched straight into LDS by global_load_lds_dwordx4 (every lane
-// moves 16 bytes; one wave instruction fills 1 KB of LDS), NS - 1 slabs ahead
-// of the one the MFMAs consume, so no VGPR holds staged tiles and ~NS-1 slab
-// times of HBM latency are covered. The loads are issued from inline assembly:
-// the compiler's own wait insertion would otherwise put vmcnt(0) -- a wait on
-// every prefetch -- before each LDS read. Each wave waits for its own loads of
-// the slab it is about to read (vmcnt = loads it issued since), then all waves
-// meet at one barrier per slab; the barrier also proves every wave has left
-// the slot the next prefetch overwrites.
+// Grid. One block per CU walks a list of BM x BN output tiles; its slabs
+// (BK = 32 deep) form one sequence across tile boundaries, so the ring keeps
+// loading the next tile's first slabs while the current tile drains: no
+// per-tile prologue latency, no block relaunch. Workgroups go round-robin
+// over the 8 XCDs, so the blocks of XCD x (blockIdx % 8 == x) share the x-th
+// eighth of the tiles (row-major over (m, n)) and walk it together: they
+// share A row-panels and W in that XCD's L2, and every XCD gets the same
+// share of the work even when the tiles do not fill whole rounds.
 //
-// LDS image. A slab is rows of 32 bf16 = 64 bytes = four 16-byte chunks. Chunk
-// c of row r is stored at position c ^ ((r >> 1) & 3) of its row, so the eight
-// lanes of one ds_read_b128 phase (rows r..r+7, same logical chunk) hit eight
-// different 16-byte bank groups. The direct load writes lane l's 16 bytes at
-// LDS offset 16*l of its 1 KB window, so the swizzle is applied to the GLOBAL
-// address each lane fetches: lane l fills row l/4, position l%4, i.e. logical
-// chunk (l%4) ^ (((l/4) >> 1) & 3).
+// Ring. NS slots; slab s + NS is fetched into slot s % NS as soon as every read
+// of slab s is done, i.e. ~NS - 1 slabs ahead of its use. The loads are issued
+// from inline assembly: the compiler's own wait insertion would otherwise put
+// vmcnt(0) -- a wait on every prefetch -- before each LDS read. Each wave waits
+// for its own loads of the slab it is about to read (vmcnt = loads it issued
+// since; loads complete in issue order), then all waves meet at one barrier
+// per slab. The first slab of each tile also moves the tile's bias into a
+// per-tile-parity LDS copy (a few lanes of one extra load per wave), so the
+// bias is on chip for the epilogue without a compiler-tracked load; the waits
+// do not count that load, which only makes them stricter.
+//
+// Fragments. Two register sets, one per 16-deep half of a slab; each half's
+// MFMAs run while the other set is read from LDS (one ds_read after each of
+// the first MFMAs, pinned by sched_group_barrier). The barrier sits between
+// the halves, when every read of the current slab has been issued.
+//
+// LDS image. A slab is rows of 32 bf16 = 64 bytes = four 16-byte chunks. gfx950
+// serves a ds_read_b128 sixteen lanes (256 bytes, all 64 banks) per cycle; the
+// sixteen lanes of one phase read rows r..r+15 at the same logical chunk.
+// Chunk c of row r is stored at position c ^ ((r >> 2) & 3) of its row, which
+// puts those sixteen 16-byte reads in sixteen different bank groups. The
+// direct load writes lane l's 16 bytes at LDS offset 16*l of its 1 KB window,
+// so the swizzle is applied to the GLOBAL address each lane fetches: lane l
+// fills row l/4, position l%4, i.e. logical chunk (l%4) ^ (((l/4) >> 2) & 3).
 //
 // Operand roles. The MFMA's first operand is the W tile and its second the A
-// tile, so the 32x32 accumulator holds C^T: each lane owns one row m of C and
-// runs of four consecutive columns, stored as 8-byte (bf16) or 16-byte (fp32)
-// vectors instead of 2- or 4-byte scalars.
+// tile, so the 32x32 accumulator holds C^T: each lane owns one row of C and
+// runs of four consecutive columns.
 //
-// Edges. Rows past M (or N) are fetched from a clamped, in-bounds row and never
-// stored. K must be a multiple of 32 (the launcher routes anything else to the
-// register-staged kernel in k_gemm.hip).
+// Epilogue. Per 32 x 32 accumulator block a wave adds the bias, applies the
+// activation, writes the fp32 block to its private LDS staging area (rows
+// padded by 16 bytes) and reads it back row-major, so every global store (and
+// residual load) of a wave covers whole 128-byte (fp32) or 64-byte (bf16) row
+// segments instead of 16-byte pieces of 32 rows.
 //
-// Blocks are numbered so that each XCD (workgroups go round-robin over the 8
-// XCDs) owns a contiguous run of tiles in row-major (m, n) order.
+// Requirements (the launcher routes anything else to k_gemm.hip's kernel):
+// K % 32 == 0 and K >= 32 * NS, N % 4 == 0, a bias, 16-byte aligned operands.
+// Rows past M (or N) are fetched from a clamped, in-bounds row and never
+// stored.
 #include "mx_common.hpp"
 #include "mx_kernels.hpp"
 
@@ -43,12 +62,14 @@ using namespace mxd;
 namespace {
 
 constexpr int BK = 32;
-constexpr int ROWB = BK * 2;  // bytes per LDS row
+constexpr int ROWB = BK * 2;   // bytes per LDS slab row
+constexpr int STG_ROWB = 144;  // staging row: 32 fp32 + 16 bytes of padding
+constexpr int STG_WAVE = 32 * STG_ROWB;
 
 template <int BM, int BN, int WGM, int WGN, int NS>
 struct LdsCfg {
-  static constexpr int NW = WGM * WGN;          // waves
-  static constexpr int NT = NW * 64;            // threads
+  static constexpr int NW = WGM * WGN;                // waves
+  static constexpr int NT = NW * 64;                  // threads
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
   static constexpr int TM = WM / 32, TN = WN / 32;    // 32x32 MFMA tiles per wave
   static constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB;
@@ -56,12 +77,16 @@ struct LdsCfg {
   static constexpr int A_LOADS = A_BYTES / 1024 / NW;  // 1 KB wave loads per wave per slab
   static constexpr int B_LOADS = B_BYTES / 1024 / NW;
   static constexpr int LOADS = A_LOADS + B_LOADS;
-  static constexpr int LDS = NS * SLOT;
+  static constexpr int BIAS_PER_WAVE = BN / NW;        // floats each wave's bias piece moves
+  static constexpr int STG_OFF = NS * SLOT;
+  static constexpr int BIAS_OFF = STG_OFF + NW * STG_WAVE;
+  static constexpr int LDS = BIAS_OFF + 2 * BN * 4;
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be whole MFMA tiles");
   static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0,
                 "each wave must issue whole 1 KB loads");
+  static_assert(BIAS_PER_WAVE % 4 == 0 && BIAS_PER_WAVE <= 256, "bias piece: 16-byte lanes");
   static_assert(LDS <= 160 * 1024, "gfx950 LDS is 160 KB");
-  static_assert(NS >= 2 && LOADS * (NS - 1) < 64, "vmcnt holds at most 63");
+  static_assert(NS >= 3 && LOADS * (NS - 2) < 64, "vmcnt holds at most 63");
 };
 
 // s_waitcnt vmcnt(N), other counters untouched.
@@ -71,16 +96,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// One wave-wide direct load: 64 lanes x 16 bytes from `src` (per lane) into
-// LDS bytes [lds, lds + 1024) in lane order.
+// One wave-wide direct load: each active lane moves 16 bytes from `src` into
+// LDS byte lds + 16 * lane.
 __device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-               ::"s"(lds), "v"(src)
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
                : "memory");
 }
 
-// Epilogue variants are compile-time: EPI (mx_epilogue), RES (fp32 residual
-// added after the activation), CBF (bf16 C).
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF>
 __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
     const uint16_t *__restrict__ A, int64_t lda, const uint16_t *__restrict__ Wt, int M, int N,
@@ -90,75 +112,77 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
   constexpr int TM = Cfg::TM, TN = Cfg::TN;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
-  const int total = tiles_m * tiles_n;
-  int tile = blockIdx.x;
-  if ((total & 7) == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-  const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
-  const int m0 = tm * BM, n0 = tn * BN;
+  // This block's tiles: t(i) = first + i * stride, i < my_tiles. With a grid
+  // that is a multiple of 8, XCD x owns tiles [x*chunk, (x+1)*chunk) and its
+  // G/8 blocks interleave over them.
+  const int ntiles = tiles_m * tiles_n;
+  const int G = gridDim.x;
+  int first = (int)blockIdx.x, stride = G, end = ntiles;
+  if ((G & 7) == 0 && G >= 16) {
+    const int chunk = (ntiles + 7) >> 3, x = (int)(blockIdx.x & 7);
+    first = x * chunk + (int)(blockIdx.x >> 3);
+    stride = G >> 3;
+    end = min(ntiles, (x + 1) * chunk);
+  }
+  if (first >= end) return;
+  const int my_tiles = (end - 1 - first) / stride + 1;
+  const int nk = K / BK;
+  const int nslab = my_tiles * nk;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave - wm * WGN;
   const int li = lane & 31, g = lane >> 5;
 
-  // Per-lane source pointers of this wave's loads (row within its 1 KB window
-  // = lane / 4, logical chunk = swizzled lane % 4). Rows are clamped in bounds.
+  // Load addressing: lane fills row lrow of a 16-row window, logical chunk
+  // lchunk (swizzled); rows are clamped in bounds.
   const int lrow = lane >> 2;
-  const int lchunk = (lane & 3) ^ ((lrow >> 1) & 3);
-  const uint16_t *srcA[Cfg::A_LOADS];
-  const uint16_t *srcB[Cfg::B_LOADS];
-#pragma unroll
-  for (int i = 0; i < Cfg::A_LOADS; ++i) {
-    int r = m0 + (wave * Cfg::A_LOADS + i) * 16 + lrow;
-    r = r < M ? r : M - 1;
-    srcA[i] = A + (int64_t)r * lda + lchunk * 8;
-  }
-#pragma unroll
-  for (int i = 0; i < Cfg::B_LOADS; ++i) {
-    int r = n0 + (wave * Cfg::B_LOADS + i) * 16 + lrow;
-    r = r < N ? r : N - 1;
-    srcB[i] = Wt + (int64_t)r * K + lchunk * 8;
-  }
+  const int lchunk = (lane & 3) ^ ((lrow >> 2) & 3);
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-  auto issue = [&](int kt) {
-    const uint32_t slot = lds0 + (uint32_t)((kt % NS) * Cfg::SLOT);
-    const int k0 = kt * BK;
-#pragma unroll
-    for (int i = 0; i < Cfg::A_LOADS; ++i)
-      dma16(srcA[i] + k0, slot + (uint32_t)((wave * Cfg::A_LOADS + i) * 1024));
-#pragma unroll
-    for (int i = 0; i < Cfg::B_LOADS; ++i)
-      dma16(srcB[i] + k0, slot + Cfg::A_BYTES + (uint32_t)((wave * Cfg::B_LOADS + i) * 1024));
+  // Issue cursor: slab is_s = tile is_ti, depth is_kt, tile origin (is_m0, is_n0).
+  int is_s = 0, is_ti = 0, is_kt = 0, is_m0 = 0, is_n0 = 0;
+  auto tile_origin = [&](int ti, int &m0, int &n0) {
+    const int t = first + ti * stride;
+    const int tm = t / tiles_n;
+    m0 = tm * BM;
+    n0 = (t - tm * tiles_n) * BN;
   };
-
-  const int nk = K / BK;
+  tile_origin(0, is_m0, is_n0);
+  // Issue the loads of slab is_s, then advance the cursor.
+  auto issue = [&]() {
+    const int ti = is_ti, kt = is_kt, m0 = is_m0, n0 = is_n0;
+    const uint32_t slot = lds0 + (uint32_t)((is_s % NS) * Cfg::SLOT);
+    const int kofs = kt * BK + lchunk * 8;
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
-    if (s < nk) issue(s);
-
-  // The bias of this lane's columns, fetched while the first slabs land:
-  // column n = n0 + wn*WN + 32*j + 8*q + 4*g + e.
-  const int cbase = n0 + wn * Cfg::WN + g * 4;
-  const bool cols_full = n0 + BN <= N;
-  float4 bv[TN][4];
-#pragma unroll
-  for (int j = 0; j < TN; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int col = cbase + j * 32 + q * 8;
-      float4 b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (bias) {
-        if (cols_full) {
-          b = *(const float4 *)(bias + col);
-        } else {
-          if (col + 0 < N) b.x = bias[col + 0];
-          if (col + 1 < N) b.y = bias[col + 1];
-          if (col + 2 < N) b.z = bias[col + 2];
-          if (col + 3 < N) b.w = bias[col + 3];
-        }
-      }
-      bv[j][q] = b;
+    for (int i = 0; i < Cfg::A_LOADS; ++i) {
+      int r = m0 + (wave * Cfg::A_LOADS + i) * 16 + lrow;
+      r = r < M ? r : M - 1;
+      dma16(A + (int64_t)r * lda + kofs, slot + (uint32_t)((wave * Cfg::A_LOADS + i) * 1024));
     }
+#pragma unroll
+    for (int i = 0; i < Cfg::B_LOADS; ++i) {
+      int r = n0 + (wave * Cfg::B_LOADS + i) * 16 + lrow;
+      r = r < N ? r : N - 1;
+      dma16(Wt + (int64_t)r * K + kofs,
+            slot + Cfg::A_BYTES + (uint32_t)((wave * Cfg::B_LOADS + i) * 1024));
+    }
+    // Bias piece, on a tile's first slab: lanes 0 .. BIAS_PER_WAVE/4 - 1 move
+    // 16 bytes each of the columns from n0 + wave * BIAS_PER_WAVE (clamped in
+    // bounds; a column >= N is never stored). The other lanes are inactive
+    // for this load and write nothing.
+    if (kt == 0 && lane < Cfg::BIAS_PER_WAVE / 4) {
+      int c = n0 + wave * Cfg::BIAS_PER_WAVE + lane * 4;
+      c = c < N ? c : N - 4;
+      dma16(bias + c,
+            lds0 + Cfg::BIAS_OFF + (uint32_t)((ti & 1) * BN * 4 + wave * Cfg::BIAS_PER_WAVE * 4));
+    }
+    ++is_s;
+    if (++is_kt == nk) {
+      is_kt = 0;
+      ++is_ti;
+      if (is_ti < my_tiles) tile_origin(is_ti, is_m0, is_n0);
+    }
+  };
 
   f32x16 acc[TN][TM];
 #pragma unroll
@@ -170,113 +194,168 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
 
   // Fragment addressing: lane (row li, k-half g) reads logical chunk 2*kk + g
   // of its row, at its swizzled position.
-  const int swz = (li >> 1) & 3;  // (row >> 1) & 3 with row = 32*x + li
+  const int swz = (li >> 2) & 3;  // (row >> 2) & 3 with row = 32*x + li
   const int pos0 = ((0 + g) ^ swz) * 16, pos1 = ((2 + g) ^ swz) * 16;
   const int rowA = (wm * Cfg::WM + li) * ROWB, rowB = (wn * Cfg::WN + li) * ROWB;
 
-  for (int kt = 0; kt < nk; ++kt) {
-    // This wave's loads of slab kt are done once at most the loads of the
-    // slabs issued after it (up to NS - 2 of them) are outstanding. The bias
-    // loads were issued after the first NS - 1 slabs, so the first wait
-    // covers them too.
-    const int ahead = nk - 1 - kt < NS - 2 ? nk - 1 - kt : NS - 2;
-    if (kt == 0) {
-      wait_vmcnt<0>();
-    } else if (ahead >= NS - 2) {
+  bf16x8 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+  auto read_set = [&](int s, int pos, bf16x8 *fa, bf16x8 *fb) {
+    const uint8_t *slot = smem + (s % NS) * Cfg::SLOT;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      fb[j] = *(const bf16x8 *)(slot + Cfg::A_BYTES + rowB + j * 32 * ROWB + pos);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[i] = *(const bf16x8 *)(slot + rowA + i * 32 * ROWB + pos);
+  };
+  auto mfma_set = [&](const bf16x8 *fa, const bf16x8 *fb) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[j][i], 0, 0, 0);
+  };
+  // MFMAs and the LDS reads of the other set, one read after each of the
+  // first TM + TN MFMAs.
+  auto interleave = []() {
+#pragma unroll
+    for (int x = 0; x < TM + TN; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
+  };
+
+  // The epilogue of this block's ti-th tile.
+  auto epilogue = [&](int ti) {
+    int m0, n0;
+    tile_origin(ti, m0, n0);
+    const float *bl = (const float *)(smem + Cfg::BIAS_OFF + (ti & 1) * BN * 4);
+    uint8_t *stg = smem + Cfg::STG_OFF + wave * STG_WAVE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int rbase = m0 + wm * Cfg::WM + i * 32;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int cl = wn * Cfg::WN + j * 32;  // tile-local first column
+        // acc layout -> fp32 staging rows (lane li's row, columns 8q + 4g + e)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 b = *(const float4 *)(bl + cl + q * 8 + g * 4);
+          float4 v;
+          v.x = gemm_epilogue(acc[j][i][q * 4 + 0] + b.x, EPI);
+          v.y = gemm_epilogue(acc[j][i][q * 4 + 1] + b.y, EPI);
+          v.z = gemm_epilogue(acc[j][i][q * 4 + 2] + b.z, EPI);
+          v.w = gemm_epilogue(acc[j][i][q * 4 + 3] + b.w, EPI);
+          *(float4 *)(stg + li * STG_ROWB + (q * 8 + g * 4) * 4) = v;
+        }
+        asm volatile("" ::: "memory");
+        if (CBF) {
+          // 8 fp32 per lane -> 16 bytes of bf16; 4 lanes per 32-column row.
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int row = r * 16 + (lane >> 2), c8 = (lane & 3) * 8;
+            const float4 x0 = *(const float4 *)(stg + row * STG_ROWB + c8 * 4);
+            const float4 x1 = *(const float4 *)(stg + row * STG_ROWB + c8 * 4 + 16);
+            const int grow = rbase + row, gcol = n0 + cl + c8;
+            if (grow < M && gcol < N) {
+              float y[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+              const int64_t off = (int64_t)grow * ldc + gcol;
+              const bool full = gcol + 8 <= N;  // else N % 8 == 4: four columns left
+              if (RES) {
+                const float4 r0 = *(const float4 *)(residual + off);
+                y[0] += r0.x;
+                y[1] += r0.y;
+                y[2] += r0.z;
+                y[3] += r0.w;
+                if (full) {
+                  const float4 r1 = *(const float4 *)(residual + off + 4);
+                  y[4] += r1.x;
+                  y[5] += r1.y;
+                  y[6] += r1.z;
+                  y[7] += r1.w;
+                }
+              }
+              uint4 w;
+              w.x = pack_bf2(y[0], y[1]);
+              w.y = pack_bf2(y[2], y[3]);
+              w.z = pack_bf2(y[4], y[5]);
+              w.w = pack_bf2(y[6], y[7]);
+              if (full)
+                *(uint4 *)((uint16_t *)C + off) = w;
+              else
+                *(uint2 *)((uint16_t *)C + off) = make_uint2(w.x, w.y);
+            }
+          }
+        } else {
+          // 4 fp32 per lane; 8 lanes per 32-column row.
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = r * 8 + (lane >> 3), c4 = (lane & 7) * 4;
+            float4 x = *(const float4 *)(stg + row * STG_ROWB + c4 * 4);
+            const int grow = rbase + row, gcol = n0 + cl + c4;
+            if (grow < M && gcol < N) {
+              const int64_t off = (int64_t)grow * ldc + gcol;
+              if (RES) {
+                const float4 rv = *(const float4 *)(residual + off);
+                x.x += rv.x;
+                x.y += rv.y;
+                x.z += rv.z;
+                x.w += rv.w;
+              }
+              *(float4 *)((float *)C + off) = x;
+            }
+          }
+        }
+        asm volatile("" ::: "memory");
+      }
+    }
+  };
+
+  // Prologue: slabs 0 .. NS-1 in flight; slab 0's first half into set 0.
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    if (s < nslab) issue();
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  read_set(0, pos0, fa0, fb0);
+
+  int ep_kt = 0, ep_ti = 0;  // tile and depth of slab s
+  for (int s = 0; s < nslab; ++s) {
+    // First half of slab s; its second half is read meanwhile.
+    mfma_set(fa0, fb0);
+    read_set(s, pos1, fa1, fb1);
+    interleave();
+    // Every read of slab s is now issued. Wait for them and for this wave's
+    // loads of slab s + 1 (the slabs issued after it, at most NS - 2, may stay
+    // in flight), then meet: slab s + 1 is in LDS and slot s % NS is free.
+    const int ahead = nslab - 2 - s;
+    if (ahead >= NS - 2) {
       wait_vmcnt<Cfg::LOADS *(NS - 2)>();
-    } else if (NS > 2 && ahead == NS - 3) {
-      wait_vmcnt<(NS > 2 ? Cfg::LOADS * (NS - 3) : 0)>();
+    } else if (NS > 3 && ahead == NS - 3) {
+      wait_vmcnt<(NS > 3 ? Cfg::LOADS * (NS - 3) : 0)>();
     } else {
       wait_vmcnt<0>();
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (kt + NS - 1 < nk) issue(kt + NS - 1);
-
-    const uint8_t *slot = smem + (kt % NS) * Cfg::SLOT;
-    bf16x8 fa[2][TM], fb[2][TN];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int pos = kk ? pos1 : pos0;
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        fb[kk][j] = *(const bf16x8 *)(slot + Cfg::A_BYTES + rowB + j * 32 * ROWB + pos);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        fa[kk][i] = *(const bf16x8 *)(slot + rowA + i * 32 * ROWB + pos);
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    if (s + NS < nslab) issue();  // slab s + NS
+    // Second half of slab s; the first half of slab s + 1 is read meanwhile
+    // (after the last slab, slab s again: in bounds, unused).
+    mfma_set(fa1, fb1);
+    read_set(s + 1 < nslab ? s + 1 : s, pos0, fa0, fb0);
+    interleave();
+    if (++ep_kt == nk) {
+      ep_kt = 0;
+      epilogue(ep_ti++);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int i = 0; i < TM; ++i)
-          acc[j][i] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk][j], fa[kk][i], acc[j][i], 0, 0, 0);
-  }
-
-  // Epilogue. acc[j][i] is the C^T tile: lane owns C row m = m0 + wm*WM +
-  // 32*i + li and columns cbase + 32*j + 8*q + e (register r = 4*q + e).
-  const bool interior = cols_full && m0 + BM <= M;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int row = m0 + wm * Cfg::WM + i * 32 + li;
-    const bool row_ok = interior || row < M;
-    const int64_t roff = (int64_t)(row_ok ? row : 0) * ldc;
-    float4 rv[TN][4];
-    if (RES) {
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int col = cbase + j * 32 + q * 8;
-          rv[j][q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          if (interior || (row_ok && col + 4 <= N)) {
-            rv[j][q] = *(const float4 *)(residual + roff + col);
-          } else if (row_ok) {
-            if (col + 0 < N) rv[j][q].x = residual[roff + col + 0];
-            if (col + 1 < N) rv[j][q].y = residual[roff + col + 1];
-            if (col + 2 < N) rv[j][q].z = residual[roff + col + 2];
-          }
-        }
+          for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
     }
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int col = cbase + j * 32 + q * 8;
-        float v[4] = {acc[j][i][q * 4 + 0] + bv[j][q].x, acc[j][i][q * 4 + 1] + bv[j][q].y,
-                      acc[j][i][q * 4 + 2] + bv[j][q].z, acc[j][i][q * 4 + 3] + bv[j][q].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = gemm_epilogue(v[e], EPI);
-        if (RES) {
-          v[0] += rv[j][q].x;
-          v[1] += rv[j][q].y;
-          v[2] += rv[j][q].z;
-          v[3] += rv[j][q].w;
-        }
-        if (interior || (row_ok && col + 4 <= N)) {
-          if (CBF) {
-            uint2 w;
-            w.x = pack_bf2(v[0], v[1]);
-            w.y = pack_bf2(v[2], v[3]);
-            *(uint2 *)((uint16_t *)C + roff + col) = w;
-          } else {
-            *(float4 *)((float *)C + roff + col) = make_float4(v[0], v[1], v[2], v[3]);
-          }
-        } else if (row_ok) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (col + e < N) {
-              if (CBF)
-                ((uint16_t *)C)[roff + col + e] = f2bf(v[e]);
-              else
-                ((float *)C)[roff + col + e] = v[e];
-            }
-          }
-        }
-      }
   }
 }
 
@@ -285,34 +364,35 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
 namespace mxk {
 
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF>
-hipError_t gemm_lds_launch_t(const GemmArgs &a, hipStream_t s) {
+hipError_t gemm_lds_launch_t(const GemmArgs &a, int grid, hipStream_t s) {
   using Cfg = LdsCfg<BM, BN, WGM, WGN, NS>;
   auto kern = gemm_lds_k<BM, BN, WGM, WGN, NS, EPI, RES, CBF>;
   static bool attr_set = false;
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute((const void *)kern,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             Cfg::LDS);
+    const hipError_t e = hipFuncSetAttribute(
+        (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
-  kern<<<tiles_m * tiles_n, Cfg::NT, Cfg::LDS, s>>>(a.A, a.lda, a.Wt, (int)a.M, (int)a.N,
-                                                     (int)a.K, a.bias, a.residual, a.C, a.ldc,
-                                                     tiles_m, tiles_n);
+  const int ntiles = tiles_m * tiles_n;
+  const int g = ntiles < grid ? ntiles : grid;
+  kern<<<g, Cfg::NT, Cfg::LDS, s>>>(a.A, a.lda, a.Wt, (int)a.M, (int)a.N, (int)a.K, a.bias,
+                                    a.residual, a.C, a.ldc, tiles_m, tiles_n);
   return hipGetLastError();
 }
 
-// One tile configuration, every epilogue variant.
+// One tile configuration, every epilogue variant. `grid` = resident blocks
+// (one per CU).
 template <int BM, int BN, int WGM, int WGN, int NS>
-hipError_t gemm_lds_launch(const GemmArgs &a, hipStream_t s) {
-#define MX_LDS_EPI(E)                                                                  \
-  if (a.epilogue == E) {                                                               \
-    if (a.residual)                                                                    \
-      return a.c_bf16 ? gemm_lds_launch_t<BM, BN, WGM, WGN, NS, E, true, true>(a, s)   \
-                      : gemm_lds_launch_t<BM, BN, WGM, WGN, NS, E, true, false>(a, s); \
-    return a.c_bf16 ? gemm_lds_launch_t<BM, BN, WGM, WGN, NS, E, false, true>(a, s)    \
-                    : gemm_lds_launch_t<BM, BN, WGM, WGN, NS, E, false, false>(a, s);  \
+hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s) {
+#define MX_LDS_EPI(E)                                                                        \
+  if (a.epilogue == E) {                                                                     \
+    if (a.residual)                                                                          \
+      return a.c_bf16 ? gemm_lds_launch_t<BM, BN, WGM, WGN, NS, E, true, true>(a, grid, s)   \
+                      : gemm_lds_launch_t<BM, BN, WGM, WGN, NS, E, true, false>(a, grid, s); \
+    return a.c_bf16 ? gemm_lds_launch_t<BM, BN, WGM, WGN, NS, E, false, true>(a, grid, s)    \
+                    : gemm_lds_launch_t<BM, BN, WGM, WGN, NS, E, false, false>(a, grid, s);  \
   }
   MX_LDS_EPI(0)
   MX_LDS_EPI(1)
@@ -321,8 +401,8 @@ hipError_t gemm_lds_launch(const GemmArgs &a, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-template hipError_t gemm_lds_launch<256, 256, 2, 4, 3>(const GemmArgs &, hipStream_t);
-template hipError_t gemm_lds_launch<128, 256, 2, 4, 4>(const GemmArgs &, hipStream_t);
-template hipError_t gemm_lds_launch<128, 128, 2, 2, 4>(const GemmArgs &, hipStream_t);
+template hipError_t gemm_lds_launch<256, 256, 2, 4, 3>(const GemmArgs &, int, hipStream_t);
+template hipError_t gemm_lds_launch<128, 256, 2, 4, 4>(const GemmArgs &, int, hipStream_t);
+template hipError_t gemm_lds_launch<128, 128, 2, 2, 4>(const GemmArgs &, int, hipStream_t);
 
 }  // namespace mxk
