@@ -27,6 +27,19 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 HBM_PEAK_GBS = 8000.0
 
 
+def kernel_name(plan, epi, res, cbf):
+    """The rocprof name of the GEMM instantiation a plan from mx_gemm_plan runs,
+    e.g. lds_128x256x32_w64x64_ns4_persistent -> gemm_lds_k<128, 256, 2, 4, 4, ...>."""
+    if not plan.startswith("lds_"):
+        return "gemm_bf16_k<128, 128, 64, 64, 64>"
+    tile, wave, ns = plan.split("_")[1:4]
+    bm, bn, _ = (int(x) for x in tile.split("x"))
+    wm, wn = (int(x) for x in wave[1:].split("x"))
+    b = lambda v: "true" if v else "false"  # noqa: E731
+    return (f"gemm_lds_k<{bm}, {bn}, {bm // wm}, {bn // wn}, {int(ns[2:])}, {epi}, {b(res)}, "
+            f"{b(cbf)}>")
+
+
 def cpu_baseline(name, sample_batch, threads):
     """The oracle's host path (the reference CPU fallback restated) over
     `sample_batch` sequences of the same workload, all layers."""
@@ -67,7 +80,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="bge_base")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=4)
+    ap.add_argument("--cpu-sample", type=int, default=16)
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only run narrow_f32_bf16 over 64 Mi fp32 values, 5 times: a "
+                         "streaming kernel of known bytes (256 MiB read, 128 MiB written "
+                         "per launch) that scales the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend runs on one GPU; multi-GPU sharding of the "
@@ -79,6 +96,19 @@ def main():
 
     import mxenc
     from mxenc import synth
+
+    if args.calibrate:
+        ctx = mxenc.Context(0)
+        n = 64 << 20
+        src = ctx.put(np.random.default_rng(0).standard_normal(n, dtype=np.float32))
+        dst = ctx.empty((n,), np.uint16)
+        for _ in range(5):
+            mxenc.narrow_f32_bf16(ctx, src, dst)
+        ctx.sync()
+        print(json.dumps({"calibration": "narrow_f32_bf16", "elements": n,
+                          "read_bytes": 4 * n, "write_bytes": 2 * n, "launches": 5}))
+        ctx.close()
+        return
 
     m = synth.make_model(args.config)
     assert m["kind"] == "bert"
@@ -110,27 +140,62 @@ def main():
     # The same steps again with a HIP event pair around every launch, on the
     # stream the kernels run on: per-kernel-family durations for the roofline.
     enc.set_timing(True)
-    g_ms = a_ms = ln_ms = o_ms = 0.0
-    g_n = a_n = 0
-    g_flop = a_flop = 0.0
+    tot = {"gemm_ms": 0.0, "attn_ms": 0.0, "ln_ms": 0.0, "other_ms": 0.0, "gemm_flop": 0.0,
+           "attn_flop": 0.0, "gemm_n": 0, "attn_n": 0}
+    site_ms, site_flop, site_n = [0.0] * 4, [0.0] * 4, [0] * 4
     for _ in range(args.steps):
         enc.embed(d_ids, d_am, B, S, out)
         t = enc.timings()
-        g_ms += t.gemm_ms
-        a_ms += t.attn_ms
-        ln_ms += t.ln_ms
-        o_ms += t.other_ms
-        g_n += t.gemm_launches
-        a_n += t.attn_launches
-        g_flop += t.gemm_flop
-        a_flop += t.attn_flop
+        tot["gemm_ms"] += t.gemm_ms
+        tot["attn_ms"] += t.attn_ms
+        tot["ln_ms"] += t.ln_ms
+        tot["other_ms"] += t.other_ms
+        tot["gemm_flop"] += t.gemm_flop
+        tot["attn_flop"] += t.attn_flop
+        tot["gemm_n"] += t.gemm_launches
+        tot["attn_n"] += t.attn_launches
+        for i in range(4):
+            site_ms[i] += t.gemm_site_ms[i]
+            site_flop[i] += t.gemm_site_flop[i]
+            site_n[i] += t.gemm_site_launches[i]
     enc.set_timing(False)
-    gemm_tflops = g_flop / (g_ms * 1e-3) / 1e12
-    attn_tflops = a_flop / (a_ms * 1e-3) / 1e12
-    print(f"bench: GEMM {g_ms/args.steps:.2f} ms/step ({gemm_tflops:.0f} TFLOP/s, "
-          f"{g_n // args.steps} launches), attention {a_ms/args.steps:.2f} ms/step "
-          f"({attn_tflops:.0f} TFLOP/s), LN {ln_ms/args.steps:.2f} ms, other "
-          f"{o_ms/args.steps:.2f} ms", file=sys.stderr, flush=True)
+    gemm_tflops = tot["gemm_flop"] / (tot["gemm_ms"] * 1e-3) / 1e12
+    attn_tflops = tot["attn_flop"] / (tot["attn_ms"] * 1e-3) / 1e12
+    print(f"bench: GEMM {tot['gemm_ms']/args.steps:.2f} ms/step ({gemm_tflops:.0f} TFLOP/s, "
+          f"{tot['gemm_n'] // args.steps} launches), attention {tot['attn_ms']/args.steps:.2f} "
+          f"ms/step ({attn_tflops:.0f} TFLOP/s), LN {tot['ln_ms']/args.steps:.2f} ms, other "
+          f"{tot['other_ms']/args.steps:.2f} ms", file=sys.stderr, flush=True)
+
+    # The dominant GEMM kernel: sites grouped by the kernel instantiation they
+    # run -- tile plan plus epilogue, residual and C type, the name rocprof
+    # reports -- and the group with the most time.
+    d, f, M = m["hidden"], m["ffn"], B * S
+    act = 2 if m.get("gelu_erf") else 1
+    # (M, N, K, epilogue, residual, bf16 C) of each site in this BERT stack
+    sites = [("qkv", (M, 3 * d, d, 0, False, True)), ("attn_out", (M, d, d, 0, False, False)),
+             ("ffn_up", (M, f, d, act, False, True)), ("ffn_down", (M, d, f, 0, False, False))]
+    groups = {}
+    for i, (sname, (mm, nn, kk, epi, res, cbf)) in enumerate(sites):
+        plan = mxenc.lib().mx_gemm_plan(mm, nn, kk).decode()
+        kname = kernel_name(plan, epi, res, cbf)
+        g = groups.setdefault(kname, {"ms": 0.0, "flop": 0.0, "n": 0, "sites": []})
+        g["ms"] += site_ms[i]
+        g["flop"] += site_flop[i]
+        g["n"] += site_n[i]
+        g["sites"].append(sname)
+        print(f"bench:   {sname:8s} M{mm} N{nn} K{kk} {kname}: "
+              f"{site_ms[i] / max(site_n[i], 1) * 1e3:.1f} us/launch, "
+              f"{site_flop[i] / (site_ms[i] * 1e-3) / 1e12:.0f} TFLOP/s", file=sys.stderr,
+              flush=True)
+    dom_name, dom = max(groups.items(), key=lambda kv: kv[1]["ms"])
+    dom_tflops = dom["flop"] / (dom["ms"] * 1e-3) / 1e12
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemm_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as fh:
+            tj = json.load(fh)
+        if tj.get("kernel") == dom_name and tj.get("workload") == args.config:
+            traffic = tj.get("hbm_bytes_per_launch")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -157,12 +222,16 @@ def main():
                                f"{'CLS' if m['cls_pool'] else 'mean'} pool + L2",
                    "batch": B, "seq_len": S, "layers": m["layers"]},
         "gemm_mfma_util_pct": 100.0 * gemm_tflops / BF16_PEAK_TFLOPS,
-        "roofline": {"bound": "mfma", "kernel": "gemm_bf16_k (all encoder GEMMs)",
-                     "achieved": gemm_tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": gemm_tflops / BF16_PEAK_TFLOPS, "traffic": None,
-                     "flop_per_launch": g_flop / max(g_n, 1),
-                     "avg_launch_ms": g_ms / max(g_n, 1)},
-        "attention": {"achieved_tflops": attn_tflops, "frac": attn_tflops / BF16_PEAK_TFLOPS},
+        "roofline": {"bound": "mfma", "kernel": dom_name, "sites": dom["sites"],
+                     "achieved": dom_tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": dom_tflops / BF16_PEAK_TFLOPS, "traffic": traffic,
+                     "flop_per_launch": dom["flop"] / max(dom["n"], 1),
+                     "avg_launch_us": dom["ms"] / max(dom["n"], 1) * 1e3},
+        "gemm_all": {"achieved_tflops": gemm_tflops, "frac": gemm_tflops / BF16_PEAK_TFLOPS,
+                     "ms_per_step": tot["gemm_ms"] / args.steps},
+        "attention": {"achieved_tflops": attn_tflops, "frac": attn_tflops / BF16_PEAK_TFLOPS,
+                      "ms_per_step": tot["attn_ms"] / args.steps},
+        "layernorm_ms_per_step": tot["ln_ms"] / args.steps,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -283,11 +283,16 @@ int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids,
                      const float *attn_mask, int64_t B, int64_t S, float *out);
 
 /* BertEncoder::Timings (runtime/include/encoders/bert_encoder.hpp:72-87) as
- * hipEvent times of the last run, in milliseconds, when timing is on. */
+ * hipEvent times of the last run, in milliseconds, when timing is on (one
+ * event pair around every launch, on the stream the kernels run on). The
+ * gemm_site_* arrays split the GEMMs by layer site: [0] QKV, [1] attention
+ * out, [2] FFN up, [3] FFN down. */
 typedef struct {
   double gemm_ms, attn_ms, ln_ms, other_ms, total_ms;
   int64_t gemm_launches, attn_launches, ln_launches, other_launches;
   double gemm_flop, attn_flop; /* algorithmic FLOPs of the last run           */
+  double gemm_site_ms[4], gemm_site_flop[4];
+  int64_t gemm_site_launches[4];
 } mx_timings;
 int mx_encoder_set_timing(mx_encoder *enc, int on);
 int mx_encoder_timings(mx_encoder *enc, mx_timings *out);

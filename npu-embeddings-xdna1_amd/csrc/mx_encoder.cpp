@@ -35,6 +35,8 @@ struct LayerW {
 };
 
 enum Cat { CAT_GEMM = 0, CAT_ATTN = 1, CAT_LN = 2, CAT_OTHER = 3 };
+// GEMM sites of a layer, in the order of mx_timings.gemm_site_*.
+enum Site { SITE_QKV = 0, SITE_AO = 1, SITE_UP = 2, SITE_DOWN = 3 };
 
 }  // namespace
 
@@ -57,6 +59,7 @@ struct mx_encoder {
   size_t ev_used = 0;
   hipEvent_t ev_all[2] = {nullptr, nullptr};
   double gemm_flop = 0, attn_flop = 0;
+  double site_flop[4] = {0, 0, 0, 0};
 };
 
 namespace {
@@ -150,11 +153,12 @@ int check_placement() {
                   "/ mx_softmax_rows / mx_layernorm / mx_gelu.");
 }
 
-int gemm_l(mx_encoder *enc, mx_stream *s, const uint16_t *A, int64_t M, int64_t K,
+int gemm_l(mx_encoder *enc, mx_stream *s, int site, const uint16_t *A, int64_t M, int64_t K,
            const uint16_t *Wt, int64_t N, const float *bias, int epi, const float *resid,
            void *C, int c_dtype) {
-  Bracket br(enc, s->stream, CAT_GEMM);
+  Bracket br(enc, s->stream, CAT_GEMM + 16 * site);
   enc->gemm_flop += 2.0 * M * N * K;
+  enc->site_flop[site] += 2.0 * M * N * K;
   return gemm_checked(s, A, M, K, K, Wt, N, bias, epi, resid, C, c_dtype, N);
 }
 
@@ -182,17 +186,17 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
   int rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, enc->emb_ln[0], enc->emb_ln[1], M, x, enc->xb);
   for (size_t l = 0; !rc && l < enc->layers.size(); ++l) {
     const LayerW &w = enc->layers[l];
-    rc = gemm_l(enc, s, enc->xb, M, d, w.w[0], 3 * d, w.b[0], MX_EPI_NONE, nullptr, enc->qkv,
+    rc = gemm_l(enc, s, SITE_QKV, enc->xb, M, d, w.w[0], 3 * d, w.b[0], MX_EPI_NONE, nullptr, enc->qkv,
                 MX_BF16);
     if (!rc) rc = attn_l(enc, s, B, S, mask, kvl);
     if (!rc)
-      rc = gemm_l(enc, s, enc->ctxb, M, d, w.w[1], d, w.b[1], MX_EPI_NONE, nullptr, enc->proj,
+      rc = gemm_l(enc, s, SITE_AO, enc->ctxb, M, d, w.w[1], d, w.b[1], MX_EPI_NONE, nullptr, enc->proj,
                   MX_F32);
     if (!rc) rc = ln_l(enc, s, x, MX_F32, enc->proj, MX_F32, w.ln[0], w.ln[1], M, x, enc->xb);
     if (!rc)
-      rc = gemm_l(enc, s, enc->xb, M, d, w.w[2], f, w.b[2], epi, nullptr, enc->up, MX_BF16);
+      rc = gemm_l(enc, s, SITE_UP, enc->xb, M, d, w.w[2], f, w.b[2], epi, nullptr, enc->up, MX_BF16);
     if (!rc)
-      rc = gemm_l(enc, s, enc->up, M, f, w.w[3], d, w.b[3], MX_EPI_NONE, nullptr, enc->proj,
+      rc = gemm_l(enc, s, SITE_DOWN, enc->up, M, f, w.w[3], d, w.b[3], MX_EPI_NONE, nullptr, enc->proj,
                   MX_F32);
     if (!rc) rc = ln_l(enc, s, x, MX_F32, enc->proj, MX_F32, w.ln[2], w.ln[3], M, x, enc->xb);
   }
@@ -208,15 +212,15 @@ int run_preln(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const 
     const LayerW &w = enc->layers[l];
     rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, w.ln[0], w.ln[1], M, nullptr, enc->xb);
     if (!rc)
-      rc = gemm_l(enc, s, enc->xb, M, d, w.w[0], 3 * d, w.b[0], MX_EPI_NONE, nullptr, enc->qkv,
+      rc = gemm_l(enc, s, SITE_QKV, enc->xb, M, d, w.w[0], 3 * d, w.b[0], MX_EPI_NONE, nullptr, enc->qkv,
                   MX_BF16);
     if (!rc) rc = attn_l(enc, s, B, S, mask, kvl);
     if (!rc)
-      rc = gemm_l(enc, s, enc->ctxb, M, d, w.w[1], d, w.b[1], MX_EPI_NONE, x, x, MX_F32);
+      rc = gemm_l(enc, s, SITE_AO, enc->ctxb, M, d, w.w[1], d, w.b[1], MX_EPI_NONE, x, x, MX_F32);
     if (!rc) rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, w.ln[2], w.ln[3], M, nullptr, enc->xb);
     if (!rc)
-      rc = gemm_l(enc, s, enc->xb, M, d, w.w[2], f, w.b[2], epi, nullptr, enc->up, MX_BF16);
-    if (!rc) rc = gemm_l(enc, s, enc->up, M, f, w.w[3], d, w.b[3], MX_EPI_NONE, x, x, MX_F32);
+      rc = gemm_l(enc, s, SITE_UP, enc->xb, M, d, w.w[2], f, w.b[2], epi, nullptr, enc->up, MX_BF16);
+    if (!rc) rc = gemm_l(enc, s, SITE_DOWN, enc->up, M, f, w.w[3], d, w.b[3], MX_EPI_NONE, x, x, MX_F32);
   }
   if (!rc) rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, enc->fin_ln[0], enc->fin_ln[1], M, x, nullptr);
   return rc;
@@ -231,6 +235,7 @@ int run_impl(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
 int begin_timing(mx_encoder *enc, mx_stream *s) {
   enc->ev_used = 0;
   enc->gemm_flop = enc->attn_flop = 0;
+  for (double &f : enc->site_flop) f = 0;
   if (!enc->timing) return MX_OK;
   for (auto &ev : enc->ev_all)
     if (!ev && hipEventCreate(&ev) != hipSuccess) return fail(MX_E_DEVICE, "hipEventCreate");
@@ -485,6 +490,7 @@ int mx_encoder_timings(mx_encoder *enc, mx_timings *out) {
   std::memset(out, 0, sizeof *out);
   out->gemm_flop = enc->gemm_flop;
   out->attn_flop = enc->attn_flop;
+  for (int i = 0; i < 4; ++i) out->gemm_site_flop[i] = enc->site_flop[i];
   if (!enc->timing) return MX_OK;
   int rc = use_device(enc->ctx);
   if (rc) return rc;
@@ -493,7 +499,12 @@ int mx_encoder_timings(mx_encoder *enc, mx_timings *out) {
     float ms = 0.0f;
     if (e == hipSuccess) e = hipEventElapsedTime(&ms, enc->events[i], enc->events[i + 1]);
     if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
-    switch (enc->ev_cat[i]) {
+    if (enc->ev_cat[i] % 16 == CAT_GEMM) {
+      const int site = enc->ev_cat[i] / 16;
+      out->gemm_site_ms[site] += ms;
+      ++out->gemm_site_launches[site];
+    }
+    switch (enc->ev_cat[i] % 16) {
       case CAT_GEMM: out->gemm_ms += ms; ++out->gemm_launches; break;
       case CAT_ATTN: out->attn_ms += ms; ++out->attn_launches; break;
       case CAT_LN: out->ln_ms += ms; ++out->ln_launches; break;

@@ -49,7 +49,9 @@ class Timings(ctypes.Structure):
                 ("ln_ms", ctypes.c_double), ("other_ms", ctypes.c_double),
                 ("total_ms", ctypes.c_double), ("gemm_launches", _i64),
                 ("attn_launches", _i64), ("ln_launches", _i64), ("other_launches", _i64),
-                ("gemm_flop", ctypes.c_double), ("attn_flop", ctypes.c_double)]
+                ("gemm_flop", ctypes.c_double), ("attn_flop", ctypes.c_double),
+                ("gemm_site_ms", ctypes.c_double * 4), ("gemm_site_flop", ctypes.c_double * 4),
+                ("gemm_site_launches", _i64 * 4)]
 
 
 # name -> (restype, argtypes); the complete exported surface of mx_encoder.h
