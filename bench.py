@@ -172,8 +172,8 @@ def main():
     d, f, M = m["hidden"], m["ffn"], B * S
     act = 2 if m.get("gelu_erf") else 1
     # (M, N, K, epilogue, residual, bf16 C) of each site in this BERT stack
-    sites = [("qkv", (M, 3 * d, d, 0, False, True)), ("attn_out", (M, d, d, 0, False, False)),
-             ("ffn_up", (M, f, d, act, False, True)), ("ffn_down", (M, d, f, 0, False, False))]
+    sites = [("qkv", (M, 3 * d, d, 0, False, True)), ("attn_out", (M, d, d, 0, False, True)),
+             ("ffn_up", (M, f, d, act, False, True)), ("ffn_down", (M, d, f, 0, False, True))]
     groups = {}
     for i, (sname, (mm, nn, kk, epi, res, cbf)) in enumerate(sites):
         plan = mxenc.lib().mx_gemm_plan(mm, nn, kk).decode()

@@ -8,7 +8,9 @@
 //   xb    bf16 [M, d]   LayerNorm output, the next GEMM's A operand
 //   qkv   bf16 [M, 3d]  fused Q|K|V (Q pre-scaled by the packer)
 //   ctx   bf16 [M, d]   attention output
-//   proj  fp32 [M, d]   attn-out / FFN-down result (BERT: fused into the LN)
+//   proj  bf16 [M, d]   attn-out / FFN-down result, narrowed once (BERT; the
+//                       residual-fused LayerNorm reads it; the array path's
+//                       bf16-C convention, kernels/narrow_f32_bf16.cc)
 //   up    bf16 [M, f]   FFN-up with bias and GELU fused into the GEMM
 // Weights are [N, K] bf16 panels; biases and LayerNorm parameters fp32.
 #include "mx_internal.hpp"
@@ -50,7 +52,8 @@ struct mx_encoder {
   // workspace
   int64_t ws_rows = 0, ws_batch = 0;
   uint16_t *xb = nullptr, *qkv = nullptr, *ctxb = nullptr, *up = nullptr;
-  float *proj = nullptr, *emb = nullptr, *add_mask = nullptr;
+  uint16_t *proj = nullptr;
+  float *emb = nullptr, *add_mask = nullptr;
   int32_t *kv_len = nullptr;
   // timing
   bool timing = false;
@@ -95,7 +98,7 @@ int ensure_ws(mx_encoder *enc, int64_t B, int64_t S) {
     if (!rc) rc = dev_alloc((void **)&enc->qkv, rows * 3 * d * 2, "workspace qkv");
     if (!rc) rc = dev_alloc((void **)&enc->ctxb, rows * d * 2, "workspace ctx");
     if (!rc) rc = dev_alloc((void **)&enc->up, rows * f * 2, "workspace up");
-    if (!rc) rc = dev_alloc((void **)&enc->proj, rows * d * 4, "workspace proj");
+    if (!rc) rc = dev_alloc((void **)&enc->proj, rows * d * 2, "workspace proj");
     if (!rc) rc = dev_alloc((void **)&enc->emb, rows * d * 4, "workspace emb");
     if (rc) return rc;
     enc->ws_rows = rows;
@@ -191,14 +194,14 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
     if (!rc) rc = attn_l(enc, s, B, S, mask, kvl);
     if (!rc)
       rc = gemm_l(enc, s, SITE_AO, enc->ctxb, M, d, w.w[1], d, w.b[1], MX_EPI_NONE, nullptr, enc->proj,
-                  MX_F32);
-    if (!rc) rc = ln_l(enc, s, x, MX_F32, enc->proj, MX_F32, w.ln[0], w.ln[1], M, x, enc->xb);
+                  MX_BF16);
+    if (!rc) rc = ln_l(enc, s, x, MX_F32, enc->proj, MX_BF16, w.ln[0], w.ln[1], M, x, enc->xb);
     if (!rc)
       rc = gemm_l(enc, s, SITE_UP, enc->xb, M, d, w.w[2], f, w.b[2], epi, nullptr, enc->up, MX_BF16);
     if (!rc)
       rc = gemm_l(enc, s, SITE_DOWN, enc->up, M, f, w.w[3], d, w.b[3], MX_EPI_NONE, nullptr, enc->proj,
-                  MX_F32);
-    if (!rc) rc = ln_l(enc, s, x, MX_F32, enc->proj, MX_F32, w.ln[2], w.ln[3], M, x, enc->xb);
+                  MX_BF16);
+    if (!rc) rc = ln_l(enc, s, x, MX_F32, enc->proj, MX_BF16, w.ln[2], w.ln[3], M, x, enc->xb);
   }
   return rc;
 }
