@@ -19,6 +19,14 @@
 // the hardware exp2. Keys at or past kv_len[b] are skipped (whole tiles) or
 // given -inf (inside the last tile); -1e30 mask entries stay finite, so a row
 // whose keys are all masked attends uniformly, as the host softmax does.
+//
+// VALU economy (the softmax, not the MFMAs, bounds this kernel): a key tile
+// whose mask entries are all zero -- a block-uniform flag set while the tile
+// is staged -- skips the per-score mask add and takes its max on the raw
+// scores (scale > 0), and each probability is one FMA into exp2. The running
+// max m moves (and O and l are rescaled) only when a tile's max exceeds it by
+// more than 8 in log2 units, so probabilities stay below 2^8 and most tiles
+// skip the rescale; the result O / l is the same quotient.
 #include "mx_common.hpp"
 #include "mx_kernels.hpp"
 
@@ -34,7 +42,7 @@ __global__ __launch_bounds__(256) void attn_fwd_k(const uint16_t *__restrict__ q
                                                   const float *__restrict__ add_mask,
                                                   const int32_t *__restrict__ kv_len,
                                                   uint16_t *__restrict__ ctx, int64_t ldo,
-                                                  int n_qblk) {
+                                                  int n_qblk, int force_logits) {
   constexpr int KS = HD + 8;   // K row stride in LDS (elements)
   constexpr int VS = BKV + 4;  // Vt row stride in LDS (elements)
   constexpr int KCH = BKV * HD / 8 / 256;  // 16-byte K chunks per thread (1 or 2)
@@ -45,6 +53,7 @@ __global__ __launch_bounds__(256) void attn_fwd_k(const uint16_t *__restrict__ q
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][BKV * KS];
   __shared__ __attribute__((aligned(16))) uint16_t sV[2][HD * VS];
   __shared__ float sM[2][BKV];
+  __shared__ int sF[2];  // 1 if the staged tile has a nonzero mask entry
 
   const int blk = blockIdx.x;
   const int qb = blk % n_qblk;
@@ -120,7 +129,11 @@ __global__ __launch_bounds__(256) void attn_fwd_k(const uint16_t *__restrict__ q
       *(uint2 *)(vt + 2 * VS) = c2;
       *(uint2 *)(vt + 3 * VS) = c3;
     }
-    if (tid < BKV) sM[buf][tid] = rm;
+    if (tid < BKV) {  // exactly wave 0
+      sM[buf][tid] = rm;
+      const bool any = __ballot(rm != 0.0f) != 0;
+      if (tid == 0) sF[buf] = any || force_logits;
+    }
   };
 
   f32x16 o[NHT];
@@ -150,28 +163,41 @@ __global__ __launch_bounds__(256) void attn_fwd_k(const uint16_t *__restrict__ q
         sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sc[sub], 0, 0, 0);
       }
     }
-    // Logits (log2 units) and the tile max of this lane's query.
-    float mx = -INFINITY;
+    // Tile max of this lane's query, in log2 units. A tile with a nonzero
+    // mask entry turns its scores into logits first (scale and mask); a
+    // mask-free tile keeps the raw scores and scales the max.
+    float mx = -INFINITY, cc;
+    if (sF[cur]) {
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = sub * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
-        const float v = sc[sub][r] * scale_log2e + sM[cur][key];
-        sc[sub][r] = v;
-        mx = fmaxf(mx, v);
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int key = sub * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+          const float v = __builtin_fmaf(sc[sub][r], scale_log2e, sM[cur][key]);
+          sc[sub][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      cc = 1.0f;
+    } else {
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[sub][r]);
+      mx *= scale_log2e;
+      cc = scale_log2e;
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    l_run *= alpha;
+    if (mx > m_run + 8.0f) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mx);
+      m_run = mx;
+      l_run *= alpha;
 #pragma unroll
-    for (int ht = 0; ht < NHT; ++ht)
+      for (int ht = 0; ht < NHT; ++ht)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[ht][r] *= alpha;
+        for (int r = 0; r < 16; ++r) o[ht][r] *= alpha;
+    }
 
-    // Probabilities -> bf16 B operands, one per 16-key chunk.
+    // Probabilities exp2(s * cc - m) -> bf16 B operands, one per 16-key chunk.
     bf16x8 pk[4];
     float ps = 0.0f;
 #pragma unroll
@@ -179,7 +205,7 @@ __global__ __launch_bounds__(256) void attn_fwd_k(const uint16_t *__restrict__ q
       const int sub = ch >> 1, c = ch & 1;
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
-        const float p = __builtin_amdgcn_exp2f(sc[sub][c * 8 + jj] - m_new);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[sub][c * 8 + jj], cc, -m_run));
         ps += p;
         pk[ch][jj] = (__bf16)p;
       }
@@ -231,12 +257,15 @@ hipError_t attention(const AttnArgs &a, hipStream_t s) {
   const int n_qblk = (int)((a.S + BQ - 1) / BQ);
   const int64_t blocks = a.B * a.H * n_qblk;
   const float sl2e = a.scale * 1.4426950408889634f;
+  const int force_logits = a.scale > 0.0f ? 0 : 1;  // raw-score max needs scale > 0
   if (a.hd == 64)
     attn_fwd_k<64><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
-                                                   a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk);
+                                                   a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
+                                                   force_logits);
   else if (a.hd == 32)
     attn_fwd_k<32><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
-                                                   a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk);
+                                                   a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
+                                                   force_logits);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

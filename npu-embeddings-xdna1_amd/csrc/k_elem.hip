@@ -193,6 +193,69 @@ __global__ __launch_bounds__(256) void layernorm_wave_k(
   }
 }
 
+// The same with four consecutive values per lane per access (16-byte fp32 /
+// 8-byte bf16 loads and stores): NQ quads of 256 columns.
+__device__ __forceinline__ float4 ld4(const void *p, int bf, int64_t off) {
+  if (bf) {
+    const uint2 u = *(const uint2 *)((const uint16_t *)p + off);
+    return make_float4(bf2f(u.x & 0xFFFFu), bf2f(u.x >> 16), bf2f(u.y & 0xFFFFu), bf2f(u.y >> 16));
+  }
+  return *(const float4 *)((const float *)p + off);
+}
+
+template <int NQ>
+__global__ __launch_bounds__(256) void layernorm_wave4_k(
+    const void *__restrict__ x, int x_bf, const void *__restrict__ y, int y_bf,
+    const float *__restrict__ gamma, const float *__restrict__ beta, float eps,
+    int64_t rows, float *out_f32, uint16_t *out_bf16) {
+  constexpr int cols = NQ * 256;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float4 v[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int64_t off = row * cols + i * 256 + lane * 4;
+    v[i] = ld4(x, x_bf, off);
+    if (y) {
+      const float4 w = ld4(y, y_bf, off);
+      v[i].x += w.x;
+      v[i].y += w.y;
+      v[i].z += w.z;
+      v[i].w += w.w;
+    }
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+  const float mean = wave_sum(s) / (float)cols;
+  float q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+    q = __builtin_fmaf(a, a, q);
+    q = __builtin_fmaf(b, b, q);
+    q = __builtin_fmaf(c, c, q);
+    q = __builtin_fmaf(d, d, q);
+  }
+  const float var = wave_sum(q) / (float)cols;
+  const float is = 1.0f / sqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int c = i * 256 + lane * 4;
+    const float4 gm = *(const float4 *)(gamma + c);
+    const float4 bt = *(const float4 *)(beta + c);
+    float4 r;
+    r.x = __builtin_fmaf((v[i].x - mean) * is, gm.x, bt.x);
+    r.y = __builtin_fmaf((v[i].y - mean) * is, gm.y, bt.y);
+    r.z = __builtin_fmaf((v[i].z - mean) * is, gm.z, bt.z);
+    r.w = __builtin_fmaf((v[i].w - mean) * is, gm.w, bt.w);
+    const int64_t off = row * cols + c;
+    if (out_f32) *(float4 *)(out_f32 + off) = r;
+    if (out_bf16) *(uint2 *)(out_bf16 + off) = make_uint2(pack_bf2(r.x, r.y), pack_bf2(r.z, r.w));
+  }
+}
+
 // Any width: one 256-thread block per row, two passes through global memory.
 __global__ __launch_bounds__(256) void layernorm_any_k(
     const void *__restrict__ x, int x_bf, const void *__restrict__ y, int y_bf,
@@ -446,6 +509,30 @@ hipError_t layernorm(const void *x, int x_bf, const void *y, int y_bf, const flo
                  ((uintptr_t)gamma % 8 == 0) && ((uintptr_t)beta % 8 == 0) &&
                  (!out_f32 || (uintptr_t)out_f32 % 8 == 0) &&
                  (!out_bf16 || (uintptr_t)out_bf16 % 4 == 0);
+  const bool aligned16 = ((uintptr_t)x % (x_bf ? 8 : 16) == 0) &&
+                         (!y || (uintptr_t)y % (y_bf ? 8 : 16) == 0) &&
+                         ((uintptr_t)gamma % 16 == 0) && ((uintptr_t)beta % 16 == 0) &&
+                         (!out_f32 || (uintptr_t)out_f32 % 16 == 0) &&
+                         (!out_bf16 || (uintptr_t)out_bf16 % 8 == 0);
+  if (aligned16 && cols % 256 == 0) {
+#define MX_LN4_CASE(nq)                                                                   \
+  case nq:                                                                                \
+    layernorm_wave4_k<nq><<<g, 256, 0, s>>>(x, x_bf, y, y_bf, gamma, beta, eps, rows,     \
+                                            out_f32, out_bf16);                           \
+    return hipGetLastError();
+    switch (cols / 256) {
+      MX_LN4_CASE(1)
+      MX_LN4_CASE(2)
+      MX_LN4_CASE(3)
+      MX_LN4_CASE(4)
+      MX_LN4_CASE(5)
+      MX_LN4_CASE(6)
+      MX_LN4_CASE(8)
+      default:
+        break;
+    }
+#undef MX_LN4_CASE
+  }
   if (aligned && cols % 128 == 0 && rows <= (int64_t)1 << 36) {
 #define MX_LN_CASE(np)                                                                     \
   case np:                                                                                 \
