@@ -37,7 +37,7 @@ namespace {
 constexpr int BQ = 128, BKV = 64;
 
 template <int HD>
-__global__ __launch_bounds__(256) void attn_fwd_k(const uint16_t *__restrict__ qkv, int64_t ldq,
+__global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict__ qkv, int64_t ldq,
                                                   int S, int H, float scale_log2e,
                                                   const float *__restrict__ add_mask,
                                                   const int32_t *__restrict__ kv_len,

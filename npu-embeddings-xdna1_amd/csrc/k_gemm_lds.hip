@@ -4,7 +4,8 @@
 //
 // C[M, N] = epilogue(A[M, K] @ W[K, N] + bias) (+ residual), A bf16 row-major,
 // W held as Wt[N, K] (K contiguous), fp32 accumulation in
-// v_mfma_f32_32x32x16_bf16, one to_bf16 rounding at the store when C is bf16.
+// v_mfma_f32_32x32x16_bf16, one round-to-nearest-even narrowing (the hardware
+// conversion) at the store when C is bf16.
 //
 // Grid. One block per CU walks a list of BM x BN output tiles; its slabs
 // (BK = 32 deep) form one sequence across tile boundaries, so the ring keeps
@@ -276,10 +277,10 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
                 }
               }
               uint4 w;
-              w.x = pack_bf2(y[0], y[1]);
-              w.y = pack_bf2(y[2], y[3]);
-              w.z = pack_bf2(y[4], y[5]);
-              w.w = pack_bf2(y[6], y[7]);
+              w.x = pack_bf2_hw(y[0], y[1]);
+              w.y = pack_bf2_hw(y[2], y[3]);
+              w.z = pack_bf2_hw(y[4], y[5]);
+              w.w = pack_bf2_hw(y[6], y[7]);
               if (full)
                 *(uint4 *)((uint16_t *)C + off) = w;
               else

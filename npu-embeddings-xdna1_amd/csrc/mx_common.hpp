@@ -20,6 +20,18 @@ __device__ __forceinline__ uint16_t f2bf(float x) {
 
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 
+// Two fp32 -> packed bf16 by the hardware conversion (v_cvt_pk_bf16_f32, round
+// to nearest even): identical to f2bf for every non-NaN input; a NaN becomes a
+// quiet NaN instead of f2bf's carry pattern. For results held to a tolerance
+// (GEMM outputs), not for the bit-exact narrowing kernels.
+__device__ __forceinline__ uint32_t pack_bf2_hw(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t v;
+  v[0] = (__bf16)a;
+  v[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
   return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
 }
