@@ -243,7 +243,13 @@ typedef struct {
   int cls_pool;       /* embed(): 1 = CLS, 0 = mean                           */
   int l2_normalize;   /* embed(): L2-normalise the pooled vector              */
   int64_t vocab, max_pos; /* embed(): word and position table rows (BERT)     */
+  int front;          /* pre-LN front end: MX_FRONT_NONE (run() only), VIT or
+                         WHISPER (mx_encoder_vit / mx_encoder_whisper)        */
+  int64_t image, patch, labels; /* ViT: image side, patch side, head labels   */
+  int64_t mels, frames;         /* Whisper: mel bins and input frames         */
 } mx_encoder_desc;
+
+typedef enum { MX_FRONT_NONE = 0, MX_FRONT_VIT = 1, MX_FRONT_WHISPER = 2 } mx_front;
 
 /* Replaces the BertEncoder + Design set wiring of setup_encoder
  * (run_setup.hpp:483-877). Tensors are then given by name with
@@ -281,6 +287,32 @@ int mx_encoder_run(mx_encoder *enc, mx_stream *s, float *x_io,
  * out [B, hidden] (device). BERT only. Synchronises s. */
 int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids,
                      const float *attn_mask, int64_t B, int64_t S, float *out);
+
+/* VitEncoder::run + head_matvec (runtime/src/vit/encoder.cpp:222-431,
+ * runtime/src/vit/head.cpp:16-49), every step on the GPU: pixels fp32
+ * [B, 3, image, image] (device) -> im2col patch rows (c, ky, kx order) -> patch
+ * GEMM + bias -> [CLS; patches] + positions -> the pre-LN layers and final
+ * LayerNorm -> CLS rows -> head GEMM + bias -> logits fp32 [B, labels]
+ * (device). hidden (nullable, device, fp32 [B*(np+1), hidden]) receives the
+ * final hidden state. Tensors: "patch_embed.weight" [3*patch^2, hidden],
+ * "patch_embed.bias", "cls_token" [hidden], "position" [np+1, hidden],
+ * "head.weight" [hidden, labels] (label fastest, as head.cpp reads it),
+ * "head.bias" [labels]. image % patch == 0, patch % 8 == 0, image % 4 == 0.
+ * Synchronises s. */
+int mx_encoder_vit(mx_encoder *enc, mx_stream *s, const float *pixels,
+                   int64_t B, float *logits, float *hidden);
+/* WhisperEncoder::run (runtime/src/whisper/encoder.cpp:114-213) with the conv
+ * front end of whisper/features.cpp:390-469 on the GPU: mel fp32
+ * [B, mels, frames] (device) -> conv1 (k3, pad 1) + exact-erf GELU -> conv2
+ * (k3, stride 2, pad 1) + GELU -> + positions -> the pre-LN layers and final
+ * LayerNorm -> hidden fp32 [B*frames/2, hidden] (device). Each convolution is
+ * one GEMM per sample over a time-major bf16 copy padded by a zero frame on
+ * each side (its im2col rows overlap, nothing is copied). Tensors:
+ * "conv1.weight" [hidden, mels, 3] and "conv2.weight" [hidden, hidden, 3]
+ * (Conv1d layout), "conv1.bias", "conv2.bias", "position" [frames/2, hidden].
+ * frames even, 3*mels and 3*hidden multiples of 32. Synchronises s. */
+int mx_encoder_whisper(mx_encoder *enc, mx_stream *s, const float *mel,
+                       int64_t B, float *hidden);
 
 /* BertEncoder::Timings (runtime/include/encoders/bert_encoder.hpp:72-87) as
  * hipEvent times of the last run, in milliseconds, when timing is on (one

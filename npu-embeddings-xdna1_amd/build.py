@@ -26,8 +26,8 @@ FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(HERE, "..", "include"),
 ]
-SOURCES = ["k_elem.hip", "k_gemm.hip", "k_gemm_lds.hip", "k_attn.hip", "mx_abi.cpp",
-           "mx_encoder.cpp"]
+SOURCES = ["k_elem.hip", "k_gemm.hip", "k_gemm_lds.hip", "k_attn.hip", "k_front.hip",
+           "mx_abi.cpp", "mx_encoder.cpp"]
 
 
 def _compile(src):

@@ -63,6 +63,13 @@ struct mx_encoder {
   hipEvent_t ev_all[2] = {nullptr, nullptr};
   double gemm_flop = 0, attn_flop = 0;
   double site_flop[4] = {0, 0, 0, 0};
+  // front ends (ViT / Whisper) and the ViT head
+  uint16_t *patch_w = nullptr, *head_w = nullptr, *conv_w[2] = {nullptr, nullptr};
+  float *patch_b = nullptr, *head_b = nullptr, *conv_b[2] = {nullptr, nullptr};
+  float *cls_tok = nullptr, *front_pos = nullptr;
+  int64_t fw_batch = 0;  // front workspace sized for this batch
+  uint16_t *f_rows = nullptr, *f_cls = nullptr, *f_mel = nullptr, *f_out1 = nullptr;
+  float *f_patch = nullptr, *f_x = nullptr;
 };
 
 namespace {
@@ -250,6 +257,59 @@ void end_timing(mx_encoder *enc, mx_stream *s) {
   if (enc->timing) (void)hipEventRecord(enc->ev_all[1], s->stream);
 }
 
+int ensure_front_ws(mx_encoder *enc, mx_stream *s, int64_t B) {
+  if (B <= enc->fw_batch) return MX_OK;
+  free_dev(enc->f_rows);
+  free_dev(enc->f_cls);
+  free_dev(enc->f_mel);
+  free_dev(enc->f_out1);
+  free_dev(enc->f_patch);
+  free_dev(enc->f_x);
+  enc->fw_batch = 0;
+  const mx_encoder_desc &dd = enc->desc;
+  const int64_t d = dd.hidden;
+  int rc = MX_OK;
+  if (dd.front == MX_FRONT_VIT) {
+    const int64_t g = dd.image / dd.patch, np = g * g, pd = 3 * dd.patch * dd.patch;
+    rc = dev_alloc((void **)&enc->f_rows, B * np * pd * 2, "workspace patch rows");
+    if (!rc) rc = dev_alloc((void **)&enc->f_patch, B * np * d * 4, "workspace patch out");
+    if (!rc) rc = dev_alloc((void **)&enc->f_x, B * (np + 1) * d * 4, "workspace hidden");
+    if (!rc) rc = dev_alloc((void **)&enc->f_cls, B * d * 2, "workspace cls rows");
+  } else {
+    const int64_t T = dd.frames;
+    rc = dev_alloc((void **)&enc->f_mel, B * (T + 2) * dd.mels * 2, "workspace mel");
+    if (!rc) rc = dev_alloc((void **)&enc->f_out1, B * (T + 2) * d * 2, "workspace conv1");
+    // The conv1 GEMM writes frames 1..T of each sample; the zero frame before
+    // and after (conv2's padding) is cleared once here and never written.
+    if (!rc) {
+      const hipError_t e = hipMemsetAsync(enc->f_out1, 0, B * (T + 2) * d * 2, s->stream);
+      if (e != hipSuccess) rc = hip_fail(e, "clearing the conv1 workspace");
+    }
+  }
+  if (rc) return rc;
+  enc->fw_batch = B;
+  return MX_OK;
+}
+
+// The front ends run under the reference's `conv` code: with a placement set,
+// it must list conv too (besides the layer's codes).
+int check_front_placement() {
+  const std::set<std::string> ops = placed_ops();
+  if (ops.empty() || ops.count("conv")) return MX_OK;
+  return fail(MX_E_INVALID,
+              "encoder front end: --npu-ops lists layer ops but not conv, which would keep the "
+              "patch/conv front end on the host; the GPU front end runs under conv");
+}
+
+int front_gemm(mx_encoder *enc, mx_stream *s, const uint16_t *A, int64_t lda, int64_t M,
+               int64_t K, const uint16_t *Wt, int64_t N, const float *bias, int epi,
+               const float *resid, void *C, int c_bf16, int64_t ldc) {
+  Bracket br(enc, s->stream, CAT_OTHER);
+  mxk::GemmArgs a{A, lda, Wt, M, N, K, bias, epi, resid, C, c_bf16, ldc};
+  const hipError_t e = mxk::gemm(a, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "front-end gemm launch");
+}
+
 const char *kGemmNames[4] = {"qkv", "attn_out", "ffn_up", "ffn_down"};
 
 }  // namespace
@@ -277,6 +337,19 @@ int mx_encoder_create(mx_ctx *ctx, const mx_encoder_desc *desc, mx_encoder **out
   if (d.gelu != MX_GELU_POLY && d.gelu != MX_GELU_ERF)
     return fail(MX_E_INVALID, "encoder_create: gelu must be MX_GELU_POLY or MX_GELU_ERF");
   if (!(d.ln_eps >= 0.0f)) return fail(MX_E_INVALID, "encoder_create: bad ln_eps");
+  if (d.front != MX_FRONT_NONE && d.arch != MX_ARCH_PRELN)
+    return fail(MX_E_INVALID, "encoder_create: a ViT/Whisper front end needs the pre-LN arch");
+  if (d.front == MX_FRONT_VIT &&
+      (d.patch <= 0 || d.patch % 8 || d.image <= 0 || d.image % d.patch || d.image % 4 ||
+       d.labels <= 0 || d.labels % 4 || (3 * d.patch * d.patch) % 32))
+    return fail(MX_E_INVALID, "encoder_create: ViT needs patch % 8 == 0, image % patch == 0, "
+                              "image % 4 == 0 and labels % 4 == 0");
+  if (d.front == MX_FRONT_WHISPER &&
+      (d.mels <= 0 || d.frames <= 0 || d.frames % 2 || (3 * d.mels) % 32 || (3 * d.hidden) % 32))
+    return fail(MX_E_INVALID, "encoder_create: Whisper needs even frames and 3*mels, "
+                              "3*hidden multiples of 32");
+  if (d.front != MX_FRONT_NONE && d.front != MX_FRONT_VIT && d.front != MX_FRONT_WHISPER)
+    return fail(MX_E_INVALID, "encoder_create: unknown front end " + std::to_string(d.front));
   int rc = use_device(ctx);
   if (rc) return rc;
   auto *e = new mx_encoder();
@@ -308,6 +381,20 @@ void mx_encoder_destroy(mx_encoder *enc) {
     free_dev(enc->emb);
     free_dev(enc->add_mask);
     free_dev(enc->kv_len);
+    free_dev(enc->patch_w);
+    free_dev(enc->head_w);
+    free_dev(enc->patch_b);
+    free_dev(enc->head_b);
+    for (auto &p : enc->conv_w) free_dev(p);
+    for (auto &p : enc->conv_b) free_dev(p);
+    free_dev(enc->cls_tok);
+    free_dev(enc->front_pos);
+    free_dev(enc->f_rows);
+    free_dev(enc->f_cls);
+    free_dev(enc->f_mel);
+    free_dev(enc->f_out1);
+    free_dev(enc->f_patch);
+    free_dev(enc->f_x);
     for (auto ev : enc->events) (void)hipEventDestroy(ev);
     for (auto ev : enc->ev_all)
       if (ev) (void)hipEventDestroy(ev);
@@ -374,6 +461,62 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
   }
   if (name == "embeddings.ln.weight") return put_f32(enc->emb_ln[0], d);
   if (name == "embeddings.ln.bias") return put_f32(enc->emb_ln[1], d);
+  // ---- front ends and the ViT head ----
+  const int64_t fr = enc->desc.front;
+  if (fr == MX_FRONT_VIT) {
+    const int64_t pd = 3 * enc->desc.patch * enc->desc.patch;
+    const int64_t np1 = (enc->desc.image / enc->desc.patch) * (enc->desc.image / enc->desc.patch) + 1;
+    if (name == "patch_embed.weight" || name == "head.weight") {
+      const bool head = name == "head.weight";
+      const int64_t K = head ? d : pd, N = head ? enc->desc.labels : d;
+      if (count != K * N)
+        return fail(MX_E_INVALID, name + ": a [" + std::to_string(K) + ", " + std::to_string(N) +
+                                      "] operand wanted");
+      uint16_t *panel = nullptr;
+      int r = stage_panel(enc->ctx, host, dtype, K, N, &panel);
+      if (r) return r;
+      uint16_t *&dst = head ? enc->head_w : enc->patch_w;
+      free_dev(dst);
+      dst = panel;
+      return MX_OK;
+    }
+    if (name == "patch_embed.bias") return put_f32(enc->patch_b, d);
+    if (name == "head.bias") return put_f32(enc->head_b, enc->desc.labels);
+    if (name == "cls_token") return put_f32(enc->cls_tok, d);
+    if (name == "position") return put_f32(enc->front_pos, np1 * d);
+  }
+  if (fr == MX_FRONT_WHISPER) {
+    for (int i = 0; i < 2; ++i) {
+      const std::string base = i == 0 ? "conv1" : "conv2";
+      const int64_t cin = i == 0 ? enc->desc.mels : d;
+      if (name == base + ".weight") {
+        // Conv1d [hidden, cin, 3] -> GEMM operand [K = 3*cin, N = hidden] with
+        // K ordered (tap, channel): the im2col row of frame t is then the three
+        // time-major rows t-1, t, t+1 back to back.
+        if (count != d * cin * 3)
+          return fail(MX_E_INVALID, name + ": a [" + std::to_string(d) + ", " +
+                                        std::to_string(cin) + ", 3] tensor wanted");
+        if (dtype != MX_F32 && dtype != MX_BF16)
+          return fail(MX_E_INVALID, name + ": MX_F32 or MX_BF16");
+        const size_t es = dtype == MX_F32 ? 4 : 2;
+        std::vector<uint8_t> kn(static_cast<size_t>(3 * cin * d) * es);
+        const uint8_t *src = static_cast<const uint8_t *>(host);
+        for (int64_t c = 0; c < d; ++c)
+          for (int64_t m = 0; m < cin; ++m)
+            for (int64_t k = 0; k < 3; ++k)
+              std::memcpy(&kn[static_cast<size_t>((k * cin + m) * d + c) * es],
+                          &src[static_cast<size_t>((c * cin + m) * 3 + k) * es], es);
+        uint16_t *panel = nullptr;
+        int r = stage_panel(enc->ctx, kn.data(), dtype, 3 * cin, d, &panel);
+        if (r) return r;
+        free_dev(enc->conv_w[i]);
+        enc->conv_w[i] = panel;
+        return MX_OK;
+      }
+      if (name == base + ".bias") return put_f32(enc->conv_b[i], d);
+    }
+    if (name == "position") return put_f32(enc->front_pos, enc->desc.frames / 2 * d);
+  }
   if (name == "final_ln.weight") return put_f32(enc->fin_ln[0], d);
   if (name == "final_ln.bias") return put_f32(enc->fin_ln[1], d);
   if (name == "embeddings.word") {
@@ -415,6 +558,18 @@ int mx_encoder_ready(mx_encoder *enc) {
       return fail(MX_E_STATE, "encoder: embeddings.ln.weight/bias were never set");
   } else if (!enc->fin_ln[0] || !enc->fin_ln[1]) {
     return fail(MX_E_STATE, "encoder: final_ln.weight/bias were never set");
+  }
+  if (enc->desc.front == MX_FRONT_VIT) {
+    const char *miss = !enc->patch_w ? "patch_embed.weight" : !enc->patch_b ? "patch_embed.bias"
+                     : !enc->cls_tok ? "cls_token" : !enc->front_pos ? "position"
+                     : !enc->head_w ? "head.weight" : !enc->head_b ? "head.bias" : nullptr;
+    if (miss) return fail(MX_E_STATE, std::string("encoder: ") + miss + " was never set");
+  }
+  if (enc->desc.front == MX_FRONT_WHISPER) {
+    const char *miss = !enc->conv_w[0] ? "conv1.weight" : !enc->conv_b[0] ? "conv1.bias"
+                     : !enc->conv_w[1] ? "conv2.weight" : !enc->conv_b[1] ? "conv2.bias"
+                     : !enc->front_pos ? "position" : nullptr;
+    if (miss) return fail(MX_E_STATE, std::string("encoder: ") + miss + " was never set");
   }
   return MX_OK;
 }
@@ -479,6 +634,95 @@ int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids, const fl
                                std::to_string(enc->desc.vocab) + ")");
   if (flags & 2) return fail(MX_E_DATA, "CLS pooling on a sequence whose first token is masked");
   return MX_OK;
+}
+
+int mx_encoder_vit(mx_encoder *enc, mx_stream *s, const float *pixels, int64_t B, float *logits,
+                   float *hidden) {
+  clear_error();
+  if (!enc || !s || !pixels || !logits) return fail(MX_E_INVALID, "encoder_vit: null argument");
+  if (enc->desc.front != MX_FRONT_VIT)
+    return fail(MX_E_INVALID, "encoder_vit: this encoder was created without the ViT front end");
+  if (B <= 0) return fail(MX_E_INVALID, "encoder_vit: empty batch");
+  const mx_encoder_desc &dd = enc->desc;
+  const int64_t d = dd.hidden, g = dd.image / dd.patch, np = g * g, S = np + 1;
+  const int64_t pd = 3 * dd.patch * dd.patch;
+  int rc = use_device(enc->ctx);
+  if (!rc) rc = check_placement();
+  if (!rc) rc = check_front_placement();
+  if (!rc) rc = mx_encoder_ready(enc);
+  if (!rc) rc = ensure_ws(enc, B, S);
+  if (!rc) rc = ensure_front_ws(enc, s, B);
+  if (!rc) rc = begin_timing(enc, s);
+  if (rc) return rc;
+  float *x = hidden ? hidden : enc->f_x;
+  {
+    Bracket br(enc, s->stream, CAT_OTHER);
+    const hipError_t e = mxk::vit_patches(pixels, B, (int)dd.image, (int)dd.patch, enc->f_rows,
+                                          s->stream);
+    if (e != hipSuccess) return hip_fail(e, "vit patches launch");
+  }
+  rc = front_gemm(enc, s, enc->f_rows, pd, B * np, pd, enc->patch_w, d, enc->patch_b,
+                  MX_EPI_NONE, nullptr, enc->f_patch, 0, d);
+  if (rc) return rc;
+  {
+    Bracket br(enc, s->stream, CAT_OTHER);
+    const hipError_t e = mxk::vit_assemble(enc->f_patch, enc->cls_tok, enc->front_pos, B,
+                                           (int)np, (int)d, x, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "vit assemble launch");
+  }
+  rc = run_preln(enc, s, x, nullptr, nullptr, B, S);
+  if (rc) return rc;
+  {
+    Bracket br(enc, s->stream, CAT_OTHER);
+    const hipError_t e = mxk::gather_rows_bf16(x, S * d, B, (int)d, enc->f_cls, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "cls gather launch");
+  }
+  rc = front_gemm(enc, s, enc->f_cls, d, B, d, enc->head_w, dd.labels, enc->head_b, MX_EPI_NONE,
+                  nullptr, logits, 0, dd.labels);
+  if (rc) return rc;
+  end_timing(enc, s);
+  return mx_sync(s);
+}
+
+int mx_encoder_whisper(mx_encoder *enc, mx_stream *s, const float *mel, int64_t B,
+                       float *hidden) {
+  clear_error();
+  if (!enc || !s || !mel || !hidden) return fail(MX_E_INVALID, "encoder_whisper: null argument");
+  if (enc->desc.front != MX_FRONT_WHISPER)
+    return fail(MX_E_INVALID,
+                "encoder_whisper: this encoder was created without the Whisper front end");
+  if (B <= 0) return fail(MX_E_INVALID, "encoder_whisper: empty batch");
+  const mx_encoder_desc &dd = enc->desc;
+  const int64_t d = dd.hidden, T = dd.frames, S = T / 2, cin = dd.mels;
+  int rc = use_device(enc->ctx);
+  if (!rc) rc = check_placement();
+  if (!rc) rc = check_front_placement();
+  if (!rc) rc = mx_encoder_ready(enc);
+  if (!rc) rc = ensure_ws(enc, B, S);
+  if (!rc) rc = ensure_front_ws(enc, s, B);
+  if (!rc) rc = begin_timing(enc, s);
+  if (rc) return rc;
+  {
+    Bracket br(enc, s->stream, CAT_OTHER);
+    const hipError_t e = mxk::mel_time_major(mel, B, (int)cin, (int)T, enc->f_mel, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "mel transpose launch");
+  }
+  for (int64_t b = 0; !rc && b < B; ++b) {
+    // conv1: the im2col row of frame t is time-major rows t..t+2 of the padded
+    // copy, i.e. row stride mels and K = 3 * mels (overlapping rows).
+    rc = front_gemm(enc, s, enc->f_mel + b * (T + 2) * cin, cin, T, 3 * cin, enc->conv_w[0], d,
+                    enc->conv_b[0], MX_EPI_GELU_ERF, nullptr,
+                    enc->f_out1 + (b * (T + 2) + 1) * d, 1, d);
+    // conv2 (stride 2): output frame u reads padded rows 2u..2u+2, row stride
+    // 2 * hidden, K = 3 * hidden; the positions enter as the fused residual.
+    if (!rc)
+      rc = front_gemm(enc, s, enc->f_out1 + b * (T + 2) * d, 2 * d, S, 3 * d, enc->conv_w[1], d,
+                      enc->conv_b[1], MX_EPI_GELU_ERF, enc->front_pos, hidden + b * S * d, 0, d);
+  }
+  if (!rc) rc = run_preln(enc, s, hidden, nullptr, nullptr, B, S);
+  if (rc) return rc;
+  end_timing(enc, s);
+  return mx_sync(s);
 }
 
 int mx_encoder_set_timing(mx_encoder *enc, int on) {

@@ -26,6 +26,15 @@ hipError_t mask_build(const float *attn_mask, int64_t B, int64_t S, float *add_m
 hipError_t pool_rows(const float *h, const float *attn_mask, int64_t B, int64_t S, int64_t d,
                      int cls, int l2, float *out, int *err, hipStream_t s);
 
+// Front ends (k_front.hip).
+hipError_t vit_patches(const float *px, int64_t B, int img, int p, uint16_t *rows, hipStream_t s);
+hipError_t vit_assemble(const float *patch, const float *cls, const float *pos, int64_t B, int np,
+                        int d, float *x, hipStream_t s);
+hipError_t gather_rows_bf16(const float *x, int64_t stride, int64_t n, int d, uint16_t *out,
+                            hipStream_t s);
+hipError_t mel_time_major(const float *mel, int64_t B, int mels, int T, uint16_t *out,
+                          hipStream_t s);
+
 // C[M,N] = epi(A[M,K] @ Wt[N,K]^T + bias) (+ residual); see k_gemm.hip.
 struct GemmArgs {
   const uint16_t *A;

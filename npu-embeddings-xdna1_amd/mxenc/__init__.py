@@ -19,6 +19,7 @@ MX_EPI_NONE, MX_EPI_GELU_POLY, MX_EPI_GELU_ERF = 0, 1, 2
 MX_GELU_POLY, MX_GELU_ERF, MX_GELU_ERF_AS = 0, 1, 2
 MX_SOFTMAX_POLY, MX_SOFTMAX_EXACT, MX_SOFTMAX_AIE = 0, 1, 2
 MX_ARCH_BERT, MX_ARCH_PRELN = 0, 1
+MX_FRONT_NONE, MX_FRONT_VIT, MX_FRONT_WHISPER = 0, 1, 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -41,7 +42,9 @@ class EncoderDesc(ctypes.Structure):
     _fields_ = [("arch", _int), ("layers", _i64), ("hidden", _i64), ("heads", _i64),
                 ("head_dim", _i64), ("ffn", _i64), ("ln_eps", ctypes.c_float),
                 ("attn_scale", ctypes.c_float), ("gelu", _int), ("cls_pool", _int),
-                ("l2_normalize", _int), ("vocab", _i64), ("max_pos", _i64)]
+                ("l2_normalize", _int), ("vocab", _i64), ("max_pos", _i64), ("front", _int),
+                ("image", _i64), ("patch", _i64), ("labels", _i64), ("mels", _i64),
+                ("frames", _i64)]
 
 
 class Timings(ctypes.Structure):
@@ -96,6 +99,8 @@ SIGNATURES = {
     "mx_encoder_ready": (_int, [_vp]),
     "mx_encoder_run": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64]),
     "mx_encoder_embed": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "mx_encoder_vit": (_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
+    "mx_encoder_whisper": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "mx_encoder_set_timing": (_int, [_vp, _int]),
     "mx_encoder_timings": (_int, [_vp, ctypes.POINTER(Timings)]),
 }
@@ -267,7 +272,9 @@ class Encoder:
     """An mx_encoder loaded from a synthetic model dict (mxenc.synth)."""
 
     def __init__(self, ctx, m, gelu=None, ln_eps=None, attn_scale=1.0, cls_pool=None,
-                 l2_normalize=True):
+                 l2_normalize=True, front=True):
+        """front: load the ViT / Whisper front end (and ViT head) when the model
+        has one; False builds the layer body only (mx_encoder_run)."""
         self.ctx = ctx
         self.m = m
         bert = m["kind"] == "bert"
@@ -282,6 +289,13 @@ class Encoder:
         d.l2_normalize = int(l2_normalize)
         d.vocab = m.get("vocab", 0) if bert else 0
         d.max_pos = m.get("max_pos", 0) if bert else 0
+        kind = m["kind"]
+        d.front = (MX_FRONT_VIT if kind == "vit" else MX_FRONT_WHISPER if kind == "whisper"
+                   else MX_FRONT_NONE) if front else MX_FRONT_NONE
+        if d.front == MX_FRONT_VIT:
+            d.image, d.patch, d.labels = m["image"], m["patch"], m["labels"]
+        elif d.front == MX_FRONT_WHISPER:
+            d.mels, d.frames = m["mels"], m["frames"]
         self.desc = d
         h = _vp()
         check(lib().mx_encoder_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)))
@@ -305,6 +319,19 @@ class Encoder:
         else:
             self.set("final_ln.weight", m["fin_ln_g"])
             self.set("final_ln.bias", m["fin_ln_b"])
+        if d.front == MX_FRONT_VIT:
+            self.set("patch_embed.weight", m["patch_w"])
+            self.set("patch_embed.bias", m["patch_b"])
+            self.set("cls_token", m["cls_token"])
+            self.set("position", m["pos"])
+            self.set("head.weight", m["head_w"])
+            self.set("head.bias", m["head_b"])
+        elif d.front == MX_FRONT_WHISPER:
+            self.set("conv1.weight", m["conv1_w"])
+            self.set("conv1.bias", m["conv1_b"])
+            self.set("conv2.weight", m["conv2_w"])
+            self.set("conv2.bias", m["conv2_b"])
+            self.set("position", m["pos"])
         check(lib().mx_encoder_ready(self.handle))
 
     def set(self, name, arr):
@@ -319,6 +346,13 @@ class Encoder:
     def embed(self, ids, attn_mask, B, S, out):
         check(lib().mx_encoder_embed(self.handle, self.ctx.stream, _p(ids), _p(attn_mask), B,
                                      S, _p(out)))
+
+    def vit(self, pixels, B, logits, hidden=None):
+        check(lib().mx_encoder_vit(self.handle, self.ctx.stream, _p(pixels), B, _p(logits),
+                                   _p(hidden)))
+
+    def whisper(self, mel, B, hidden):
+        check(lib().mx_encoder_whisper(self.handle, self.ctx.stream, _p(mel), B, _p(hidden)))
 
     def set_timing(self, on):
         check(lib().mx_encoder_set_timing(self.handle, int(on)))

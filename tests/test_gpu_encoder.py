@@ -140,3 +140,108 @@ def test_partial_placement_refused(ctx):
     finally:
         L.mx_ops_parse(b"")
         enc.close()
+
+
+def test_bge_large_full_batch_subset_checked(ctx, orc):
+    """bge-large geometry at its full shape (batch 128 x seq 512, 24 layers,
+    d 1024, 16 heads, every sequence full length): the whole batch on the GPU,
+    two sequences rerun on the host path."""
+    m = synth.make_model("bge_large")
+    ids, am, _ = synth.make_text_inputs(m)
+    enc = mxenc.Encoder(ctx, m)
+    got = gpu_embed(ctx, enc, ids, am)
+    enc.close()
+    assert np.all(np.isfinite(got))
+    pick = [0, 77]
+    want, _ = oracle_embed(orc, m, np.ascontiguousarray(ids[pick]), np.ascontiguousarray(am[pick]))
+    cos = cosines(got[pick], want)
+    assert np.min(cos) >= COS_MIN, cos
+
+
+def oracle_vit(orc, m, px):
+    """VitEncoder::run + head_matvec on the host: im2col, patch GEMM + bias,
+    [CLS; patches] + positions, pre-LN layers + final LN, head on the CLS row."""
+    B, p, img, d = px.shape[0], m["patch"], m["image"], m["hidden"]
+    npch, pd, labels = (img // p) ** 2, 3 * p * p, m["labels"]
+    rows = np.empty((B * npch, pd), np.float32)
+    for b in range(B):
+        one = np.ascontiguousarray(px[b])
+        blk = np.empty((npch, pd), np.float32)
+        orc.orc_vit_patches(P(one), img, p, P(blk))
+        rows[b * npch:(b + 1) * npch] = blk
+    patch = np.empty((B * npch, d), np.float32)
+    orc.orc_gemm_nt(P(rows), B * npch, P(m["patch_w"]), pd, d, P(m["patch_b"]), P(patch))
+    S = npch + 1
+    x = np.empty((B * S, d), np.float32)
+    for b in range(B):
+        x[b * S] = m["cls_token"]
+        x[b * S + 1:(b + 1) * S] = patch[b * npch:(b + 1) * npch]
+    x += np.tile(m["pos"], (B, 1))
+    keep = []
+    orc.orc_preln_run(encoder_struct(m, keep), P(x), B, S, 1e-12, 1.0, -1)
+    logits = np.empty((B, labels), np.float32)
+    for b in range(B):
+        cls = np.ascontiguousarray(x[b * S])
+        lg = np.empty(labels, np.float32)
+        orc.orc_head_matvec(P(m["head_w"]), P(m["head_b"]), P(cls), d, labels, P(lg))
+        logits[b] = lg
+    return logits, x
+
+
+def test_vit_full_config(ctx, orc):
+    """ViT-B/16 at 224x224, the configuration's batch of 256 images: patch
+    embedding, CLS + positions, 12 pre-LN layers over 197 tokens, final LN and
+    the 1000-way head, all on the GPU; two images rerun on the host path
+    (hidden state per token and the logits)."""
+    m = synth.make_model("vit_base", ln_random=True)
+    B, d, S = m["batch"], m["hidden"], m["seq"]
+    px = synth.make_pixels(m)
+    enc = mxenc.Encoder(ctx, m)
+    d_px = ctx.put(px)
+    logits = ctx.empty((B, m["labels"]), np.float32)
+    hid = ctx.empty((B * S, d), np.float32)
+    enc.vit(d_px, B, logits, hid)
+    lg, h = logits.host(), hid.host()
+    enc.close()
+    assert np.all(np.isfinite(lg)) and np.all(np.isfinite(h))
+    pick = [0, B - 1]
+    want_lg, want_x = oracle_vit(orc, m, np.ascontiguousarray(px[pick]))
+    for i, b in enumerate(pick):
+        cos = cosines(h[b * S:(b + 1) * S], want_x[i * S:(i + 1) * S])
+        assert np.min(cos) >= COS_MIN, (b, np.min(cos))
+        err = np.max(np.abs(lg[b] - want_lg[i])) / np.max(np.abs(want_lg[i]))
+        assert err < 1e-2, (b, err)
+
+
+def oracle_whisper(orc, m, mel):
+    B, T, d = mel.shape[0], m["frames"], m["hidden"]
+    S = T // 2
+    x = np.empty((B * S, d), np.float32)
+    for b in range(B):
+        out = np.empty((S, d), np.float32)
+        orc.orc_conv_front_end(P(np.ascontiguousarray(mel[b])), m["mels"], T, P(m["conv1_w"]),
+                               P(m["conv1_b"]), P(m["conv2_w"]), P(m["conv2_b"]), d, P(out))
+        x[b * S:(b + 1) * S] = out + m["pos"]
+    keep = []
+    orc.orc_preln_run(encoder_struct(m, keep), P(x), B, S, 1e-5, 1.0, -1)
+    return x
+
+
+def test_whisper_full_config(ctx, orc):
+    """Whisper-large-v3 encoder geometry, the configuration's 8 x 128 mels x
+    3000 frames: conv1 + GELU, conv2 (stride 2) + GELU, positions, 32 pre-LN
+    layers over 1500 positions (unmasked) and the final LN on the GPU; one
+    sample rerun on the host path, every one of its 1500 rows checked."""
+    m = synth.make_model("whisper_enc", ln_random=True)
+    B, d, S = m["batch"], m["hidden"], m["seq"]
+    mel = synth.make_mel(m)
+    enc = mxenc.Encoder(ctx, m)
+    d_mel = ctx.put(mel)
+    hid = ctx.empty((B * S, d), np.float32)
+    enc.whisper(d_mel, B, hid)
+    h = hid.host()
+    enc.close()
+    assert np.all(np.isfinite(h))
+    want = oracle_whisper(orc, m, np.ascontiguousarray(mel[:1]))
+    cos = cosines(h[:S], want)
+    assert np.min(cos) >= COS_MIN, np.min(cos)
