@@ -40,6 +40,18 @@ def kernel_name(plan, epi, res, cbf):
             f"{b(cbf)}>")
 
 
+def workload_name(config, m):
+    geo = f"d {m['hidden']}, {m['heads']} heads, FFN {m['ffn']}"
+    if m["kind"] == "bert":
+        return (f"{config} encoder embed: ids -> {m['layers']}-layer BERT ({geo}) -> "
+                f"{'CLS' if m['cls_pool'] else 'mean'} pool + L2")
+    if m["kind"] == "vit":
+        return (f"{config}: pixels -> patch embed -> {m['layers']} pre-LN layers over "
+                f"{m['seq']} tokens ({geo}) -> {m['labels']}-way head")
+    return (f"{config}: log-mel -> conv1d x2 -> {m['layers']} pre-LN layers over "
+            f"{m['seq']} positions ({geo}) -> final LN")
+
+
 def cpu_baseline(name, sample_batch, threads):
     """The oracle's host path (the reference CPU fallback restated) over
     `sample_batch` sequences of the same workload, all layers."""
@@ -111,18 +123,33 @@ def main():
         return
 
     m = synth.make_model(args.config)
-    assert m["kind"] == "bert"
-    ids, am, lens = synth.make_text_inputs(m)
-    B, S = ids.shape
+    kind = m["kind"]
     ctx = mxenc.Context(0)
     enc = mxenc.Encoder(ctx, m)
-    d_ids, d_am = ctx.put(ids), ctx.put(am)
-    out = ctx.empty((B, m["hidden"]), np.float32)
+    if kind == "bert":
+        ids, am, lens = synth.make_text_inputs(m)
+        B, S = ids.shape
+        d_ids, d_am = ctx.put(ids), ctx.put(am)
+        out = ctx.empty((B, m["hidden"]), np.float32)
+        step = lambda: enc.embed(d_ids, d_am, B, S, out)  # noqa: E731
+        unit = "sequences/s"
+    elif kind == "vit":
+        B, S = m["batch"], m["seq"]
+        d_px = ctx.put(synth.make_pixels(m))
+        logits = ctx.empty((B, m["labels"]), np.float32)
+        step = lambda: enc.vit(d_px, B, logits)  # noqa: E731
+        unit = "images/s"
+    else:
+        B, S = m["batch"], m["seq"]
+        d_mel = ctx.put(synth.make_mel(m))
+        hid = ctx.empty((B * S, m["hidden"]), np.float32)
+        step = lambda: enc.whisper(d_mel, B, hid)  # noqa: E731
+        unit = "samples/s"
     print(f"bench: {args.config} B={B} S={S} L={m['layers']} on {ctx.props.arch.decode()} "
           f"({ctx.props.compute_units} CUs)", file=sys.stderr, flush=True)
 
     for _ in range(args.warmup):
-        enc.embed(d_ids, d_am, B, S, out)
+        step()
     ctx.sync()
 
     # Timed region: throughput without per-launch events.
@@ -130,11 +157,11 @@ def main():
     ctx.sync()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        enc.embed(d_ids, d_am, B, S, out)
+        step()
     ctx.sync()
     dt = time.perf_counter() - t0
     seq_s = args.steps * B / dt
-    print(f"bench: {args.steps} steps in {dt*1e3:.1f} ms -> {seq_s:.1f} seq/s",
+    print(f"bench: {args.steps} steps in {dt*1e3:.1f} ms -> {seq_s:.1f} {unit}",
           file=sys.stderr, flush=True)
 
     # The same steps again with a HIP event pair around every launch, on the
@@ -144,7 +171,7 @@ def main():
            "attn_flop": 0.0, "gemm_n": 0, "attn_n": 0}
     site_ms, site_flop, site_n = [0.0] * 4, [0.0] * 4, [0] * 4
     for _ in range(args.steps):
-        enc.embed(d_ids, d_am, B, S, out)
+        step()
         t = enc.timings()
         tot["gemm_ms"] += t.gemm_ms
         tot["attn_ms"] += t.attn_ms
@@ -170,10 +197,15 @@ def main():
     # run -- tile plan plus epilogue, residual and C type, the name rocprof
     # reports -- and the group with the most time.
     d, f, M = m["hidden"], m["ffn"], B * S
-    act = 2 if m.get("gelu_erf") else 1
-    # (M, N, K, epilogue, residual, bf16 C) of each site in this BERT stack
-    sites = [("qkv", (M, 3 * d, d, 0, False, True)), ("attn_out", (M, d, d, 0, False, True)),
-             ("ffn_up", (M, f, d, act, False, True)), ("ffn_down", (M, d, f, 0, False, True))]
+    # (M, N, K, epilogue, residual, bf16 C) of each site: the BERT stack
+    # narrows its projections to bf16 for the residual-fused LayerNorm; the
+    # pre-LN stacks add them into the fp32 residual stream in the epilogue.
+    if kind == "bert":
+        sites = [("qkv", (M, 3 * d, d, 0, False, True)), ("attn_out", (M, d, d, 0, False, True)),
+                 ("ffn_up", (M, f, d, 1, False, True)), ("ffn_down", (M, d, f, 0, False, True))]
+    else:
+        sites = [("qkv", (M, 3 * d, d, 0, False, True)), ("attn_out", (M, d, d, 0, True, False)),
+                 ("ffn_up", (M, f, d, 2, False, True)), ("ffn_down", (M, d, f, 0, True, False))]
     groups = {}
     for i, (sname, (mm, nn, kk, epi, res, cbf)) in enumerate(sites):
         plan = mxenc.lib().mx_gemm_plan(mm, nn, kk).decode()
@@ -198,16 +230,17 @@ def main():
             traffic = tj.get("hbm_bytes_per_launch")
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and kind == "bert":
         threads = min(16, os.cpu_count() or 1)
         cpu = cpu_baseline(args.config, args.cpu_sample, threads)
         print(f"bench: cpu baseline {cpu['value']:.3f} seq/s ({cpu['sample']})",
               file=sys.stderr, flush=True)
 
     line = {
-        "metric": "sequences/sec (bge-base, seq 512, b64) + GEMM MFMA util % of bf16 peak",
+        "metric": ("sequences/sec (bge-base, seq 512, b64) + GEMM MFMA util % of bf16 peak"
+                   if args.config == "bge_base" else f"{unit} ({args.config})"),
         "value": seq_s,
-        "unit": "sequences/s",
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -216,11 +249,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded token ids and valid lengths; random-init N(0,0.02) weights)",
-        "config": {"workload": f"{args.config} encoder embed: ids -> {m['layers']}-layer "
-                               f"BERT (d {m['hidden']}, {m['heads']} heads, FFN {m['ffn']}) -> "
-                               f"{'CLS' if m['cls_pool'] else 'mean'} pool + L2",
-                   "batch": B, "seq_len": S, "layers": m["layers"]},
+        "data": "synthetic (seeded token ids and valid lengths; random-init N(0,0.02) weights)"
+                if kind == "bert" else "synthetic (seeded inputs; random-init N(0,0.02) weights)",
+        "config": {"workload": workload_name(args.config, m), "batch": B, "seq_len": S,
+                   "layers": m["layers"]},
         "gemm_mfma_util_pct": 100.0 * gemm_tflops / BF16_PEAK_TFLOPS,
         "roofline": {"bound": "mfma", "kernel": dom_name, "sites": dom["sites"],
                      "achieved": dom_tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
