@@ -174,7 +174,13 @@ hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s);
 
 namespace {
 
-enum GemmPath { PATH_STAGED, PATH_LDS_256x256, PATH_LDS_128x256, PATH_LDS_128x128 };
+enum GemmPath {
+  PATH_STAGED,
+  PATH_LDS_256x256,
+  PATH_LDS_256x192,
+  PATH_LDS_128x256,
+  PATH_LDS_128x128
+};
 
 bool lds_path_ok(const GemmArgs &a) {
   const uintptr_t c = (uintptr_t)a.C;
@@ -183,15 +189,38 @@ bool lds_path_ok(const GemmArgs &a) {
          (!a.residual || (uintptr_t)a.residual % 16 == 0);
 }
 
+int cu_count();
+
+// The tile with the least estimated time: rounds of tiles over the CUs (the
+// last round costs a whole one) times the tile's area over its relative
+// throughput per unit area, measured on MI355X on the encoder's GEMM shapes
+// when every tile count is a whole number of rounds (256 x 256: 1.0, 256 x
+// 192: 0.88, 128 x 256: 0.86, 128 x 128: 0.65). The 256 x 192 tile wins
+// where N = 768 leaves 256 x 256 tiles at 1.5 rounds; small problems take
+// the small tiles that spread over the most CUs.
 GemmPath pick(const GemmArgs &a) {
   if (!lds_path_ok(a)) return PATH_STAGED;
-  const int64_t t256 = ((a.M + 255) / 256) * ((a.N + 255) / 256);
-  const int64_t t128x256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
-  // 256x256 tiles once there are at least two rounds of them over the 256
-  // CUs and N is wide; else 128x256; small problems take 128x128.
-  if (a.N >= 1536 && t256 >= 512) return PATH_LDS_256x256;
-  if (t128x256 >= 256) return PATH_LDS_128x256;
-  return PATH_LDS_128x128;
+  struct Cand {
+    GemmPath path;
+    int bm, bn;
+    double eff;
+  };
+  static const Cand cands[] = {{PATH_LDS_256x256, 256, 256, 1.0},
+                               {PATH_LDS_256x192, 256, 192, 0.88},
+                               {PATH_LDS_128x256, 128, 256, 0.86},
+                               {PATH_LDS_128x128, 128, 128, 0.65}};
+  const int64_t G = cu_count();
+  GemmPath best = PATH_LDS_128x128;
+  double best_t = 0.0;
+  for (const Cand &c : cands) {
+    const int64_t tiles = ((a.M + c.bm - 1) / c.bm) * ((a.N + c.bn - 1) / c.bn);
+    const double t = (double)((tiles + G - 1) / G) * c.bm * c.bn / c.eff;
+    if (best_t == 0.0 || t < best_t) {
+      best = c.path;
+      best_t = t;
+    }
+  }
+  return best;
 }
 
 // Resident blocks of the persistent kernel: one per CU of the current device.
@@ -223,6 +252,7 @@ const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
   a.C = (void *)aligned_probe;
   switch (pick(a)) {
     case PATH_LDS_256x256: return "lds_256x256x32_w128x64_ns3_persistent";
+    case PATH_LDS_256x192: return "lds_256x192x32_w64x96_ns4_persistent";
     case PATH_LDS_128x256: return "lds_128x256x32_w64x64_ns4_persistent";
     case PATH_LDS_128x128: return "lds_128x128x32_w64x64_ns4_persistent";
     default: return "staged_128x128x64_w64x64";
@@ -232,6 +262,7 @@ const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
 hipError_t gemm(const GemmArgs &a, hipStream_t s) {
   switch (pick(a)) {
     case PATH_LDS_256x256: return gemm_lds_launch<256, 256, 2, 4, 3>(a, cu_count(), s);
+    case PATH_LDS_256x192: return gemm_lds_launch<256, 192, 4, 2, 4>(a, cu_count(), s);
     case PATH_LDS_128x256: return gemm_lds_launch<128, 256, 2, 4, 4>(a, cu_count(), s);
     case PATH_LDS_128x128: return gemm_lds_launch<128, 128, 2, 2, 4>(a, cu_count(), s);
     default: return launch<128, 128, 64, 64, 64>(a, s);

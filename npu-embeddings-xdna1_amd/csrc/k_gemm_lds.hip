@@ -75,19 +75,21 @@ struct LdsCfg {
   static constexpr int TM = WM / 32, TN = WN / 32;    // 32x32 MFMA tiles per wave
   static constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB;
   static constexpr int SLOT = A_BYTES + B_BYTES;
-  static constexpr int A_LOADS = A_BYTES / 1024 / NW;  // 1 KB wave loads per wave per slab
-  static constexpr int B_LOADS = B_BYTES / 1024 / NW;
-  static constexpr int LOADS = A_LOADS + B_LOADS;
+  // A slab is PIECES 1 KB wave loads of 16 rows each, A's first; wave w
+  // issues pieces w, w + NW, ...: LOADS_HI of them if w < NHI, else LOADS_LO
+  // (a 256 x 192 slab is 28 pieces: four waves issue 4, four issue 3).
+  static constexpr int A_PIECES = A_BYTES / 1024, PIECES = (A_BYTES + B_BYTES) / 1024;
+  static constexpr int LOADS_LO = PIECES / NW, LOADS_HI = (PIECES + NW - 1) / NW;
+  static constexpr int NHI = PIECES % NW == 0 ? NW : PIECES % NW;
   static constexpr int BIAS_PER_WAVE = BN / NW;        // floats each wave's bias piece moves
   static constexpr int STG_OFF = NS * SLOT;
   static constexpr int BIAS_OFF = STG_OFF + NW * STG_WAVE;
   static constexpr int LDS = BIAS_OFF + 2 * BN * 4;
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be whole MFMA tiles");
-  static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0,
-                "each wave must issue whole 1 KB loads");
+  static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "slabs are whole 1 KB pieces");
   static_assert(BIAS_PER_WAVE % 4 == 0 && BIAS_PER_WAVE <= 256, "bias piece: 16-byte lanes");
   static_assert(LDS <= 160 * 1024, "gfx950 LDS is 160 KB");
-  static_assert(NS >= 3 && LOADS * (NS - 2) < 64, "vmcnt holds at most 63");
+  static_assert(NS >= 3 && LOADS_HI * (NS - 2) < 64, "vmcnt holds at most 63");
 };
 
 // s_waitcnt vmcnt(N), other counters untouched.
@@ -155,17 +157,19 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
     const uint32_t slot = lds0 + (uint32_t)((is_s % NS) * Cfg::SLOT);
     const int kofs = kt * BK + lchunk * 8;
 #pragma unroll
-    for (int i = 0; i < Cfg::A_LOADS; ++i) {
-      int r = m0 + (wave * Cfg::A_LOADS + i) * 16 + lrow;
-      r = r < M ? r : M - 1;
-      dma16(A + (int64_t)r * lda + kofs, slot + (uint32_t)((wave * Cfg::A_LOADS + i) * 1024));
-    }
-#pragma unroll
-    for (int i = 0; i < Cfg::B_LOADS; ++i) {
-      int r = n0 + (wave * Cfg::B_LOADS + i) * 16 + lrow;
-      r = r < N ? r : N - 1;
-      dma16(Wt + (int64_t)r * K + kofs,
-            slot + Cfg::A_BYTES + (uint32_t)((wave * Cfg::B_LOADS + i) * 1024));
+    for (int k = 0; k < Cfg::LOADS_HI; ++k) {
+      const int p = wave + Cfg::NW * k;  // wave-uniform
+      if (k < Cfg::LOADS_LO || p < Cfg::PIECES) {
+        if (p < Cfg::A_PIECES) {
+          int r = m0 + p * 16 + lrow;
+          r = r < M ? r : M - 1;
+          dma16(A + (int64_t)r * lda + kofs, slot + (uint32_t)(p * 1024));
+        } else {
+          int r = n0 + (p - Cfg::A_PIECES) * 16 + lrow;
+          r = r < N ? r : N - 1;
+          dma16(Wt + (int64_t)r * K + kofs, slot + (uint32_t)(p * 1024));
+        }
+      }
     }
     // Bias piece, on a tile's first slab: lanes 0 .. BIAS_PER_WAVE/4 - 1 move
     // 16 bytes each of the columns from n0 + wave * BIAS_PER_WAVE (clamped in
@@ -331,10 +335,17 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
     // loads of slab s + 1 (the slabs issued after it, at most NS - 2, may stay
     // in flight), then meet: slab s + 1 is in LDS and slot s % NS is free.
     const int ahead = nslab - 2 - s;
+    const bool hi = wave < Cfg::NHI;
     if (ahead >= NS - 2) {
-      wait_vmcnt<Cfg::LOADS *(NS - 2)>();
+      if (hi)
+        wait_vmcnt<Cfg::LOADS_HI *(NS - 2)>();
+      else
+        wait_vmcnt<Cfg::LOADS_LO *(NS - 2)>();
     } else if (NS > 3 && ahead == NS - 3) {
-      wait_vmcnt<(NS > 3 ? Cfg::LOADS * (NS - 3) : 0)>();
+      if (hi)
+        wait_vmcnt<(NS > 3 ? Cfg::LOADS_HI * (NS - 3) : 0)>();
+      else
+        wait_vmcnt<(NS > 3 ? Cfg::LOADS_LO * (NS - 3) : 0)>();
     } else {
       wait_vmcnt<0>();
     }
@@ -405,5 +416,6 @@ hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s) {
 template hipError_t gemm_lds_launch<256, 256, 2, 4, 3>(const GemmArgs &, int, hipStream_t);
 template hipError_t gemm_lds_launch<128, 256, 2, 4, 4>(const GemmArgs &, int, hipStream_t);
 template hipError_t gemm_lds_launch<128, 128, 2, 2, 4>(const GemmArgs &, int, hipStream_t);
+template hipError_t gemm_lds_launch<256, 192, 4, 2, 4>(const GemmArgs &, int, hipStream_t);
 
 }  // namespace mxk

@@ -297,10 +297,12 @@ def test_gemm_epilogues_and_residual(ctx, orc):
 
 GEMM_PATHS = [
     # M, K, N, epilogue, C dtype, residual, expected kernel
-    (16384, 768, 2304, mxenc.MX_EPI_NONE, np.uint16, False, "lds_256x256"),     # QKV
+    (16384, 768, 2304, mxenc.MX_EPI_NONE, np.uint16, False, "lds_256x192"),     # QKV at M = 16384
     (16384, 768, 3072, mxenc.MX_EPI_GELU_POLY, np.uint16, False, "lds_256x256"),  # FFN-up
-    (16384, 3072, 768, mxenc.MX_EPI_NONE, np.float32, False, "lds_128x256"),    # FFN-down
-    (16384, 768, 768, mxenc.MX_EPI_NONE, np.float32, True, "lds_128x256"),      # x += proj
+    (16384, 3072, 768, mxenc.MX_EPI_NONE, np.float32, False, "lds_256x192"),    # FFN-down
+    (16384, 768, 768, mxenc.MX_EPI_NONE, np.float32, True, "lds_256x192"),      # x += proj
+    (16000, 768, 1532, mxenc.MX_EPI_GELU_ERF, np.float32, True, "lds_256x192"),  # ragged M, N
+    (4096, 384, 1536, mxenc.MX_EPI_GELU_POLY, np.uint16, False, "lds_128x256"),  # MiniLM FFN-up
     (1000, 1280, 3840, mxenc.MX_EPI_GELU_ERF, np.float32, True, "lds_128x128"),  # ragged M
     (777, 512, 1004, mxenc.MX_EPI_GELU_ERF, np.uint16, False, "lds_128x128"),   # ragged M, N
 ]
