@@ -19,7 +19,12 @@
 // Ring. NS slots; slab s + NS is fetched into slot s % NS as soon as every read
 // of slab s is done, i.e. ~NS - 1 slabs ahead of its use. The loads are issued
 // from inline assembly: the compiler's own wait insertion would otherwise put
-// vmcnt(0) -- a wait on every prefetch -- before each LDS read. Each wave waits
+// vmcnt(0) -- a wait on every prefetch -- before each LDS read. Each load is
+// addressed as a scalar base (the operand's tile origin plus the slab's depth)
+// and a 32-bit per-lane offset fixed for the tile, so issuing a slab costs a
+// few scalar adds: building 64-bit addresses per load (quarter-rate integer
+// multiplies on the vector ALU, right after the barrier) cost up to a tenth
+// of the kernel. Each wave waits
 // for its own loads of the slab it is about to read (vmcnt = loads it issued
 // since; loads complete in issue order), then all waves meet at one barrier
 // per slab. The first slab of each tile also moves the tile's bias into a
@@ -106,6 +111,20 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
                : "memory");
 }
 
+// The same load addressed as a wave-uniform base (SGPRs) plus a 32-bit
+// per-lane byte offset: the per-slab advance is a scalar add.
+__device__ __forceinline__ void dma16s(uint64_t base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff),
+               "s"(base)
+               : "memory");
+}
+
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF>
 __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
     const uint16_t *__restrict__ A, int64_t lda, const uint16_t *__restrict__ Wt, int M, int N,
@@ -151,25 +170,38 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
     n0 = (t - tm * tiles_n) * BN;
   };
   tile_origin(0, is_m0, is_n0);
+  // Per issue tile: each piece's per-lane byte offset from its operand's tile
+  // origin (rows clamped in bounds), and the two origins as scalars.
+  uint32_t poff[Cfg::LOADS_HI];
+  uint64_t abase = 0, bbase = 0;
+  auto set_tile = [&](int m0, int n0) {
+#pragma unroll
+    for (int k = 0; k < Cfg::LOADS_HI; ++k) {
+      const int p = wave + Cfg::NW * k;
+      if (p < Cfg::A_PIECES) {
+        int r = m0 + p * 16 + lrow;
+        r = (r < M ? r : M - 1) - m0;
+        poff[k] = (uint32_t)((r * lda + lchunk * 8) * 2);
+      } else {
+        int r = n0 + (p - Cfg::A_PIECES) * 16 + lrow;
+        r = (r < N ? r : N - 1) - n0;
+        poff[k] = (uint32_t)(((int64_t)r * K + lchunk * 8) * 2);
+      }
+    }
+    abase = uniform64((uint64_t)(uintptr_t)(A + (int64_t)m0 * lda));
+    bbase = uniform64((uint64_t)(uintptr_t)(Wt + (int64_t)n0 * K));
+  };
+  set_tile(is_m0, is_n0);
   // Issue the loads of slab is_s, then advance the cursor.
   auto issue = [&]() {
-    const int ti = is_ti, kt = is_kt, m0 = is_m0, n0 = is_n0;
+    const int ti = is_ti, kt = is_kt, n0 = is_n0;
     const uint32_t slot = lds0 + (uint32_t)((is_s % NS) * Cfg::SLOT);
-    const int kofs = kt * BK + lchunk * 8;
+    const uint64_t kb = (uint64_t)kt * (BK * 2);
 #pragma unroll
     for (int k = 0; k < Cfg::LOADS_HI; ++k) {
       const int p = wave + Cfg::NW * k;  // wave-uniform
-      if (k < Cfg::LOADS_LO || p < Cfg::PIECES) {
-        if (p < Cfg::A_PIECES) {
-          int r = m0 + p * 16 + lrow;
-          r = r < M ? r : M - 1;
-          dma16(A + (int64_t)r * lda + kofs, slot + (uint32_t)(p * 1024));
-        } else {
-          int r = n0 + (p - Cfg::A_PIECES) * 16 + lrow;
-          r = r < N ? r : N - 1;
-          dma16(Wt + (int64_t)r * K + kofs, slot + (uint32_t)(p * 1024));
-        }
-      }
+      if (k < Cfg::LOADS_LO || p < Cfg::PIECES)
+        dma16s((p < Cfg::A_PIECES ? abase : bbase) + kb, poff[k], slot + (uint32_t)(p * 1024));
     }
     // Bias piece, on a tile's first slab: lanes 0 .. BIAS_PER_WAVE/4 - 1 move
     // 16 bytes each of the columns from n0 + wave * BIAS_PER_WAVE (clamped in
@@ -185,7 +217,10 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
     if (++is_kt == nk) {
       is_kt = 0;
       ++is_ti;
-      if (is_ti < my_tiles) tile_origin(is_ti, is_m0, is_n0);
+      if (is_ti < my_tiles) {
+        tile_origin(is_ti, is_m0, is_n0);
+        set_tile(is_m0, is_n0);
+      }
     }
   };
 
