@@ -173,7 +173,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
   // Per issue tile: each piece's per-lane byte offset from its operand's tile
   // origin (rows clamped in bounds), and the two origins as scalars.
   uint32_t poff[Cfg::LOADS_HI];
-  uint64_t abase = 0, bbase = 0;
+  uint64_t pbase[Cfg::LOADS_HI];
   auto set_tile = [&](int m0, int n0) {
 #pragma unroll
     for (int k = 0; k < Cfg::LOADS_HI; ++k) {
@@ -188,20 +188,24 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
         poff[k] = (uint32_t)(((int64_t)r * K + lchunk * 8) * 2);
       }
     }
-    abase = uniform64((uint64_t)(uintptr_t)(A + (int64_t)m0 * lda));
-    bbase = uniform64((uint64_t)(uintptr_t)(Wt + (int64_t)n0 * K));
+    const uint64_t abase = uniform64((uint64_t)(uintptr_t)(A + (int64_t)m0 * lda));
+    const uint64_t bbase = uniform64((uint64_t)(uintptr_t)(Wt + (int64_t)n0 * K));
+#pragma unroll
+    for (int k = 0; k < Cfg::LOADS_HI; ++k)
+      pbase[k] = wave + Cfg::NW * k < Cfg::A_PIECES ? abase : bbase;
   };
   set_tile(is_m0, is_n0);
   // Issue the loads of slab is_s, then advance the cursor.
+  uint32_t is_slot = 0;  // byte offset of slot is_s % NS
+  uint64_t is_kb = 0;    // byte depth of slab is_kt
   auto issue = [&]() {
     const int ti = is_ti, kt = is_kt, n0 = is_n0;
-    const uint32_t slot = lds0 + (uint32_t)((is_s % NS) * Cfg::SLOT);
-    const uint64_t kb = (uint64_t)kt * (BK * 2);
+    const uint32_t slot = lds0 + is_slot;
 #pragma unroll
     for (int k = 0; k < Cfg::LOADS_HI; ++k) {
       const int p = wave + Cfg::NW * k;  // wave-uniform
       if (k < Cfg::LOADS_LO || p < Cfg::PIECES)
-        dma16s((p < Cfg::A_PIECES ? abase : bbase) + kb, poff[k], slot + (uint32_t)(p * 1024));
+        dma16s(pbase[k] + is_kb, poff[k], slot + (uint32_t)(p * 1024));
     }
     // Bias piece, on a tile's first slab: lanes 0 .. BIAS_PER_WAVE/4 - 1 move
     // 16 bytes each of the columns from n0 + wave * BIAS_PER_WAVE (clamped in
@@ -214,8 +218,11 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
             lds0 + Cfg::BIAS_OFF + (uint32_t)((ti & 1) * BN * 4 + wave * Cfg::BIAS_PER_WAVE * 4));
     }
     ++is_s;
+    is_slot = is_slot + Cfg::SLOT == NS * Cfg::SLOT ? 0 : is_slot + Cfg::SLOT;
+    is_kb += BK * 2;
     if (++is_kt == nk) {
       is_kt = 0;
+      is_kb = 0;
       ++is_ti;
       if (is_ti < my_tiles) {
         tile_origin(is_ti, is_m0, is_n0);
@@ -387,12 +394,32 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (s + NS < nslab) issue();  // slab s + NS
     // Second half of slab s; the first half of slab s + 1 is read meanwhile
-    // (after the last slab, slab s again: in bounds, unused).
-    mfma_set(fa1, fb1);
+    // (after the last slab, slab s again: in bounds, unused). The loads of
+    // slab s + NS are issued after the first MFMAs, which keep the matrix
+    // pipe busy while the scalar unit addresses them.
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb1[0], fa1[i], acc[0][i], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + NS < nslab) issue();  // slab s + NS
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 1; j < TN; ++j)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb1[j], fa1[i], acc[j][i], 0, 0, 0);
     read_set(s + 1 < nslab ? s + 1 : s, pos0, fa0, fb0);
-    interleave();
+    {
+      constexpr int NM = TM * (TN - 1), NR = TM + TN, NP = NM < NR ? NM : NR;
+#pragma unroll
+      for (int x = 0; x < NP; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      if (NM > NP) __builtin_amdgcn_sched_group_barrier(0x008, NM - NP, 0);
+      if (NR > NP) __builtin_amdgcn_sched_group_barrier(0x100, NR - NP, 0);
+    }
     if (++ep_kt == nk) {
       ep_kt = 0;
       epilogue(ep_ti++);
