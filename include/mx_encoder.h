@@ -329,6 +329,62 @@ typedef struct {
 int mx_encoder_set_timing(mx_encoder *enc, int on);
 int mx_encoder_timings(mx_encoder *enc, mx_timings *out);
 
+/* ---- the .npue weight container ------------------------------------------
+ * npue::File (runtime/include/runtime/model.hpp, runtime/src/model.cpp:
+ * 214-380): the container is mapped read-only; the 64-byte header is checked
+ * (magic "NPUE", version 1, data_offset 4096-aligned, file size = data_offset
+ * + data_length) and the JSON directory read. Refusals name the file and the
+ * reason, like the reference's std::runtime_error messages. */
+typedef struct mx_npue mx_npue;
+typedef struct {
+  char dtype[8];               /* "BF16", "F32", "I8", "I4", "U8", ...       */
+  int ndim;                    /* of padded_shape (at most 4 kept)           */
+  int64_t padded_shape[4], logical_shape[4];
+  int block_panel;             /* layout.kind == "block_panel"               */
+  int64_t tile_k, tile_n, mac_s, mac_t; /* the layout, when block_panel       */
+  const void *data;            /* into the mapping; valid until close        */
+  uint64_t nbytes;
+} mx_npue_tensor_info;
+int mx_npue_open(const char *path, mx_npue **out);
+void mx_npue_close(mx_npue *f);
+/* File::config_string (model.cpp:374-379): the value's text -- a JSON string
+ * unescaped, a number or literal as written, an object or array as its raw
+ * JSON. Copies at most len-1 bytes plus a NUL into buf (nullable); returns
+ * the full length, or MX_E_INVALID naming a missing key. */
+int mx_npue_config(const mx_npue *f, const char *key, char *buf, size_t len);
+int mx_npue_tensor_count(const mx_npue *f);
+const char *mx_npue_tensor_name(const mx_npue *f, int index);
+/* File::info + File::raw (model.cpp:352-364). */
+int mx_npue_tensor(const mx_npue *f, const char *name, mx_npue_tensor_info *out);
+
+/* Design::stage (design.hpp:236) of a container's pre-tiled GEMM operand: the
+ * bf16 bytes exactly as the container stores them -- a [K, N] operand tiled
+ * (tile_k, tile_n) in k,n order, each tile in (mac_s, mac_t) sub-tiles
+ * (tools/lib/npue.py:491-556) -- are copied to the GPU once and untiled there
+ * into the MFMA-ready [N, K] panel. The same element lands where
+ * hostb::host_b_kn (common/host_b.hpp:74-224) puts it; that function's
+ * shape refusals are kept (K % tile_k, N % tile_n, tile_k % mac_s,
+ * tile_n % mac_t). */
+int mx_stage_weight_panel(mx_ctx *ctx, const uint16_t *panel_host, int64_t K, int64_t N,
+                          int64_t tile_k, int64_t tile_n, int64_t mac_s, int64_t mac_t,
+                          int *slot);
+/* mx_encoder_set for a pre-tiled container operand ("layer.{i}.qkv", ...). */
+int mx_encoder_set_panel(mx_encoder *enc, const char *name, const uint16_t *panel_host,
+                         int64_t K, int64_t N, int64_t tile_k, int64_t tile_n,
+                         int64_t mac_s, int64_t mac_t);
+/* setup_encoder for a BERT container (run_setup.hpp:483-877 with
+ * app::set_model_shape, app_state.hpp:380-620, and BertEncoder::stage_all,
+ * bert_encoder.cpp:40-160): arch "bert_abs_gelu_postln" only (RoPE and gated
+ * FFNs are refused by name); geometry from num_layers / hidden / num_heads /
+ * head_dim / intermediate / max_seq_len; pooling "cls" or "mean";
+ * l2_normalize (default true); LayerNorm eps 1e-12 and the polynomial GELU
+ * (gelu_cpu), as BertEncoder hard-codes them. Every tensor is set from the
+ * mapping: pre-tiled BF16 GEMM operands through mx_encoder_set_panel. A
+ * "host" container (F32 row-major operands) is refused for the GEMM, as the
+ * reference refuses --npu-ops gemm on one (bert_encoder.cpp:79-87). The
+ * encoder is ready on MX_OK. */
+int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out);
+
 #ifdef __cplusplus
 }
 #endif

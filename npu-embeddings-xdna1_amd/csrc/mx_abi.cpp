@@ -72,6 +72,58 @@ int stage_panel(mx_ctx *ctx, const void *kn_host, int dtype, int64_t K, int64_t 
   return MX_OK;
 }
 
+int check_panel(const std::string &what, int64_t K, int64_t N, int64_t tile_k, int64_t tile_n,
+                int64_t mac_s, int64_t mac_t) {
+  if (K <= 0 || N <= 0) return fail(MX_E_INVALID, what + ": GEMM operand with a zero dimension");
+  if (tile_k <= 0 || tile_n <= 0 || mac_s <= 0 || mac_t <= 0)
+    return fail(MX_E_INVALID, what + ": the block_panel layout needs positive tile_k, tile_n, "
+                                     "mac_s and mac_t");
+  if (K % tile_k || N % tile_n || tile_k % mac_s || tile_n % mac_t)
+    return fail(MX_E_INVALID, what + ": layout (" + std::to_string(tile_k) + "," +
+                                  std::to_string(tile_n) + ") mac (" + std::to_string(mac_s) +
+                                  "," + std::to_string(mac_t) + ") does not tile [" +
+                                  std::to_string(K) + "," + std::to_string(N) + "]");
+  if ((tile_k + 2) * tile_n * 2 > 65536)
+    return fail(MX_E_UNSUPPORTED, what + ": a " + std::to_string(tile_k) + " x " +
+                                      std::to_string(tile_n) +
+                                      " tile does not fit the untile kernel's 64 KB of LDS");
+  if (K % 8)
+    return fail(MX_E_INVALID, what + ": K = " + std::to_string(K) +
+                                  " is not a multiple of 8 (the GEMM reads K in 16-byte chunks)");
+  return MX_OK;
+}
+
+int stage_tiled_panel(mx_ctx *ctx, const uint16_t *panel_host, int64_t K, int64_t N,
+                      int64_t tile_k, int64_t tile_n, int64_t mac_s, int64_t mac_t,
+                      uint16_t **out) {
+  if (!panel_host) return fail(MX_E_INVALID, "stage_weight_panel: null panel");
+  int rc = check_panel("stage_weight_panel", K, N, tile_k, tile_n, mac_s, mac_t);
+  if (rc) return rc;
+  rc = use_device(ctx);
+  if (rc) return rc;
+  const size_t bytes = static_cast<size_t>(K) * N * 2;
+  void *tiled = nullptr, *wt = nullptr;
+  hipError_t e = hipMalloc(&tiled, bytes);
+  if (e != hipSuccess) return hip_fail(e, "stage_weight_panel: hipMalloc");
+  e = hipMalloc(&wt, bytes);
+  if (e != hipSuccess) {
+    (void)hipFree(tiled);
+    return hip_fail(e, "stage_weight_panel: hipMalloc");
+  }
+  e = hipMemcpy(tiled, panel_host, bytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess)
+    e = mxk::untile_panel(static_cast<const uint16_t *>(tiled), K, N, (int)tile_k, (int)tile_n,
+                          (int)mac_s, (int)mac_t, static_cast<uint16_t *>(wt), nullptr);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  (void)hipFree(tiled);
+  if (e != hipSuccess) {
+    (void)hipFree(wt);
+    return hip_fail(e, "stage_weight_panel: untile");
+  }
+  *out = static_cast<uint16_t *>(wt);
+  return MX_OK;
+}
+
 static bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t lda,
@@ -298,6 +350,20 @@ int mx_stage_weight(mx_ctx *ctx, const void *kn_host, int dtype, int64_t K, int6
   if (!ctx || !slot) return fail(MX_E_INVALID, "mx_stage_weight: null argument");
   uint16_t *p = nullptr;
   const int rc = stage_panel(ctx, kn_host, dtype, K, N, &p);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  ctx->slots.push_back(WeightSlot{p, K, N});
+  *slot = static_cast<int>(ctx->slots.size());
+  return MX_OK;
+}
+
+int mx_stage_weight_panel(mx_ctx *ctx, const uint16_t *panel_host, int64_t K, int64_t N,
+                          int64_t tile_k, int64_t tile_n, int64_t mac_s, int64_t mac_t,
+                          int *slot) {
+  clear_error();
+  if (!ctx || !slot) return fail(MX_E_INVALID, "mx_stage_weight_panel: null argument");
+  uint16_t *p = nullptr;
+  const int rc = stage_tiled_panel(ctx, panel_host, K, N, tile_k, tile_n, mac_s, mac_t, &p);
   if (rc) return rc;
   std::lock_guard<std::mutex> lk(ctx->mu);
   ctx->slots.push_back(WeightSlot{p, K, N});

@@ -767,4 +767,170 @@ int mx_encoder_timings(mx_encoder *enc, mx_timings *out) {
   return MX_OK;
 }
 
+// A pre-tiled container operand by its container name: the layer GEMMs, and
+// the ViT patch embedding and head.
+int mx_encoder_set_panel(mx_encoder *enc, const char *name_c, const uint16_t *panel, int64_t K,
+                         int64_t N, int64_t tile_k, int64_t tile_n, int64_t mac_s,
+                         int64_t mac_t) {
+  clear_error();
+  if (!enc || !name_c || !panel) return fail(MX_E_INVALID, "encoder_set_panel: null argument");
+  const std::string name(name_c);
+  const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
+  uint16_t **dst = nullptr;
+  int64_t wantK = 0, wantN = 0;
+  if (name.rfind("layer.", 0) == 0) {
+    size_t p = 6;
+    int64_t L = 0;
+    bool digits = false;
+    while (p < name.size() && std::isdigit(static_cast<unsigned char>(name[p]))) {
+      L = L * 10 + (name[p] - '0');
+      ++p;
+      digits = true;
+    }
+    if (digits && p < name.size() && name[p] == '.' && L < enc->desc.layers) {
+      const std::string rest = name.substr(p + 1);
+      const int64_t Ks[4] = {d, d, d, f}, Ns[4] = {3 * d, d, f, d};
+      for (int i = 0; i < 4; ++i)
+        if (rest == kGemmNames[i]) {
+          dst = &enc->layers[static_cast<size_t>(L)].w[i];
+          wantK = Ks[i];
+          wantN = Ns[i];
+        }
+    }
+  } else if (enc->desc.front == MX_FRONT_VIT && name == "patch_embed.weight") {
+    dst = &enc->patch_w;
+    wantK = 3 * enc->desc.patch * enc->desc.patch;
+    wantN = d;
+  } else if (enc->desc.front == MX_FRONT_VIT && name == "head.weight") {
+    dst = &enc->head_w;
+    wantK = d;
+    wantN = enc->desc.labels;
+  }
+  if (!dst) return fail(MX_E_INVALID, "encoder_set_panel: '" + name + "' is not a GEMM operand "
+                                      "of this encoder");
+  if (K != wantK || N != wantN)
+    return fail(MX_E_INVALID, name + ": a [" + std::to_string(K) + ", " + std::to_string(N) +
+                                  "] panel, a [" + std::to_string(wantK) + ", " +
+                                  std::to_string(wantN) + "] operand wanted");
+  uint16_t *wt = nullptr;
+  const int rc = stage_tiled_panel(enc->ctx, panel, K, N, tile_k, tile_n, mac_s, mac_t, &wt);
+  if (rc) return rc;
+  free_dev(*dst);
+  *dst = wt;
+  return MX_OK;
+}
+
+int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
+  clear_error();
+  if (!ctx || !f || !out) return fail(MX_E_INVALID, "encoder_from_npue: null argument");
+  *out = nullptr;
+  auto cfg = [&](const char *key, std::string &v) -> int {
+    if (!npue_config(f, key, v)) return fail(MX_E_INVALID, std::string(".npue: no config key ") + key);
+    return MX_OK;
+  };
+  auto cfg_int = [&](const char *key, int64_t &v) -> int {
+    std::string t;
+    int rc = cfg(key, t);
+    if (rc) return rc;
+    char *end = nullptr;
+    v = std::strtoll(t.c_str(), &end, 10);
+    if (t.empty() || *end)
+      return fail(MX_E_INVALID, std::string(".npue: config ") + key + " = '" + t +
+                                    "' is not an integer");
+    return MX_OK;
+  };
+  std::string arch;
+  int rc = cfg("arch", arch);
+  if (rc) return rc;
+  // The whitelist of app::encoder_implemented (app_state.hpp:175-200), cut to
+  // what this backend's stack computes: the absolute-position, plain-GELU,
+  // post-LN BERT. The other BERT-named archs share tensor names on purpose, so
+  // reading them here would compute the wrong model without a sign.
+  if (arch != "bert_abs_gelu_postln")
+    return fail(MX_E_UNSUPPORTED,
+                ".npue: container arch '" + arch + "' -- this loader builds the post-LN BERT "
+                "stack (bert_abs_gelu_postln); RoPE and gated-FFN archs share its tensor names "
+                "but not its maths, and are refused rather than run as BERT");
+  mx_encoder_desc d{};
+  d.arch = MX_ARCH_BERT;
+  if ((rc = cfg_int("num_layers", d.layers)) || (rc = cfg_int("hidden", d.hidden)) ||
+      (rc = cfg_int("num_heads", d.heads)) || (rc = cfg_int("head_dim", d.head_dim)) ||
+      (rc = cfg_int("intermediate", d.ffn)) || (rc = cfg_int("max_seq_len", d.max_pos)))
+    return rc;
+  std::string pool;
+  if ((rc = cfg("pooling", pool))) return rc;
+  if (pool == "cls") d.cls_pool = 1;
+  else if (pool == "mean") d.cls_pool = 0;
+  else
+    return fail(MX_E_INVALID, ".npue: unknown pooling mode '" + pool + "' -- expected mean or cls");
+  std::string l2;
+  d.l2_normalize = npue_config(f, "l2_normalize", l2) ? (l2 == "true" ? 1 : 0) : 1;
+  std::string layout;
+  if (npue_config(f, "gemm_layout", layout) && layout == "host")
+    return fail(MX_E_UNSUPPORTED,
+                ".npue: this container is gemm_layout \"host\" -- its GEMM operands are "
+                "row-major F32 for the CPU, and the GPU GEMM multiplies bf16; repack with bf16 "
+                "operands (the reference refuses --npu-ops gemm on such a container too)");
+  d.ln_eps = 1e-12f;
+  d.attn_scale = 1.0f;  // 1/sqrt(head_dim) is folded into the packed Q block
+  d.gelu = MX_GELU_POLY;
+  const TensorRecView word = npue_tensor(f, "embeddings.word");
+  if (!word.found || word.padded.size() != 2)
+    return fail(MX_E_INVALID, ".npue: embeddings.word missing or not [vocab, hidden]");
+  d.vocab = word.padded[0];
+  mx_encoder *enc = nullptr;
+  if ((rc = mx_encoder_create(ctx, &d, &enc))) return rc;
+  auto refuse = [&](int code) {
+    const std::string msg = mx_last_error();
+    mx_encoder_destroy(enc);
+    return fail(code, msg);
+  };
+  auto set_f32 = [&](const std::string &name) -> int {
+    const TensorRecView t = npue_tensor(f, name);
+    if (!t.found) return fail(MX_E_INVALID, ".npue: no tensor named " + name);
+    if (t.dtype != "F32")
+      return fail(MX_E_INVALID, name + ": " + t.dtype + " in the container, F32 wanted");
+    return mx_encoder_set(enc, name.c_str(), t.data, MX_F32, static_cast<int64_t>(t.nbytes / 4));
+  };
+  std::vector<std::string> names = {"embeddings.word", "embeddings.position",
+                                    "embeddings.token_type", "embeddings.ln.weight",
+                                    "embeddings.ln.bias"};
+  for (int64_t L = 0; L < d.layers; ++L) {
+    const std::string p = "layer." + std::to_string(L) + ".";
+    for (int i = 0; i < 4; ++i) names.push_back(p + kGemmNames[i] + ".bias");
+    for (const char *n : {"ln1.weight", "ln1.bias", "ln2.weight", "ln2.bias"})
+      names.push_back(p + n);
+  }
+  for (const std::string &n : names)
+    if ((rc = set_f32(n))) return refuse(rc);
+  for (int64_t L = 0; L < d.layers; ++L)
+    for (int i = 0; i < 4; ++i) {
+      const std::string n = "layer." + std::to_string(L) + "." + kGemmNames[i];
+      const TensorRecView t = npue_tensor(f, n);
+      if (!t.found) return refuse(fail(MX_E_INVALID, ".npue: no tensor named " + n));
+      if (t.padded.size() != 2)
+        return refuse(fail(MX_E_INVALID, n + ": GEMM operand is not two-dimensional"));
+      if (!t.logical.empty() && t.logical != t.padded)
+        return refuse(fail(MX_E_INVALID, n + ": logical and padded shapes differ; the GEMM "
+                                             "needs them equal (repack)"));
+      if (t.dtype == "I8" || t.dtype == "I4")
+        return refuse(fail(MX_E_UNSUPPORTED, n + ": " + t.dtype + " operand -- the int8 "
+                                                 "datapath is not built in this backend"));
+      if (t.dtype != "BF16" || !t.block_panel)
+        return refuse(fail(MX_E_INVALID, n + ": " + t.dtype + " without a block_panel "
+                                             "layout; a pre-tiled BF16 operand is wanted"));
+      const int64_t K = t.padded[0], N = t.padded[1];
+      if (t.nbytes != static_cast<uint64_t>(K * N * 2))
+        return refuse(fail(MX_E_INVALID, n + ": " + std::to_string(t.nbytes) + " bytes for a [" +
+                                             std::to_string(K) + "," + std::to_string(N) +
+                                             "] bf16 operand"));
+      rc = mx_encoder_set_panel(enc, n.c_str(), static_cast<const uint16_t *>(t.data), K, N,
+                                t.tile_k, t.tile_n, t.mac_s, t.mac_t);
+      if (rc) return refuse(rc);
+    }
+  if ((rc = mx_encoder_ready(enc))) return refuse(rc);
+  *out = enc;
+  return MX_OK;
+}
+
 }  // extern "C"

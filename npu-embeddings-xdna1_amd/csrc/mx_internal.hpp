@@ -56,4 +56,24 @@ int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t
 // Read and clear the stream's data-refusal flag (synchronises the stream).
 int take_data_error(mx_stream *s, int *flags);
 
+// A container tensor as the loaders use it (mx_npue.cpp).
+struct TensorRecView {
+  bool found = false, has_layout = false, block_panel = false;
+  std::string dtype;
+  std::vector<int64_t> padded, logical;
+  int64_t tile_k = 0, tile_n = 0, mac_s = 0, mac_t = 0;
+  const void *data = nullptr;
+  uint64_t nbytes = 0;
+};
+const TensorRecView npue_tensor(const mx_npue *f, const std::string &name);
+bool npue_config(const mx_npue *f, const std::string &key, std::string &out);
+// Check a block_panel tiling of a [K, N] operand; MX_OK or a refusal naming it.
+int check_panel(const std::string &what, int64_t K, int64_t N, int64_t tile_k, int64_t tile_n,
+                int64_t mac_s, int64_t mac_t);
+// Copy a pre-tiled bf16 [K, N] operand to the GPU and untile it into a new
+// [N, K] panel (synchronous).
+int stage_tiled_panel(mx_ctx *ctx, const uint16_t *panel_host, int64_t K, int64_t N,
+                      int64_t tile_k, int64_t tile_n, int64_t mac_s, int64_t mac_t,
+                      uint16_t **out);
+
 }  // namespace mx

@@ -49,6 +49,11 @@ struct GemmArgs {
   int64_t ldc;
 };
 hipError_t gemm(const GemmArgs &a, hipStream_t s);
+
+// Container operand tiled (tile_k, tile_n) with (mac_s, mac_t) sub-tiles ->
+// [N, K] panel (k_panel.hip). Shapes checked by the caller.
+hipError_t untile_panel(const uint16_t *panel, int64_t K, int64_t N, int tile_k, int tile_n,
+                        int mac_s, int mac_t, uint16_t *wt, hipStream_t s);
 // Tile configuration the launcher would pick (for tests and reports).
 const char *gemm_config_name(int64_t M, int64_t N, int64_t K);
 

@@ -57,6 +57,13 @@ class Timings(ctypes.Structure):
                 ("gemm_site_launches", _i64 * 4)]
 
 
+class NpueTensorInfo(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_char * 8), ("ndim", _int), ("padded_shape", _i64 * 4),
+                ("logical_shape", _i64 * 4), ("block_panel", _int), ("tile_k", _i64),
+                ("tile_n", _i64), ("mac_s", _i64), ("mac_t", _i64), ("data", _vp),
+                ("nbytes", ctypes.c_uint64)]
+
+
 # name -> (restype, argtypes); the complete exported surface of mx_encoder.h
 SIGNATURES = {
     "mx_last_error": (ctypes.c_char_p, []),
@@ -103,6 +110,17 @@ SIGNATURES = {
     "mx_encoder_whisper": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "mx_encoder_set_timing": (_int, [_vp, _int]),
     "mx_encoder_timings": (_int, [_vp, ctypes.POINTER(Timings)]),
+    "mx_npue_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "mx_npue_close": (None, [_vp]),
+    "mx_npue_config": (_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
+    "mx_npue_tensor_count": (_int, [_vp]),
+    "mx_npue_tensor_name": (ctypes.c_char_p, [_vp, _int]),
+    "mx_npue_tensor": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(NpueTensorInfo)]),
+    "mx_stage_weight_panel": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                                     ctypes.POINTER(_int)]),
+    "mx_encoder_set_panel": (_int, [_vp, ctypes.c_char_p, _vp, _i64, _i64, _i64, _i64, _i64,
+                                    _i64]),
+    "mx_encoder_from_npue": (_int, [_vp, _vp, ctypes.POINTER(_vp)]),
 }
 
 _lib = None
@@ -266,6 +284,54 @@ def from_bf16_bits(h):
     return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+# ---- the .npue container --------------------------------------------------------
+
+class Npue:
+    """A mapped .npue container (mx_npue_open); tensors are views of the mapping."""
+
+    def __init__(self, path):
+        h = _vp()
+        check(lib().mx_npue_open(str(path).encode(), ctypes.byref(h)))
+        self.handle = h.value
+
+    def config(self, key):
+        n = lib().mx_npue_config(self.handle, key.encode(), None, 0)
+        if n < 0:
+            check(n)
+        buf = ctypes.create_string_buffer(n + 1)
+        check(min(0, lib().mx_npue_config(self.handle, key.encode(), buf, n + 1)))
+        return buf.raw[:n].decode("utf-8")
+
+    def names(self):
+        return [lib().mx_npue_tensor_name(self.handle, i).decode()
+                for i in range(lib().mx_npue_tensor_count(self.handle))]
+
+    def info(self, name):
+        t = NpueTensorInfo()
+        check(lib().mx_npue_tensor(self.handle, name.encode(), ctypes.byref(t)))
+        return t
+
+    def bytes(self, name):
+        """The tensor's bytes, copied out of the mapping."""
+        t = self.info(name)
+        return ctypes.string_at(t.data, t.nbytes)
+
+    def close(self):
+        if self.handle:
+            lib().mx_npue_close(self.handle)
+            self.handle = None
+
+
+def stage_weight_panel(ctx, panel, K, N, tile_k, tile_n, mac_s, mac_t):
+    """A container's pre-tiled bf16 operand -> a context weight slot (untiled on
+    the GPU)."""
+    a = np.ascontiguousarray(panel, dtype=np.uint16)
+    slot = _int()
+    check(lib().mx_stage_weight_panel(ctx.handle, a.ctypes.data, K, N, tile_k, tile_n, mac_s,
+                                      mac_t, ctypes.byref(slot)))
+    return slot.value
+
+
 # ---- the encoder ---------------------------------------------------------------
 
 class Encoder:
@@ -333,6 +399,18 @@ class Encoder:
             self.set("conv2.bias", m["conv2_b"])
             self.set("position", m["pos"])
         check(lib().mx_encoder_ready(self.handle))
+
+    @classmethod
+    def from_npue(cls, ctx, npue):
+        """mx_encoder_from_npue: a BERT container straight from the mapping."""
+        self = cls.__new__(cls)
+        self.ctx, self.m = ctx, None
+        self.desc = EncoderDesc()
+        self.desc.hidden = int(npue.config("hidden"))
+        h = _vp()
+        check(lib().mx_encoder_from_npue(ctx.handle, npue.handle, ctypes.byref(h)))
+        self.handle = h.value
+        return self
 
     def set(self, name, arr):
         a = np.ascontiguousarray(arr)

@@ -222,6 +222,18 @@ void orc_vit_patches(const float *pixels, int64_t img, int64_t patch,
 void orc_head_matvec(const float *head, const float *bias, const float *cls_row,
                      int64_t d_model, int64_t num_labels, float *logits);
 
+/* ---- the .npue container's B panels --------------------------------------
+ * hostb::host_b_kn's untile (common/host_b.hpp:74-224, the BF16 branch of the
+ * loop at :206-243): a [K, N] operand stored as (tile_k, tile_n) tiles in k,n
+ * order, each tile as (mac_s, mac_t) sub-tiles, back to row-major [K, N] bf16
+ * bits (the widening to fp32 is orc_bf16_read). Returns 0, or -1 for a shape
+ * host_b_kn refuses (K % tile_k, N % tile_n, tile_k % mac_s, tile_n % mac_t,
+ * a non-positive dimension). Pinned bit-exact against oracle/_ref's
+ * host_b_kn reading the same container file, and as the exact inverse of the
+ * tiling written as reshapes and transposes (tools/lib/npue.py:491-556). */
+int orc_untile_b_panel(const uint16_t *panel, int64_t K, int64_t N, int64_t tile_k,
+                       int64_t tile_n, int64_t mac_s, int64_t mac_t, uint16_t *kn);
+
 #ifdef __cplusplus
 }
 #endif

@@ -410,3 +410,22 @@ void orc_head_matvec(const float *head, const float *bias, const float *cls_row,
     logits[j] = (float)acc;
   }
 }
+
+/* ---- hostb::host_b_kn's untile (host_b.hpp:206-243) ----------------------- */
+int orc_untile_b_panel(const uint16_t *panel, int64_t K, int64_t N, int64_t tile_k,
+                       int64_t tile_n, int64_t mac_s, int64_t mac_t, uint16_t *kn) {
+  if (K <= 0 || N <= 0 || tile_k <= 0 || tile_n <= 0 || mac_s <= 0 || mac_t <= 0) return -1;
+  if (K % tile_k || N % tile_n || tile_k % mac_s || tile_n % mac_t) return -1;
+  const int64_t kblocks = K / tile_k, nblocks = N / tile_n;
+  const int64_t rows = tile_k / mac_s, cols = tile_n / mac_t;
+  size_t src = 0; /* the container is read strictly in order */
+  for (int64_t bk = 0; bk < kblocks; ++bk)
+    for (int64_t bn = 0; bn < nblocks; ++bn)
+      for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+          for (int64_t si = 0; si < mac_s; ++si) {
+            uint16_t *dst = kn + (bk * tile_k + r * mac_s + si) * N + bn * tile_n + c * mac_t;
+            for (int64_t ti = 0; ti < mac_t; ++ti) dst[ti] = panel[src++];
+          }
+  return 0;
+}

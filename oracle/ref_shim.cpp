@@ -3,10 +3,14 @@
 //
 // Compiled by oracle/Makefile (target `ref`) directly against the headers in
 // the reference checkout (runtime/include/common/host_kernels.hpp,
-// runtime/include/common/conv_host.hpp) and runtime/src/pool.cpp; nothing of
-// the reference is copied here. The output lives in oracle/_ref/ only.
+// runtime/include/common/conv_host.hpp, runtime/include/common/host_b.hpp)
+// and runtime/src/pool.cpp and runtime/src/model.cpp (the .npue reader);
+// nothing of the reference is copied here. The output lives in oracle/_ref/
+// only.
 #include "common/conv_host.hpp"
+#include "common/host_b.hpp"
 #include "common/host_kernels.hpp"
+#include "runtime/model.hpp"
 #include "runtime/pool.hpp"
 
 #include <cstdint>
@@ -60,6 +64,84 @@ void ref_gemm_nt(const float *A, int64_t M, const float *B, int64_t K, int64_t N
                  const float *bias, float *C, int threads) {
   app::Pool pool(threads > 0 ? threads : 1);
   npue::hostconv::gemm_nt(A, M, B, K, N, bias, C, pool);
+}
+
+// ---- the .npue reader and B-panel untile (model.cpp, host_b.hpp) ----------
+// Each returns a negative value when the reference throws; *err (when given)
+// receives the exception text.
+static void put_err(const std::exception &e, char *err, size_t len) {
+  if (err && len) {
+    std::strncpy(err, e.what(), len - 1);
+    err[len - 1] = 0;
+  }
+}
+
+// hostb::host_b_kn(File(path), name): fp32 [K, N] into out (cap floats).
+long long ref_npue_host_b_kn(const char *path, const char *name, float *out, long long cap,
+                             char *err, size_t len) {
+  try {
+    npue::File f(path);
+    const std::vector<float> v = npue::hostb::host_b_kn(f, name);
+    if (static_cast<long long>(v.size()) > cap) return -2;
+    std::memcpy(out, v.data(), v.size() * sizeof(float));
+    return static_cast<long long>(v.size());
+  } catch (const std::exception &e) {
+    put_err(e, err, len);
+    return -1;
+  }
+}
+
+// File::config_string(key) into buf; its length, or -1.
+long long ref_npue_config(const char *path, const char *key, char *buf, size_t buflen,
+                          char *err, size_t len) {
+  try {
+    npue::File f(path);
+    const std::string v = f.config_string(key);
+    if (buf && buflen) {
+      const size_t n = v.size() < buflen - 1 ? v.size() : buflen - 1;
+      std::memcpy(buf, v.data(), n);
+      buf[n] = 0;
+    }
+    return static_cast<long long>(v.size());
+  } catch (const std::exception &e) {
+    put_err(e, err, len);
+    return -1;
+  }
+}
+
+// File(path) opens: 0, or -1 with the refusal in err.
+int ref_npue_open(const char *path, char *err, size_t len) {
+  try {
+    npue::File f(path);
+    return 0;
+  } catch (const std::exception &e) {
+    put_err(e, err, len);
+    return -1;
+  }
+}
+
+// File::info + File::raw: dtype, padded shape, layout numbers and the bytes.
+int ref_npue_tensor(const char *path, const char *name, char *dtype, int64_t *padded,
+                    int *ndim, int64_t *layout4, unsigned char *bytes, size_t cap,
+                    unsigned long long *nbytes) {
+  try {
+    npue::File f(path);
+    const npue::TensorInfo &t = f.info(name);
+    std::strncpy(dtype, t.dtype.c_str(), 7);
+    dtype[7] = 0;
+    *ndim = static_cast<int>(t.padded_shape.size());
+    for (size_t i = 0; i < t.padded_shape.size() && i < 4; ++i) padded[i] = t.padded_shape[i];
+    layout4[0] = t.tile_k;
+    layout4[1] = t.tile_n;
+    layout4[2] = t.mac_s;
+    layout4[3] = t.mac_t;
+    const npue::Span s = f.raw(name);
+    *nbytes = s.bytes;
+    if (bytes && s.bytes <= cap) std::memcpy(bytes, s.data, s.bytes);
+    return 0;
+  } catch (const std::exception &) {
+    return -1;
+  }
 }
 
 }  // extern "C"

@@ -80,6 +80,8 @@ def load():
         "orc_conv_front_end": (None, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _c_i64, _vp]),
         "orc_vit_patches": (None, [_vp, _c_i64, _c_i64, _vp]),
         "orc_head_matvec": (None, [_vp, _vp, _vp, _c_i64, _c_i64, _vp]),
+        "orc_untile_b_panel": (ctypes.c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                              _c_i64, _vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -102,6 +104,15 @@ def load_ref():
         "ref_exp2_avx2": (None, [_vp, _vp, ctypes.c_size_t]),
         "ref_hsum8": (ctypes.c_float, [_vp]),
         "ref_gemm_nt": (None, [_vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, ctypes.c_int]),
+        "ref_npue_host_b_kn": (ctypes.c_longlong, [ctypes.c_char_p, ctypes.c_char_p, _vp,
+                                                   ctypes.c_longlong, ctypes.c_char_p,
+                                                   ctypes.c_size_t]),
+        "ref_npue_config": (ctypes.c_longlong, [ctypes.c_char_p, ctypes.c_char_p,
+                                                ctypes.c_char_p, ctypes.c_size_t,
+                                                ctypes.c_char_p, ctypes.c_size_t]),
+        "ref_npue_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
+        "ref_npue_tensor": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+                                           _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)

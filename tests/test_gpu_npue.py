@@ -1,0 +1,128 @@
+"""The .npue container on the GPU: pre-tiled bf16 operands untiled by the GPU
+kernel land exactly where the host untile puts them, and an encoder built
+straight from a BERT container computes bit for bit what the same weights
+given tensor by tensor compute (whose parity with the host path
+test_gpu_encoder pins)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import mxenc
+import npue_writer as nw
+from mxenc import synth
+from orc import P
+from test_gpu_encoder import COS_MIN, cosines, gpu_embed, oracle_embed
+
+pytestmark = pytest.mark.gpu
+
+TILINGS = [(768, 2304, 64, 48, 8, 4), (3072, 768, 64, 64, 8, 8), (384, 1152, 32, 32, 4, 8),
+           (1024, 96, 128, 96, 8, 8)]
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = mxenc.Context(0)
+    yield c
+    c.close()
+
+
+def _gemm_slot(ctx, A, M, K, slot, N, bias):
+    C = ctx.empty((M, N), np.float32)
+    mxenc.check(mxenc.lib().mx_gemm(ctx.stream, A.p, M, K, K, slot, bias.p, mxenc.MX_EPI_NONE,
+                                    None, C.p, mxenc.MX_F32, N))
+    return C.host()
+
+
+@pytest.mark.parametrize("K,N,tk,tn,s,t", TILINGS)
+def test_panel_staging_equals_row_major_staging(ctx, orc, K, N, tk, tn, s, t):
+    """mx_stage_weight_panel (container bytes, untiled on the GPU) and
+    mx_stage_weight (row-major) of the same operand give bit-identical GEMMs,
+    and the untiled operand is the oracle's untile of the same bytes."""
+    rng = np.random.default_rng(K + N + tk)
+    W = (rng.standard_normal((K, N)) * 0.05).astype(np.float32)
+    bits = nw.to_bf16_bits(W)
+    panel = nw.tile_panel(bits, tk, tn, s, t)
+    kn = np.zeros_like(bits)
+    assert orc.orc_untile_b_panel(P(panel), K, N, tk, tn, s, t, P(kn)) == 0
+    assert np.array_equal(kn, bits)
+    sp = mxenc.stage_weight_panel(ctx, panel, K, N, tk, tn, s, t)
+    sr = ctypes.c_int()
+    mxenc.check(mxenc.lib().mx_stage_weight(ctx.handle, bits.ctypes.data, mxenc.MX_BF16, K, N,
+                                            ctypes.byref(sr)))
+    M = 512
+    A = ctx.put(nw.to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32)))
+    bias = ctx.put((rng.standard_normal(N) * 0.1).astype(np.float32))
+    a = _gemm_slot(ctx, A, M, K, sp, N, bias)
+    b = _gemm_slot(ctx, A, M, K, sr.value, N, bias)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    mxenc.check(mxenc.lib().mx_release_weight(ctx.handle, sp))
+    mxenc.check(mxenc.lib().mx_release_weight(ctx.handle, sr.value))
+
+
+def test_panel_staging_refusals(ctx):
+    panel = np.zeros(64 * 96, np.uint16)
+    with pytest.raises(mxenc.MxError, match="does not tile"):
+        mxenc.stage_weight_panel(ctx, panel, 64, 96, 64, 64, 8, 8)
+    with pytest.raises(mxenc.MxError, match="does not tile"):
+        mxenc.stage_weight_panel(ctx, panel, 64, 96, 64, 48, 6, 4)
+    with pytest.raises(mxenc.MxError, match="64 KB of LDS"):
+        mxenc.stage_weight_panel(ctx, np.zeros(512 * 512, np.uint16), 512, 512, 512, 512, 8, 8)
+
+
+@pytest.mark.parametrize("tiling,cls_pool", [((64, 48, (8, 4)), False), ((32, 64, (4, 8)), True)])
+def test_encoder_from_npue_is_bitwise_the_set_encoder(tmp_path, ctx, orc, tiling, cls_pool):
+    m = synth.make_model("minilm", layers=2, ln_random=True, cls_pool=cls_pool)
+    tk, tn, mac = tiling
+    path = str(tmp_path / "minilm.npue")
+    nw.bert_container(m, tk, tn, mac).write(path)
+    f = mxenc.Npue(path)
+    a_enc = mxenc.Encoder.from_npue(ctx, f)
+    b_enc = mxenc.Encoder(ctx, m)
+    ids, am, lens = synth.make_text_inputs(m, batch=8)
+    a = gpu_embed(ctx, a_enc, ids, am)
+    b = gpu_embed(ctx, b_enc, ids, am)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    want, _ = oracle_embed(orc, m, ids, am)
+    assert np.min(cosines(a, want)) >= COS_MIN
+    a_enc.close()
+    b_enc.close()
+    f.close()
+
+
+@pytest.mark.parametrize("over,why", [
+    (dict(arch="nomic_bert_rope_swiglu"), "RoPE and gated-FFN archs"),
+    (dict(gemm_layout="host"), "gemm_layout \"host\""),
+    (dict(pooling="max"), "unknown pooling mode 'max'"),
+])
+def test_encoder_from_npue_refusals(tmp_path, ctx, over, why):
+    m = synth.make_model("minilm", layers=1)
+    path = str(tmp_path / "bad.npue")
+    arch = over.pop("arch", "bert_abs_gelu_postln")
+    nw.bert_container(m, 64, 64, (8, 8), arch=arch, extra_config=over).write(path)
+    f = mxenc.Npue(path)
+    with pytest.raises(mxenc.MxError, match=why):
+        mxenc.Encoder.from_npue(ctx, f)
+    f.close()
+
+
+def test_encoder_from_npue_refuses_int8_and_missing_tensors(tmp_path, ctx):
+    m = synth.make_model("minilm", layers=1)
+    c = nw.bert_container(m, 64, 64, (8, 8))
+    for e in c.entries:
+        if e["name"] == "layer.0.attn_out":
+            e["dtype"] = "I8"
+    path = str(tmp_path / "i8.npue")
+    c.write(path)
+    f = mxenc.Npue(path)
+    with pytest.raises(mxenc.MxError, match="int8 datapath"):
+        mxenc.Encoder.from_npue(ctx, f)
+    f.close()
+    c = nw.bert_container(m, 64, 64, (8, 8))
+    c.entries = [e for e in c.entries if e["name"] != "layer.0.ln2.bias"]
+    path = str(tmp_path / "missing.npue")
+    c.write(path)
+    f = mxenc.Npue(path)
+    with pytest.raises(mxenc.MxError, match="no tensor named layer.0.ln2.bias"):
+        mxenc.Encoder.from_npue(ctx, f)
+    f.close()
