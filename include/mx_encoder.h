@@ -265,6 +265,11 @@ typedef enum { MX_FRONT_NONE = 0, MX_FRONT_VIT = 1, MX_FRONT_WHISPER = 2 } mx_fr
 int mx_encoder_create(mx_ctx *ctx, const mx_encoder_desc *desc,
                       mx_encoder **out);
 void mx_encoder_destroy(mx_encoder *enc);
+/* A --pipeline lane's encoder (run_setup.hpp:778-874): the same weights,
+ * borrowed from a ready `enc`, with a workspace of its own, so lanes on
+ * different streams run concurrently. It must be destroyed before `enc`;
+ * setting a tensor on it is refused (the weights are the parent's). */
+int mx_encoder_clone(mx_encoder *enc, mx_encoder **out);
 int mx_encoder_set(mx_encoder *enc, const char *name, const void *host,
                    int dtype, int64_t count);
 /* Every tensor the architecture needs has been set: MX_OK, else MX_E_STATE
@@ -328,6 +333,24 @@ typedef struct {
 } mx_timings;
 int mx_encoder_set_timing(mx_encoder *enc, int on);
 int mx_encoder_timings(mx_encoder *enc, mx_timings *out);
+
+/* ---- the embedding service ----------------------------------------------
+ * EmbedService::embed (runtime/src/server/embed_service.cpp:12-108) minus the
+ * tokenizer: n sequences of token ids (host int32 [n, seq]) and their 1/0
+ * attention masks (host fp32 [n, seq]) -> pooled rows (host fp32
+ * [n, hidden]). The request is cut into chunks of `batch` sequences (plan(),
+ * :12-27), taken by `lanes` workers -- each a thread with its own stream,
+ * device buffers and encoder clone -- and each chunk is chunk() (:29-64):
+ * embedding sum, the encoder, pooling, into its rows of out_host. The first
+ * failing chunk stops the rest and its refusal is returned (:80-92). Results
+ * do not depend on the lane count or the chunk size. One call at a time per
+ * service; `enc` must outlive it. */
+typedef struct mx_embed_service mx_embed_service;
+int mx_embed_service_create(mx_encoder *enc, int lanes, int64_t batch, int64_t seq,
+                            mx_embed_service **out);
+void mx_embed_service_destroy(mx_embed_service *svc);
+int mx_embed_service_embed(mx_embed_service *svc, const int32_t *ids_host,
+                           const float *mask_host, int64_t n, float *out_host);
 
 /* ---- the .npue weight container ------------------------------------------
  * npue::File (runtime/include/runtime/model.hpp, runtime/src/model.cpp:

@@ -27,7 +27,7 @@ FLAGS = [
     "-I", os.path.join(HERE, "..", "include"),
 ]
 SOURCES = ["k_elem.hip", "k_gemm.hip", "k_gemm_lds.hip", "k_attn.hip", "k_front.hip",
-           "k_panel.hip", "mx_abi.cpp", "mx_encoder.cpp", "mx_npue.cpp"]
+           "k_panel.hip", "mx_abi.cpp", "mx_encoder.cpp", "mx_npue.cpp", "mx_service.cpp"]
 
 
 def _compile(src):

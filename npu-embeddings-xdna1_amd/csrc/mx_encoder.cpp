@@ -28,6 +28,11 @@ std::set<std::string> placed_ops();
 
 using namespace mx;
 
+namespace mx {
+mx_ctx *encoder_ctx(const mx_encoder *enc);
+int64_t encoder_hidden(const mx_encoder *enc);
+}  // namespace mx
+
 namespace {
 
 struct LayerW {
@@ -45,6 +50,7 @@ enum Site { SITE_QKV = 0, SITE_AO = 1, SITE_UP = 2, SITE_DOWN = 3 };
 struct mx_encoder {
   mx_ctx *ctx = nullptr;
   mx_encoder_desc desc{};
+  bool owns_weights = true;  // false for a lane clone, which borrows its parent's
   std::vector<LayerW> layers;
   float *emb_ln[2] = {nullptr, nullptr};
   float *fin_ln[2] = {nullptr, nullptr};
@@ -363,16 +369,26 @@ int mx_encoder_create(mx_ctx *ctx, const mx_encoder_desc *desc, mx_encoder **out
 void mx_encoder_destroy(mx_encoder *enc) {
   if (!enc) return;
   if (use_device(enc->ctx) == MX_OK) {
-    for (auto &l : enc->layers) {
-      for (auto &p : l.w) free_dev(p);
-      for (auto &p : l.b) free_dev(p);
-      for (auto &p : l.ln) free_dev(p);
+    if (enc->owns_weights) {
+      for (auto &l : enc->layers) {
+        for (auto &p : l.w) free_dev(p);
+        for (auto &p : l.b) free_dev(p);
+        for (auto &p : l.ln) free_dev(p);
+      }
+      for (auto &p : enc->emb_ln) free_dev(p);
+      for (auto &p : enc->fin_ln) free_dev(p);
+      free_dev(enc->word);
+      free_dev(enc->pos);
+      free_dev(enc->type);
+      free_dev(enc->patch_w);
+      free_dev(enc->head_w);
+      free_dev(enc->patch_b);
+      free_dev(enc->head_b);
+      for (auto &p : enc->conv_w) free_dev(p);
+      for (auto &p : enc->conv_b) free_dev(p);
+      free_dev(enc->cls_tok);
+      free_dev(enc->front_pos);
     }
-    for (auto &p : enc->emb_ln) free_dev(p);
-    for (auto &p : enc->fin_ln) free_dev(p);
-    free_dev(enc->word);
-    free_dev(enc->pos);
-    free_dev(enc->type);
     free_dev(enc->xb);
     free_dev(enc->qkv);
     free_dev(enc->ctxb);
@@ -381,14 +397,6 @@ void mx_encoder_destroy(mx_encoder *enc) {
     free_dev(enc->emb);
     free_dev(enc->add_mask);
     free_dev(enc->kv_len);
-    free_dev(enc->patch_w);
-    free_dev(enc->head_w);
-    free_dev(enc->patch_b);
-    free_dev(enc->head_b);
-    for (auto &p : enc->conv_w) free_dev(p);
-    for (auto &p : enc->conv_b) free_dev(p);
-    free_dev(enc->cls_tok);
-    free_dev(enc->front_pos);
     free_dev(enc->f_rows);
     free_dev(enc->f_cls);
     free_dev(enc->f_mel);
@@ -402,10 +410,50 @@ void mx_encoder_destroy(mx_encoder *enc) {
   delete enc;
 }
 
+}  // extern "C"
+
+mx_ctx *mx::encoder_ctx(const mx_encoder *enc) { return enc->ctx; }
+int64_t mx::encoder_hidden(const mx_encoder *enc) { return enc->desc.hidden; }
+
+extern "C" {
+
+int mx_encoder_clone(mx_encoder *enc, mx_encoder **out) {
+  clear_error();
+  if (!enc || !out) return fail(MX_E_INVALID, "encoder_clone: null argument");
+  *out = nullptr;
+  int rc = mx_encoder_ready(enc);
+  if (rc) return rc;
+  auto *c = new mx_encoder();
+  c->ctx = enc->ctx;
+  c->desc = enc->desc;
+  c->owns_weights = false;
+  c->layers = enc->layers;
+  for (int i = 0; i < 2; ++i) {
+    c->emb_ln[i] = enc->emb_ln[i];
+    c->fin_ln[i] = enc->fin_ln[i];
+    c->conv_w[i] = enc->conv_w[i];
+    c->conv_b[i] = enc->conv_b[i];
+  }
+  c->word = enc->word;
+  c->pos = enc->pos;
+  c->type = enc->type;
+  c->patch_w = enc->patch_w;
+  c->head_w = enc->head_w;
+  c->patch_b = enc->patch_b;
+  c->head_b = enc->head_b;
+  c->cls_tok = enc->cls_tok;
+  c->front_pos = enc->front_pos;
+  *out = c;
+  return MX_OK;
+}
+
 int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dtype,
                    int64_t count) {
   clear_error();
   if (!enc || !name_c || !host) return fail(MX_E_INVALID, "encoder_set: null argument");
+  if (!enc->owns_weights)
+    return fail(MX_E_STATE, "encoder_set: a lane clone borrows its parent's weights; set them "
+                            "on the parent");
   int rc = use_device(enc->ctx);
   if (rc) return rc;
   const std::string name(name_c);
@@ -774,6 +822,8 @@ int mx_encoder_set_panel(mx_encoder *enc, const char *name_c, const uint16_t *pa
                          int64_t mac_t) {
   clear_error();
   if (!enc || !name_c || !panel) return fail(MX_E_INVALID, "encoder_set_panel: null argument");
+  if (!enc->owns_weights)
+    return fail(MX_E_STATE, "encoder_set_panel: a lane clone borrows its parent's weights");
   const std::string name(name_c);
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
   uint16_t **dst = nullptr;

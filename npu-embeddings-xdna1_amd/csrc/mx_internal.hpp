@@ -56,6 +56,10 @@ int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t
 // Read and clear the stream's data-refusal flag (synchronises the stream).
 int take_data_error(mx_stream *s, int *flags);
 
+// The context and width of an encoder (for mx_service.cpp).
+mx_ctx *encoder_ctx(const mx_encoder *enc);
+int64_t encoder_hidden(const mx_encoder *enc);
+
 // A container tensor as the loaders use it (mx_npue.cpp).
 struct TensorRecView {
   bool found = false, has_layout = false, block_panel = false;

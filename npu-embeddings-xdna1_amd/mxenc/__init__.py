@@ -121,6 +121,10 @@ SIGNATURES = {
     "mx_encoder_set_panel": (_int, [_vp, ctypes.c_char_p, _vp, _i64, _i64, _i64, _i64, _i64,
                                     _i64]),
     "mx_encoder_from_npue": (_int, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "mx_encoder_clone": (_int, [_vp, ctypes.POINTER(_vp)]),
+    "mx_embed_service_create": (_int, [_vp, _int, _i64, _i64, ctypes.POINTER(_vp)]),
+    "mx_embed_service_destroy": (None, [_vp]),
+    "mx_embed_service_embed": (_int, [_vp, _vp, _vp, _i64, _vp]),
 }
 
 _lib = None
@@ -443,4 +447,28 @@ class Encoder:
     def close(self):
         if self.handle:
             lib().mx_encoder_destroy(self.handle)
+            self.handle = None
+
+
+class EmbedService:
+    """mx_embed_service over a ready Encoder: host ids/masks in, pooled rows out."""
+
+    def __init__(self, enc, lanes, batch, seq):
+        self.enc, self.seq, self.hidden = enc, seq, int(enc.desc.hidden)
+        h = _vp()
+        check(lib().mx_embed_service_create(enc.handle, lanes, batch, seq, ctypes.byref(h)))
+        self.handle = h.value
+
+    def embed(self, ids, mask):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        mask = np.ascontiguousarray(mask, dtype=np.float32)
+        assert ids.shape == mask.shape and ids.shape[1] == self.seq
+        out = np.zeros((ids.shape[0], self.hidden), np.float32)
+        check(lib().mx_embed_service_embed(self.handle, ids.ctypes.data, mask.ctypes.data,
+                                           ids.shape[0], out.ctypes.data))
+        return out
+
+    def close(self):
+        if self.handle:
+            lib().mx_embed_service_destroy(self.handle)
             self.handle = None

@@ -1,0 +1,80 @@
+"""The embedding service (mx_embed_service, EmbedService::embed minus the
+tokenizer) on the GPU: chunks over lanes give exactly the rows one encoder
+call over the whole request gives, whatever the lane count and chunk size,
+and the first failing chunk's refusal is the call's."""
+import numpy as np
+import pytest
+
+import mxenc
+from mxenc import synth
+from test_gpu_encoder import COS_MIN, cosines, gpu_embed, oracle_embed
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = mxenc.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def model():
+    return synth.make_model("minilm", layers=2, ln_random=True)
+
+
+@pytest.fixture(scope="module")
+def enc(ctx, model):
+    e = mxenc.Encoder(ctx, model)
+    yield e
+    e.close()
+
+
+@pytest.mark.parametrize("lanes,batch", [(1, 8), (3, 8), (4, 5), (2, 64)])
+def test_service_rows_equal_one_call(ctx, model, enc, orc, lanes, batch):
+    ids, am, _ = synth.make_text_inputs(model, batch=37)
+    want = gpu_embed(ctx, enc, ids, am)
+    svc = mxenc.EmbedService(enc, lanes, batch, ids.shape[1])
+    got = svc.embed(ids, am)
+    svc.close()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    if lanes == 3:
+        ref, _ = oracle_embed(orc, model, ids[:6].copy(), am[:6].copy())
+        assert np.min(cosines(got[:6], ref)) >= COS_MIN
+
+
+def test_service_repeated_calls_and_empty_request(ctx, model, enc):
+    ids, am, _ = synth.make_text_inputs(model, batch=20)
+    svc = mxenc.EmbedService(enc, 3, 4, ids.shape[1])
+    a = svc.embed(ids, am)
+    b = svc.embed(ids, am)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert svc.embed(ids[:0], am[:0]).shape == (0, model["hidden"])
+    svc.close()
+
+
+def test_service_first_error_is_the_calls(ctx):
+    m = synth.make_model("minilm", layers=1, cls_pool=True)
+    e = mxenc.Encoder(ctx, m)
+    ids, am, _ = synth.make_text_inputs(m, batch=24)
+    am[13, 0] = 0.0  # CLS pooling refuses a sequence whose first token is masked
+    svc = mxenc.EmbedService(e, 3, 4, ids.shape[1])
+    with pytest.raises(mxenc.MxError, match="first token is masked"):
+        svc.embed(ids, am)
+    am[13, 0] = 1.0
+    assert np.all(np.isfinite(svc.embed(ids, am)))  # the service recovers
+    svc.close()
+    e.close()
+
+
+def test_service_and_clone_refusals(ctx, enc):
+    with pytest.raises(mxenc.MxError, match="lanes must be 1..64"):
+        mxenc.EmbedService(enc, 0, 8, 128)
+    import ctypes
+    h = ctypes.c_void_p()
+    mxenc.check(mxenc.lib().mx_encoder_clone(enc.handle, ctypes.byref(h)))
+    a = np.zeros(8, np.float32)
+    rc = mxenc.lib().mx_encoder_set(h.value, b"layer.0.ln1.bias", a.ctypes.data, mxenc.MX_F32, 8)
+    assert rc == -4 and b"borrows" in mxenc.lib().mx_last_error()
+    mxenc.lib().mx_encoder_destroy(h.value)
