@@ -222,6 +222,48 @@ void orc_vit_patches(const float *pixels, int64_t img, int64_t patch,
 void orc_head_matvec(const float *head, const float *bias, const float *cls_row,
                      int64_t d_model, int64_t num_labels, float *logits);
 
+/* ---- int8 W8A8: the array datapath's host halves --------------------------
+ * quantise_a_int8 (host_kernels.hpp:263-320): per row, mx = max_j |a*ias|,
+ * sc = mx > 0 ? mx/127 : 1, q = rint(clamp((a*ias)*(1/sc), -127, 127)) (the
+ * AVX2 order: two rounded multiplies, clamp, nearest-even; the scalar tail
+ * rounds before clamping, which gives the same integer). a_scale[r] = sc.
+ * Pinned bit-exact against oracle/_ref's quantise_a_int8.
+ * gemm_i8: C[M,N] = sum_k Aq[m,k] * Wq[k,n] in exact integer arithmetic (the
+ * AIE int8 MMAC accumulates int32 exactly, tools/lib/gemm_i8.py:54-57; K*127^2
+ * < 2^31 keeps it exact). Pinned against a 64-bit integer product.
+ * dequantise_c (host_kernels.hpp:529-600, the int32-C AVX2 form):
+ * out = fma(float(C) * sa[r], wscale[n], bias[n]). Pinned bit-exact against
+ * oracle/_ref's dequantise_c.
+ * gemm_i8_dequant: quantise -> gemm_i8 -> dequantise_c, the array branch of
+ * BertEncoder::gemm (bert_encoder.cpp:741-924) for an int8 design. */
+void orc_quantise_a_int8(const float *a, int64_t rows, int64_t K, const float *ias,
+                         int8_t *q, float *a_scale);
+void orc_gemm_i8(const int8_t *Aq, int64_t M, int64_t K, const int8_t *Wq, int64_t N,
+                 int32_t *C);
+void orc_dequantise_c(const int32_t *C, int64_t rows, int64_t N, const float *a_scale,
+                      const float *wscale, const float *bias, float *out);
+void orc_gemm_i8_dequant(const float *A, int64_t M, int64_t K, const float *ias,
+                         const int8_t *Wq, const float *wscale, const float *bias,
+                         int64_t N, float *out);
+
+/* The int8 operands of a BERT stack: per layer and GEMM (qkv, attn_out,
+ * ffn_up, ffn_down) the [K, N] int8 weight, its [N] column scale and the [K]
+ * reciprocal smoothing 1/asmooth (the reference reciprocates once, :764-772). */
+typedef struct {
+  const int8_t *wq[4];        /* each [layers][K*N]                         */
+  const float *wscale[4];     /* each [layers][N]                           */
+  const float *ias[4];        /* each [layers][K]                           */
+} orc_i8_operands;
+
+/* BertEncoder::run on an int8 container with gemm on the array and every
+ * other op on the host, unfused (bert_encoder.cpp:1419-1598 with
+ * fuse_ffn_epilogue off): each GEMM is gemm_i8_dequant; attention, GELU and
+ * LayerNorm as orc_bert_run. The fused forms (add_norm_quant :1197-1300,
+ * dequant_act_quant host_kernels.hpp:405-500) compute the same values in
+ * one pass: LayerNorm then quantise, dequantise then GELU then quantise. */
+void orc_bert_run_i8(const orc_encoder *m, const orc_i8_operands *q, float *x_io,
+                     const float *add_mask, int64_t B, int64_t S, int64_t layers_to_run);
+
 /* ---- the .npue container's B panels --------------------------------------
  * hostb::host_b_kn's untile (common/host_b.hpp:74-224, the BF16 branch of the
  * loop at :206-243): a [K, N] operand stored as (tile_k, tile_n) tiles in k,n

@@ -49,6 +49,51 @@ void orc_bert_run(const orc_encoder *m, float *x, const float *add_mask,
   free(residual);
 }
 
+/* BertEncoder::run on an int8 container, the GEMMs on the array
+ * (bert_encoder.cpp:741-924 int8 branch), everything else on the host. */
+void orc_bert_run_i8(const orc_encoder *m, const orc_i8_operands *q, float *x,
+                     const float *add_mask, int64_t B, int64_t S, int64_t layers_to_run) {
+  const int64_t d = m->hidden, f = m->ffn, H = m->heads, hd = m->head_dim;
+  const int64_t rows = B * S;
+  const int64_t L = layers_to_run < 0 || layers_to_run > m->layers ? m->layers
+                                                                   : layers_to_run;
+  const float eps = 1e-12f;
+  const int64_t Ks[4] = {d, d, d, f}, Ns[4] = {3 * d, d, f, d};
+  float *qkv = falloc((size_t)(rows * 3 * d));
+  float *scores = falloc((size_t)(B * H * S * S));
+  float *ctx = falloc((size_t)(rows * d));
+  float *proj = falloc((size_t)(rows * d));
+  float *up = falloc((size_t)(rows * f));
+  float *residual = falloc((size_t)(rows * d));
+#define GEMM_I8(i, A, bias, out)                                                        \
+  orc_gemm_i8_dequant((A), rows, Ks[i], q->ias[i] + l * Ks[i], q->wq[i] + l * Ks[i] * Ns[i], \
+                      q->wscale[i] + l * Ns[i], (bias), Ns[i], (out))
+  orc_layer_norm_rows(x, rows, d, m->emb_ln_g, m->emb_ln_b, eps);
+  for (int64_t l = 0; l < L; ++l) {
+    memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
+    GEMM_I8(0, x, m->b_qkv + l * 3 * d, qkv);
+    orc_qk(qkv, B, S, H, hd, scores);
+    orc_softmax_rows_poly(scores, B * H * S, S, add_mask, H * S);
+    orc_av(scores, qkv, B, S, H, hd, ctx);
+    GEMM_I8(1, ctx, m->b_ao + l * d, proj);
+    orc_add_into(x, proj, residual, (size_t)(rows * d));
+    orc_layer_norm_rows(x, rows, d, m->ln1_g + l * d, m->ln1_b + l * d, eps);
+    memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
+    GEMM_I8(2, x, m->b_up + l * f, up);
+    orc_gelu_poly_inplace(up, (size_t)(rows * f));
+    GEMM_I8(3, up, m->b_down + l * d, proj);
+    orc_add_into(x, proj, residual, (size_t)(rows * d));
+    orc_layer_norm_rows(x, rows, d, m->ln2_g + l * d, m->ln2_b + l * d, eps);
+  }
+#undef GEMM_I8
+  free(qkv);
+  free(scores);
+  free(ctx);
+  free(proj);
+  free(up);
+  free(residual);
+}
+
 /* VitEncoder::run (vit/encoder.cpp:347-431) / WhisperEncoder::run
  * (whisper/encoder.cpp:156-213) body, host branch: pre-LN, the whole
  * sequence in one chunk (chunking by the design's rows does not change a

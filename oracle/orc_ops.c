@@ -429,3 +429,100 @@ int orc_untile_b_panel(const uint16_t *panel, int64_t K, int64_t N, int64_t tile
           }
   return 0;
 }
+
+/* ---- int8 W8A8 (host_kernels.hpp:263-320, 529-600) ------------------------ */
+typedef struct {
+  const float *a, *ias;
+  int8_t *q;
+  float *sc;
+  int64_t rows, K;
+} quant_task;
+
+static void quant_worker(void *p, int w, int nw) {
+  const quant_task *t = (const quant_task *)p;
+  for (int64_t r = w; r < t->rows; r += nw) {
+    const float *x = t->a + r * t->K;
+    int8_t *q = t->q + r * t->K;
+    float mx = 0.0f;
+    for (int64_t j = 0; j < t->K; ++j) {
+      const float v = fabsf(x[j] * t->ias[j]);
+      if (v > mx) mx = v;
+    }
+    const float sc = mx > 0.0f ? mx / 127.0f : 1.0f;
+    t->sc[r] = sc;
+    const float inv = 1.0f / sc;
+    for (int64_t j = 0; j < t->K; ++j) {
+      float v = (x[j] * t->ias[j]) * inv;
+      v = v < -127.0f ? -127.0f : (v > 127.0f ? 127.0f : v);
+      q[j] = (int8_t)nearbyintf(v);
+    }
+  }
+}
+
+void orc_quantise_a_int8(const float *a, int64_t rows, int64_t K, const float *ias,
+                         int8_t *q, float *a_scale) {
+  quant_task t = {a, ias, q, a_scale, rows, K};
+  orc_run(quant_worker, &t);
+}
+
+typedef struct {
+  const int8_t *A, *W;
+  int32_t *C;
+  int64_t M, K, N;
+} gemm_i8_task;
+
+static void gemm_i8_worker(void *p, int w, int nw) {
+  const gemm_i8_task *t = (const gemm_i8_task *)p;
+  for (int64_t m = w; m < t->M; m += nw) {
+    int32_t *c = t->C + m * t->N;
+    for (int64_t n = 0; n < t->N; ++n) c[n] = 0;
+    const int8_t *a = t->A + m * t->K;
+    for (int64_t k = 0; k < t->K; ++k) {
+      const int32_t av = a[k];
+      const int8_t *wr = t->W + k * t->N;
+      for (int64_t n = 0; n < t->N; ++n) c[n] += av * (int32_t)wr[n];
+    }
+  }
+}
+
+void orc_gemm_i8(const int8_t *Aq, int64_t M, int64_t K, const int8_t *Wq, int64_t N,
+                 int32_t *C) {
+  gemm_i8_task t = {Aq, Wq, C, M, K, N};
+  orc_run(gemm_i8_worker, &t);
+}
+
+typedef struct {
+  const int32_t *C;
+  const float *sa, *ws, *bias;
+  float *out;
+  int64_t rows, N;
+} deq_task;
+
+static void deq_worker(void *p, int w, int nw) {
+  const deq_task *t = (const deq_task *)p;
+  for (int64_t r = w; r < t->rows; r += nw) {
+    const float sa = t->sa[r];
+    for (int64_t n = 0; n < t->N; ++n)
+      t->out[r * t->N + n] = fmaf((float)t->C[r * t->N + n] * sa, t->ws[n], t->bias[n]);
+  }
+}
+
+void orc_dequantise_c(const int32_t *C, int64_t rows, int64_t N, const float *a_scale,
+                      const float *wscale, const float *bias, float *out) {
+  deq_task t = {C, a_scale, wscale, bias, out, rows, N};
+  orc_run(deq_worker, &t);
+}
+
+void orc_gemm_i8_dequant(const float *A, int64_t M, int64_t K, const float *ias,
+                         const int8_t *Wq, const float *wscale, const float *bias,
+                         int64_t N, float *out) {
+  int8_t *q = (int8_t *)malloc((size_t)(M * K));
+  float *sa = (float *)malloc((size_t)M * sizeof(float));
+  int32_t *c = (int32_t *)malloc((size_t)(M * N) * sizeof(int32_t));
+  orc_quantise_a_int8(A, M, K, ias, q, sa);
+  orc_gemm_i8(q, M, K, Wq, N, c);
+  orc_dequantise_c(c, M, N, sa, wscale, bias, out);
+  free(q);
+  free(sa);
+  free(c);
+}

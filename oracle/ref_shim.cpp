@@ -66,6 +66,27 @@ void ref_gemm_nt(const float *A, int64_t M, const float *B, int64_t K, int64_t N
   npue::hostconv::gemm_nt(A, M, B, K, N, bias, C, pool);
 }
 
+// ---- int8: quantise_a_int8 and dequantise_c (host_kernels.hpp:263-320,
+// 529-600), rows serially --------------------------------------------------
+static auto serial_rows = [](int64_t n, auto f) { f(0, n); };
+
+void ref_quantise_a_int8(const float *a, int64_t rows, int64_t K, const float *ias, int8_t *q,
+                         float *a_scale) {
+  app::quantise_a_int8(a, rows, K, ias, q, a_scale, serial_rows);
+}
+
+// C must be 32-byte aligned with 32-byte rows (the reference's streaming
+// loads require it and refuse otherwise): 0, or -1 when refused.
+int ref_dequantise_c(const int32_t *c, int64_t rows, int64_t N, const float *a_scale,
+                     const float *wscale, const float *bias, float *out) {
+  try {
+    app::dequantise_c(c, 4, rows, N, a_scale, wscale, bias, out, serial_rows);
+    return 0;
+  } catch (const std::exception &) {
+    return -1;
+  }
+}
+
 // ---- the .npue reader and B-panel untile (model.cpp, host_b.hpp) ----------
 // Each returns a negative value when the reference throws; *err (when given)
 // receives the exception text.

@@ -32,6 +32,10 @@ class OrcEncoder(ctypes.Structure):
                            "emb_ln_g", "emb_ln_b", "fin_ln_g", "fin_ln_b")]
 
 
+class OrcI8(ctypes.Structure):
+    _fields_ = [("wq", _vp * 4), ("wscale", _vp * 4), ("ias", _vp * 4)]
+
+
 _lib = None
 
 
@@ -82,6 +86,12 @@ def load():
         "orc_head_matvec": (None, [_vp, _vp, _vp, _c_i64, _c_i64, _vp]),
         "orc_untile_b_panel": (ctypes.c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                               _c_i64, _vp]),
+        "orc_quantise_a_int8": (None, [_vp, _c_i64, _c_i64, _vp, _vp, _vp]),
+        "orc_gemm_i8": (None, [_vp, _c_i64, _c_i64, _vp, _c_i64, _vp]),
+        "orc_dequantise_c": (None, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
+        "orc_gemm_i8_dequant": (None, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _c_i64, _vp]),
+        "orc_bert_run_i8": (None, [ctypes.POINTER(OrcEncoder), ctypes.POINTER(OrcI8), _vp, _vp,
+                                   _c_i64, _c_i64, _c_i64]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -104,6 +114,8 @@ def load_ref():
         "ref_exp2_avx2": (None, [_vp, _vp, ctypes.c_size_t]),
         "ref_hsum8": (ctypes.c_float, [_vp]),
         "ref_gemm_nt": (None, [_vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, ctypes.c_int]),
+        "ref_quantise_a_int8": (None, [_vp, _c_i64, _c_i64, _vp, _vp, _vp]),
+        "ref_dequantise_c": (ctypes.c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
         "ref_npue_host_b_kn": (ctypes.c_longlong, [ctypes.c_char_p, ctypes.c_char_p, _vp,
                                                    ctypes.c_longlong, ctypes.c_char_p,
                                                    ctypes.c_size_t]),
@@ -145,3 +157,25 @@ def encoder_struct(m, keep):
             keep.append(a)
             setattr(s, n, a.ctypes.data)
     return s
+
+
+def aligned_empty(shape, dtype, align=64):
+    """An uninitialised array whose data starts on an `align`-byte boundary."""
+    dtype = np.dtype(dtype)
+    n = int(np.prod(shape)) * dtype.itemsize
+    raw = np.empty(n + align, np.uint8)
+    off = (-raw.ctypes.data) % align
+    return raw[off:off + n].view(dtype).reshape(shape)
+
+
+def quantise_weights(w_kn, asmooth=None):
+    """The packer's int8 operand scheme (tools/lib/gemm_i8.py:21-90): per column
+    s = max_k |W*asmooth| / 127 (1 for an all-zero column), q = rint(W/s)
+    clipped to [-127, 127]. Returns (q int8 [K, N], s fp32 [N])."""
+    w = np.asarray(w_kn, np.float32)
+    if asmooth is not None:
+        w = w * np.asarray(asmooth, np.float32)[:, None]
+    s = (np.abs(w).max(axis=0) / np.float32(127.0)).astype(np.float32)
+    s = np.where(s > 0, s, np.float32(1.0)).astype(np.float32)
+    q = np.rint(w / s[None, :]).clip(-127, 127).astype(np.int8)
+    return q, s
