@@ -43,7 +43,7 @@ extern "C" {
 #define MX_E_STATE (-4)       /* object not ready (e.g. missing weights)       */
 #define MX_E_DATA (-5)        /* the data itself was refused (e.g. CLS masked) */
 
-typedef enum { MX_F32 = 0, MX_BF16 = 1, MX_I32 = 2 } mx_dtype;
+typedef enum { MX_F32 = 0, MX_BF16 = 1, MX_I32 = 2, MX_I8 = 3 } mx_dtype;
 
 /* GEMM epilogues: applied to acc + bias in fp32 before narrowing. */
 typedef enum {
@@ -208,6 +208,66 @@ int mx_pool_rows(mx_stream *s, const float *h, const float *attn_mask,
                  int64_t B, int64_t S, int64_t hidden, int cls_pool,
                  int l2_normalize, float *out);
 
+/* ---- the int8 (W8A8) datapath ---------------------------------------------
+ * The reference's int8 design (a_elem_bytes == 1): A is quantised per row to
+ * int8 on the way in, the array multiplies int8 x int8 into exact int32, and
+ * C is dequantised with the row's scale, the column's weight scale and the
+ * bias (BertEncoder::gemm's int8 branch, bert_encoder.cpp:741-924). The
+ * container carries per operand the int8 [K, N] weight, `.wscale` [N] and the
+ * SmoothQuant factor `.asmooth` [K] (bert_encoder.cpp:40-160); A is scaled by
+ * ias = 1 / asmooth before it is quantised. */
+
+/* Design::stage of an int8 design's B operand: [K, N] row-major int8 (host),
+ * wscale [N] and asmooth [K] (host fp32). Stored as an [N, K] int8 panel with
+ * wscale and ias = 1/asmooth (one fp32 division per element, as the reference
+ * reciprocates, bert_encoder.cpp:764-772) on the device. K % 16 == 0. */
+int mx_stage_weight_i8(mx_ctx *ctx, const int8_t *kn_host, const float *wscale_host,
+                       const float *asmooth_host, int64_t K, int64_t N, int *slot);
+/* The same from a container's pre-tiled I8 operand (block_panel layout, the
+ * tiling of mx_stage_weight_panel), untiled on the GPU. */
+int mx_stage_weight_panel_i8(mx_ctx *ctx, const int8_t *panel_host, const float *wscale_host,
+                             const float *asmooth_host, int64_t K, int64_t N, int64_t tile_k,
+                             int64_t tile_n, int64_t mac_s, int64_t mac_t, int *slot);
+/* The device vectors of a staged int8 operand: wscale [N] and ias [K] (the
+ * ias to quantise this GEMM's A with). */
+int mx_weight_i8_scales(mx_ctx *ctx, int slot, const float **wscale, const float **ias);
+
+/* quantise_a_int8 (common/host_kernels.hpp:263-320): per row of a (fp32 or
+ * bf16, [rows, K] contiguous), t = a * ias, sc = max|t| > 0 ? max|t| / 127 : 1,
+ * q = rint(clamp(t * (1/sc), -127, 127)); a_scale[row] = sc. Bit-identical to
+ * the host for finite input. K % 4 == 0, K <= 8192. */
+int mx_quantise_a_int8(mx_stream *s, const void *a, int a_dtype, int64_t rows, int64_t K,
+                       const float *ias, int8_t *q, float *a_scale);
+
+/* gemm on an int8 design: Aq int8 [M, K] (row stride lda) with its a_scale [M]
+ * times the int8 operand in `wslot`, exact int32 accumulation, then
+ * dequantise_c (host_kernels.hpp:529-600) fused: y = fma(float(acc) *
+ * a_scale[m], wscale[n], bias[n]) (bias nullable), bit-identical to the host's
+ * int32-C form; then the epilogue (dequant_act_quant's activation, :405-500),
+ * the optional fp32 residual, and C as fp32 or bf16. c_dtype MX_I32 stores
+ * the raw int32 accumulators (the design's C before dequantise_c; no bias,
+ * residual or epilogue). K % 64 == 0, 256 <= K <= 133144 (K * 127^2 < 2^31),
+ * N % 4 == 0, lda % 16 == 0, 16-byte aligned A, C, bias and wscale. */
+int mx_gemm_i8(mx_stream *s, const int8_t *A, const float *a_scale, int64_t M, int64_t K,
+               int64_t lda, int wslot, const float *bias, int epilogue, const float *residual,
+               void *C, int c_dtype, int64_t ldc);
+/* The same with the operand given directly: Wt int8 [N, K] (row stride K),
+ * wscale [N] on the device. */
+int mx_gemm_i8_wt(mx_stream *s, const int8_t *A, const float *a_scale, int64_t M, int64_t K,
+                  int64_t lda, const int8_t *Wt, const float *wscale, int64_t N,
+                  const float *bias, int epilogue, const float *residual, void *C, int c_dtype,
+                  int64_t ldc);
+
+/* add_norm_quant (bert_encoder.cpp:1197-1300): the residual LayerNorm of
+ * mx_layernorm (x fp32, y fp32 or bf16 nullable, out_f32 nullable and may
+ * alias x) whose output is quantised in the same pass for the next int8 GEMM
+ * (that GEMM's ias) into q [rows, cols] and a_scale [rows], as
+ * mx_quantise_a_int8 would quantise out_f32. cols % 4 == 0, cols <= 4096. */
+int mx_layernorm_i8(mx_stream *s, const float *x, const void *y, int y_dtype,
+                    const float *gamma, const float *beta, float eps, int64_t rows,
+                    int64_t cols, float *out_f32, const float *ias, int8_t *q,
+                    float *a_scale);
+
 /* ---- placement registry (common/npu_ops_flag.hpp:75-214) ------------------ */
 
 /* parse_npu_ops: comma list of codes (spaces ignored, empty items skipped);
@@ -261,7 +321,13 @@ typedef enum { MX_FRONT_NONE = 0, MX_FRONT_VIT = 1, MX_FRONT_WHISPER = 2 } mx_fr
  * "embeddings.ln.weight", "embeddings.ln.bias", "embeddings.word",
  * "embeddings.position", "embeddings.token_type" (BERT), "final_ln.weight",
  * "final_ln.bias" (pre-LN). GEMM operands are [K, N] (fp32 values rounded
- * to bf16 by to_bf16, or bf16 bits); everything else fp32. */
+ * to bf16 by to_bf16, or bf16 bits); everything else fp32.
+ * An int8 design's operands (BertEncoder::stage_all, bert_encoder.cpp:40-160)
+ * are set as MX_I8 [K, N] with "layer.{i}.<gemm>.wscale" [N] and
+ * "layer.{i}.<gemm>.asmooth" [K] beside them; the stack then runs the int8
+ * datapath (each GEMM's A quantised per row by mx_layernorm_i8 or
+ * mx_quantise_a_int8, the GEMM dequantising in its epilogue). Every GEMM
+ * operand of a stack must be of one kind (mx_encoder_ready refuses a mix). */
 int mx_encoder_create(mx_ctx *ctx, const mx_encoder_desc *desc,
                       mx_encoder **out);
 void mx_encoder_destroy(mx_encoder *enc);
@@ -402,10 +468,12 @@ int mx_encoder_set_panel(mx_encoder *enc, const char *name, const uint16_t *pane
  * head_dim / intermediate / max_seq_len; pooling "cls" or "mean";
  * l2_normalize (default true); LayerNorm eps 1e-12 and the polynomial GELU
  * (gelu_cpu), as BertEncoder hard-codes them. Every tensor is set from the
- * mapping: pre-tiled BF16 GEMM operands through mx_encoder_set_panel. A
- * "host" container (F32 row-major operands) is refused for the GEMM, as the
- * reference refuses --npu-ops gemm on one (bert_encoder.cpp:79-87). The
- * encoder is ready on MX_OK. */
+ * mapping: pre-tiled BF16 GEMM operands through mx_encoder_set_panel, and an
+ * --int8 pack's pre-tiled I8 operands with their .wscale/.asmooth through the
+ * int8 staging of mx_stage_weight_panel_i8 (the int4 pack's I4 nibbles are
+ * refused by name). A "host" container (F32 row-major operands) is refused
+ * for the GEMM, as the reference refuses --npu-ops gemm on one
+ * (bert_encoder.cpp:79-87). The encoder is ready on MX_OK. */
 int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out);
 
 #ifdef __cplusplus

@@ -26,8 +26,9 @@ FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(HERE, "..", "include"),
 ]
-SOURCES = ["k_elem.hip", "k_gemm.hip", "k_gemm_lds.hip", "k_attn.hip", "k_front.hip",
-           "k_panel.hip", "mx_abi.cpp", "mx_encoder.cpp", "mx_npue.cpp", "mx_service.cpp"]
+SOURCES = ["k_gemm_lds.hip", "k_gemm_i8.hip", "k_elem.hip", "k_gemm.hip", "k_attn.hip",
+           "k_front.hip", "k_panel.hip", "k_quant.hip", "mx_abi.cpp", "mx_i8.cpp",
+           "mx_encoder.cpp", "mx_npue.cpp", "mx_service.cpp"]
 
 
 def _compile(src):

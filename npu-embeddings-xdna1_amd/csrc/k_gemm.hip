@@ -189,7 +189,14 @@ bool lds_path_ok(const GemmArgs &a) {
          (!a.residual || (uintptr_t)a.residual % 16 == 0);
 }
 
-int cu_count();
+GemmPath pick(const GemmArgs &a) {
+  if (!lds_path_ok(a)) return PATH_STAGED;
+  static const GemmPath paths[] = {PATH_LDS_256x256, PATH_LDS_256x192, PATH_LDS_128x256,
+                                   PATH_LDS_128x128};
+  return paths[gemm_lds_tile(a.M, a.N)];
+}
+
+}  // namespace
 
 // The tile with the least estimated time: rounds of tiles over the CUs (the
 // last round costs a whole one) times the tile's area over its relative
@@ -198,25 +205,22 @@ int cu_count();
 // 192: 0.88, 128 x 256: 0.86, 128 x 128: 0.65). The 256 x 192 tile wins
 // where N = 768 leaves 256 x 256 tiles at 1.5 rounds; small problems take
 // the small tiles that spread over the most CUs.
-GemmPath pick(const GemmArgs &a) {
-  if (!lds_path_ok(a)) return PATH_STAGED;
+int gemm_lds_tile(int64_t M, int64_t N) {
   struct Cand {
-    GemmPath path;
     int bm, bn;
     double eff;
   };
-  static const Cand cands[] = {{PATH_LDS_256x256, 256, 256, 1.0},
-                               {PATH_LDS_256x192, 256, 192, 0.88},
-                               {PATH_LDS_128x256, 128, 256, 0.86},
-                               {PATH_LDS_128x128, 128, 128, 0.65}};
+  static const Cand cands[] = {{256, 256, 1.0}, {256, 192, 0.88}, {128, 256, 0.86},
+                               {128, 128, 0.65}};
   const int64_t G = cu_count();
-  GemmPath best = PATH_LDS_128x128;
+  int best = 3;
   double best_t = 0.0;
-  for (const Cand &c : cands) {
-    const int64_t tiles = ((a.M + c.bm - 1) / c.bm) * ((a.N + c.bn - 1) / c.bn);
+  for (int i = 0; i < 4; ++i) {
+    const Cand &c = cands[i];
+    const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
     const double t = (double)((tiles + G - 1) / G) * c.bm * c.bn / c.eff;
     if (best_t == 0.0 || t < best_t) {
-      best = c.path;
+      best = i;
       best_t = t;
     }
   }
@@ -238,7 +242,6 @@ int cu_count() {
   return cached[dev];
 }
 
-}  // namespace
 
 const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
   static const float aligned_probe[4] __attribute__((aligned(16))) = {0, 0, 0, 0};

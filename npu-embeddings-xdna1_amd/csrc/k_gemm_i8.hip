@@ -1,0 +1,74 @@
+// k_gemm_i8.hip -- the int8 (W8A8) instantiations of the persistent
+// LDS-pipelined GEMM (kernel body and design in k_gemm_lds.hpp): exact int32
+// accumulation in v_mfma_i32_32x32x32_i8 with dequantise_c fused into the
+// epilogue, or the raw int32 accumulators.
+#include "k_gemm_lds.hpp"
+
+using namespace mxlds;
+
+namespace {
+
+// OUT: 0 fp32 C, 1 bf16 C, 2 raw int32 C.
+template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, int OUT>
+__global__ __launch_bounds__(WGM *WGN * 64) void gemm_i8_k(
+    const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wt, int M, int N,
+    int K, const float *__restrict__ a_scale, const float *__restrict__ wscale,
+    const float *__restrict__ bias, const float *residual, void *C, int64_t ldc, int tiles_m,
+    int tiles_n) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  gemm_lds_body<BM, BN, WGM, WGN, NS, EPI, RES, OUT == 1, true, OUT == 2>(
+      A, lda, Wt, M, N, K, bias, residual, C, ldc, tiles_m, tiles_n, a_scale, wscale, smem);
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, int OUT>
+hipError_t launch_t(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, true>;
+  auto kern = gemm_i8_k<BM, BN, WGM, WGN, NS, EPI, RES, OUT>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute(
+        (const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
+  const int ntiles = tiles_m * tiles_n;
+  const int g = ntiles < grid ? ntiles : grid;
+  kern<<<g, Cfg::NT, Cfg::LDS, s>>>(a.A, a.lda, a.Wt, (int)a.M, (int)a.N, (int)a.K, a.a_scale,
+                                    a.wscale, a.bias, a.residual, a.C, a.ldc, tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int WGM, int WGN, int NS>
+hipError_t launch(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
+  if (a.c_dtype == 2) return launch_t<BM, BN, WGM, WGN, NS, 0, false, 2>(a, grid, s);
+#define MX_I8_EPI(E)                                                                 \
+  if (a.epilogue == E) {                                                             \
+    if (a.residual)                                                                  \
+      return a.c_dtype == 1 ? launch_t<BM, BN, WGM, WGN, NS, E, true, 1>(a, grid, s) \
+                            : launch_t<BM, BN, WGM, WGN, NS, E, true, 0>(a, grid, s);  \
+    return a.c_dtype == 1 ? launch_t<BM, BN, WGM, WGN, NS, E, false, 1>(a, grid, s)  \
+                          : launch_t<BM, BN, WGM, WGN, NS, E, false, 0>(a, grid, s);   \
+  }
+  MX_I8_EPI(0)
+  MX_I8_EPI(1)
+  MX_I8_EPI(2)
+#undef MX_I8_EPI
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+namespace mxk {
+
+hipError_t gemm_i8(const GemmI8Args &a, hipStream_t s) {
+  const int grid = cu_count();
+  switch (gemm_lds_tile(a.M, a.N)) {
+    case 0: return launch<256, 256, 2, 4, 3>(a, grid, s);
+    case 1: return launch<256, 192, 4, 2, 4>(a, grid, s);
+    case 2: return launch<128, 256, 2, 4, 4>(a, grid, s);
+    default: return launch<128, 128, 2, 2, 4>(a, grid, s);
+  }
+}
+
+}  // namespace mxk

@@ -1,436 +1,19 @@
-// k_gemm_lds.hip -- the encoder's bf16 GEMM on gfx950: a persistent kernel
-// whose operand tiles reach LDS by direct global->LDS loads
-// (global_load_lds_dwordx4) through a ring of slabs.
-//
-// C[M, N] = epilogue(A[M, K] @ W[K, N] + bias) (+ residual), A bf16 row-major,
-// W held as Wt[N, K] (K contiguous), fp32 accumulation in
-// v_mfma_f32_32x32x16_bf16, one round-to-nearest-even narrowing (the hardware
-// conversion) at the store when C is bf16.
-//
-// Grid. One block per CU walks a list of BM x BN output tiles; its slabs
-// (BK = 32 deep) form one sequence across tile boundaries, so the ring keeps
-// loading the next tile's first slabs while the current tile drains: no
-// per-tile prologue latency, no block relaunch. Workgroups go round-robin
-// over the 8 XCDs, so the blocks of XCD x (blockIdx % 8 == x) share the x-th
-// eighth of the tiles (row-major over (m, n)) and walk it together: they
-// share A row-panels and W in that XCD's L2, and every XCD gets the same
-// share of the work even when the tiles do not fill whole rounds.
-//
-// Ring. NS slots; slab s + NS is fetched into slot s % NS as soon as every read
-// of slab s is done, i.e. ~NS - 1 slabs ahead of its use. The loads are issued
-// from inline assembly: the compiler's own wait insertion would otherwise put
-// vmcnt(0) -- a wait on every prefetch -- before each LDS read. Each load is
-// addressed as a scalar base (the operand's tile origin plus the slab's depth)
-// and a 32-bit per-lane offset fixed for the tile, so issuing a slab costs a
-// few scalar adds: building 64-bit addresses per load (quarter-rate integer
-// multiplies on the vector ALU, right after the barrier) cost up to a tenth
-// of the kernel. Each wave waits
-// for its own loads of the slab it is about to read (vmcnt = loads it issued
-// since; loads complete in issue order), then all waves meet at one barrier
-// per slab. The first slab of each tile also moves the tile's bias into a
-// per-tile-parity LDS copy (a few lanes of one extra load per wave), so the
-// bias is on chip for the epilogue without a compiler-tracked load; the waits
-// do not count that load, which only makes them stricter.
-//
-// Fragments. Two register sets, one per 16-deep half of a slab; each half's
-// MFMAs run while the other set is read from LDS (one ds_read after each of
-// the first MFMAs, pinned by sched_group_barrier). The barrier sits between
-// the halves, when every read of the current slab has been issued.
-//
-// LDS image. A slab is rows of 32 bf16 = 64 bytes = four 16-byte chunks. gfx950
-// serves a ds_read_b128 sixteen lanes (256 bytes, all 64 banks) per cycle; the
-// sixteen lanes of one phase read rows r..r+15 at the same logical chunk.
-// Chunk c of row r is stored at position c ^ ((r >> 2) & 3) of its row, which
-// puts those sixteen 16-byte reads in sixteen different bank groups. The
-// direct load writes lane l's 16 bytes at LDS offset 16*l of its 1 KB window,
-// so the swizzle is applied to the GLOBAL address each lane fetches: lane l
-// fills row l/4, position l%4, i.e. logical chunk (l%4) ^ (((l/4) >> 2) & 3).
-//
-// Operand roles. The MFMA's first operand is the W tile and its second the A
-// tile, so the 32x32 accumulator holds C^T: each lane owns one row of C and
-// runs of four consecutive columns.
-//
-// Epilogue. Per 32 x 32 accumulator block a wave adds the bias, applies the
-// activation, writes the fp32 block to its private LDS staging area (rows
-// padded by 16 bytes) and reads it back row-major, so every global store (and
-// residual load) of a wave covers whole 128-byte (fp32) or 64-byte (bf16) row
-// segments instead of 16-byte pieces of 32 rows.
-//
-// Requirements (the launcher routes anything else to k_gemm.hip's kernel):
-// K % 32 == 0 and K >= 32 * NS, N % 4 == 0, a bias, 16-byte aligned operands.
-// Rows past M (or N) are fetched from a clamped, in-bounds row and never
-// stored.
-#include "mx_common.hpp"
-#include "mx_kernels.hpp"
+// k_gemm_lds.hip -- the bf16 instantiations of the persistent LDS-pipelined
+// GEMM (the kernel body and its design are in k_gemm_lds.hpp).
+#include "k_gemm_lds.hpp"
 
-using namespace mxd;
+using namespace mxlds;
 
 namespace {
-
-constexpr int BK = 32;
-constexpr int ROWB = BK * 2;   // bytes per LDS slab row
-constexpr int STG_ROWB = 144;  // staging row: 32 fp32 + 16 bytes of padding
-constexpr int STG_WAVE = 32 * STG_ROWB;
-
-template <int BM, int BN, int WGM, int WGN, int NS>
-struct LdsCfg {
-  static constexpr int NW = WGM * WGN;                // waves
-  static constexpr int NT = NW * 64;                  // threads
-  static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
-  static constexpr int TM = WM / 32, TN = WN / 32;    // 32x32 MFMA tiles per wave
-  static constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB;
-  static constexpr int SLOT = A_BYTES + B_BYTES;
-  // A slab is PIECES 1 KB wave loads of 16 rows each, A's first; wave w
-  // issues pieces w, w + NW, ...: LOADS_HI of them if w < NHI, else LOADS_LO
-  // (a 256 x 192 slab is 28 pieces: four waves issue 4, four issue 3).
-  static constexpr int A_PIECES = A_BYTES / 1024, PIECES = (A_BYTES + B_BYTES) / 1024;
-  static constexpr int LOADS_LO = PIECES / NW, LOADS_HI = (PIECES + NW - 1) / NW;
-  static constexpr int NHI = PIECES % NW == 0 ? NW : PIECES % NW;
-  static constexpr int BIAS_PER_WAVE = BN / NW;        // floats each wave's bias piece moves
-  static constexpr int STG_OFF = NS * SLOT;
-  static constexpr int BIAS_OFF = STG_OFF + NW * STG_WAVE;
-  static constexpr int LDS = BIAS_OFF + 2 * BN * 4;
-  static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be whole MFMA tiles");
-  static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "slabs are whole 1 KB pieces");
-  static_assert(BIAS_PER_WAVE % 4 == 0 && BIAS_PER_WAVE <= 256, "bias piece: 16-byte lanes");
-  static_assert(LDS <= 160 * 1024, "gfx950 LDS is 160 KB");
-  static_assert(NS >= 3 && LOADS_HI * (NS - 2) < 64, "vmcnt holds at most 63");
-};
-
-// s_waitcnt vmcnt(N), other counters untouched.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// One wave-wide direct load: each active lane moves 16 bytes from `src` into
-// LDS byte lds + 16 * lane.
-__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
-               : "memory");
-}
-
-// The same load addressed as a wave-uniform base (SGPRs) plus a 32-bit
-// per-lane byte offset: the per-slab advance is a scalar add.
-__device__ __forceinline__ void dma16s(uint64_t base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff),
-               "s"(base)
-               : "memory");
-}
-
-__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return ((uint64_t)hi << 32) | lo;
-}
 
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF>
 __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
     const uint16_t *__restrict__ A, int64_t lda, const uint16_t *__restrict__ Wt, int M, int N,
     int K, const float *__restrict__ bias, const float *residual, void *C, int64_t ldc,
     int tiles_m, int tiles_n) {
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS>;
-  constexpr int TM = Cfg::TM, TN = Cfg::TN;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-
-  // This block's tiles: t(i) = first + i * stride, i < my_tiles. With a grid
-  // that is a multiple of 8, XCD x owns tiles [x*chunk, (x+1)*chunk) and its
-  // G/8 blocks interleave over them.
-  const int ntiles = tiles_m * tiles_n;
-  const int G = gridDim.x;
-  int first = (int)blockIdx.x, stride = G, end = ntiles;
-  if ((G & 7) == 0 && G >= 16) {
-    const int chunk = (ntiles + 7) >> 3, x = (int)(blockIdx.x & 7);
-    first = x * chunk + (int)(blockIdx.x >> 3);
-    stride = G >> 3;
-    end = min(ntiles, (x + 1) * chunk);
-  }
-  if (first >= end) return;
-  const int my_tiles = (end - 1 - first) / stride + 1;
-  const int nk = K / BK;
-  const int nslab = my_tiles * nk;
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WGN, wn = wave - wm * WGN;
-  const int li = lane & 31, g = lane >> 5;
-
-  // Load addressing: lane fills row lrow of a 16-row window, logical chunk
-  // lchunk (swizzled); rows are clamped in bounds.
-  const int lrow = lane >> 2;
-  const int lchunk = (lane & 3) ^ ((lrow >> 2) & 3);
-  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-  // Issue cursor: slab is_s = tile is_ti, depth is_kt, tile origin (is_m0, is_n0).
-  int is_s = 0, is_ti = 0, is_kt = 0, is_m0 = 0, is_n0 = 0;
-  auto tile_origin = [&](int ti, int &m0, int &n0) {
-    const int t = first + ti * stride;
-    const int tm = t / tiles_n;
-    m0 = tm * BM;
-    n0 = (t - tm * tiles_n) * BN;
-  };
-  tile_origin(0, is_m0, is_n0);
-  // Per issue tile: each piece's per-lane byte offset from its operand's tile
-  // origin (rows clamped in bounds), and the two origins as scalars.
-  uint32_t poff[Cfg::LOADS_HI];
-  uint64_t pbase[Cfg::LOADS_HI];
-  auto set_tile = [&](int m0, int n0) {
-#pragma unroll
-    for (int k = 0; k < Cfg::LOADS_HI; ++k) {
-      const int p = wave + Cfg::NW * k;
-      if (p < Cfg::A_PIECES) {
-        int r = m0 + p * 16 + lrow;
-        r = (r < M ? r : M - 1) - m0;
-        poff[k] = (uint32_t)((r * lda + lchunk * 8) * 2);
-      } else {
-        int r = n0 + (p - Cfg::A_PIECES) * 16 + lrow;
-        r = (r < N ? r : N - 1) - n0;
-        poff[k] = (uint32_t)(((int64_t)r * K + lchunk * 8) * 2);
-      }
-    }
-    const uint64_t abase = uniform64((uint64_t)(uintptr_t)(A + (int64_t)m0 * lda));
-    const uint64_t bbase = uniform64((uint64_t)(uintptr_t)(Wt + (int64_t)n0 * K));
-#pragma unroll
-    for (int k = 0; k < Cfg::LOADS_HI; ++k)
-      pbase[k] = wave + Cfg::NW * k < Cfg::A_PIECES ? abase : bbase;
-  };
-  set_tile(is_m0, is_n0);
-  // Issue the loads of slab is_s, then advance the cursor.
-  uint32_t is_slot = 0;  // byte offset of slot is_s % NS
-  uint64_t is_kb = 0;    // byte depth of slab is_kt
-  auto issue = [&]() {
-    const int ti = is_ti, kt = is_kt, n0 = is_n0;
-    const uint32_t slot = lds0 + is_slot;
-#pragma unroll
-    for (int k = 0; k < Cfg::LOADS_HI; ++k) {
-      const int p = wave + Cfg::NW * k;  // wave-uniform
-      if (k < Cfg::LOADS_LO || p < Cfg::PIECES)
-        dma16s(pbase[k] + is_kb, poff[k], slot + (uint32_t)(p * 1024));
-    }
-    // Bias piece, on a tile's first slab: lanes 0 .. BIAS_PER_WAVE/4 - 1 move
-    // 16 bytes each of the columns from n0 + wave * BIAS_PER_WAVE (clamped in
-    // bounds; a column >= N is never stored). The other lanes are inactive
-    // for this load and write nothing.
-    if (kt == 0 && lane < Cfg::BIAS_PER_WAVE / 4) {
-      int c = n0 + wave * Cfg::BIAS_PER_WAVE + lane * 4;
-      c = c < N ? c : N - 4;
-      dma16(bias + c,
-            lds0 + Cfg::BIAS_OFF + (uint32_t)((ti & 1) * BN * 4 + wave * Cfg::BIAS_PER_WAVE * 4));
-    }
-    ++is_s;
-    is_slot = is_slot + Cfg::SLOT == NS * Cfg::SLOT ? 0 : is_slot + Cfg::SLOT;
-    is_kb += BK * 2;
-    if (++is_kt == nk) {
-      is_kt = 0;
-      is_kb = 0;
-      ++is_ti;
-      if (is_ti < my_tiles) {
-        tile_origin(is_ti, is_m0, is_n0);
-        set_tile(is_m0, is_n0);
-      }
-    }
-  };
-
-  f32x16 acc[TN][TM];
-#pragma unroll
-  for (int j = 0; j < TN; ++j)
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
-
-  // Fragment addressing: lane (row li, k-half g) reads logical chunk 2*kk + g
-  // of its row, at its swizzled position.
-  const int swz = (li >> 2) & 3;  // (row >> 2) & 3 with row = 32*x + li
-  const int pos0 = ((0 + g) ^ swz) * 16, pos1 = ((2 + g) ^ swz) * 16;
-  const int rowA = (wm * Cfg::WM + li) * ROWB, rowB = (wn * Cfg::WN + li) * ROWB;
-
-  bf16x8 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
-  auto read_set = [&](int s, int pos, bf16x8 *fa, bf16x8 *fb) {
-    const uint8_t *slot = smem + (s % NS) * Cfg::SLOT;
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-      fb[j] = *(const bf16x8 *)(slot + Cfg::A_BYTES + rowB + j * 32 * ROWB + pos);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) fa[i] = *(const bf16x8 *)(slot + rowA + i * 32 * ROWB + pos);
-  };
-  auto mfma_set = [&](const bf16x8 *fa, const bf16x8 *fb) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[j][i], 0, 0, 0);
-  };
-  // MFMAs and the LDS reads of the other set, one read after each of the
-  // first TM + TN MFMAs.
-  auto interleave = []() {
-#pragma unroll
-    for (int x = 0; x < TM + TN; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
-  };
-
-  // The epilogue of this block's ti-th tile.
-  auto epilogue = [&](int ti) {
-    int m0, n0;
-    tile_origin(ti, m0, n0);
-    const float *bl = (const float *)(smem + Cfg::BIAS_OFF + (ti & 1) * BN * 4);
-    uint8_t *stg = smem + Cfg::STG_OFF + wave * STG_WAVE;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int rbase = m0 + wm * Cfg::WM + i * 32;
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int cl = wn * Cfg::WN + j * 32;  // tile-local first column
-        // acc layout -> fp32 staging rows (lane li's row, columns 8q + 4g + e)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 b = *(const float4 *)(bl + cl + q * 8 + g * 4);
-          float4 v;
-          v.x = gemm_epilogue(acc[j][i][q * 4 + 0] + b.x, EPI);
-          v.y = gemm_epilogue(acc[j][i][q * 4 + 1] + b.y, EPI);
-          v.z = gemm_epilogue(acc[j][i][q * 4 + 2] + b.z, EPI);
-          v.w = gemm_epilogue(acc[j][i][q * 4 + 3] + b.w, EPI);
-          *(float4 *)(stg + li * STG_ROWB + (q * 8 + g * 4) * 4) = v;
-        }
-        asm volatile("" ::: "memory");
-        if (CBF) {
-          // 8 fp32 per lane -> 16 bytes of bf16; 4 lanes per 32-column row.
-#pragma unroll
-          for (int r = 0; r < 2; ++r) {
-            const int row = r * 16 + (lane >> 2), c8 = (lane & 3) * 8;
-            const float4 x0 = *(const float4 *)(stg + row * STG_ROWB + c8 * 4);
-            const float4 x1 = *(const float4 *)(stg + row * STG_ROWB + c8 * 4 + 16);
-            const int grow = rbase + row, gcol = n0 + cl + c8;
-            if (grow < M && gcol < N) {
-              float y[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-              const int64_t off = (int64_t)grow * ldc + gcol;
-              const bool full = gcol + 8 <= N;  // else N % 8 == 4: four columns left
-              if (RES) {
-                const float4 r0 = *(const float4 *)(residual + off);
-                y[0] += r0.x;
-                y[1] += r0.y;
-                y[2] += r0.z;
-                y[3] += r0.w;
-                if (full) {
-                  const float4 r1 = *(const float4 *)(residual + off + 4);
-                  y[4] += r1.x;
-                  y[5] += r1.y;
-                  y[6] += r1.z;
-                  y[7] += r1.w;
-                }
-              }
-              uint4 w;
-              w.x = pack_bf2_hw(y[0], y[1]);
-              w.y = pack_bf2_hw(y[2], y[3]);
-              w.z = pack_bf2_hw(y[4], y[5]);
-              w.w = pack_bf2_hw(y[6], y[7]);
-              if (full)
-                *(uint4 *)((uint16_t *)C + off) = w;
-              else
-                *(uint2 *)((uint16_t *)C + off) = make_uint2(w.x, w.y);
-            }
-          }
-        } else {
-          // 4 fp32 per lane; 8 lanes per 32-column row.
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = r * 8 + (lane >> 3), c4 = (lane & 7) * 4;
-            float4 x = *(const float4 *)(stg + row * STG_ROWB + c4 * 4);
-            const int grow = rbase + row, gcol = n0 + cl + c4;
-            if (grow < M && gcol < N) {
-              const int64_t off = (int64_t)grow * ldc + gcol;
-              if (RES) {
-                const float4 rv = *(const float4 *)(residual + off);
-                x.x += rv.x;
-                x.y += rv.y;
-                x.z += rv.z;
-                x.w += rv.w;
-              }
-              *(float4 *)((float *)C + off) = x;
-            }
-          }
-        }
-        asm volatile("" ::: "memory");
-      }
-    }
-  };
-
-  // Prologue: slabs 0 .. NS-1 in flight; slab 0's first half into set 0.
-#pragma unroll
-  for (int s = 0; s < NS; ++s)
-    if (s < nslab) issue();
-  wait_vmcnt<0>();
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  read_set(0, pos0, fa0, fb0);
-
-  int ep_kt = 0, ep_ti = 0;  // tile and depth of slab s
-  for (int s = 0; s < nslab; ++s) {
-    // First half of slab s; its second half is read meanwhile.
-    mfma_set(fa0, fb0);
-    read_set(s, pos1, fa1, fb1);
-    interleave();
-    // Every read of slab s is now issued. Wait for them and for this wave's
-    // loads of slab s + 1 (the slabs issued after it, at most NS - 2, may stay
-    // in flight), then meet: slab s + 1 is in LDS and slot s % NS is free.
-    const int ahead = nslab - 2 - s;
-    const bool hi = wave < Cfg::NHI;
-    if (ahead >= NS - 2) {
-      if (hi)
-        wait_vmcnt<Cfg::LOADS_HI *(NS - 2)>();
-      else
-        wait_vmcnt<Cfg::LOADS_LO *(NS - 2)>();
-    } else if (NS > 3 && ahead == NS - 3) {
-      if (hi)
-        wait_vmcnt<(NS > 3 ? Cfg::LOADS_HI * (NS - 3) : 0)>();
-      else
-        wait_vmcnt<(NS > 3 ? Cfg::LOADS_LO * (NS - 3) : 0)>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    // Second half of slab s; the first half of slab s + 1 is read meanwhile
-    // (after the last slab, slab s again: in bounds, unused). The loads of
-    // slab s + NS are issued after the first MFMAs, which keep the matrix
-    // pipe busy while the scalar unit addresses them.
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb1[0], fa1[i], acc[0][i], 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    if (s + NS < nslab) issue();  // slab s + NS
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 1; j < TN; ++j)
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb1[j], fa1[i], acc[j][i], 0, 0, 0);
-    read_set(s + 1 < nslab ? s + 1 : s, pos0, fa0, fb0);
-    {
-      constexpr int NM = TM * (TN - 1), NR = TM + TN, NP = NM < NR ? NM : NR;
-#pragma unroll
-      for (int x = 0; x < NP; ++x) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      if (NM > NP) __builtin_amdgcn_sched_group_barrier(0x008, NM - NP, 0);
-      if (NR > NP) __builtin_amdgcn_sched_group_barrier(0x100, NR - NP, 0);
-    }
-    if (++ep_kt == nk) {
-      ep_kt = 0;
-      epilogue(ep_ti++);
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
-    }
-  }
+  gemm_lds_body<BM, BN, WGM, WGN, NS, EPI, RES, CBF, false, false>(
+      A, lda, Wt, M, N, K, bias, residual, C, ldc, tiles_m, tiles_n, nullptr, nullptr, smem);
 }
 
 }  // namespace
@@ -439,7 +22,7 @@ namespace mxk {
 
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF>
 hipError_t gemm_lds_launch_t(const GemmArgs &a, int grid, hipStream_t s) {
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS>;
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, false>;
   auto kern = gemm_lds_k<BM, BN, WGM, WGN, NS, EPI, RES, CBF>;
   static bool attr_set = false;
   if (!attr_set) {
@@ -451,8 +34,9 @@ hipError_t gemm_lds_launch_t(const GemmArgs &a, int grid, hipStream_t s) {
   const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
   const int ntiles = tiles_m * tiles_n;
   const int g = ntiles < grid ? ntiles : grid;
-  kern<<<g, Cfg::NT, Cfg::LDS, s>>>(a.A, a.lda, a.Wt, (int)a.M, (int)a.N, (int)a.K, a.bias,
-                                    a.residual, a.C, a.ldc, tiles_m, tiles_n);
+  kern<<<g, Cfg::NT, Cfg::LDS, s>>>((const uint16_t *)a.A, a.lda, (const uint16_t *)a.Wt,
+                                    (int)a.M, (int)a.N, (int)a.K, a.bias, a.residual, a.C, a.ldc,
+                                    tiles_m, tiles_n);
   return hipGetLastError();
 }
 

@@ -12,21 +12,24 @@
 // One workgroup per tile: the tile's contiguous run of the container is read
 // in order (coalesced) and scattered into LDS as [n][k]; each row n of the
 // tile then leaves as tile_k consecutive bf16 of the panel row (coalesced).
-// A pure byte permutation -- every element is copied, none is converted.
+// A pure permutation of bf16 or int8 elements -- every element is copied, none
+// is converted.
 #include "mx_common.hpp"
 #include "mx_kernels.hpp"
 
 namespace {
 
-__global__ __launch_bounds__(256) void untile_panel_k(const uint16_t *__restrict__ panel,
-                                                      int64_t K, int64_t N, int tk, int tn,
-                                                      int ms, int mt, uint16_t *__restrict__ wt) {
-  extern __shared__ uint16_t tile[];  // [tn][tk + 2]
+template <typename T>
+__global__ __launch_bounds__(256) void untile_panel_k(const T *__restrict__ panel, int64_t K,
+                                                      int64_t N, int tk, int tn, int ms, int mt,
+                                                      T *__restrict__ wt) {
+  extern __shared__ uint8_t lds[];
+  T *tile = (T *)lds;  // [tn][tk + 2]
   const int pitch = tk + 2;
   const int64_t nb = N / tn;
   const int64_t b = blockIdx.x;  // k,n order: b = bk * nb + bn
   const int64_t bk = b / nb, bn = b - bk * nb;
-  const uint16_t *src = panel + b * (int64_t)tk * tn;
+  const T *src = panel + b * (int64_t)tk * tn;
   const int c0 = tn / mt, elems = tk * tn;
   for (int e = threadIdx.x; e < elems; e += blockDim.x) {
     int q = e;
@@ -53,7 +56,17 @@ hipError_t untile_panel(const uint16_t *panel, int64_t K, int64_t N, int tile_k,
                         int mac_s, int mac_t, uint16_t *wt, hipStream_t s) {
   const int64_t tiles = (K / tile_k) * (N / tile_n);
   const size_t lds = (size_t)(tile_k + 2) * tile_n * 2;
-  untile_panel_k<<<(unsigned)tiles, 256, lds, s>>>(panel, K, N, tile_k, tile_n, mac_s, mac_t, wt);
+  untile_panel_k<uint16_t><<<(unsigned)tiles, 256, lds, s>>>(panel, K, N, tile_k, tile_n, mac_s,
+                                                             mac_t, wt);
+  return hipGetLastError();
+}
+
+hipError_t untile_panel_i8(const int8_t *panel, int64_t K, int64_t N, int tile_k, int tile_n,
+                           int mac_s, int mac_t, int8_t *wt, hipStream_t s) {
+  const int64_t tiles = (K / tile_k) * (N / tile_n);
+  const size_t lds = (size_t)(tile_k + 2) * tile_n;
+  untile_panel_k<int8_t><<<(unsigned)tiles, 256, lds, s>>>(panel, K, N, tile_k, tile_n, mac_s,
+                                                           mac_t, wt);
   return hipGetLastError();
 }
 

@@ -264,8 +264,11 @@ int mx_create(int device, mx_ctx **out) {
 void mx_destroy(mx_ctx *ctx) {
   if (!ctx) return;
   if (use_device(ctx) == MX_OK)
-    for (auto &w : ctx->slots)
+    for (auto &w : ctx->slots) {
       if (w.wt) (void)hipFree(w.wt);
+      I8Operand op{w.wq, w.wscale, w.ias};
+      free_i8(op);
+    }
   delete ctx;
 }
 
@@ -374,12 +377,16 @@ int mx_stage_weight_panel(mx_ctx *ctx, const uint16_t *panel_host, int64_t K, in
 int mx_release_weight(mx_ctx *ctx, int slot) {
   if (!ctx) return fail(MX_E_INVALID, "mx_release_weight: null context");
   std::lock_guard<std::mutex> lk(ctx->mu);
-  if (slot < 1 || slot > static_cast<int>(ctx->slots.size()) || !ctx->slots[slot - 1].wt)
+  if (slot < 1 || slot > static_cast<int>(ctx->slots.size()) ||
+      (!ctx->slots[slot - 1].wt && !ctx->slots[slot - 1].wq))
     return fail(MX_E_INVALID, "mx_release_weight: no weight in slot " + std::to_string(slot));
   int rc = use_device(ctx);
   if (rc) return rc;
-  (void)hipFree(ctx->slots[slot - 1].wt);
-  ctx->slots[slot - 1] = WeightSlot{};
+  WeightSlot &w = ctx->slots[slot - 1];
+  if (w.wt) (void)hipFree(w.wt);
+  I8Operand op{w.wq, w.wscale, w.ias};
+  free_i8(op);
+  w = WeightSlot{};
   return MX_OK;
 }
 
@@ -392,9 +399,12 @@ int mx_gemm(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t lda, 
   {
     std::lock_guard<std::mutex> lk(s->ctx->mu);
     if (wslot < 1 || wslot > static_cast<int>(s->ctx->slots.size()) ||
-        !s->ctx->slots[wslot - 1].wt)
+        (!s->ctx->slots[wslot - 1].wt && !s->ctx->slots[wslot - 1].wq))
       return fail(MX_E_INVALID, "gemm: no weight staged in slot " + std::to_string(wslot));
     w = s->ctx->slots[wslot - 1];
+    if (!w.wt)
+      return fail(MX_E_INVALID, "gemm: slot " + std::to_string(wslot) +
+                                    " holds an int8 operand; it is multiplied by mx_gemm_i8");
   }
   if (w.K != K)
     return fail(MX_E_INVALID, "gemm: A has K = " + std::to_string(K) + " but slot " +

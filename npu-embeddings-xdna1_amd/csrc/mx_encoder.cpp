@@ -13,6 +13,15 @@
 //                       bf16-C convention, kernels/narrow_f32_bf16.cc)
 //   up    bf16 [M, f]   FFN-up with bias and GELU fused into the GEMM
 // Weights are [N, K] bf16 panels; biases and LayerNorm parameters fp32.
+//
+// An int8 container (every GEMM operand int8 with its wscale and asmooth)
+// runs the W8A8 datapath of the reference's int8 design: each GEMM's A is
+// quantised per row into
+//   xq    int8 [M, max(d, f)]  the quantised A operand
+//   sa    fp32 [M]             its row scales
+// by the residual LayerNorm itself (add_norm_quant) or by a quantise pass
+// over ctx / up, and the GEMM dequantises in its epilogue; the other buffers
+// keep their roles (xb is then unused).
 #include "mx_internal.hpp"
 #include "mx_kernels.hpp"
 
@@ -39,6 +48,10 @@ struct LayerW {
   uint16_t *w[4] = {nullptr, nullptr, nullptr, nullptr};  // qkv, attn_out, ffn_up, ffn_down
   float *b[4] = {nullptr, nullptr, nullptr, nullptr};
   float *ln[4] = {nullptr, nullptr, nullptr, nullptr};  // ln1.w, ln1.b, ln2.w, ln2.b
+  // int8 operands: [N, K] int8 panel, wscale [N], ias = 1/asmooth [K]
+  int8_t *wq[4] = {nullptr, nullptr, nullptr, nullptr};
+  float *ws[4] = {nullptr, nullptr, nullptr, nullptr};
+  float *ias[4] = {nullptr, nullptr, nullptr, nullptr};
 };
 
 enum Cat { CAT_GEMM = 0, CAT_ATTN = 1, CAT_LN = 2, CAT_OTHER = 3 };
@@ -56,10 +69,13 @@ struct mx_encoder {
   float *fin_ln[2] = {nullptr, nullptr};
   float *word = nullptr, *pos = nullptr, *type = nullptr;
   // workspace
-  int64_t ws_rows = 0, ws_batch = 0;
+  int64_t ws_rows = 0, ws_batch = 0, ws_mask_rows = 0;
   uint16_t *xb = nullptr, *qkv = nullptr, *ctxb = nullptr, *up = nullptr;
   uint16_t *proj = nullptr;
   float *emb = nullptr, *add_mask = nullptr;
+  int8_t *xq = nullptr;  // int8 datapath: quantised A and its row scales
+  float *sa = nullptr;
+  bool i8 = false;       // set by mx_encoder_ready: every GEMM operand is int8
   int32_t *kv_len = nullptr;
   // timing
   bool timing = false;
@@ -80,11 +96,6 @@ struct mx_encoder {
 
 namespace {
 
-void free_dev(void *&p) {
-  if (p) (void)hipFree(p);
-  p = nullptr;
-}
-
 template <typename T>
 void free_dev(T *&p) {
   if (p) (void)hipFree(p);
@@ -96,16 +107,29 @@ int dev_alloc(void **p, size_t bytes, const char *what) {
   return e == hipSuccess ? MX_OK : hip_fail(e, what);
 }
 
+int ensure_ws_rows(mx_encoder *enc, int64_t rows, int64_t B);
+int ensure_mask_ws(mx_encoder *enc, int64_t B, int64_t rows);
+
 int ensure_ws(mx_encoder *enc, int64_t B, int64_t S) {
   const int64_t rows = B * S;
+  if (rows > enc->ws_rows || (enc->i8 && !enc->xq)) {
+    const int64_t want = rows > enc->ws_rows ? rows : enc->ws_rows;
+    return ensure_ws_rows(enc, want, B);
+  }
+  return ensure_mask_ws(enc, B, rows);
+}
+
+int ensure_ws_rows(mx_encoder *enc, int64_t rows, int64_t B) {
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
-  if (rows > enc->ws_rows) {
+  {
     free_dev(enc->xb);
     free_dev(enc->qkv);
     free_dev(enc->ctxb);
     free_dev(enc->up);
     free_dev(enc->proj);
     free_dev(enc->emb);
+    free_dev(enc->xq);
+    free_dev(enc->sa);
     enc->ws_rows = 0;
     int rc = dev_alloc((void **)&enc->xb, rows * d * 2, "workspace xb");
     if (!rc) rc = dev_alloc((void **)&enc->qkv, rows * 3 * d * 2, "workspace qkv");
@@ -113,17 +137,29 @@ int ensure_ws(mx_encoder *enc, int64_t B, int64_t S) {
     if (!rc) rc = dev_alloc((void **)&enc->up, rows * f * 2, "workspace up");
     if (!rc) rc = dev_alloc((void **)&enc->proj, rows * d * 2, "workspace proj");
     if (!rc) rc = dev_alloc((void **)&enc->emb, rows * d * 4, "workspace emb");
+    if (!rc && enc->i8)
+      rc = dev_alloc((void **)&enc->xq, rows * (d > f ? d : f), "workspace xq");
+    if (!rc && enc->i8) rc = dev_alloc((void **)&enc->sa, rows * 4, "workspace sa");
     if (rc) return rc;
     enc->ws_rows = rows;
   }
-  if (B > enc->ws_batch || rows > enc->ws_rows) {
+  return ensure_mask_ws(enc, B, rows);
+}
+
+// The mask ([B, S] fp32) and kv_len ([B]) buffers, sized by their own
+// capacities: a longer sequence at the same batch needs a larger mask.
+int ensure_mask_ws(mx_encoder *enc, int64_t B, int64_t rows) {
+  if (B > enc->ws_batch || rows > enc->ws_mask_rows) {
+    const int64_t nb = B > enc->ws_batch ? B : enc->ws_batch;
+    const int64_t nr = rows > enc->ws_mask_rows ? rows : enc->ws_mask_rows;
     free_dev(enc->add_mask);
     free_dev(enc->kv_len);
-    enc->ws_batch = 0;
-    int rc = dev_alloc((void **)&enc->add_mask, rows * 4, "workspace mask");
-    if (!rc) rc = dev_alloc((void **)&enc->kv_len, B * 4, "workspace kv_len");
+    enc->ws_batch = enc->ws_mask_rows = 0;
+    int rc = dev_alloc((void **)&enc->add_mask, nr * 4, "workspace mask");
+    if (!rc) rc = dev_alloc((void **)&enc->kv_len, nb * 4, "workspace kv_len");
     if (rc) return rc;
-    enc->ws_batch = B;
+    enc->ws_batch = nb;
+    enc->ws_mask_rows = nr;
   }
   return MX_OK;
 }
@@ -186,6 +222,32 @@ int ln_l(mx_encoder *enc, mx_stream *s, const void *x, int x_dt, const void *y, 
   return e == hipSuccess ? MX_OK : hip_fail(e, "layernorm launch");
 }
 
+// The int8 datapath's three steps: the GEMM on the quantised A, the residual
+// LayerNorm that quantises its output for the next GEMM, and the quantise pass
+// over an activation another kernel produced (ctx, up).
+int gemm_i8_l(mx_encoder *enc, mx_stream *s, int site, int64_t M, int64_t K, const int8_t *Wq,
+              const float *ws, int64_t N, const float *bias, int epi, const float *resid,
+              void *C, int c_dtype) {
+  Bracket br(enc, s->stream, CAT_GEMM + 16 * site);
+  enc->gemm_flop += 2.0 * M * N * K;
+  enc->site_flop[site] += 2.0 * M * N * K;
+  return gemm_i8_checked(s, enc->xq, enc->sa, M, K, K, Wq, ws, N, bias, epi, resid, C, c_dtype,
+                         N);
+}
+
+int lnq_l(mx_encoder *enc, mx_stream *s, const float *x, const void *y, int y_dt, const float *g,
+          const float *b, int64_t rows, float *of, const float *ias) {
+  Bracket br(enc, s->stream, CAT_LN);
+  return layernorm_i8_checked(s, x, y, y_dt, g, b, enc->desc.ln_eps, rows, enc->desc.hidden, of,
+                              ias, enc->xq, enc->sa);
+}
+
+int quant_l(mx_encoder *enc, mx_stream *s, const uint16_t *a, int64_t rows, int64_t K,
+            const float *ias) {
+  Bracket br(enc, s->stream, CAT_OTHER);
+  return quantise_checked(s, a, MX_BF16, K, rows, K, ias, enc->xq, K, enc->sa);
+}
+
 int attn_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, const float *mask,
            const int32_t *kv_len) {
   Bracket br(enc, s->stream, CAT_ATTN);
@@ -195,26 +257,52 @@ int attn_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, const float *mas
                            enc->desc.attn_scale, mask, kv_len, enc->ctxb, d);
 }
 
+// One GEMM site of a layer on the encoder's datapath: bf16 A (A_bf) times
+// the bf16 panel, or the quantised A in xq/sa times the int8 operand.
+int site_gemm(mx_encoder *enc, mx_stream *s, const LayerW &w, int site, const uint16_t *A_bf,
+              int64_t M, int64_t K, int64_t N, int epi, const float *resid, void *C,
+              int c_dtype) {
+  if (enc->i8)
+    return gemm_i8_l(enc, s, site, M, K, w.wq[site], w.ws[site], N, w.b[site], epi, resid, C,
+                     c_dtype);
+  return gemm_l(enc, s, site, A_bf, M, K, w.w[site], N, w.b[site], epi, resid, C, c_dtype);
+}
+
+// The LayerNorm ahead of a GEMM: x (+ y) normalised into out_f32, and the
+// next GEMM's A -- bf16 into xb, or (int8) quantised with that GEMM's ias.
+// ias_next null on the int8 datapath: nothing follows, no A is written.
+int site_ln(mx_encoder *enc, mx_stream *s, float *x, const void *y, int y_dt, const float *g,
+            const float *b, int64_t M, float *out_f32, const float *ias_next) {
+  if (enc->i8 && ias_next) return lnq_l(enc, s, x, y, y_dt, g, b, M, out_f32, ias_next);
+  return ln_l(enc, s, x, MX_F32, y, y_dt, g, b, M, out_f32, enc->i8 ? nullptr : enc->xb);
+}
+
 int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
              int64_t B, int64_t S) {
   const int64_t M = B * S, d = enc->desc.hidden, f = enc->desc.ffn;
   const int epi = enc->desc.gelu == MX_GELU_ERF ? MX_EPI_GELU_ERF : MX_EPI_GELU_POLY;
-  int rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, enc->emb_ln[0], enc->emb_ln[1], M, x, enc->xb);
-  for (size_t l = 0; !rc && l < enc->layers.size(); ++l) {
+  const size_t L = enc->layers.size();
+  int rc = site_ln(enc, s, x, nullptr, MX_F32, enc->emb_ln[0], enc->emb_ln[1], M, x,
+                   enc->layers[0].ias[SITE_QKV]);
+  for (size_t l = 0; !rc && l < L; ++l) {
     const LayerW &w = enc->layers[l];
-    rc = gemm_l(enc, s, SITE_QKV, enc->xb, M, d, w.w[0], 3 * d, w.b[0], MX_EPI_NONE, nullptr, enc->qkv,
-                MX_BF16);
+    rc = site_gemm(enc, s, w, SITE_QKV, enc->xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->qkv,
+                   MX_BF16);
     if (!rc) rc = attn_l(enc, s, B, S, mask, kvl);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->ctxb, M, d, w.ias[SITE_AO]);
     if (!rc)
-      rc = gemm_l(enc, s, SITE_AO, enc->ctxb, M, d, w.w[1], d, w.b[1], MX_EPI_NONE, nullptr, enc->proj,
-                  MX_BF16);
-    if (!rc) rc = ln_l(enc, s, x, MX_F32, enc->proj, MX_BF16, w.ln[0], w.ln[1], M, x, enc->xb);
+      rc = site_gemm(enc, s, w, SITE_AO, enc->ctxb, M, d, d, MX_EPI_NONE, nullptr, enc->proj,
+                     MX_BF16);
     if (!rc)
-      rc = gemm_l(enc, s, SITE_UP, enc->xb, M, d, w.w[2], f, w.b[2], epi, nullptr, enc->up, MX_BF16);
+      rc = site_ln(enc, s, x, enc->proj, MX_BF16, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
+    if (!rc) rc = site_gemm(enc, s, w, SITE_UP, enc->xb, M, d, f, epi, nullptr, enc->up, MX_BF16);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->up, M, f, w.ias[SITE_DOWN]);
     if (!rc)
-      rc = gemm_l(enc, s, SITE_DOWN, enc->up, M, f, w.w[3], d, w.b[3], MX_EPI_NONE, nullptr, enc->proj,
-                  MX_BF16);
-    if (!rc) rc = ln_l(enc, s, x, MX_F32, enc->proj, MX_BF16, w.ln[2], w.ln[3], M, x, enc->xb);
+      rc = site_gemm(enc, s, w, SITE_DOWN, enc->up, M, f, d, MX_EPI_NONE, nullptr, enc->proj,
+                     MX_BF16);
+    if (!rc)
+      rc = site_ln(enc, s, x, enc->proj, MX_BF16, w.ln[2], w.ln[3], M, x,
+                   l + 1 < L ? enc->layers[l + 1].ias[SITE_QKV] : nullptr);
   }
   return rc;
 }
@@ -226,17 +314,17 @@ int run_preln(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const 
   int rc = MX_OK;
   for (size_t l = 0; !rc && l < enc->layers.size(); ++l) {
     const LayerW &w = enc->layers[l];
-    rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, w.ln[0], w.ln[1], M, nullptr, enc->xb);
+    rc = site_ln(enc, s, x, nullptr, MX_F32, w.ln[0], w.ln[1], M, nullptr, w.ias[SITE_QKV]);
     if (!rc)
-      rc = gemm_l(enc, s, SITE_QKV, enc->xb, M, d, w.w[0], 3 * d, w.b[0], MX_EPI_NONE, nullptr, enc->qkv,
-                  MX_BF16);
+      rc = site_gemm(enc, s, w, SITE_QKV, enc->xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->qkv,
+                     MX_BF16);
     if (!rc) rc = attn_l(enc, s, B, S, mask, kvl);
-    if (!rc)
-      rc = gemm_l(enc, s, SITE_AO, enc->ctxb, M, d, w.w[1], d, w.b[1], MX_EPI_NONE, x, x, MX_F32);
-    if (!rc) rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, w.ln[2], w.ln[3], M, nullptr, enc->xb);
-    if (!rc)
-      rc = gemm_l(enc, s, SITE_UP, enc->xb, M, d, w.w[2], f, w.b[2], epi, nullptr, enc->up, MX_BF16);
-    if (!rc) rc = gemm_l(enc, s, SITE_DOWN, enc->up, M, f, w.w[3], d, w.b[3], MX_EPI_NONE, x, x, MX_F32);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->ctxb, M, d, w.ias[SITE_AO]);
+    if (!rc) rc = site_gemm(enc, s, w, SITE_AO, enc->ctxb, M, d, d, MX_EPI_NONE, x, x, MX_F32);
+    if (!rc) rc = site_ln(enc, s, x, nullptr, MX_F32, w.ln[2], w.ln[3], M, nullptr, w.ias[SITE_UP]);
+    if (!rc) rc = site_gemm(enc, s, w, SITE_UP, enc->xb, M, d, f, epi, nullptr, enc->up, MX_BF16);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->up, M, f, w.ias[SITE_DOWN]);
+    if (!rc) rc = site_gemm(enc, s, w, SITE_DOWN, enc->up, M, f, d, MX_EPI_NONE, x, x, MX_F32);
   }
   if (!rc) rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, enc->fin_ln[0], enc->fin_ln[1], M, x, nullptr);
   return rc;
@@ -318,6 +406,26 @@ int front_gemm(mx_encoder *enc, mx_stream *s, const uint16_t *A, int64_t lda, in
 
 const char *kGemmNames[4] = {"qkv", "attn_out", "ffn_up", "ffn_down"};
 
+// A row-major int8 [K, N] operand -> a new [N, K] device panel.
+int stage_i8_panel(mx_ctx *ctx, const int8_t *kn, int64_t K, int64_t N, int8_t **out) {
+  if (K % 16)
+    return fail(MX_E_INVALID, "int8 operand: K = " + std::to_string(K) +
+                                  " is not a multiple of 16");
+  std::vector<int8_t> panel(static_cast<size_t>(K) * N);
+  for (int64_t k = 0; k < K; ++k)
+    for (int64_t n = 0; n < N; ++n)
+      panel[static_cast<size_t>(n) * K + k] = kn[static_cast<size_t>(k) * N + n];
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, panel.size());
+  if (e == hipSuccess) e = hipMemcpy(p, panel.data(), panel.size(), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    if (p) (void)hipFree(p);
+    return hip_fail(e, "int8 operand upload");
+  }
+  *out = static_cast<int8_t *>(p);
+  return MX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -374,6 +482,9 @@ void mx_encoder_destroy(mx_encoder *enc) {
         for (auto &p : l.w) free_dev(p);
         for (auto &p : l.b) free_dev(p);
         for (auto &p : l.ln) free_dev(p);
+        for (auto &p : l.wq) free_dev(p);
+        for (auto &p : l.ws) free_dev(p);
+        for (auto &p : l.ias) free_dev(p);
       }
       for (auto &p : enc->emb_ln) free_dev(p);
       for (auto &p : enc->fin_ln) free_dev(p);
@@ -395,6 +506,8 @@ void mx_encoder_destroy(mx_encoder *enc) {
     free_dev(enc->up);
     free_dev(enc->proj);
     free_dev(enc->emb);
+    free_dev(enc->xq);
+    free_dev(enc->sa);
     free_dev(enc->add_mask);
     free_dev(enc->kv_len);
     free_dev(enc->f_rows);
@@ -428,6 +541,7 @@ int mx_encoder_clone(mx_encoder *enc, mx_encoder **out) {
   c->desc = enc->desc;
   c->owns_weights = false;
   c->layers = enc->layers;
+  c->i8 = enc->i8;
   for (int i = 0; i < 2; ++i) {
     c->emb_ln[i] = enc->emb_ln[i];
     c->fin_ln[i] = enc->fin_ln[i];
@@ -458,16 +572,19 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
   if (rc) return rc;
   const std::string name(name_c);
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
+  auto put_f32_from = [&](float *&dst, const void *src, int64_t want) -> int {
+    free_dev(dst);
+    int r = dev_alloc((void **)&dst, want * 4, name.c_str());
+    if (r) return r;
+    const hipError_t e = hipMemcpy(dst, src, want * 4, hipMemcpyHostToDevice);
+    return e == hipSuccess ? MX_OK : hip_fail(e, name.c_str());
+  };
   auto put_f32 = [&](float *&dst, int64_t want) -> int {
     if (dtype != MX_F32) return fail(MX_E_INVALID, name + ": must be MX_F32");
     if (count != want)
       return fail(MX_E_INVALID, name + ": " + std::to_string(count) + " values, " +
                                     std::to_string(want) + " wanted");
-    free_dev(dst);
-    int r = dev_alloc((void **)&dst, want * 4, name.c_str());
-    if (r) return r;
-    const hipError_t e = hipMemcpy(dst, host, want * 4, hipMemcpyHostToDevice);
-    return e == hipSuccess ? MX_OK : hip_fail(e, name.c_str());
+    return put_f32_from(dst, host, want);
   };
   if (name.rfind("layer.", 0) == 0) {
     size_t p = 6;
@@ -492,14 +609,39 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
           return fail(MX_E_INVALID, name + ": " + std::to_string(count) + " values, a [" +
                                         std::to_string(K[i]) + ", " + std::to_string(N[i]) +
                                         "] operand wanted");
+        if (dtype == MX_I8) {
+          // An int8 design's operand: its wscale and asmooth come by their
+          // own names; the datapath is chosen by mx_encoder_ready.
+          int8_t *panel = nullptr;
+          int r = stage_i8_panel(enc->ctx, static_cast<const int8_t *>(host), K[i], N[i], &panel);
+          if (r) return r;
+          free_dev(w.w[i]);
+          free_dev(w.wq[i]);
+          w.wq[i] = panel;
+          return MX_OK;
+        }
         uint16_t *panel = nullptr;
         int r = stage_panel(enc->ctx, host, dtype, K[i], N[i], &panel);
         if (r) return r;
         free_dev(w.w[i]);
+        free_dev(w.wq[i]);
         w.w[i] = panel;
         return MX_OK;
       }
       if (rest == std::string(kGemmNames[i]) + ".bias") return put_f32(w.b[i], N[i]);
+      if (rest == std::string(kGemmNames[i]) + ".wscale") return put_f32(w.ws[i], N[i]);
+      if (rest == std::string(kGemmNames[i]) + ".asmooth") {
+        // Kept as its reciprocal, computed once here in fp32 as the reference
+        // does per operand (bert_encoder.cpp:764-772).
+        if (dtype != MX_F32) return fail(MX_E_INVALID, name + ": must be MX_F32");
+        if (count != K[i])
+          return fail(MX_E_INVALID, name + ": " + std::to_string(count) + " values, " +
+                                        std::to_string(K[i]) + " wanted");
+        std::vector<float> ias(static_cast<size_t>(K[i]));
+        const float *a = static_cast<const float *>(host);
+        for (int64_t k = 0; k < K[i]; ++k) ias[k] = 1.0f / a[k];
+        return put_f32_from(w.ias[i], ias.data(), K[i]);
+      }
     }
     if (rest == "ln1.weight") return put_f32(w.ln[0], d);
     if (rest == "ln1.bias") return put_f32(w.ln[1], d);
@@ -589,11 +731,24 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
 
 int mx_encoder_ready(mx_encoder *enc) {
   if (!enc) return fail(MX_E_INVALID, "encoder_ready: null encoder");
+  // The datapath is the first operand's: bf16, or int8 (BertEncoder's
+  // int8 design set). A stack mixing the two is refused by name.
+  const bool i8 = !enc->layers.empty() && enc->layers[0].wq[0] != nullptr;
   for (size_t l = 0; l < enc->layers.size(); ++l) {
     const LayerW &w = enc->layers[l];
     const std::string p = "layer." + std::to_string(l) + ".";
     for (int i = 0; i < 4; ++i) {
-      if (!w.w[i]) return fail(MX_E_STATE, "encoder: " + p + kGemmNames[i] + " was never set");
+      if (!w.w[i] && !w.wq[i])
+        return fail(MX_E_STATE, "encoder: " + p + kGemmNames[i] + " was never set");
+      if (i8 != (w.wq[i] != nullptr))
+        return fail(MX_E_STATE, "encoder: " + p + kGemmNames[i] + " is " +
+                                    (i8 ? "bf16" : "int8") + " but layer.0.qkv is " +
+                                    (i8 ? "int8" : "bf16") +
+                                    "; the stack runs one datapath (repack the container)");
+      if (i8 && !w.ws[i])
+        return fail(MX_E_STATE, "encoder: " + p + kGemmNames[i] + ".wscale was never set");
+      if (i8 && !w.ias[i])
+        return fail(MX_E_STATE, "encoder: " + p + kGemmNames[i] + ".asmooth was never set");
       if (!w.b[i])
         return fail(MX_E_STATE, "encoder: " + p + kGemmNames[i] + ".bias was never set");
     }
@@ -619,6 +774,7 @@ int mx_encoder_ready(mx_encoder *enc) {
                      : !enc->front_pos ? "position" : nullptr;
     if (miss) return fail(MX_E_STATE, std::string("encoder: ") + miss + " was never set");
   }
+  enc->i8 = i8;
   return MX_OK;
 }
 
@@ -963,20 +1119,58 @@ int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
       if (!t.logical.empty() && t.logical != t.padded)
         return refuse(fail(MX_E_INVALID, n + ": logical and padded shapes differ; the GEMM "
                                              "needs them equal (repack)"));
-      if (t.dtype == "I8" || t.dtype == "I4")
-        return refuse(fail(MX_E_UNSUPPORTED, n + ": " + t.dtype + " operand -- the int8 "
-                                                 "datapath is not built in this backend"));
-      if (t.dtype != "BF16" || !t.block_panel)
+      if (t.dtype == "I4")
+        return refuse(fail(MX_E_UNSUPPORTED, n + ": I4 operand -- the int4 container's nibble "
+                                             "widening is not built in this backend"));
+      const bool i8 = t.dtype == "I8";
+      if ((t.dtype != "BF16" && !i8) || !t.block_panel)
         return refuse(fail(MX_E_INVALID, n + ": " + t.dtype + " without a block_panel "
-                                             "layout; a pre-tiled BF16 operand is wanted"));
+                                             "layout; a pre-tiled BF16 or I8 operand is wanted"));
       const int64_t K = t.padded[0], N = t.padded[1];
-      if (t.nbytes != static_cast<uint64_t>(K * N * 2))
+      if (t.nbytes != static_cast<uint64_t>(K * N * (i8 ? 1 : 2)))
         return refuse(fail(MX_E_INVALID, n + ": " + std::to_string(t.nbytes) + " bytes for a [" +
                                              std::to_string(K) + "," + std::to_string(N) +
-                                             "] bf16 operand"));
-      rc = mx_encoder_set_panel(enc, n.c_str(), static_cast<const uint16_t *>(t.data), K, N,
-                                t.tile_k, t.tile_n, t.mac_s, t.mac_t);
+                                             "] " + (i8 ? "int8" : "bf16") + " operand"));
+      if (!i8) {
+        rc = mx_encoder_set_panel(enc, n.c_str(), static_cast<const uint16_t *>(t.data), K, N,
+                                  t.tile_k, t.tile_n, t.mac_s, t.mac_t);
+        if (rc) return refuse(rc);
+        continue;
+      }
+      // An int8 design's operand (tools/lib/gemm_i8.py's scheme): the panel,
+      // its per-column .wscale and per-row .asmooth, all from the mapping.
+      const TensorRecView ws = npue_tensor(f, n + ".wscale");
+      const TensorRecView sm = npue_tensor(f, n + ".asmooth");
+      if (!ws.found || !sm.found)
+        return refuse(fail(MX_E_INVALID, n + ": an I8 operand without its " +
+                                             (ws.found ? ".asmooth" : ".wscale") +
+                                             " -- the container is not a complete int8 pack"));
+      if (ws.dtype != "F32" || sm.dtype != "F32" || ws.nbytes != static_cast<uint64_t>(N * 4) ||
+          sm.nbytes != static_cast<uint64_t>(K * 4))
+        return refuse(fail(MX_E_INVALID, n + ": .wscale must be F32 [" + std::to_string(N) +
+                                             "] and .asmooth F32 [" + std::to_string(K) + "]"));
+      I8Operand op;
+      rc = stage_i8(ctx, static_cast<const int8_t *>(t.data), static_cast<const float *>(ws.data),
+                    static_cast<const float *>(sm.data), K, N, t.tile_k, t.tile_n, t.mac_s,
+                    t.mac_t, &op);
       if (rc) return refuse(rc);
+      const int64_t d = enc->desc.hidden, fw = enc->desc.ffn;
+      const int64_t Ks[4] = {d, d, d, fw}, Ns[4] = {3 * d, d, fw, d};
+      if (K != Ks[i] || N != Ns[i]) {
+        free_i8(op);
+        return refuse(fail(MX_E_INVALID, n + ": a [" + std::to_string(K) + ", " +
+                                             std::to_string(N) + "] operand, a [" +
+                                             std::to_string(Ks[i]) + ", " +
+                                             std::to_string(Ns[i]) + "] one wanted"));
+      }
+      LayerW &w = enc->layers[static_cast<size_t>(L)];
+      free_dev(w.w[i]);
+      free_dev(w.wq[i]);
+      free_dev(w.ws[i]);
+      free_dev(w.ias[i]);
+      w.wq[i] = op.wq;
+      w.ws[i] = op.wscale;
+      w.ias[i] = op.ias;
     }
   if ((rc = mx_encoder_ready(enc))) return refuse(rc);
   *out = enc;

@@ -19,8 +19,11 @@ int fail(int code, const std::string &msg);
 int hip_fail(hipError_t e, const char *what);
 
 struct WeightSlot {
-  uint16_t *wt = nullptr;  // [N, K] bf16
+  uint16_t *wt = nullptr;  // [N, K] bf16 (a bf16 operand)
   int64_t K = 0, N = 0;
+  int8_t *wq = nullptr;     // [N, K] int8 (an int8 operand; wt is then null)
+  float *wscale = nullptr;  // int8: per-column scale [N]
+  float *ias = nullptr;     // int8: 1 / asmooth [K]
 };
 
 }  // namespace mx
@@ -53,6 +56,27 @@ int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t 
 int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
                       int64_t H, int64_t hd, float scale, const float *add_mask,
                       const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx);
+// An int8 operand on the device: the [K, N] weight as an [N, K] int8 panel
+// (from row-major int8, or untiled from a container's block panel when tile_k
+// > 0), wscale [N] copied, ias = 1 / asmooth [K] computed once in fp32.
+struct I8Operand {
+  int8_t *wq = nullptr;
+  float *wscale = nullptr, *ias = nullptr;
+};
+int stage_i8(mx_ctx *ctx, const int8_t *kn_host, const float *wscale_host,
+             const float *asmooth_host, int64_t K, int64_t N, int64_t tile_k, int64_t tile_n,
+             int64_t mac_s, int64_t mac_t, I8Operand *out);
+void free_i8(I8Operand &op);
+int gemm_i8_checked(mx_stream *s, const int8_t *A, const float *a_scale, int64_t M, int64_t K,
+                    int64_t lda, const int8_t *Wt, const float *wscale, int64_t N,
+                    const float *bias, int epilogue, const float *residual, void *C,
+                    int c_dtype, int64_t ldc);
+int quantise_checked(mx_stream *s, const void *a, int a_dtype, int64_t lda, int64_t rows,
+                     int64_t K, const float *ias, int8_t *q, int64_t ldq, float *a_scale);
+int layernorm_i8_checked(mx_stream *s, const float *x, const void *y, int y_dtype,
+                         const float *gamma, const float *beta, float eps, int64_t rows,
+                         int64_t cols, float *out_f32, const float *ias, int8_t *q,
+                         float *a_scale);
 // Read and clear the stream's data-refusal flag (synchronises the stream).
 int take_data_error(mx_stream *s, int *flags);
 

@@ -50,10 +50,51 @@ struct GemmArgs {
 };
 hipError_t gemm(const GemmArgs &a, hipStream_t s);
 
+// The LDS-pipelined kernel's tile for an M x N product (0: 256x256, 1: 256x192,
+// 2: 128x256, 3: 128x128) and the resident blocks of a persistent launch.
+int gemm_lds_tile(int64_t M, int64_t N);
+int cu_count();
+
+// int8 W8A8 (k_gemm_i8.hip): C[M,N] = epi(fma(float(Aq @ Wq^T) * a_scale[m],
+// wscale[n], bias[n])) (+ residual), or the raw int32 product (c_dtype 2).
+// Requires K % 64 == 0, K >= 256, N % 4 == 0, lda % 16 == 0, 16-byte aligned
+// operands and vectors.
+struct GemmI8Args {
+  const int8_t *A;
+  int64_t lda;
+  const int8_t *Wt;  // [N, K], row stride K
+  int64_t M, N, K;
+  const float *a_scale;  // [M]
+  const float *wscale;   // [N]
+  const float *bias;     // [N] or null
+  int epilogue;          // mx_epilogue
+  const float *residual; // fp32, row stride ldc, or null
+  void *C;
+  int c_dtype;  // 0 fp32, 1 bf16, 2 int32 (raw accumulators)
+  int64_t ldc;
+};
+hipError_t gemm_i8(const GemmI8Args &a, hipStream_t s);
+
+// quantise_a_int8 over rows of K (k_quant.hip): a fp32 or bf16 (row stride
+// lda), ias [K] -> q int8 (row stride ldq) and a_scale [rows]. K % 4 == 0,
+// K <= 8192.
+hipError_t quantise_rows(const void *a, int a_bf, int64_t lda, int64_t rows, int64_t K,
+                         const float *ias, int8_t *q, int64_t ldq, float *a_scale,
+                         hipStream_t s);
+// add_norm_quant: LayerNorm(x + y) -> out_f32 (nullable) and its quantisation
+// with ias -> q, a_scale. cols % 4 == 0, cols <= 4096.
+hipError_t layernorm_quant(const float *x, const void *y, int y_bf, const float *gamma,
+                           const float *beta, float eps, int64_t rows, int64_t cols,
+                           float *out_f32, const float *ias, int8_t *q, float *a_scale,
+                           hipStream_t s);
+int quant_groups(int64_t K);
+
 // Container operand tiled (tile_k, tile_n) with (mac_s, mac_t) sub-tiles ->
 // [N, K] panel (k_panel.hip). Shapes checked by the caller.
 hipError_t untile_panel(const uint16_t *panel, int64_t K, int64_t N, int tile_k, int tile_n,
                         int mac_s, int mac_t, uint16_t *wt, hipStream_t s);
+hipError_t untile_panel_i8(const int8_t *panel, int64_t K, int64_t N, int tile_k, int tile_n,
+                           int mac_s, int mac_t, int8_t *wt, hipStream_t s);
 // Tile configuration the launcher would pick (for tests and reports).
 const char *gemm_config_name(int64_t M, int64_t N, int64_t K);
 

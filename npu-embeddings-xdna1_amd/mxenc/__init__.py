@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(HERE), "_build", "libmx_encoder.so")
 
 MX_OK = 0
-MX_F32, MX_BF16, MX_I32 = 0, 1, 2
+MX_F32, MX_BF16, MX_I32, MX_I8 = 0, 1, 2, 3
 MX_EPI_NONE, MX_EPI_GELU_POLY, MX_EPI_GELU_ERF = 0, 1, 2
 MX_GELU_POLY, MX_GELU_ERF, MX_GELU_ERF_AS = 0, 1, 2
 MX_SOFTMAX_POLY, MX_SOFTMAX_EXACT, MX_SOFTMAX_AIE = 0, 1, 2
@@ -125,6 +125,17 @@ SIGNATURES = {
     "mx_embed_service_create": (_int, [_vp, _int, _i64, _i64, ctypes.POINTER(_vp)]),
     "mx_embed_service_destroy": (None, [_vp]),
     "mx_embed_service_embed": (_int, [_vp, _vp, _vp, _i64, _vp]),
+    "mx_stage_weight_i8": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, ctypes.POINTER(_int)]),
+    "mx_stage_weight_panel_i8": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        ctypes.POINTER(_int)]),
+    "mx_weight_i8_scales": (_int, [_vp, _int, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
+    "mx_quantise_a_int8": (_int, [_vp, _vp, _int, _i64, _i64, _vp, _vp, _vp]),
+    "mx_gemm_i8": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp, _int, _vp, _vp, _int,
+                          _i64]),
+    "mx_gemm_i8_wt": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _int, _vp,
+                             _vp, _int, _i64]),
+    "mx_layernorm_i8": (_int, [_vp, _vp, _vp, _int, _vp, _vp, ctypes.c_float, _i64, _i64, _vp,
+                               _vp, _vp, _vp]),
 }
 
 _lib = None
@@ -159,6 +170,8 @@ def _np_dtype_code(a):
         return MX_BF16
     if a.dtype == np.int32:
         return MX_I32
+    if a.dtype == np.int8:
+        return MX_I8
     raise TypeError(a.dtype)
 
 
@@ -278,6 +291,51 @@ def attention(ctx, qkv, ld_qkv, B, S, H, hd, scale, mask, kv_len, out, ld_out):
                              _p(kv_len), _p(out), ld_out))
 
 
+# ---- the int8 (W8A8) datapath ----------------------------------------------------
+
+def stage_weight_i8(ctx, wq_kn, wscale, asmooth):
+    """An int8 [K, N] operand with its scales -> a context weight slot."""
+    q = np.ascontiguousarray(wq_kn, dtype=np.int8)
+    ws = np.ascontiguousarray(wscale, dtype=np.float32)
+    sm = np.ascontiguousarray(asmooth, dtype=np.float32)
+    K, N = q.shape
+    assert ws.shape == (N,) and sm.shape == (K,)
+    slot = _int()
+    check(lib().mx_stage_weight_i8(ctx.handle, q.ctypes.data, ws.ctypes.data, sm.ctypes.data,
+                                   K, N, ctypes.byref(slot)))
+    return slot.value
+
+
+def weight_i8_scales(ctx, slot):
+    """(wscale, ias) device pointers of a staged int8 operand."""
+    ws, ias = _vp(), _vp()
+    check(lib().mx_weight_i8_scales(ctx.handle, slot, ctypes.byref(ws), ctypes.byref(ias)))
+    return ws, ias
+
+
+def quantise_a_int8(ctx, a, rows, K, ias, q, a_scale):
+    check(lib().mx_quantise_a_int8(ctx.stream, _p(a), _np_dtype_code(np.empty(0, a.dtype)), rows,
+                                   K, _p(ias), _p(q), _p(a_scale)))
+
+
+def gemm_i8(ctx, A, a_scale, M, K, lda, slot, bias, epilogue, residual, C, ldc):
+    cd = _np_dtype_code(np.empty(0, C.dtype))
+    check(lib().mx_gemm_i8(ctx.stream, _p(A), _p(a_scale), M, K, lda, slot, _p(bias), epilogue,
+                           _p(residual), _p(C), cd, ldc))
+
+
+def gemm_i8_wt(ctx, A, a_scale, M, K, lda, Wt, wscale, N, bias, epilogue, residual, C, ldc):
+    cd = _np_dtype_code(np.empty(0, C.dtype))
+    check(lib().mx_gemm_i8_wt(ctx.stream, _p(A), _p(a_scale), M, K, lda, _p(Wt), _p(wscale), N,
+                              _p(bias), epilogue, _p(residual), _p(C), cd, ldc))
+
+
+def layernorm_i8(ctx, x, y, gamma, beta, eps, rows, cols, out_f32, ias, q, a_scale):
+    yd = _np_dtype_code(np.empty(0, y.dtype)) if y is not None else MX_F32
+    check(lib().mx_layernorm_i8(ctx.stream, _p(x), _p(y), yd, _p(gamma), _p(beta), eps, rows,
+                                cols, _p(out_f32), _p(ias), _p(q), _p(a_scale)))
+
+
 def to_bf16_bits(x):
     """fp32 -> bf16 bit patterns by the reference's to_bf16 formula."""
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
@@ -342,9 +400,11 @@ class Encoder:
     """An mx_encoder loaded from a synthetic model dict (mxenc.synth)."""
 
     def __init__(self, ctx, m, gelu=None, ln_eps=None, attn_scale=1.0, cls_pool=None,
-                 l2_normalize=True, front=True):
+                 l2_normalize=True, front=True, int8=None):
         """front: load the ViT / Whisper front end (and ViT head) when the model
-        has one; False builds the layer body only (mx_encoder_run)."""
+        has one; False builds the layer body only (mx_encoder_run). int8: the
+        model's int8 operands (synth.quantise_model) -- the stack then runs the
+        W8A8 datapath."""
         self.ctx = ctx
         self.m = m
         bert = m["kind"] == "bert"
@@ -373,8 +433,14 @@ class Encoder:
         names = [("qkv", "w_qkv", "b_qkv"), ("attn_out", "w_ao", "b_ao"),
                  ("ffn_up", "w_up", "b_up"), ("ffn_down", "w_down", "b_down")]
         for l in range(m["layers"]):
-            for n, w, b in names:
-                self.set(f"layer.{l}.{n}", m[w][l])
+            for i, (n, w, b) in enumerate(names):
+                if int8 is not None:
+                    q, ws, sm = int8[i]
+                    self.set(f"layer.{l}.{n}", q[l])
+                    self.set(f"layer.{l}.{n}.wscale", ws[l])
+                    self.set(f"layer.{l}.{n}.asmooth", sm[l])
+                else:
+                    self.set(f"layer.{l}.{n}", m[w][l])
                 self.set(f"layer.{l}.{n}.bias", m[b][l])
             self.set(f"layer.{l}.ln1.weight", m["ln1_g"][l])
             self.set(f"layer.{l}.ln1.bias", m["ln1_b"][l])

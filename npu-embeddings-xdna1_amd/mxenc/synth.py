@@ -156,3 +156,40 @@ def make_mel(cfg, seed=SEED + 3, batch=None):
     rng = np.random.default_rng(seed)
     B = batch or cfg["batch"]
     return rng.standard_normal(size=(B, cfg["mels"], cfg["frames"]), dtype=np.float32)
+
+
+def quantise_weights(w_kn, asmooth=None):
+    """The reference packer's int8 operand scheme (tools/lib/gemm_i8.py:21-90):
+    W' = W * asmooth[:, None] (the SmoothQuant fold), per column
+    s = max_k |W'| / 127 (1 for an all-zero column), q = rint(W' / s) clipped
+    to [-127, 127]. Returns (q int8 [K, N], s fp32 [N])."""
+    w = np.asarray(w_kn, np.float32)
+    if asmooth is not None:
+        w = w * np.asarray(asmooth, np.float32)[:, None]
+    s = (np.abs(w).max(axis=0) / np.float32(127.0)).astype(np.float32)
+    s = np.where(s > 0, s, np.float32(1.0)).astype(np.float32)
+    q = np.rint(w / s[None, :]).clip(-127, 127).astype(np.int8)
+    return q, s
+
+
+GEMM_KEYS = ("w_qkv", "w_ao", "w_up", "w_down")
+
+
+def quantise_model(m, seed=SEED + 7, smooth=(0.5, 2.0)):
+    """The int8 operands of a synthetic encoder, as an --int8 pack would carry
+    them: per GEMM site a tuple (q [L, K, N] int8, wscale [L, N], asmooth
+    [L, K]), the smoothing factors drawn uniform in `smooth` (None: all ones).
+    Sites in the order qkv, attn_out, ffn_up, ffn_down."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for key in GEMM_KEYS:
+        W = m[key]
+        L, K, _ = W.shape
+        if smooth is None:
+            sm = np.ones((L, K), np.float32)
+        else:
+            sm = rng.uniform(smooth[0], smooth[1], (L, K)).astype(np.float32)
+        qs, ss = zip(*[quantise_weights(W[l], sm[l]) for l in range(L)])
+        out.append((np.ascontiguousarray(np.stack(qs)), np.ascontiguousarray(np.stack(ss)),
+                    np.ascontiguousarray(sm)))
+    return out

@@ -88,6 +88,17 @@ class Container:
         return self.add(name, flat, "BF16", "gemm_b", list(kn.shape),
                         layout=panel_layout(tile_k, tile_n, mac_s, mac_t))
 
+    def add_gemm_i8(self, name, q_kn, wscale, asmooth, tile_k, tile_n, mac_s, mac_t):
+        """An int8 design's operand (tools/lib/gemm_i8.py:21-90): the [K, N] int8
+        panel pre-tiled with an I8 layout, then .wscale [N] and .asmooth [K]."""
+        q_kn = np.asarray(q_kn, np.int8)
+        K, N = q_kn.shape
+        flat = tile_panel(q_kn, tile_k, tile_n, mac_s, mac_t)
+        self.add(name, flat, "I8", "gemm_b", [K, N],
+                 layout=panel_layout(tile_k, tile_n, mac_s, mac_t, dtype="I8"))
+        self.add_f32(name + ".wscale", wscale, "quant_scale")
+        self.add_f32(name + ".asmooth", asmooth, "quant_smooth")
+
     def write(self, path, version=1, magic=b"NPUE", data_align=ALIGN, raw_json=None,
               trailing=b""):
         """raw_json (bytes) replaces the directory; trailing bytes are appended
@@ -110,10 +121,11 @@ class Container:
 
 
 def bert_container(m, tile_k=64, tile_n=64, mac=(8, 8), arch="bert_abs_gelu_postln",
-                   pooling=None, extra_config=None):
+                   pooling=None, extra_config=None, int8=None):
     """A BERT container of a synthetic model dict (mxenc.synth.make_model):
     the packer's tensor names, roles and config keys
-    (tools/pack/pack_npue.py:2630-2760)."""
+    (tools/pack/pack_npue.py:2630-2760). int8: the model's int8 operands
+    (mxenc.synth.quantise_model) -- the container is then an --int8 pack."""
     d, f, L = m["hidden"], m["ffn"], m["layers"]
     cfg = {"arch": arch, "source_repo": "synthetic/bert", "source_sha256": "0" * 64,
            "num_layers": L, "num_heads": m["heads"], "hidden": d, "head_dim": m["head_dim"],
@@ -122,7 +134,7 @@ def bert_container(m, tile_k=64, tile_n=64, mac=(8, 8), arch="bert_abs_gelu_post
            "pooling": pooling or ("cls" if m.get("cls_pool") else "mean"),
            "l2_normalize": True, "activation": "gelu_erf_exact", "gemm_layout": "pretiled_bf16",
            "tile_k": tile_k, "tile_n": tile_n, "mac_s": mac[0], "mac_t": mac[1],
-           "a_dtype": "bf16",
+           "a_dtype": "i8" if int8 else "bf16",
            "fusions": {"qkv_fused": True, "transposed_to_kn": True,
                        "qk_scale_folded_into_q": True}}
     cfg.update(extra_config or {})
@@ -135,8 +147,13 @@ def bert_container(m, tile_k=64, tile_n=64, mac=(8, 8), arch="bert_abs_gelu_post
     names = [("qkv", "w_qkv", "b_qkv"), ("attn_out", "w_ao", "b_ao"),
              ("ffn_up", "w_up", "b_up"), ("ffn_down", "w_down", "b_down")]
     for l in range(L):
-        for n, w, b in names:
-            c.add_gemm(f"layer.{l}.{n}", m[w][l], tile_k, tile_n, mac[0], mac[1])
+        for i, (n, w, b) in enumerate(names):
+            if int8:
+                q, ws, sm = int8[i]
+                c.add_gemm_i8(f"layer.{l}.{n}", q[l], ws[l], sm[l], tile_k, tile_n, mac[0],
+                              mac[1])
+            else:
+                c.add_gemm(f"layer.{l}.{n}", m[w][l], tile_k, tile_n, mac[0], mac[1])
             c.add_f32(f"layer.{l}.{n}.bias", m[b][l], "bias")
         for n, key in (("ln1.weight", "ln1_g"), ("ln1.bias", "ln1_b"),
                        ("ln2.weight", "ln2_g"), ("ln2.bias", "ln2_b")):

@@ -169,13 +169,7 @@ def aligned_empty(shape, dtype, align=64):
 
 
 def quantise_weights(w_kn, asmooth=None):
-    """The packer's int8 operand scheme (tools/lib/gemm_i8.py:21-90): per column
-    s = max_k |W*asmooth| / 127 (1 for an all-zero column), q = rint(W/s)
-    clipped to [-127, 127]. Returns (q int8 [K, N], s fp32 [N])."""
-    w = np.asarray(w_kn, np.float32)
-    if asmooth is not None:
-        w = w * np.asarray(asmooth, np.float32)[:, None]
-    s = (np.abs(w).max(axis=0) / np.float32(127.0)).astype(np.float32)
-    s = np.where(s > 0, s, np.float32(1.0)).astype(np.float32)
-    q = np.rint(w / s[None, :]).clip(-127, 127).astype(np.int8)
-    return q, s
+    """The packer's int8 operand scheme (tools/lib/gemm_i8.py:21-90), as the
+    synthetic-model generator implements it."""
+    from mxenc import synth
+    return synth.quantise_weights(w_kn, asmooth)

@@ -106,16 +106,28 @@ def test_encoder_from_npue_refusals(tmp_path, ctx, over, why):
     f.close()
 
 
-def test_encoder_from_npue_refuses_int8_and_missing_tensors(tmp_path, ctx):
+def test_encoder_from_npue_refuses_int4_mixed_and_missing_tensors(tmp_path, ctx):
     m = synth.make_model("minilm", layers=1)
     c = nw.bert_container(m, 64, 64, (8, 8))
     for e in c.entries:
         if e["name"] == "layer.0.attn_out":
-            e["dtype"] = "I8"
-    path = str(tmp_path / "i8.npue")
+            e["dtype"] = "I4"
+    path = str(tmp_path / "i4.npue")
     c.write(path)
     f = mxenc.Npue(path)
-    with pytest.raises(mxenc.MxError, match="int8 datapath"):
+    with pytest.raises(mxenc.MxError, match="I4 operand"):
+        mxenc.Encoder.from_npue(ctx, f)
+    f.close()
+    # an int8 operand among bf16 ones: one datapath per stack
+    q8 = synth.quantise_model(m)
+    c = nw.bert_container(m, 64, 64, (8, 8))
+    c.entries = [e for e in c.entries if e["name"] != "layer.0.attn_out"]
+    q, ws, sm = q8[1]
+    c.add_gemm_i8("layer.0.attn_out", q[0], ws[0], sm[0], 64, 64, 8, 8)
+    path = str(tmp_path / "mixed.npue")
+    c.write(path)
+    f = mxenc.Npue(path)
+    with pytest.raises(mxenc.MxError, match="one datapath"):
         mxenc.Encoder.from_npue(ctx, f)
     f.close()
     c = nw.bert_container(m, 64, 64, (8, 8))
