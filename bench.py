@@ -1,7 +1,7 @@
 """Throughput of the encoder hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config bge_base]
-                    [--no-cpu-baseline]
+                    [--int8] [--no-cpu-baseline]
 
 A step is one pass of the hot path over one batch: token ids and the
 attention mask (already in HBM) -> embedding sum -> the whole encoder stack ->
@@ -12,6 +12,8 @@ bge-base geometry at batch 64 x seq 512 by default. Weights are random-init
 Prints one JSON line: sequences/s, the GEMM family's MFMA roofline (HIP event
 time of every GEMM launch in the timed steps, on the stream they run on), and
 the oracle's host path timed on a bounded sample of the same workload.
+--int8 runs a BERT config on the W8A8 datapath (the packer's int8 operand
+scheme over the same random weights); its roofline is the int8 MFMA peak.
 """
 import argparse
 import json
@@ -24,18 +26,23 @@ sys.path.insert(0, os.path.join(ROOT, "npu-embeddings-xdna1_amd"))
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
 HBM_PEAK_GBS = 8000.0
 
 
-def kernel_name(plan, epi, res, cbf):
+def kernel_name(plan, epi, res, cbf, i8=False):
     """The rocprof name of the GEMM instantiation a plan from mx_gemm_plan runs,
-    e.g. lds_128x256x32_w64x64_ns4_persistent -> gemm_lds_k<128, 256, 2, 4, 4, ...>."""
+    e.g. lds_128x256x32_w64x64_ns4_persistent -> gemm_lds_k<128, 256, 2, 4, 4, ...>
+    (gemm_i8_k<...> on the int8 datapath, whose tiles are the same)."""
     if not plan.startswith("lds_"):
         return "gemm_bf16_k<128, 128, 64, 64, 64>"
     tile, wave, ns = plan.split("_")[1:4]
     bm, bn, _ = (int(x) for x in tile.split("x"))
     wm, wn = (int(x) for x in wave[1:].split("x"))
     b = lambda v: "true" if v else "false"  # noqa: E731
+    if i8:
+        return (f"gemm_i8_k<{bm}, {bn}, {bm // wm}, {bn // wn}, {int(ns[2:])}, {epi}, {b(res)}, "
+                f"{1 if cbf else 0}>")
     return (f"gemm_lds_k<{bm}, {bn}, {bm // wm}, {bn // wn}, {int(ns[2:])}, {epi}, {b(res)}, "
             f"{b(cbf)}>")
 
@@ -52,9 +59,11 @@ def workload_name(config, m):
             f"{m['seq']} positions ({geo}) -> final LN")
 
 
-def cpu_baseline(name, sample_batch, threads):
+def cpu_baseline(name, sample_batch, threads, int8=False):
     """The oracle's host path (the reference CPU fallback restated) over
-    `sample_batch` sequences of the same workload, all layers."""
+    `sample_batch` sequences of the same workload, all layers; int8: the
+    int8 design's host halves with the exact integer product
+    (orc_bert_run_i8)."""
     import numpy as np
 
     import orc as orc_mod
@@ -71,18 +80,29 @@ def cpu_baseline(name, sample_batch, threads):
     P = orc_mod.P
     keep = []
     enc = orc_mod.encoder_struct(m, keep)
+    ops = None
+    if int8:  # the operand quantisation is packing, outside the timed region
+        ops = orc_mod.OrcI8()
+        for i, (q, ws, sm) in enumerate(synth.quantise_model(m)):
+            ias = np.ascontiguousarray((np.float32(1.0) / sm).astype(np.float32))
+            keep += [q, ws, ias]
+            ops.wq[i], ops.wscale[i], ops.ias[i] = q.ctypes.data, ws.ctypes.data, ias.ctypes.data
     emb = np.empty((B * S, d), np.float32)
     cm = np.empty((B, S), np.float32)
     out = np.empty((B, d), np.float32)
     t0 = time.perf_counter()
     orc.orc_embed_sum(P(ids), P(am), B, S, d, P(m["word"]), P(m["pos"]), P(m["type"]), P(emb),
                       P(cm))
-    orc.orc_bert_run(enc, P(emb), P(cm), B, S, -1)
+    if int8:
+        orc.orc_bert_run_i8(enc, ops, P(emb), P(cm), B, S, -1)
+    else:
+        orc.orc_bert_run(enc, P(emb), P(cm), B, S, -1)
     orc.orc_pool_rows(P(emb), P(am), B, S, d, int(m["cls_pool"]), 1, P(out))
     dt = time.perf_counter() - t0
     return {"value": B / dt, "unit": "sequences/s", "cores": threads, "kind": "port",
             "sample": f"{B} of the {m['batch']} sequences (seq {S}, {m['layers']} layers, "
-                      f"embed+run+pool) through the oracle's host path, {dt:.1f} s wall"}
+                      f"embed+run+pool) through the oracle's host path"
+                      f"{' (int8 design)' if int8 else ''}, {dt:.1f} s wall"}
 
 
 def main():
@@ -91,6 +111,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="bge_base")
+    ap.add_argument("--int8", action="store_true",
+                    help="the W8A8 datapath (BERT configs): int8 operands by the packer's "
+                         "scheme over the same random weights")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=16)
     ap.add_argument("--calibrate", action="store_true",
@@ -124,8 +147,11 @@ def main():
 
     m = synth.make_model(args.config)
     kind = m["kind"]
+    if args.int8 and kind != "bert":
+        print(json.dumps({"error": "--int8 is benchmarked on the BERT configs"}))
+        sys.exit(2)
     ctx = mxenc.Context(0)
-    enc = mxenc.Encoder(ctx, m)
+    enc = mxenc.Encoder(ctx, m, int8=synth.quantise_model(m) if args.int8 else None)
     if kind == "bert":
         ids, am, lens = synth.make_text_inputs(m)
         B, S = ids.shape
@@ -209,7 +235,7 @@ def main():
     groups = {}
     for i, (sname, (mm, nn, kk, epi, res, cbf)) in enumerate(sites):
         plan = mxenc.lib().mx_gemm_plan(mm, nn, kk).decode()
-        kname = kernel_name(plan, epi, res, cbf)
+        kname = kernel_name(plan, epi, res, cbf, args.int8)
         g = groups.setdefault(kname, {"ms": 0.0, "flop": 0.0, "n": 0, "sites": []})
         g["ms"] += site_ms[i]
         g["flop"] += site_flop[i]
@@ -232,13 +258,16 @@ def main():
     cpu = None
     if not args.no_cpu_baseline and kind == "bert":
         threads = min(16, os.cpu_count() or 1)
-        cpu = cpu_baseline(args.config, args.cpu_sample, threads)
+        cpu = cpu_baseline(args.config, args.cpu_sample, threads, args.int8)
         print(f"bench: cpu baseline {cpu['value']:.3f} seq/s ({cpu['sample']})",
               file=sys.stderr, flush=True)
 
+    peak = INT8_PEAK_TOPS if args.int8 else BF16_PEAK_TFLOPS
+    punit = "TOP/s" if args.int8 else "TFLOP/s"
     line = {
         "metric": ("sequences/sec (bge-base, seq 512, b64) + GEMM MFMA util % of bf16 peak"
-                   if args.config == "bge_base" else f"{unit} ({args.config})"),
+                   if args.config == "bge_base" and not args.int8 else
+                   f"{unit} ({args.config}{', int8 W8A8' if args.int8 else ''})"),
         "value": seq_s,
         "unit": unit,
         "n_gpus": 1,
@@ -248,18 +277,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "int8" if args.int8 else "bf16",
         "data": "synthetic (seeded token ids and valid lengths; random-init N(0,0.02) weights)"
                 if kind == "bert" else "synthetic (seeded inputs; random-init N(0,0.02) weights)",
         "config": {"workload": workload_name(args.config, m), "batch": B, "seq_len": S,
                    "layers": m["layers"]},
-        "gemm_mfma_util_pct": 100.0 * gemm_tflops / BF16_PEAK_TFLOPS,
+        "gemm_mfma_util_pct": 100.0 * gemm_tflops / peak,
         "roofline": {"bound": "mfma", "kernel": dom_name, "sites": dom["sites"],
-                     "achieved": dom_tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": dom_tflops / BF16_PEAK_TFLOPS, "traffic": traffic,
+                     "achieved": dom_tflops, "peak": peak, "unit": punit,
+                     "frac": dom_tflops / peak, "traffic": traffic,
                      "flop_per_launch": dom["flop"] / max(dom["n"], 1),
                      "avg_launch_us": dom["ms"] / max(dom["n"], 1) * 1e3},
-        "gemm_all": {"achieved_tflops": gemm_tflops, "frac": gemm_tflops / BF16_PEAK_TFLOPS,
+        "gemm_all": {"achieved_tflops": gemm_tflops, "frac": gemm_tflops / peak,
                      "ms_per_step": tot["gemm_ms"] / args.steps},
         "attention": {"achieved_tflops": attn_tflops, "frac": attn_tflops / BF16_PEAK_TFLOPS,
                       "ms_per_step": tot["attn_ms"] / args.steps},

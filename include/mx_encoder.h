@@ -268,6 +268,37 @@ int mx_layernorm_i8(mx_stream *s, const float *x, const void *y, int y_dtype,
                     int64_t cols, float *out_f32, const float *ias, int8_t *q,
                     float *a_scale);
 
+/* ---- the RoPE and gated-FFN BERT archs ---------------------------------------
+ * nomic_bert_rope_swiglu and gte_new_rope_geglu (app_state.hpp:440-550): the
+ * BERT stack with rotary positions on Q and K after the QKV GEMM and a gated
+ * FFN (FFN-up [d, 2f] = up | gate, then lo * act(hi) into FFN-down). */
+typedef enum {
+  MX_GATED_NONE = 0,     /* the plain GELU FFN                                */
+  MX_GATED_SILU = 1,     /* SwiGLU: lo * silu(hi), the exp2 polynomial (nomic) */
+  MX_GATED_GELU_ERF = 2  /* GeGLU: lo * gelu_erf(hi) (gte)                     */
+} mx_gated;
+
+/* apply_rope_qkv's tables (bert_encoder.cpp:926-950), on the host: cos/sin
+ * [S, hd] fp32 (host memory), angle s * inv_freq_j in double rounded once,
+ * the half duplicated; inv_freq_host [hd/2] (the container's rope_inv_freq,
+ * gte) or, when null, gemma_rope_tables' inv_freq_j = 1/theta^(2j/hd)
+ * (encoders/gemma_kernels.cpp:114-136, nomic). hd even. */
+int mx_rope_tables(int64_t S, int64_t hd, double theta, const float *inv_freq_host,
+                   float *cos_host, float *sin_host);
+/* apply_rope_qkv (bert_encoder.cpp:951-990): Q and K (never V) of bf16
+ * [B*S, ld_qkv] Q|K|V rows rotated in place, position s = row % S, pairs
+ * (j, j + hd/2) of each head: o1 = x1*c - x2*s, o2 = x2*c + x1*s (each
+ * product rounded, as the host's AVX2 form), narrowed once to bf16.
+ * cos_t/sin_t: device fp32 [S, hd]. hd % 4 == 0. */
+int mx_rope_qkv(mx_stream *s, uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
+                int64_t H, int64_t hd, const float *cos_t, const float *sin_t);
+/* swiglu_cpu (bert_encoder.cpp:582-627): up [rows, 2f] = lo | hi (fp32 or
+ * bf16) -> out [rows, f] (fp32 or bf16) = lo * act(hi), act MX_GATED_SILU
+ * (x / (1 + exp2_poly(max(-x log2e, -120))), bit-identical to the host for
+ * fp32 input) or MX_GATED_GELU_ERF. f % 4 == 0. */
+int mx_glu(mx_stream *s, const void *up, int up_dtype, void *out, int out_dtype, int64_t rows,
+           int64_t f, int act);
+
 /* ---- placement registry (common/npu_ops_flag.hpp:75-214) ------------------ */
 
 /* parse_npu_ops: comma list of codes (spaces ignored, empty items skipped);
@@ -307,6 +338,13 @@ typedef struct {
                          WHISPER (mx_encoder_vit / mx_encoder_whisper)        */
   int64_t image, patch, labels; /* ViT: image side, patch side, head labels   */
   int64_t mels, frames;         /* Whisper: mel bins and input frames         */
+  int gated_ffn;      /* BERT: mx_gated; gated -> "layer.{i}.ffn_up" is
+                         [hidden, 2*ffn] (up half first) and its bias [2*ffn] */
+  int rope;           /* BERT: rotary positions on Q and K (no position
+                         table is needed then, but embed() still adds
+                         "embeddings.position", as EmbedService::chunk does) */
+  double rope_theta;  /* rope: the base when no "rope.inv_freq" [hd/2] tensor
+                         is set (nomic); gte sets the frequencies instead     */
 } mx_encoder_desc;
 
 typedef enum { MX_FRONT_NONE = 0, MX_FRONT_VIT = 1, MX_FRONT_WHISPER = 2 } mx_front;

@@ -27,7 +27,7 @@ FLAGS = [
     "-I", os.path.join(HERE, "..", "include"),
 ]
 SOURCES = ["k_gemm_lds.hip", "k_gemm_i8.hip", "k_elem.hip", "k_gemm.hip", "k_attn.hip",
-           "k_front.hip", "k_panel.hip", "k_quant.hip", "mx_abi.cpp", "mx_i8.cpp",
+           "k_front.hip", "k_panel.hip", "k_quant.hip", "k_glu.hip", "mx_abi.cpp", "mx_i8.cpp",
            "mx_encoder.cpp", "mx_npue.cpp", "mx_service.cpp"]
 
 

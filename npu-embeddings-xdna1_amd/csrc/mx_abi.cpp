@@ -176,6 +176,58 @@ int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t
   return e == hipSuccess ? MX_OK : hip_fail(e, "attention launch");
 }
 
+void rope_tables_host(int64_t S, int64_t hd, double theta, const float *inv_freq, float *cos_t,
+                      float *sin_t) {
+  const int64_t half = hd / 2;
+  std::vector<double> inv(static_cast<size_t>(half));
+  for (int64_t j = 0; j < half; ++j)
+    inv[j] = inv_freq ? static_cast<double>(inv_freq[j])
+                      : 1.0 / std::pow(theta, (2.0 * static_cast<double>(j)) /
+                                                  static_cast<double>(hd));
+  for (int64_t p = 0; p < S; ++p)
+    for (int64_t j = 0; j < half; ++j) {
+      const double ang = static_cast<double>(p) * inv[j];
+      const float c = static_cast<float>(std::cos(ang)), sn = static_cast<float>(std::sin(ang));
+      cos_t[p * hd + j] = cos_t[p * hd + half + j] = c;
+      sin_t[p * hd + j] = sin_t[p * hd + half + j] = sn;
+    }
+}
+
+int rope_checked(mx_stream *s, uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S, int64_t H,
+                 int64_t hd, const float *cos_t, const float *sin_t) {
+  if (!s) return fail(MX_E_INVALID, "rope_qkv: null stream");
+  if (!qkv || !cos_t || !sin_t) return fail(MX_E_INVALID, "rope_qkv: null qkv or table");
+  if (B <= 0 || S <= 0 || H <= 0 || hd <= 0) return fail(MX_E_INVALID, "rope_qkv: zero dimension");
+  if (hd % 4)
+    return fail(MX_E_UNSUPPORTED, "rope_qkv: head_dim " + std::to_string(hd) +
+                                      " (the kernel rotates two pairs at a time: hd % 4 == 0)");
+  if (ld_qkv < 2 * H * hd || ld_qkv % 2)
+    return fail(MX_E_INVALID, "rope_qkv: row stride cannot hold Q|K or is odd");
+  if (!aligned(qkv, 4) || !aligned(cos_t, 8) || !aligned(sin_t, 8))
+    return fail(MX_E_INVALID, "rope_qkv: misaligned qkv or table");
+  if (B * S > INT32_MAX) return fail(MX_E_INVALID, "rope_qkv: too many rows");
+  const hipError_t e = mxk::rope_qkv(qkv, ld_qkv, B * S, (int)S, (int)H, (int)hd, cos_t, sin_t,
+                                     s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "rope_qkv launch");
+}
+
+int glu_checked(mx_stream *s, const void *up, int up_dtype, void *out, int out_dtype,
+                int64_t rows, int64_t f, int act) {
+  if (!s) return fail(MX_E_INVALID, "glu: null stream");
+  if (!up || !out) return fail(MX_E_INVALID, "glu: null up or out");
+  if (rows <= 0 || f <= 0) return fail(MX_E_INVALID, "glu: zero dimension");
+  if (f % 4) return fail(MX_E_UNSUPPORTED, "glu: f % 4 != 0");
+  if ((up_dtype != MX_F32 && up_dtype != MX_BF16) || (out_dtype != MX_F32 && out_dtype != MX_BF16))
+    return fail(MX_E_INVALID, "glu: dtypes must be MX_F32 or MX_BF16");
+  if (act != MX_GATED_SILU && act != MX_GATED_GELU_ERF)
+    return fail(MX_E_INVALID, "glu: act must be MX_GATED_SILU or MX_GATED_GELU_ERF");
+  if (!aligned(up, up_dtype == MX_F32 ? 16 : 8) || !aligned(out, out_dtype == MX_F32 ? 16 : 8))
+    return fail(MX_E_INVALID, "glu: misaligned up or out");
+  const hipError_t e = mxk::glu(up, up_dtype == MX_BF16, out, out_dtype == MX_BF16, rows, f, act,
+                                s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "glu launch");
+}
+
 int take_data_error(mx_stream *s, int *flags) {
   int h = 0;
   hipError_t e = hipMemcpyAsync(&h, s->err_dev, sizeof(int), hipMemcpyDeviceToHost, s->stream);
@@ -509,6 +561,30 @@ int mx_narrow_i32_bf16(mx_stream *s, const int32_t *in, uint16_t *out, int64_t n
   if (n == 0) return MX_OK;
   const hipError_t e = mxk::narrow_i32_bf16(in, out, n, s->stream);
   return e == hipSuccess ? MX_OK : hip_fail(e, "narrow_i32_bf16 launch");
+}
+
+int mx_rope_tables(int64_t S, int64_t hd, double theta, const float *inv_freq, float *cos_t,
+                   float *sin_t) {
+  clear_error();
+  if (!cos_t || !sin_t) return fail(MX_E_INVALID, "rope_tables: null table");
+  if (S <= 0 || hd <= 0 || hd % 2)
+    return fail(MX_E_INVALID, "rope_tables: S > 0 and an even head_dim wanted");
+  if (!inv_freq && !(theta > 0.0))
+    return fail(MX_E_INVALID, "rope_tables: a non-positive rope_theta and no inv_freq");
+  rope_tables_host(S, hd, theta, inv_freq, cos_t, sin_t);
+  return MX_OK;
+}
+
+int mx_rope_qkv(mx_stream *s, uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S, int64_t H,
+                int64_t hd, const float *cos_t, const float *sin_t) {
+  clear_error();
+  return rope_checked(s, qkv, ld_qkv, B, S, H, hd, cos_t, sin_t);
+}
+
+int mx_glu(mx_stream *s, const void *up, int up_dtype, void *out, int out_dtype, int64_t rows,
+           int64_t f, int act) {
+  clear_error();
+  return glu_checked(s, up, up_dtype, out, out_dtype, rows, f, act);
 }
 
 int mx_embed_sum(mx_stream *s, const int32_t *ids, const float *attn_mask, int64_t B, int64_t S,

@@ -75,6 +75,12 @@ struct mx_encoder {
   float *emb = nullptr, *add_mask = nullptr;
   int8_t *xq = nullptr;  // int8 datapath: quantised A and its row scales
   float *sa = nullptr;
+  uint16_t *glu = nullptr;  // gated FFN: lo * act(hi), [M, f] bf16
+  // RoPE: the frequencies when the container gives them ("rope.inv_freq"),
+  // and the device cos/sin tables [rope_rows, head_dim], built on first use.
+  std::vector<float> rope_inv;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  int64_t rope_rows = 0;
   bool i8 = false;       // set by mx_encoder_ready: every GEMM operand is int8
   int32_t *kv_len = nullptr;
   // timing
@@ -130,11 +136,15 @@ int ensure_ws_rows(mx_encoder *enc, int64_t rows, int64_t B) {
     free_dev(enc->emb);
     free_dev(enc->xq);
     free_dev(enc->sa);
+    free_dev(enc->glu);
     enc->ws_rows = 0;
+    const int64_t fu = enc->desc.gated_ffn ? 2 * f : f;
     int rc = dev_alloc((void **)&enc->xb, rows * d * 2, "workspace xb");
     if (!rc) rc = dev_alloc((void **)&enc->qkv, rows * 3 * d * 2, "workspace qkv");
     if (!rc) rc = dev_alloc((void **)&enc->ctxb, rows * d * 2, "workspace ctx");
-    if (!rc) rc = dev_alloc((void **)&enc->up, rows * f * 2, "workspace up");
+    if (!rc) rc = dev_alloc((void **)&enc->up, rows * fu * 2, "workspace up");
+    if (!rc && enc->desc.gated_ffn)
+      rc = dev_alloc((void **)&enc->glu, rows * f * 2, "workspace gated");
     if (!rc) rc = dev_alloc((void **)&enc->proj, rows * d * 2, "workspace proj");
     if (!rc) rc = dev_alloc((void **)&enc->emb, rows * d * 4, "workspace emb");
     if (!rc && enc->i8)
@@ -248,6 +258,39 @@ int quant_l(mx_encoder *enc, mx_stream *s, const uint16_t *a, int64_t rows, int6
   return quantise_checked(s, a, MX_BF16, K, rows, K, ias, enc->xq, K, enc->sa);
 }
 
+// RoPE tables for positions [0, S), built on the host once (double angles,
+// as apply_rope_qkv builds them) and kept on the device.
+int ensure_rope(mx_encoder *enc, int64_t S) {
+  if (S <= enc->rope_rows) return MX_OK;
+  const int64_t hd = enc->desc.head_dim;
+  std::vector<float> c(static_cast<size_t>(S * hd)), sn(static_cast<size_t>(S * hd));
+  rope_tables_host(S, hd, enc->desc.rope_theta, enc->rope_inv.empty() ? nullptr : enc->rope_inv.data(),
+                   c.data(), sn.data());
+  free_dev(enc->rope_cos);
+  free_dev(enc->rope_sin);
+  enc->rope_rows = 0;
+  int rc = dev_alloc((void **)&enc->rope_cos, c.size() * 4, "rope table");
+  if (!rc) rc = dev_alloc((void **)&enc->rope_sin, sn.size() * 4, "rope table");
+  if (rc) return rc;
+  hipError_t e = hipMemcpy(enc->rope_cos, c.data(), c.size() * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(enc->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(e, "rope table upload");
+  enc->rope_rows = S;
+  return MX_OK;
+}
+
+int rope_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S) {
+  Bracket br(enc, s->stream, CAT_OTHER);
+  return rope_checked(s, enc->qkv, 3 * enc->desc.hidden, B, S, enc->desc.heads,
+                      enc->desc.head_dim, enc->rope_cos, enc->rope_sin);
+}
+
+int glu_l(mx_encoder *enc, mx_stream *s, int64_t M) {
+  Bracket br(enc, s->stream, CAT_OTHER);
+  return glu_checked(s, enc->up, MX_BF16, enc->glu, MX_BF16, M, enc->desc.ffn,
+                     enc->desc.gated_ffn);
+}
+
 int attn_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, const float *mask,
            const int32_t *kv_len) {
   Bracket br(enc, s->stream, CAT_ATTN);
@@ -282,12 +325,18 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
   const int64_t M = B * S, d = enc->desc.hidden, f = enc->desc.ffn;
   const int epi = enc->desc.gelu == MX_GELU_ERF ? MX_EPI_GELU_ERF : MX_EPI_GELU_POLY;
   const size_t L = enc->layers.size();
-  int rc = site_ln(enc, s, x, nullptr, MX_F32, enc->emb_ln[0], enc->emb_ln[1], M, x,
-                   enc->layers[0].ias[SITE_QKV]);
+  const bool gated = enc->desc.gated_ffn != MX_GATED_NONE;
+  const int64_t fu = gated ? 2 * f : f;
+  uint16_t *act = gated ? enc->glu : enc->up;  // FFN-down's A (bf16 datapath)
+  int rc = enc->desc.rope ? ensure_rope(enc, S) : MX_OK;
+  if (!rc)
+    rc = site_ln(enc, s, x, nullptr, MX_F32, enc->emb_ln[0], enc->emb_ln[1], M, x,
+                 enc->layers[0].ias[SITE_QKV]);
   for (size_t l = 0; !rc && l < L; ++l) {
     const LayerW &w = enc->layers[l];
     rc = site_gemm(enc, s, w, SITE_QKV, enc->xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->qkv,
                    MX_BF16);
+    if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S);
     if (!rc) rc = attn_l(enc, s, B, S, mask, kvl);
     if (!rc && enc->i8) rc = quant_l(enc, s, enc->ctxb, M, d, w.ias[SITE_AO]);
     if (!rc)
@@ -295,10 +344,13 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
                      MX_BF16);
     if (!rc)
       rc = site_ln(enc, s, x, enc->proj, MX_BF16, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
-    if (!rc) rc = site_gemm(enc, s, w, SITE_UP, enc->xb, M, d, f, epi, nullptr, enc->up, MX_BF16);
-    if (!rc && enc->i8) rc = quant_l(enc, s, enc->up, M, f, w.ias[SITE_DOWN]);
     if (!rc)
-      rc = site_gemm(enc, s, w, SITE_DOWN, enc->up, M, f, d, MX_EPI_NONE, nullptr, enc->proj,
+      rc = site_gemm(enc, s, w, SITE_UP, enc->xb, M, d, fu, gated ? MX_EPI_NONE : epi, nullptr,
+                     enc->up, MX_BF16);
+    if (!rc && gated) rc = glu_l(enc, s, M);
+    if (!rc && enc->i8) rc = quant_l(enc, s, act, M, f, w.ias[SITE_DOWN]);
+    if (!rc)
+      rc = site_gemm(enc, s, w, SITE_DOWN, act, M, f, d, MX_EPI_NONE, nullptr, enc->proj,
                      MX_BF16);
     if (!rc)
       rc = site_ln(enc, s, x, enc->proj, MX_BF16, w.ln[2], w.ln[3], M, x,
@@ -464,6 +516,14 @@ int mx_encoder_create(mx_ctx *ctx, const mx_encoder_desc *desc, mx_encoder **out
                               "3*hidden multiples of 32");
   if (d.front != MX_FRONT_NONE && d.front != MX_FRONT_VIT && d.front != MX_FRONT_WHISPER)
     return fail(MX_E_INVALID, "encoder_create: unknown front end " + std::to_string(d.front));
+  if (d.gated_ffn != MX_GATED_NONE && d.gated_ffn != MX_GATED_SILU &&
+      d.gated_ffn != MX_GATED_GELU_ERF)
+    return fail(MX_E_INVALID, "encoder_create: unknown gated_ffn " + std::to_string(d.gated_ffn));
+  if ((d.gated_ffn != MX_GATED_NONE || d.rope) && d.arch != MX_ARCH_BERT)
+    return fail(MX_E_UNSUPPORTED, "encoder_create: RoPE and the gated FFN are the BERT-family "
+                                  "archs' (nomic, gte); the pre-LN stacks have neither");
+  if (d.rope && (d.head_dim % 4))
+    return fail(MX_E_UNSUPPORTED, "encoder_create: RoPE needs head_dim % 4 == 0");
   int rc = use_device(ctx);
   if (rc) return rc;
   auto *e = new mx_encoder();
@@ -508,6 +568,9 @@ void mx_encoder_destroy(mx_encoder *enc) {
     free_dev(enc->emb);
     free_dev(enc->xq);
     free_dev(enc->sa);
+    free_dev(enc->glu);
+    free_dev(enc->rope_cos);
+    free_dev(enc->rope_sin);
     free_dev(enc->add_mask);
     free_dev(enc->kv_len);
     free_dev(enc->f_rows);
@@ -542,6 +605,7 @@ int mx_encoder_clone(mx_encoder *enc, mx_encoder **out) {
   c->owns_weights = false;
   c->layers = enc->layers;
   c->i8 = enc->i8;
+  c->rope_inv = enc->rope_inv;
   for (int i = 0; i < 2; ++i) {
     c->emb_ln[i] = enc->emb_ln[i];
     c->fin_ln[i] = enc->fin_ln[i];
@@ -602,7 +666,8 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
                                     " of a " + std::to_string(enc->desc.layers) + "-layer stack");
     const std::string rest = name.substr(p + 1);
     LayerW &w = enc->layers[static_cast<size_t>(L)];
-    const int64_t K[4] = {d, d, d, f}, N[4] = {3 * d, d, f, d};
+    const int64_t fu = enc->desc.gated_ffn ? 2 * f : f;
+    const int64_t K[4] = {d, d, d, f}, N[4] = {3 * d, d, fu, d};
     for (int i = 0; i < 4; ++i) {
       if (rest == kGemmNames[i]) {
         if (count != K[i] * N[i])
@@ -648,6 +713,17 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
     if (rest == "ln2.weight") return put_f32(w.ln[2], d);
     if (rest == "ln2.bias") return put_f32(w.ln[3], d);
     return fail(MX_E_INVALID, "encoder_set: unknown tensor '" + name + "'");
+  }
+  if (name == "rope.inv_freq") {
+    if (!enc->desc.rope) return fail(MX_E_INVALID, "rope.inv_freq: this encoder has no RoPE");
+    if (dtype != MX_F32 || count != enc->desc.head_dim / 2)
+      return fail(MX_E_INVALID, "rope.inv_freq: MX_F32 [head_dim/2] wanted");
+    const float *v = static_cast<const float *>(host);
+    enc->rope_inv.assign(v, v + count);
+    free_dev(enc->rope_cos);
+    free_dev(enc->rope_sin);
+    enc->rope_rows = 0;
+    return MX_OK;
   }
   if (name == "embeddings.ln.weight") return put_f32(enc->emb_ln[0], d);
   if (name == "embeddings.ln.bias") return put_f32(enc->emb_ln[1], d);
@@ -774,6 +850,9 @@ int mx_encoder_ready(mx_encoder *enc) {
                      : !enc->front_pos ? "position" : nullptr;
     if (miss) return fail(MX_E_STATE, std::string("encoder: ") + miss + " was never set");
   }
+  if (enc->desc.rope && enc->rope_inv.empty() && !(enc->desc.rope_theta > 0.0))
+    return fail(MX_E_STATE, "encoder: RoPE without a frequency set -- a positive rope_theta or "
+                            "rope.inv_freq is needed");
   enc->i8 = i8;
   return MX_OK;
 }
@@ -995,7 +1074,8 @@ int mx_encoder_set_panel(mx_encoder *enc, const char *name_c, const uint16_t *pa
     }
     if (digits && p < name.size() && name[p] == '.' && L < enc->desc.layers) {
       const std::string rest = name.substr(p + 1);
-      const int64_t Ks[4] = {d, d, d, f}, Ns[4] = {3 * d, d, f, d};
+      const int64_t Ks[4] = {d, d, d, f};
+      const int64_t Ns[4] = {3 * d, d, enc->desc.gated_ffn ? 2 * f : f, d};
       for (int i = 0; i < 4; ++i)
         if (rest == kGemmNames[i]) {
           dst = &enc->layers[static_cast<size_t>(L)].w[i];
@@ -1049,14 +1129,76 @@ int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
   int rc = cfg("arch", arch);
   if (rc) return rc;
   // The whitelist of app::encoder_implemented (app_state.hpp:175-200), cut to
-  // what this backend's stack computes: the absolute-position, plain-GELU,
-  // post-LN BERT. The other BERT-named archs share tensor names on purpose, so
-  // reading them here would compute the wrong model without a sign.
-  if (arch != "bert_abs_gelu_postln")
+  // what this backend's stack computes: the post-LN BERT and its RoPE /
+  // gated-FFN variants. Each variant's keys are checked as set_model_shape
+  // checks them (app_state.hpp:440-550), so a container that leaves the
+  // fusion order or the frequencies to guesswork is refused, not guessed.
+  const bool nomic = arch == "nomic_bert_rope_swiglu", gte = arch == "gte_new_rope_geglu";
+  if (arch != "bert_abs_gelu_postln" && !nomic && !gte)
     return fail(MX_E_UNSUPPORTED,
                 ".npue: container arch '" + arch + "' -- this loader builds the post-LN BERT "
-                "stack (bert_abs_gelu_postln); RoPE and gated-FFN archs share its tensor names "
-                "but not its maths, and are refused rather than run as BERT");
+                "stack (bert_abs_gelu_postln) and its RoPE/gated-FFN variants "
+                "(nomic_bert_rope_swiglu, gte_new_rope_geglu); other archs share its tensor "
+                "names but not its maths, and are refused rather than run as BERT");
+  int gated = MX_GATED_NONE;
+  double rope_theta = 0.0;
+  std::vector<float> inv_freq;
+  std::string v;
+  if (npue_config(f, "gated_ffn", v) && v == "true") gated = MX_GATED_SILU;
+  if (nomic || gte) {
+    if (!npue_config(f, "position_embedding_type", v) || v != "rope")
+      return fail(MX_E_INVALID, ".npue: container arch is " + arch + " but "
+                                "position_embedding_type is not 'rope' -- refusing rather than "
+                                "guessing how position is encoded");
+    if (gated == MX_GATED_NONE)
+      return fail(MX_E_INVALID, ".npue: container arch is " + arch + " but gated_ffn is not "
+                                "true -- refusing rather than running a plain FFN over a fused "
+                                "up|gate weight");
+    if (nomic) {
+      if (!npue_config(f, "swiglu_halves", v) || v != "fc11_up|fc12_gate")
+        return fail(MX_E_INVALID, ".npue: unrecognised swiglu_halves ordering -- expected "
+                                  "'fc11_up|fc12_gate'; refusing rather than guessing which half "
+                                  "of the fused ffn_up gets SiLU");
+      if (!npue_config(f, "rope_theta", v) || !((rope_theta = std::strtod(v.c_str(), nullptr)) > 0))
+        return fail(MX_E_INVALID, ".npue: nomic_bert_rope_swiglu container has a non-positive "
+                                  "rope_theta");
+    } else {
+      if (!npue_config(f, "glu_halves", v) || v.rfind("up_first|gate_second", 0) != 0)
+        return fail(MX_E_INVALID, ".npue: unrecognised glu_halves ordering -- expected it to "
+                                  "begin 'up_first|gate_second'; refusing rather than guessing "
+                                  "which half of the fused ffn_up gets the activation");
+      if (!npue_config(f, "rope_inv_freq", v))
+        return fail(MX_E_INVALID, ".npue: gte_new_rope_geglu container carries no "
+                                  "'rope_inv_freq' -- the frequency set is not derivable from "
+                                  "rope_theta, so refusing rather than falling back");
+      // A JSON array of numbers.
+      const char *p = v.c_str();
+      while (*p && *p != '[') ++p;
+      if (*p == '[') ++p;
+      for (;;) {
+        while (*p == ' ' || *p == ',' || *p == '\n' || *p == '\t') ++p;
+        if (*p == ']' || !*p) break;
+        char *e = nullptr;
+        const double x = std::strtod(p, &e);
+        if (e == p) return fail(MX_E_INVALID, ".npue: rope_inv_freq is not an array of numbers");
+        inv_freq.push_back(static_cast<float>(x));
+        p = e;
+      }
+    }
+    std::string act;
+    if (!npue_config(f, "activation", act)) {
+      if (gte)
+        return fail(MX_E_INVALID, ".npue: gte_new_rope_geglu container carries no "
+                                  "'activation' key -- refusing rather than guessing which "
+                                  "activation the gate half gets");
+      act = "silu";
+    }
+    if (act == "silu") gated = MX_GATED_SILU;
+    else if (act == "gelu") gated = MX_GATED_GELU_ERF;
+    else
+      return fail(MX_E_INVALID, ".npue: unknown gated-FFN activation '" + act + "' -- this "
+                                "build implements 'silu' and 'gelu' (exact erf)");
+  }
   mx_encoder_desc d{};
   d.arch = MX_ARCH_BERT;
   if ((rc = cfg_int("num_layers", d.layers)) || (rc = cfg_int("hidden", d.hidden)) ||
@@ -1080,6 +1222,13 @@ int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
   d.ln_eps = 1e-12f;
   d.attn_scale = 1.0f;  // 1/sqrt(head_dim) is folded into the packed Q block
   d.gelu = MX_GELU_POLY;
+  d.gated_ffn = gated;
+  d.rope = nomic || gte;
+  d.rope_theta = rope_theta;
+  if (gte && static_cast<int64_t>(inv_freq.size()) * 2 != d.head_dim)
+    return fail(MX_E_INVALID, ".npue: rope_inv_freq has " + std::to_string(inv_freq.size()) +
+                                  " entries, expected head_dim/2 = " +
+                                  std::to_string(d.head_dim / 2));
   const TensorRecView word = npue_tensor(f, "embeddings.word");
   if (!word.found || word.padded.size() != 2)
     return fail(MX_E_INVALID, ".npue: embeddings.word missing or not [vocab, hidden]");
@@ -1109,6 +1258,10 @@ int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
   }
   for (const std::string &n : names)
     if ((rc = set_f32(n))) return refuse(rc);
+  if (!inv_freq.empty() &&
+      (rc = mx_encoder_set(enc, "rope.inv_freq", inv_freq.data(), MX_F32,
+                           static_cast<int64_t>(inv_freq.size()))))
+    return refuse(rc);
   for (int64_t L = 0; L < d.layers; ++L)
     for (int i = 0; i < 4; ++i) {
       const std::string n = "layer." + std::to_string(L) + "." + kGemmNames[i];
@@ -1155,7 +1308,7 @@ int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
                     t.mac_t, &op);
       if (rc) return refuse(rc);
       const int64_t d = enc->desc.hidden, fw = enc->desc.ffn;
-      const int64_t Ks[4] = {d, d, d, fw}, Ns[4] = {3 * d, d, fw, d};
+      const int64_t Ks[4] = {d, d, d, fw}, Ns[4] = {3 * d, d, gated ? 2 * fw : fw, d};
       if (K != Ks[i] || N != Ns[i]) {
         free_i8(op);
         return refuse(fail(MX_E_INVALID, n + ": a [" + std::to_string(K) + ", " +

@@ -77,6 +77,13 @@ int layernorm_i8_checked(mx_stream *s, const float *x, const void *y, int y_dtyp
                          const float *gamma, const float *beta, float eps, int64_t rows,
                          int64_t cols, float *out_f32, const float *ias, int8_t *q,
                          float *a_scale);
+// The RoPE / gated-FFN archs: host tables, and validated launches.
+void rope_tables_host(int64_t S, int64_t hd, double theta, const float *inv_freq, float *cos_t,
+                      float *sin_t);
+int rope_checked(mx_stream *s, uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S, int64_t H,
+                 int64_t hd, const float *cos_t, const float *sin_t);
+int glu_checked(mx_stream *s, const void *up, int up_dtype, void *out, int out_dtype,
+                int64_t rows, int64_t f, int act);
 // Read and clear the stream's data-refusal flag (synchronises the stream).
 int take_data_error(mx_stream *s, int *flags);
 

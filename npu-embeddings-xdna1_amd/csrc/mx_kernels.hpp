@@ -89,6 +89,13 @@ hipError_t layernorm_quant(const float *x, const void *y, int y_bf, const float 
                            hipStream_t s);
 int quant_groups(int64_t K);
 
+// The RoPE / gated-FFN archs (k_glu.hip): in-place RoPE of Q and K in bf16
+// fused rows (tables [S, hd]); lo | hi -> lo * act(hi) (act 1 SiLU, 2 GELU).
+hipError_t rope_qkv(uint16_t *qkv, int64_t ld, int64_t rows, int S, int H, int hd,
+                    const float *cos_t, const float *sin_t, hipStream_t s);
+hipError_t glu(const void *in, int in_bf, void *out, int out_bf, int64_t rows, int64_t f, int act,
+               hipStream_t s);
+
 // Container operand tiled (tile_k, tile_n) with (mac_s, mac_t) sub-tiles ->
 // [N, K] panel (k_panel.hip). Shapes checked by the caller.
 hipError_t untile_panel(const uint16_t *panel, int64_t K, int64_t N, int tile_k, int tile_n,

@@ -20,6 +20,7 @@ MX_GELU_POLY, MX_GELU_ERF, MX_GELU_ERF_AS = 0, 1, 2
 MX_SOFTMAX_POLY, MX_SOFTMAX_EXACT, MX_SOFTMAX_AIE = 0, 1, 2
 MX_ARCH_BERT, MX_ARCH_PRELN = 0, 1
 MX_FRONT_NONE, MX_FRONT_VIT, MX_FRONT_WHISPER = 0, 1, 2
+MX_GATED_NONE, MX_GATED_SILU, MX_GATED_GELU_ERF = 0, 1, 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -44,7 +45,8 @@ class EncoderDesc(ctypes.Structure):
                 ("attn_scale", ctypes.c_float), ("gelu", _int), ("cls_pool", _int),
                 ("l2_normalize", _int), ("vocab", _i64), ("max_pos", _i64), ("front", _int),
                 ("image", _i64), ("patch", _i64), ("labels", _i64), ("mels", _i64),
-                ("frames", _i64)]
+                ("frames", _i64), ("gated_ffn", _int), ("rope", _int),
+                ("rope_theta", ctypes.c_double)]
 
 
 class Timings(ctypes.Structure):
@@ -136,6 +138,9 @@ SIGNATURES = {
                              _vp, _int, _i64]),
     "mx_layernorm_i8": (_int, [_vp, _vp, _vp, _int, _vp, _vp, ctypes.c_float, _i64, _i64, _vp,
                                _vp, _vp, _vp]),
+    "mx_rope_tables": (_int, [_i64, _i64, ctypes.c_double, _vp, _vp, _vp]),
+    "mx_rope_qkv": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "mx_glu": (_int, [_vp, _vp, _int, _vp, _int, _i64, _i64, _int]),
 }
 
 _lib = None
@@ -336,6 +341,27 @@ def layernorm_i8(ctx, x, y, gamma, beta, eps, rows, cols, out_f32, ias, q, a_sca
                                 cols, _p(out_f32), _p(ias), _p(q), _p(a_scale)))
 
 
+# ---- the RoPE / gated-FFN archs ----------------------------------------------------
+
+def rope_tables(S, hd, theta, inv_freq=None):
+    """(cos, sin) [S, hd] fp32 host tables of apply_rope_qkv."""
+    c = np.empty((S, hd), np.float32)
+    sn = np.empty((S, hd), np.float32)
+    inv = None if inv_freq is None else np.ascontiguousarray(inv_freq, np.float32)
+    check(lib().mx_rope_tables(S, hd, float(theta), None if inv is None else inv.ctypes.data,
+                               c.ctypes.data, sn.ctypes.data))
+    return c, sn
+
+
+def rope_qkv(ctx, qkv, ld_qkv, B, S, H, hd, cos_t, sin_t):
+    check(lib().mx_rope_qkv(ctx.stream, _p(qkv), ld_qkv, B, S, H, hd, _p(cos_t), _p(sin_t)))
+
+
+def glu(ctx, up, out, rows, f, act):
+    check(lib().mx_glu(ctx.stream, _p(up), _np_dtype_code(np.empty(0, up.dtype)), _p(out),
+                       _np_dtype_code(np.empty(0, out.dtype)), rows, f, act))
+
+
 def to_bf16_bits(x):
     """fp32 -> bf16 bit patterns by the reference's to_bf16 formula."""
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
@@ -426,6 +452,9 @@ class Encoder:
             d.image, d.patch, d.labels = m["image"], m["patch"], m["labels"]
         elif d.front == MX_FRONT_WHISPER:
             d.mels, d.frames = m["mels"], m["frames"]
+        d.gated_ffn = int(m.get("gated", MX_GATED_NONE))
+        d.rope = int(bool(m.get("rope", False)))
+        d.rope_theta = float(m.get("rope_theta", 0.0))
         self.desc = d
         h = _vp()
         check(lib().mx_encoder_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)))
@@ -446,6 +475,8 @@ class Encoder:
             self.set(f"layer.{l}.ln1.bias", m["ln1_b"][l])
             self.set(f"layer.{l}.ln2.weight", m["ln2_g"][l])
             self.set(f"layer.{l}.ln2.bias", m["ln2_b"][l])
+        if m.get("rope_inv_freq") is not None:
+            self.set("rope.inv_freq", m["rope_inv_freq"])
         if bert:
             self.set("embeddings.ln.weight", m["emb_ln_g"])
             self.set("embeddings.ln.bias", m["emb_ln_b"])

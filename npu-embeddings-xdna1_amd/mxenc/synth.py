@@ -30,6 +30,17 @@ CONFIGS = {
     "bge_large": dict(kind="bert", layers=24, hidden=1024, heads=16, head_dim=64, ffn=4096,
                       vocab=30522, max_pos=512, batch=128, seq=512, len_lo=512, len_hi=512,
                       cls_pool=True, sep=False),
+    # The RoPE / gated-FFN BERT archs at bge-base geometry (no BASELINE
+    # workload names them; they exercise the nomic and gte encoder paths):
+    # nomic-embed-text (SwiGLU, RoPE base 1000, mean pooling) and
+    # gte-multilingual-base (exact-erf GeGLU, RoPE from an explicit frequency
+    # set, CLS pooling).
+    "nomic": dict(kind="bert", layers=12, hidden=768, heads=12, head_dim=64, ffn=3072,
+                  vocab=30522, max_pos=512, batch=64, seq=512, len_lo=64, len_hi=512,
+                  cls_pool=False, sep=True, gated=1, rope=True, rope_theta=1000.0),
+    "gte": dict(kind="bert", layers=12, hidden=768, heads=12, head_dim=64, ffn=3072,
+                vocab=30522, max_pos=512, batch=64, seq=512, len_lo=64, len_hi=512,
+                cls_pool=True, sep=True, gated=2, rope=True, rope_theta=0.0),
     # ViT-base/16 at 224x224: 196 patches + CLS = 197 tokens, pre-LN.
     "vit_base": dict(kind="vit", layers=12, hidden=768, heads=12, head_dim=64, ffn=3072,
                      batch=256, image=224, patch=16, labels=1000, eps=1e-12),
@@ -49,8 +60,9 @@ def _normal(rng, shape, std=0.02):
     return (rng.standard_normal(size=shape, dtype=np.float32) * np.float32(std))
 
 
-def make_layers(rng, L, d, heads, hd, f, ln_random=False):
-    """Per-layer tensors, contiguous over layers."""
+def make_layers(rng, L, d, heads, hd, f, ln_random=False, gated=0):
+    """Per-layer tensors, contiguous over layers. gated: FFN-up is [d, 2f]
+    (up half, then gate half) with a [2f] bias."""
     m = {}
     scale = np.float32(1.0 / math.sqrt(hd))
     w_qkv = _normal(rng, (L, d, 3 * d))
@@ -61,8 +73,9 @@ def make_layers(rng, L, d, heads, hd, f, ln_random=False):
     m["b_qkv"] = b_qkv
     m["w_ao"] = _bf16(_normal(rng, (L, d, d)))
     m["b_ao"] = _normal(rng, (L, d))
-    m["w_up"] = _bf16(_normal(rng, (L, d, f)))
-    m["b_up"] = _normal(rng, (L, f))
+    fu = 2 * f if gated else f
+    m["w_up"] = _bf16(_normal(rng, (L, d, fu)))
+    m["b_up"] = _normal(rng, (L, fu))
     m["w_down"] = _bf16(_normal(rng, (L, f, d)))
     m["b_down"] = _normal(rng, (L, d))
     for n in ("ln1", "ln2"):
@@ -86,7 +99,12 @@ def make_model(name, seed=SEED, layers=None, ln_random=False, **over):
     L, d, H, hd, f = cfg["layers"], cfg["hidden"], cfg["heads"], cfg["head_dim"], cfg["ffn"]
     assert H * hd == d
     m = dict(cfg)
-    m.update(make_layers(rng, L, d, H, hd, f, ln_random))
+    m.update(make_layers(rng, L, d, H, hd, f, ln_random, cfg.get("gated", 0)))
+    if cfg.get("rope") and not cfg.get("rope_theta"):
+        # gte-multilingual-base's frequency set: 160000^(-j/(hd/2)) / 8^(1/(hd/2))
+        half = hd // 2
+        j = np.arange(half, dtype=np.float64)
+        m["rope_inv_freq"] = (160000.0 ** (-j / half) / 8.0 ** (1.0 / half)).astype(np.float32)
     ln = (lambda n: (1.0 + _normal(rng, (n,), 0.1)).astype(np.float32)) if ln_random else \
         (lambda n: np.ones((n,), np.float32))
     lb = (lambda n: _normal(rng, (n,), 0.05)) if ln_random else \

@@ -185,11 +185,42 @@ typedef struct {
   const float *ln1_g, *ln1_b, *ln2_g, *ln2_b;
   const float *emb_ln_g, *emb_ln_b; /* BERT only: the embedding LayerNorm   */
   const float *fin_ln_g, *fin_ln_b; /* pre-LN only: the final LayerNorm     */
+  /* The RoPE / gated-FFN BERT archs (nomic_bert_rope_swiglu,
+   * gte_new_rope_geglu; app_state.hpp:440-550), BERT only. gated: 0 plain
+   * GELU FFN, 1 SwiGLU (SiLU gate), 2 exact-erf GeGLU; w_up is then [d, 2f]
+   * (up half first, gate half second) and b_up [2f]. rope_cos/rope_sin:
+   * [S, head_dim] tables (orc_rope_tables), null = no RoPE. */
+  int64_t gated;
+  const float *rope_cos, *rope_sin;
 } orc_encoder;
 
+/* The RoPE tables of BertEncoder::apply_rope_qkv (bert_encoder.cpp:926-950):
+ * cos/sin [S, head_dim], angle s * inv_freq_j in double, rounded once to
+ * fp32, the half duplicated (column j and half + j equal). inv_freq from the
+ * container's rope_inv_freq when given (gte), else gemma_rope_tables
+ * (encoders/gemma_kernels.cpp:114-136): inv_freq_j = 1 / theta^(2j/hd) in
+ * double (nomic). Pinned against oracle/_ref's gemma_rope_tables and by the
+ * rotation invariants in the tests. */
+void orc_rope_tables(int64_t S, int64_t head_dim, double theta, const float *inv_freq,
+                     float *cos_t, float *sin_t);
+/* apply_rope_qkv's rotation (bert_encoder.cpp:951-990) of Q and K (never V)
+ * in a fused [rows, 3*H*hd] buffer, position s = row % S: per head, pairs
+ * (j, j + half): o1 = x1*c - x2*s, o2 = x2*c + x1*s with every product
+ * rounded (the AVX2 form: two multiplies and a subtract/add, no FMA). Pinned
+ * by the complex-rotation closed form and the relative-position property. */
+void orc_rope_qkv(float *qkv, int64_t rows, int64_t S, int64_t H, int64_t hd,
+                  const float *cos_t, const float *sin_t);
+/* swiglu_cpu (bert_encoder.cpp:582-627): up [rows, 2f] = lo | hi ->
+ * out [rows, f]. act 1 (SiLU): a = max((-hi) * log2e, -120), out = lo *
+ * (hi / (1 + exp2_avx2(a))); act 2 (exact-erf GeLU): out = lo *
+ * gelu_erf_exact(hi). Pinned: exp2_avx2 against oracle/_ref, SiLU and GeLU
+ * against their closed forms. */
+void orc_glu(const float *up, int64_t rows, int64_t f, int act, float *out);
+
 /* BertEncoder::run, host branch (bert_encoder.cpp:1419-1598): embedding LN,
- * then per layer QKV GEMM -> qk -> softmax_cpu (mask) -> av -> attn-out GEMM
- * -> add_into + layer_norm_cpu -> FFN-up GEMM -> gelu_cpu -> FFN-down GEMM ->
+ * then per layer QKV GEMM (-> apply_rope_qkv when m->rope_cos) -> qk ->
+ * softmax_cpu (mask) -> av -> attn-out GEMM -> add_into + layer_norm_cpu ->
+ * FFN-up GEMM -> gelu_cpu (or swiglu_cpu when m->gated) -> FFN-down GEMM ->
  * add_into + layer_norm_cpu. eps 1e-12 (hard-coded, :438/:456). x_io is
  * [B*S, hidden] fp32, updated in place (emb_in -> final hidden). add_mask is
  * [B, S] (0 / -1e30). layers_to_run < 0 means all. */

@@ -4,6 +4,7 @@
  */
 #include "orc_internal.h"
 
+#include <math.h>
 #include <stdlib.h>
 
 static float *falloc(size_t n) { return (float *)malloc(n * sizeof(float)); }
@@ -17,17 +18,20 @@ void orc_bert_run(const orc_encoder *m, float *x, const float *add_mask,
   const int64_t L = layers_to_run < 0 || layers_to_run > m->layers ? m->layers
                                                                    : layers_to_run;
   const float eps = 1e-12f; /* hard-coded in layer_norm_cpu (:438) */
+  const int64_t fu = m->gated ? 2 * f : f; /* FFN-up width: up | gate when gated */
   float *qkv = falloc((size_t)(rows * 3 * d));
   float *scores = falloc((size_t)(B * H * S * S));
   float *ctx = falloc((size_t)(rows * d));
   float *proj = falloc((size_t)(rows * d));
-  float *up = falloc((size_t)(rows * f));
+  float *up = falloc((size_t)(rows * fu));
+  float *gated = m->gated ? falloc((size_t)(rows * f)) : NULL;
   float *residual = falloc((size_t)(rows * d));
 
   orc_layer_norm_rows(x, rows, d, m->emb_ln_g, m->emb_ln_b, eps);
   for (int64_t l = 0; l < L; ++l) {
     memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
     orc_gemm_nt(x, rows, m->w_qkv + l * d * 3 * d, d, 3 * d, m->b_qkv + l * 3 * d, qkv);
+    if (m->rope_cos) orc_rope_qkv(qkv, rows, S, H, hd, m->rope_cos, m->rope_sin);
     orc_qk(qkv, B, S, H, hd, scores);
     orc_softmax_rows_poly(scores, B * H * S, S, add_mask, H * S);
     orc_av(scores, qkv, B, S, H, hd, ctx);
@@ -35,9 +39,14 @@ void orc_bert_run(const orc_encoder *m, float *x, const float *add_mask,
     orc_add_into(x, proj, residual, (size_t)(rows * d));
     orc_layer_norm_rows(x, rows, d, m->ln1_g + l * d, m->ln1_b + l * d, eps);
     memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
-    orc_gemm_nt(x, rows, m->w_up + l * d * f, d, f, m->b_up + l * f, up);
-    orc_gelu_poly_inplace(up, (size_t)(rows * f));
-    orc_gemm_nt(up, rows, m->w_down + l * f * d, f, d, m->b_down + l * d, proj);
+    orc_gemm_nt(x, rows, m->w_up + l * d * fu, d, fu, m->b_up + l * fu, up);
+    if (m->gated) {
+      orc_glu(up, rows, f, (int)m->gated, gated);
+    } else {
+      orc_gelu_poly_inplace(up, (size_t)(rows * f));
+    }
+    orc_gemm_nt(m->gated ? gated : up, rows, m->w_down + l * f * d, f, d, m->b_down + l * d,
+                proj);
     orc_add_into(x, proj, residual, (size_t)(rows * d));
     orc_layer_norm_rows(x, rows, d, m->ln2_g + l * d, m->ln2_b + l * d, eps);
   }
@@ -46,7 +55,88 @@ void orc_bert_run(const orc_encoder *m, float *x, const float *add_mask,
   free(ctx);
   free(proj);
   free(up);
+  free(gated);
   free(residual);
+}
+
+/* ---- RoPE and the gated FFN (the nomic / gte BERT archs) ------------------ */
+
+void orc_rope_tables(int64_t S, int64_t hd, double theta, const float *inv_freq,
+                     float *cos_t, float *sin_t) {
+  const int64_t half = hd / 2;
+  double *inv = (double *)malloc((size_t)half * sizeof(double));
+  for (int64_t j = 0; j < half; ++j)
+    inv[j] = inv_freq ? (double)inv_freq[j] : 1.0 / pow(theta, (2.0 * (double)j) / (double)hd);
+  for (int64_t s = 0; s < S; ++s)
+    for (int64_t j = 0; j < half; ++j) {
+      const double ang = (double)s * inv[j];
+      const float c = (float)cos(ang), sn = (float)sin(ang);
+      cos_t[s * hd + j] = cos_t[s * hd + half + j] = c;
+      sin_t[s * hd + j] = sin_t[s * hd + half + j] = sn;
+    }
+  free(inv);
+}
+
+typedef struct {
+  float *qkv;
+  const float *c, *sn;
+  int64_t rows, S, H, hd;
+} rope_task;
+
+static void rope_rotate(float *v, const float *c, const float *sn, int64_t half) {
+  for (int64_t j = 0; j < half; ++j) {
+    const float x1 = v[j], x2 = v[j + half];
+    v[j] = x1 * c[j] - x2 * sn[j];
+    v[j + half] = x2 * c[j] + x1 * sn[j];
+  }
+}
+
+static void rope_worker(void *p, int w, int nw) {
+  const rope_task *t = (const rope_task *)p;
+  const int64_t d = t->H * t->hd, half = t->hd / 2;
+  for (int64_t r = w; r < t->rows; r += nw) {
+    const int64_t s = r % t->S;
+    float *row = t->qkv + r * 3 * d;
+    for (int64_t h = 0; h < t->H; ++h) {
+      rope_rotate(row + h * t->hd, t->c + s * t->hd, t->sn + s * t->hd, half);
+      rope_rotate(row + d + h * t->hd, t->c + s * t->hd, t->sn + s * t->hd, half);
+    }
+  }
+}
+
+void orc_rope_qkv(float *qkv, int64_t rows, int64_t S, int64_t H, int64_t hd,
+                  const float *cos_t, const float *sin_t) {
+  rope_task t = {qkv, cos_t, sin_t, rows, S, H, hd};
+  orc_run(rope_worker, &t);
+}
+
+typedef struct {
+  const float *up;
+  float *out;
+  int64_t rows, f;
+  int act;
+} glu_task;
+
+static void glu_worker(void *p, int w, int nw) {
+  const glu_task *t = (const glu_task *)p;
+  for (int64_t r = w; r < t->rows; r += nw) {
+    const float *lo = t->up + r * 2 * t->f, *hi = lo + t->f;
+    float *dst = t->out + r * t->f;
+    for (int64_t j = 0; j < t->f; ++j) {
+      if (t->act == 2) {
+        dst[j] = lo[j] * orc_gelu_erf_exact(hi[j]);
+      } else {
+        float a = (0.0f - hi[j]) * 1.4426950408889634f;
+        if (a < -120.0f) a = -120.0f;
+        dst[j] = lo[j] * (hi[j] / (1.0f + orc_exp2_s(a)));
+      }
+    }
+  }
+}
+
+void orc_glu(const float *up, int64_t rows, int64_t f, int act, float *out) {
+  glu_task t = {up, out, rows, f, act};
+  orc_run(glu_worker, &t);
 }
 
 /* BertEncoder::run on an int8 container, the GEMMs on the array
@@ -58,12 +148,14 @@ void orc_bert_run_i8(const orc_encoder *m, const orc_i8_operands *q, float *x,
   const int64_t L = layers_to_run < 0 || layers_to_run > m->layers ? m->layers
                                                                    : layers_to_run;
   const float eps = 1e-12f;
-  const int64_t Ks[4] = {d, d, d, f}, Ns[4] = {3 * d, d, f, d};
+  const int64_t fu = m->gated ? 2 * f : f; /* FFN-up width: up | gate when gated */
+  const int64_t Ks[4] = {d, d, d, f}, Ns[4] = {3 * d, d, fu, d};
   float *qkv = falloc((size_t)(rows * 3 * d));
   float *scores = falloc((size_t)(B * H * S * S));
   float *ctx = falloc((size_t)(rows * d));
   float *proj = falloc((size_t)(rows * d));
-  float *up = falloc((size_t)(rows * f));
+  float *up = falloc((size_t)(rows * fu));
+  float *gated = m->gated ? falloc((size_t)(rows * f)) : NULL;
   float *residual = falloc((size_t)(rows * d));
 #define GEMM_I8(i, A, bias, out)                                                        \
   orc_gemm_i8_dequant((A), rows, Ks[i], q->ias[i] + l * Ks[i], q->wq[i] + l * Ks[i] * Ns[i], \
@@ -72,6 +164,7 @@ void orc_bert_run_i8(const orc_encoder *m, const orc_i8_operands *q, float *x,
   for (int64_t l = 0; l < L; ++l) {
     memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
     GEMM_I8(0, x, m->b_qkv + l * 3 * d, qkv);
+    if (m->rope_cos) orc_rope_qkv(qkv, rows, S, H, hd, m->rope_cos, m->rope_sin);
     orc_qk(qkv, B, S, H, hd, scores);
     orc_softmax_rows_poly(scores, B * H * S, S, add_mask, H * S);
     orc_av(scores, qkv, B, S, H, hd, ctx);
@@ -79,9 +172,13 @@ void orc_bert_run_i8(const orc_encoder *m, const orc_i8_operands *q, float *x,
     orc_add_into(x, proj, residual, (size_t)(rows * d));
     orc_layer_norm_rows(x, rows, d, m->ln1_g + l * d, m->ln1_b + l * d, eps);
     memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
-    GEMM_I8(2, x, m->b_up + l * f, up);
-    orc_gelu_poly_inplace(up, (size_t)(rows * f));
-    GEMM_I8(3, up, m->b_down + l * d, proj);
+    GEMM_I8(2, x, m->b_up + l * fu, up);
+    if (m->gated) {
+      orc_glu(up, rows, f, (int)m->gated, gated);
+    } else {
+      orc_gelu_poly_inplace(up, (size_t)(rows * f));
+    }
+    GEMM_I8(3, m->gated ? gated : up, m->b_down + l * d, proj);
     orc_add_into(x, proj, residual, (size_t)(rows * d));
     orc_layer_norm_rows(x, rows, d, m->ln2_g + l * d, m->ln2_b + l * d, eps);
   }
@@ -91,6 +188,7 @@ void orc_bert_run_i8(const orc_encoder *m, const orc_i8_operands *q, float *x,
   free(ctx);
   free(proj);
   free(up);
+  free(gated);
   free(residual);
 }
 

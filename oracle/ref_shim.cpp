@@ -4,9 +4,11 @@
 // Compiled by oracle/Makefile (target `ref`) directly against the headers in
 // the reference checkout (runtime/include/common/host_kernels.hpp,
 // runtime/include/common/conv_host.hpp, runtime/include/common/host_b.hpp)
-// and runtime/src/pool.cpp and runtime/src/model.cpp (the .npue reader);
+// and runtime/src/pool.cpp, runtime/src/model.cpp (the .npue reader) and
+// runtime/src/encoders/gemma_kernels.cpp (the RoPE tables);
 // nothing of the reference is copied here. The output lives in oracle/_ref/
 // only.
+#include "encoders/gemma_kernels.hpp"
 #include "common/conv_host.hpp"
 #include "common/host_b.hpp"
 #include "common/host_kernels.hpp"
@@ -163,6 +165,16 @@ int ref_npue_tensor(const char *path, const char *name, char *dtype, int64_t *pa
   } catch (const std::exception &) {
     return -1;
   }
+}
+
+}  // extern "C"
+
+extern "C" {
+
+// gemma_rope_tables (encoders/gemma_kernels.cpp:114-136): the RoPE cos/sin
+// tables from a base, the form BertEncoder::apply_rope_qkv uses for nomic.
+void ref_gemma_rope_tables(int64_t S, int64_t hd, double theta, float *cos_t, float *sin_t) {
+  npue::gemma_rope_tables(S, hd, theta, cos_t, sin_t);
 }
 
 }  // extern "C"

@@ -137,6 +137,17 @@ def bert_container(m, tile_k=64, tile_n=64, mac=(8, 8), arch="bert_abs_gelu_post
            "a_dtype": "i8" if int8 else "bf16",
            "fusions": {"qkv_fused": True, "transposed_to_kn": True,
                        "qk_scale_folded_into_q": True}}
+    if m.get("rope"):
+        # the RoPE / gated-FFN archs' keys (tools/pack/pack_npue.py; read by
+        # app::set_model_shape, app_state.hpp:440-550)
+        cfg.update({"position_embedding_type": "rope", "gated_ffn": True})
+        if m.get("rope_inv_freq") is not None:
+            cfg.update({"glu_halves": "up_first|gate_second (ffn_up = [up | gate])",
+                        "rope_inv_freq": [float(v) for v in m["rope_inv_freq"]],
+                        "activation": "gelu"})
+        else:
+            cfg.update({"swiglu_halves": "fc11_up|fc12_gate", "rope_theta": m["rope_theta"],
+                        "activation": "silu"})
     cfg.update(extra_config or {})
     c = Container(cfg)
     c.add_f32("embeddings.word", m["word"], "embedding")

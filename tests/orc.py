@@ -29,7 +29,8 @@ class OrcEncoder(ctypes.Structure):
                 ("head_dim", _c_i64), ("ffn", _c_i64)] + [
         (n, _vp) for n in ("w_qkv", "b_qkv", "w_ao", "b_ao", "w_up", "b_up",
                            "w_down", "b_down", "ln1_g", "ln1_b", "ln2_g", "ln2_b",
-                           "emb_ln_g", "emb_ln_b", "fin_ln_g", "fin_ln_b")]
+                           "emb_ln_g", "emb_ln_b", "fin_ln_g", "fin_ln_b")] + [
+        ("gated", _c_i64), ("rope_cos", _vp), ("rope_sin", _vp)]
 
 
 class OrcI8(ctypes.Structure):
@@ -92,6 +93,9 @@ def load():
         "orc_gemm_i8_dequant": (None, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _c_i64, _vp]),
         "orc_bert_run_i8": (None, [ctypes.POINTER(OrcEncoder), ctypes.POINTER(OrcI8), _vp, _vp,
                                    _c_i64, _c_i64, _c_i64]),
+        "orc_rope_tables": (None, [_c_i64, _c_i64, ctypes.c_double, _vp, _vp, _vp]),
+        "orc_rope_qkv": (None, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp]),
+        "orc_glu": (None, [_vp, _c_i64, _c_i64, ctypes.c_int, _vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -125,6 +129,7 @@ def load_ref():
         "ref_npue_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
         "ref_npue_tensor": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
                                            _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+        "ref_gemma_rope_tables": (None, [_c_i64, _c_i64, ctypes.c_double, _vp, _vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -156,6 +161,18 @@ def encoder_struct(m, keep):
             a = np.ascontiguousarray(a, dtype=np.float32)
             keep.append(a)
             setattr(s, n, a.ctypes.data)
+    s.gated = int(m.get("gated", 0))
+    if m.get("rope"):
+        # tables for every position the model has; a run indexes rows s < S
+        n_pos, hd = int(m.get("max_pos", 512)), m["head_dim"]
+        c = np.empty((n_pos, hd), np.float32)
+        sn = np.empty((n_pos, hd), np.float32)
+        inv = m.get("rope_inv_freq")
+        inv = None if inv is None else np.ascontiguousarray(inv, np.float32)
+        load().orc_rope_tables(n_pos, hd, float(m.get("rope_theta", 0.0)),
+                               None if inv is None else inv.ctypes.data, P(c), P(sn))
+        keep += [c, sn] + ([inv] if inv is not None else [])
+        s.rope_cos, s.rope_sin = c.ctypes.data, sn.ctypes.data
     return s
 
 

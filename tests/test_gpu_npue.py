@@ -91,7 +91,8 @@ def test_encoder_from_npue_is_bitwise_the_set_encoder(tmp_path, ctx, orc, tiling
 
 
 @pytest.mark.parametrize("over,why", [
-    (dict(arch="nomic_bert_rope_swiglu"), "RoPE and gated-FFN archs"),
+    (dict(arch="gemma3_mqa_rope_geglu"), "other archs share its tensor names"),
+    (dict(arch="nomic_bert_rope_swiglu"), "position_embedding_type is not 'rope'"),
     (dict(gemm_layout="host"), "gemm_layout \"host\""),
     (dict(pooling="max"), "unknown pooling mode 'max'"),
 ])
