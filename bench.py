@@ -6,7 +6,11 @@
 A step is one pass of the hot path over one batch: token ids and the
 attention mask (already in HBM) -> embedding sum -> the whole encoder stack ->
 pooling + L2 normalisation (EmbedService::chunk minus the tokenizer), on the
-bge-base geometry at batch 64 x seq 512 by default. Weights are random-init
+bge-base geometry at batch 64 x seq 512 by default. The embed path packs each
+sequence's rows before its kv_len (the padding past it is never attended and
+never pooled; the pooled output is the padded computation's bit for bit);
+the same steps are also timed padded, as EmbedService::chunk computes them,
+and reported beside (--padded makes the padded run the headline). Weights are random-init
 (N(0, 0.02), Q scale folded, bf16), inputs synthetic; see mxenc/synth.py.
 
 Prints one JSON line: sequences/s, the GEMM family's MFMA roofline (HIP event
@@ -111,6 +115,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="bge_base")
+    ap.add_argument("--padded", action="store_true",
+                    help="the headline computes every padded row (token packing off)")
     ap.add_argument("--int8", action="store_true",
                     help="the W8A8 datapath (BERT configs): int8 operands by the packer's "
                          "scheme over the same random weights")
@@ -152,9 +158,11 @@ def main():
         sys.exit(2)
     ctx = mxenc.Context(0)
     enc = mxenc.Encoder(ctx, m, int8=synth.quantise_model(m) if args.int8 else None)
+    packing = kind == "bert" and not args.padded
     if kind == "bert":
         ids, am, lens = synth.make_text_inputs(m)
         B, S = ids.shape
+        enc.set_packing(packing)
         d_ids, d_am = ctx.put(ids), ctx.put(am)
         out = ctx.empty((B, m["hidden"]), np.float32)
         step = lambda: enc.embed(d_ids, d_am, B, S, out)  # noqa: E731
@@ -187,8 +195,24 @@ def main():
     ctx.sync()
     dt = time.perf_counter() - t0
     seq_s = args.steps * B / dt
-    print(f"bench: {args.steps} steps in {dt*1e3:.1f} ms -> {seq_s:.1f} {unit}",
-          file=sys.stderr, flush=True)
+    print(f"bench: {args.steps} steps in {dt*1e3:.1f} ms -> {seq_s:.1f} {unit}"
+          f"{' (token packing)' if packing else ''}", file=sys.stderr, flush=True)
+    padded = None
+    if packing:
+        # The same steps with every padded row computed (EmbedService::chunk).
+        enc.set_packing(False)
+        step()
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        ctx.sync()
+        pdt = time.perf_counter() - t0
+        enc.set_packing(True)
+        padded = {"value": args.steps * B / pdt, "ms_per_step": pdt / args.steps * 1e3,
+                  "rows_per_step": B * S}
+        print(f"bench: padded {padded['value']:.1f} {unit} ({padded['ms_per_step']:.2f} ms/step)",
+              file=sys.stderr, flush=True)
 
     # The same steps again with a HIP event pair around every launch, on the
     # stream the kernels run on: per-kernel-family durations for the roofline.
@@ -222,7 +246,8 @@ def main():
     # The dominant GEMM kernel: sites grouped by the kernel instantiation they
     # run -- tile plan plus epilogue, residual and C type, the name rocprof
     # reports -- and the group with the most time.
-    d, f, M = m["hidden"], m["ffn"], B * S
+    # rows the stack ran over: the packed rows (the valid lengths) or B*S
+    d, f, M = m["hidden"], m["ffn"], int(lens.sum()) if packing else B * S
     # (M, N, K, epilogue, residual, bf16 C) of each site: the BERT stack
     # narrows its projections to bf16 for the residual-fused LayerNorm; the
     # pre-LN stacks add them into the fp32 residual stream in the epilogue.
@@ -293,6 +318,8 @@ def main():
         "attention": {"achieved_tflops": attn_tflops, "frac": attn_tflops / BF16_PEAK_TFLOPS,
                       "ms_per_step": tot["attn_ms"] / args.steps},
         "layernorm_ms_per_step": tot["ln_ms"] / args.steps,
+        "token_packing": {"on": packing, "rows_per_step": M, "padded_rows_per_step": B * S,
+                          "padded": padded} if kind == "bert" else None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

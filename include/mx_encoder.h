@@ -397,6 +397,17 @@ int mx_encoder_run(mx_encoder *enc, mx_stream *s, float *x_io,
 int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids,
                      const float *attn_mask, int64_t B, int64_t S, float *out);
 
+/* Token packing in mx_encoder_embed (on by default): the only rows of a
+ * sequence that reach its pooled row are those before kv_len (every later
+ * row is masked: never attended as a key, never pooled), so embed computes
+ * only those -- each sequence's rows packed back to back, the GEMMs and
+ * LayerNorms over the packed row count, attention per sequence over its own
+ * rows. The pooled output is the padded computation's, bit for bit;
+ * EmbedService::chunk (embed_service.cpp:29-64) computes the padded batch,
+ * which off restores. The packed row count is read back to the host once
+ * per batch. mx_encoder_run always computes every row (it returns them all). */
+int mx_encoder_set_packing(mx_encoder *enc, int on);
+
 /* VitEncoder::run + head_matvec (runtime/src/vit/encoder.cpp:222-431,
  * runtime/src/vit/head.cpp:16-49), every step on the GPU: pixels fp32
  * [B, 3, image, image] (device) -> im2col patch rows (c, ky, kx order) -> patch

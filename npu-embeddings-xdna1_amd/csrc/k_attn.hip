@@ -42,7 +42,8 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
                                                   const float *__restrict__ add_mask,
                                                   const int32_t *__restrict__ kv_len,
                                                   uint16_t *__restrict__ ctx, int64_t ldo,
-                                                  int n_qblk, int force_logits) {
+                                                  int n_qblk, int force_logits,
+                                                  const int32_t *__restrict__ seq_start) {
   constexpr int KS = HD + 8;   // K row stride in LDS (elements)
   constexpr int VS = BKV + 4;  // Vt row stride in LDS (elements)
   constexpr int KCH = BKV * HD / 8 / 256;  // 16-byte K chunks per thread (1 or 2)
@@ -60,11 +61,18 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
   const int bh = blk / n_qblk;
   const int h = bh % H, b = bh / H;
   const int d = H * HD;
-  const uint16_t *base = qkv + (int64_t)b * S * ldq;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, li = lane & 31;
   int kvl = kv_len ? kv_len[b] : S;
   kvl = kvl < 1 ? 1 : (kvl > S ? S : kvl);
+  // Dense rows: sequence b is rows b*S .. b*S + S - 1, every query is
+  // computed and keys past kv_len are read but weighted 0. Packed rows: only
+  // the sequence's kv_len rows exist, so queries and keys stop there (a key
+  // past it would be the next sequence's row).
+  const int64_t row0 = seq_start ? (int64_t)seq_start[b] : (int64_t)b * S;
+  const int lim = seq_start ? kvl : S;
+  if (qb * BQ >= lim) return;
+  const uint16_t *base = qkv + row0 * ldq;
 
   // Q fragments: B operand of S^T = K Q^T (column = query, k = head dim).
   const int q = qb * BQ + wave * 32 + li;
@@ -72,7 +80,7 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
 #pragma unroll
   for (int kk = 0; kk < NKK; ++kk) {
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (q < S) v = *(const uint4 *)(base + (int64_t)q * ldq + h * HD + kk * 16 + g * 8);
+    if (q < lim) v = *(const uint4 *)(base + (int64_t)q * ldq + h * HD + kk * 16 + g * 8);
     qf[kk] = __builtin_bit_cast(bf16x8, v);
   }
 
@@ -86,7 +94,7 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int c = tid + i * 256, key = c / (HD / 8), c8 = (c % (HD / 8)) * 8;
-      rk[i] = (k0 + key < S)
+      rk[i] = (k0 + key < lim)
                   ? *(const uint4 *)(base + (int64_t)(k0 + key) * ldq + d + h * HD + c8)
                   : make_uint4(0, 0, 0, 0);
     }
@@ -94,7 +102,7 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = k0 + vkb * 4 + r;
-        rv[r] = key < S ? *(const uint2 *)(base + (int64_t)key * ldq + 2 * d + h * HD + vhb * 4)
+        rv[r] = key < lim ? *(const uint2 *)(base + (int64_t)key * ldq + 2 * d + h * HD + vhb * 4)
                         : make_uint2(0, 0);
       }
     }
@@ -234,8 +242,8 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
 
   const float l = l_run + __shfl_xor(l_run, 32);
   const float inv = 1.0f / l;
-  if (q < S) {
-    uint16_t *dst = ctx + ((int64_t)b * S + q) * ldo + h * HD;
+  if (q < lim) {
+    uint16_t *dst = ctx + (row0 + q) * ldo + h * HD;
 #pragma unroll
     for (int ht = 0; ht < NHT; ++ht)
 #pragma unroll
@@ -261,11 +269,11 @@ hipError_t attention(const AttnArgs &a, hipStream_t s) {
   if (a.hd == 64)
     attn_fwd_k<64><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
                                                    a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
-                                                   force_logits);
+                                                   force_logits, a.seq_start);
   else if (a.hd == 32)
     attn_fwd_k<32><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
                                                    a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
-                                                   force_logits);
+                                                   force_logits, a.seq_start);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

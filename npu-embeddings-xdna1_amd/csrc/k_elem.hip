@@ -403,18 +403,61 @@ __global__ __launch_bounds__(256) void mask_k(const float *__restrict__ am, int6
   if (threadIdx.x == 0 && kv_len) kv_len[b] = last > 0 ? last : (int32_t)S;
 }
 
+// ---- token packing: only the rows pooling can see ---------------------------
+// Sequence b keeps its rows s < kv_len[b] (every row past it is masked: it is
+// never attended as a key and its output is never pooled). seq_start is the
+// exclusive scan of kv_len, seq_start[B] the packed row count; packed row
+// seq_start[b] + s is dense row b*S + s, and row_pos records its position s.
+
+__global__ void pack_plan_k(const int32_t *__restrict__ kv_len, int64_t B,
+                            int32_t *__restrict__ seq_start) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int32_t acc = 0;
+  for (int64_t b = 0; b < B; ++b) {
+    seq_start[b] = acc;
+    acc += kv_len[b];
+  }
+  seq_start[B] = acc;
+}
+
+__global__ __launch_bounds__(256) void embed_sum_packed_k(
+    const int32_t *__restrict__ ids, int64_t rows, int64_t S, int64_t d,
+    const float *__restrict__ word, int64_t vocab, const float *__restrict__ pos,
+    const float *__restrict__ type0, const int32_t *__restrict__ kv_len,
+    const int32_t *__restrict__ seq_start, float *__restrict__ emb, int32_t *__restrict__ row_pos,
+    int *err) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int64_t b = r / S, s = r - b * S;
+  if (s >= kv_len[b]) return;
+  const int64_t p = seq_start[b] + s;
+  if (lane == 0) row_pos[p] = (int32_t)s;
+  const int32_t id = ids[r];
+  if (id < 0 || id >= vocab) {
+    if (lane == 0) atomicOr(err, 1);
+    for (int64_t c = lane; c < d; c += 64) emb[p * d + c] = 0.0f;
+    return;
+  }
+  const float *wv = word + (int64_t)id * d;
+  const float *pv = pos + s * d;
+  for (int64_t c = lane; c < d; c += 64) emb[p * d + c] = (wv[c] + pv[c]) + type0[c];
+}
+
 // ---- pooling (app_state.hpp:335-374), bit-exact with the host form ----------
 
 __global__ __launch_bounds__(256) void pool_k(const float *__restrict__ h,
                                               const float *__restrict__ am, int64_t S,
                                               int64_t d, int cls, int l2, float *out,
-                                              int *err) {
+                                              int *err, const int32_t *__restrict__ seq_start) {
   extern __shared__ double acc[];
   __shared__ double nrm_s;
   __shared__ float denom_s;
   const int64_t b = blockIdx.x;
   const float *amb = am + b * S;
-  const float *hb = h + b * S * d;
+  // Packed rows: the loop below reads row s only where the mask is nonzero,
+  // i.e. only rows s < kv_len[b], the ones packing kept.
+  const float *hb = h + (seq_start ? (int64_t)seq_start[b] : b * S) * d;
   if (cls) {
     if (amb[0] == 0.0f) {
       if (threadIdx.x == 0) atomicOr(err, 2);
@@ -596,8 +639,24 @@ hipError_t mask_build(const float *am, int64_t B, int64_t S, float *add_mask, in
 }
 
 hipError_t pool_rows(const float *h, const float *am, int64_t B, int64_t S, int64_t d, int cls,
-                     int l2, float *out, int *err, hipStream_t s) {
-  pool_k<<<(unsigned)B, 256, (size_t)d * sizeof(double), s>>>(h, am, S, d, cls, l2, out, err);
+                     int l2, float *out, int *err, hipStream_t s, const int32_t *seq_start) {
+  pool_k<<<(unsigned)B, 256, (size_t)d * sizeof(double), s>>>(h, am, S, d, cls, l2, out, err,
+                                                              seq_start);
+  return hipGetLastError();
+}
+
+hipError_t pack_plan(const int32_t *kv_len, int64_t B, int32_t *seq_start, hipStream_t s) {
+  pack_plan_k<<<1, 64, 0, s>>>(kv_len, B, seq_start);
+  return hipGetLastError();
+}
+
+hipError_t embed_sum_packed(const int32_t *ids, int64_t B, int64_t S, int64_t d,
+                            const float *word, int64_t vocab, const float *pos,
+                            const float *type0, const int32_t *kv_len, const int32_t *seq_start,
+                            float *emb, int32_t *row_pos, int *err, hipStream_t s) {
+  const int64_t rows = B * S;
+  embed_sum_packed_k<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(
+      ids, rows, S, d, word, vocab, pos, type0, kv_len, seq_start, emb, row_pos, err);
   return hipGetLastError();
 }
 

@@ -2,7 +2,8 @@
 // gte_new_rope_geglu) on gfx950, both memory-bound passes:
 //
 // rope_qkv_k: BertEncoder::apply_rope_qkv (bert_encoder.cpp:951-990) on the
-// bf16 fused Q|K|V rows, in place, Q and K only. Position s = row % S; per
+// bf16 fused Q|K|V rows, in place, Q and K only. Position s = row % S (or the
+// packed row's recorded position); per
 // head the pairs (j, j + hd/2) rotate by the table's angle:
 //   o1 = x1*c - x2*s,  o2 = x2*c + x1*s
 // each product rounded as the host's AVX2 form (no fused multiply-add), the
@@ -31,9 +32,10 @@ namespace {
 __global__ __launch_bounds__(256) void rope_qkv_k(uint16_t *__restrict__ qkv, int64_t ld,
                                                   int S, int H, int hd,
                                                   const float *__restrict__ cos_t,
-                                                  const float *__restrict__ sin_t) {
+                                                  const float *__restrict__ sin_t,
+                                                  const int32_t *__restrict__ row_pos) {
   const int64_t row = blockIdx.x;
-  const int s = (int)(row % S), half = hd / 2, d = H * hd;
+  const int s = row_pos ? row_pos[row] : (int)(row % S), half = hd / 2, d = H * hd;
   const int per_head = half / 2;  // thread units (two pairs) per head
   const int units = 2 * H * per_head;
   uint16_t *base = qkv + row * ld;
@@ -103,8 +105,9 @@ __global__ __launch_bounds__(256) void glu_k(const void *__restrict__ in, void *
 namespace mxk {
 
 hipError_t rope_qkv(uint16_t *qkv, int64_t ld, int64_t rows, int S, int H, int hd,
-                    const float *cos_t, const float *sin_t, hipStream_t s) {
-  rope_qkv_k<<<(unsigned)rows, 256, 0, s>>>(qkv, ld, S, H, hd, cos_t, sin_t);
+                    const float *cos_t, const float *sin_t, hipStream_t s,
+                    const int32_t *row_pos) {
+  rope_qkv_k<<<(unsigned)rows, 256, 0, s>>>(qkv, ld, S, H, hd, cos_t, sin_t, row_pos);
   return hipGetLastError();
 }
 

@@ -153,7 +153,8 @@ int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t 
 
 int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
                       int64_t H, int64_t hd, float scale, const float *add_mask,
-                      const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx) {
+                      const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx,
+                      const int32_t *seq_start) {
   if (!s) return fail(MX_E_INVALID, "attention: null stream");
   if (!qkv || !ctx) return fail(MX_E_INVALID, "attention: null qkv or ctx");
   if (B <= 0 || S <= 0 || H <= 0) return fail(MX_E_INVALID, "attention: zero dimension");
@@ -171,7 +172,9 @@ int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t
   if (B * H * ((S + 127) / 128) > INT32_MAX || S > INT32_MAX / 4)
     return fail(MX_E_INVALID, "attention: grid too large");
   if (!std::isfinite(scale)) return fail(MX_E_INVALID, "attention: non-finite scale");
-  mxk::AttnArgs a{qkv, ld_qkv, B, S, H, hd, scale, add_mask, kv_len, ctx, ld_ctx};
+  if (seq_start && !kv_len)
+    return fail(MX_E_INVALID, "attention: packed rows need kv_len");
+  mxk::AttnArgs a{qkv, ld_qkv, B, S, H, hd, scale, add_mask, kv_len, ctx, ld_ctx, seq_start};
   const hipError_t e = mxk::attention(a, s->stream);
   return e == hipSuccess ? MX_OK : hip_fail(e, "attention launch");
 }
@@ -194,7 +197,8 @@ void rope_tables_host(int64_t S, int64_t hd, double theta, const float *inv_freq
 }
 
 int rope_checked(mx_stream *s, uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S, int64_t H,
-                 int64_t hd, const float *cos_t, const float *sin_t) {
+                 int64_t hd, const float *cos_t, const float *sin_t, int64_t rows,
+                 const int32_t *row_pos) {
   if (!s) return fail(MX_E_INVALID, "rope_qkv: null stream");
   if (!qkv || !cos_t || !sin_t) return fail(MX_E_INVALID, "rope_qkv: null qkv or table");
   if (B <= 0 || S <= 0 || H <= 0 || hd <= 0) return fail(MX_E_INVALID, "rope_qkv: zero dimension");
@@ -206,8 +210,8 @@ int rope_checked(mx_stream *s, uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t
   if (!aligned(qkv, 4) || !aligned(cos_t, 8) || !aligned(sin_t, 8))
     return fail(MX_E_INVALID, "rope_qkv: misaligned qkv or table");
   if (B * S > INT32_MAX) return fail(MX_E_INVALID, "rope_qkv: too many rows");
-  const hipError_t e = mxk::rope_qkv(qkv, ld_qkv, B * S, (int)S, (int)H, (int)hd, cos_t, sin_t,
-                                     s->stream);
+  const hipError_t e = mxk::rope_qkv(qkv, ld_qkv, rows < 0 ? B * S : rows, (int)S, (int)H,
+                                     (int)hd, cos_t, sin_t, s->stream, row_pos);
   return e == hipSuccess ? MX_OK : hip_fail(e, "rope_qkv launch");
 }
 

@@ -83,6 +83,9 @@ struct mx_encoder {
   int64_t rope_rows = 0;
   bool i8 = false;       // set by mx_encoder_ready: every GEMM operand is int8
   int32_t *kv_len = nullptr;
+  // Token packing (embed): seq_start [B + 1] and each packed row's position.
+  bool packing = true;
+  int32_t *seq_start = nullptr, *row_pos = nullptr;
   // timing
   bool timing = false;
   std::vector<hipEvent_t> events;
@@ -164,9 +167,13 @@ int ensure_mask_ws(mx_encoder *enc, int64_t B, int64_t rows) {
     const int64_t nr = rows > enc->ws_mask_rows ? rows : enc->ws_mask_rows;
     free_dev(enc->add_mask);
     free_dev(enc->kv_len);
+    free_dev(enc->seq_start);
+    free_dev(enc->row_pos);
     enc->ws_batch = enc->ws_mask_rows = 0;
     int rc = dev_alloc((void **)&enc->add_mask, nr * 4, "workspace mask");
     if (!rc) rc = dev_alloc((void **)&enc->kv_len, nb * 4, "workspace kv_len");
+    if (!rc) rc = dev_alloc((void **)&enc->seq_start, (nb + 1) * 4, "workspace seq_start");
+    if (!rc) rc = dev_alloc((void **)&enc->row_pos, nr * 4, "workspace row_pos");
     if (rc) return rc;
     enc->ws_batch = nb;
     enc->ws_mask_rows = nr;
@@ -279,10 +286,11 @@ int ensure_rope(mx_encoder *enc, int64_t S) {
   return MX_OK;
 }
 
-int rope_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S) {
+int rope_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, int64_t M,
+           const int32_t *row_pos) {
   Bracket br(enc, s->stream, CAT_OTHER);
   return rope_checked(s, enc->qkv, 3 * enc->desc.hidden, B, S, enc->desc.heads,
-                      enc->desc.head_dim, enc->rope_cos, enc->rope_sin);
+                      enc->desc.head_dim, enc->rope_cos, enc->rope_sin, M, row_pos);
 }
 
 int glu_l(mx_encoder *enc, mx_stream *s, int64_t M) {
@@ -292,13 +300,20 @@ int glu_l(mx_encoder *enc, mx_stream *s, int64_t M) {
 }
 
 int attn_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, const float *mask,
-           const int32_t *kv_len) {
+           const int32_t *kv_len, const int32_t *seq_start = nullptr) {
   Bracket br(enc, s->stream, CAT_ATTN);
   const int64_t d = enc->desc.hidden;
   enc->attn_flop += 4.0 * B * enc->desc.heads * (double)S * S * enc->desc.head_dim;
   return attention_checked(s, enc->qkv, 3 * d, B, S, enc->desc.heads, enc->desc.head_dim,
-                           enc->desc.attn_scale, mask, kv_len, enc->ctxb, d);
+                           enc->desc.attn_scale, mask, kv_len, enc->ctxb, d, seq_start);
 }
+
+// The rows one pass runs over: M = B*S dense rows, or the packed rows of
+// token packing (seq_start / row_pos non-null, M = seq_start[B]).
+struct Rows {
+  int64_t M;
+  const int32_t *seq_start = nullptr, *row_pos = nullptr;
+};
 
 // One GEMM site of a layer on the encoder's datapath: bf16 A (A_bf) times
 // the bf16 panel, or the quantised A in xq/sa times the int8 operand.
@@ -321,8 +336,8 @@ int site_ln(mx_encoder *enc, mx_stream *s, float *x, const void *y, int y_dt, co
 }
 
 int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
-             int64_t B, int64_t S) {
-  const int64_t M = B * S, d = enc->desc.hidden, f = enc->desc.ffn;
+             int64_t B, int64_t S, const Rows &rows) {
+  const int64_t M = rows.M, d = enc->desc.hidden, f = enc->desc.ffn;
   const int epi = enc->desc.gelu == MX_GELU_ERF ? MX_EPI_GELU_ERF : MX_EPI_GELU_POLY;
   const size_t L = enc->layers.size();
   const bool gated = enc->desc.gated_ffn != MX_GATED_NONE;
@@ -336,8 +351,8 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
     const LayerW &w = enc->layers[l];
     rc = site_gemm(enc, s, w, SITE_QKV, enc->xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->qkv,
                    MX_BF16);
-    if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S);
-    if (!rc) rc = attn_l(enc, s, B, S, mask, kvl);
+    if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S, M, rows.row_pos);
+    if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, rows.seq_start);
     if (!rc && enc->i8) rc = quant_l(enc, s, enc->ctxb, M, d, w.ias[SITE_AO]);
     if (!rc)
       rc = site_gemm(enc, s, w, SITE_AO, enc->ctxb, M, d, d, MX_EPI_NONE, nullptr, enc->proj,
@@ -383,8 +398,9 @@ int run_preln(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const 
 }
 
 int run_impl(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
-             int64_t B, int64_t S) {
-  return enc->desc.arch == MX_ARCH_BERT ? run_bert(enc, s, x, mask, kvl, B, S)
+             int64_t B, int64_t S, const Rows *rows = nullptr) {
+  const Rows dense{B * S};
+  return enc->desc.arch == MX_ARCH_BERT ? run_bert(enc, s, x, mask, kvl, B, S, rows ? *rows : dense)
                                         : run_preln(enc, s, x, mask, kvl, B, S);
 }
 
@@ -573,6 +589,8 @@ void mx_encoder_destroy(mx_encoder *enc) {
     free_dev(enc->rope_sin);
     free_dev(enc->add_mask);
     free_dev(enc->kv_len);
+    free_dev(enc->seq_start);
+    free_dev(enc->row_pos);
     free_dev(enc->f_rows);
     free_dev(enc->f_cls);
     free_dev(enc->f_mel);
@@ -606,6 +624,7 @@ int mx_encoder_clone(mx_encoder *enc, mx_encoder **out) {
   c->layers = enc->layers;
   c->i8 = enc->i8;
   c->rope_inv = enc->rope_inv;
+  c->packing = enc->packing;
   for (int i = 0; i < 2; ++i) {
     c->emb_ln[i] = enc->emb_ln[i];
     c->fin_ln[i] = enc->fin_ln[i];
@@ -891,21 +910,37 @@ int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids, const fl
   if (!rc) rc = ensure_ws(enc, B, S);
   if (!rc) rc = begin_timing(enc, s);
   if (rc) return rc;
+  Rows rows{B * S};
   {
     Bracket br(enc, s->stream, CAT_OTHER);
-    hipError_t e = mxk::embed_sum(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab,
-                                  enc->pos, enc->type, enc->emb, s->err_dev, s->stream);
-    if (e == hipSuccess)
-      e = mxk::mask_build(attn_mask, B, S, enc->add_mask, enc->kv_len, s->stream);
+    hipError_t e = mxk::mask_build(attn_mask, B, S, enc->add_mask, enc->kv_len, s->stream);
+    if (e == hipSuccess && enc->packing) {
+      // Token packing: the packed row count is needed on the host for the
+      // launches, so the plan is read back (one small copy per batch).
+      int32_t total = 0;
+      e = mxk::pack_plan(enc->kv_len, B, enc->seq_start, s->stream);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(&total, enc->seq_start + B, sizeof total, hipMemcpyDeviceToHost,
+                           s->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+      if (e == hipSuccess)
+        e = mxk::embed_sum_packed(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab,
+                                  enc->pos, enc->type, enc->kv_len, enc->seq_start, enc->emb,
+                                  enc->row_pos, s->err_dev, s->stream);
+      rows = Rows{total, enc->seq_start, enc->row_pos};
+    } else if (e == hipSuccess) {
+      e = mxk::embed_sum(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab, enc->pos,
+                         enc->type, enc->emb, s->err_dev, s->stream);
+    }
     if (e != hipSuccess) return hip_fail(e, "embed launch");
   }
-  rc = run_impl(enc, s, enc->emb, enc->add_mask, enc->kv_len, B, S);
+  rc = run_impl(enc, s, enc->emb, enc->add_mask, enc->kv_len, B, S, &rows);
   if (rc) return rc;
   {
     Bracket br(enc, s->stream, CAT_OTHER);
     const hipError_t e =
         mxk::pool_rows(enc->emb, attn_mask, B, S, enc->desc.hidden, enc->desc.cls_pool,
-                       enc->desc.l2_normalize, out, s->err_dev, s->stream);
+                       enc->desc.l2_normalize, out, s->err_dev, s->stream, rows.seq_start);
     if (e != hipSuccess) return hip_fail(e, "pool launch");
   }
   end_timing(enc, s);
@@ -1006,6 +1041,13 @@ int mx_encoder_whisper(mx_encoder *enc, mx_stream *s, const float *mel, int64_t 
   if (rc) return rc;
   end_timing(enc, s);
   return mx_sync(s);
+}
+
+int mx_encoder_set_packing(mx_encoder *enc, int on) {
+  clear_error();
+  if (!enc) return fail(MX_E_INVALID, "encoder_set_packing: null encoder");
+  enc->packing = on != 0;
+  return MX_OK;
 }
 
 int mx_encoder_set_timing(mx_encoder *enc, int on) {

@@ -55,7 +55,8 @@ int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t 
                  const float *residual, void *C, int c_dtype, int64_t ldc);
 int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
                       int64_t H, int64_t hd, float scale, const float *add_mask,
-                      const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx);
+                      const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx,
+                      const int32_t *seq_start = nullptr);
 // An int8 operand on the device: the [K, N] weight as an [N, K] int8 panel
 // (from row-major int8, or untiled from a container's block panel when tile_k
 // > 0), wscale [N] copied, ias = 1 / asmooth [K] computed once in fp32.
@@ -80,8 +81,10 @@ int layernorm_i8_checked(mx_stream *s, const float *x, const void *y, int y_dtyp
 // The RoPE / gated-FFN archs: host tables, and validated launches.
 void rope_tables_host(int64_t S, int64_t hd, double theta, const float *inv_freq, float *cos_t,
                       float *sin_t);
+// rows / row_pos: packed rows (rows < 0: the dense B*S).
 int rope_checked(mx_stream *s, uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S, int64_t H,
-                 int64_t hd, const float *cos_t, const float *sin_t);
+                 int64_t hd, const float *cos_t, const float *sin_t, int64_t rows = -1,
+                 const int32_t *row_pos = nullptr);
 int glu_checked(mx_stream *s, const void *up, int up_dtype, void *out, int out_dtype,
                 int64_t rows, int64_t f, int act);
 // Read and clear the stream's data-refusal flag (synchronises the stream).

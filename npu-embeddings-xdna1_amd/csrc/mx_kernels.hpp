@@ -23,8 +23,18 @@ hipError_t embed_sum(const int32_t *ids, int64_t B, int64_t S, int64_t d, const 
                      hipStream_t s);
 hipError_t mask_build(const float *attn_mask, int64_t B, int64_t S, float *add_mask,
                       int32_t *kv_len, hipStream_t s);
+// seq_start (nullable): the packed layout of the rows (pack_plan).
 hipError_t pool_rows(const float *h, const float *attn_mask, int64_t B, int64_t S, int64_t d,
-                     int cls, int l2, float *out, int *err, hipStream_t s);
+                     int cls, int l2, float *out, int *err, hipStream_t s,
+                     const int32_t *seq_start = nullptr);
+// Token packing: seq_start[0..B] = exclusive scan of kv_len (seq_start[B] =
+// packed rows); the embedding sum of the rows s < kv_len[b] into packed row
+// seq_start[b] + s, with row_pos[packed row] = s.
+hipError_t pack_plan(const int32_t *kv_len, int64_t B, int32_t *seq_start, hipStream_t s);
+hipError_t embed_sum_packed(const int32_t *ids, int64_t B, int64_t S, int64_t d,
+                            const float *word, int64_t vocab, const float *pos,
+                            const float *type0, const int32_t *kv_len, const int32_t *seq_start,
+                            float *emb, int32_t *row_pos, int *err, hipStream_t s);
 
 // Front ends (k_front.hip).
 hipError_t vit_patches(const float *px, int64_t B, int img, int p, uint16_t *rows, hipStream_t s);
@@ -91,8 +101,10 @@ int quant_groups(int64_t K);
 
 // The RoPE / gated-FFN archs (k_glu.hip): in-place RoPE of Q and K in bf16
 // fused rows (tables [S, hd]); lo | hi -> lo * act(hi) (act 1 SiLU, 2 GELU).
+// row_pos (nullable): each row's position (packed rows), else row % S.
 hipError_t rope_qkv(uint16_t *qkv, int64_t ld, int64_t rows, int S, int H, int hd,
-                    const float *cos_t, const float *sin_t, hipStream_t s);
+                    const float *cos_t, const float *sin_t, hipStream_t s,
+                    const int32_t *row_pos = nullptr);
 hipError_t glu(const void *in, int in_bf, void *out, int out_bf, int64_t rows, int64_t f, int act,
                hipStream_t s);
 
@@ -114,6 +126,10 @@ struct AttnArgs {
   const int32_t *kv_len;  // [B] or null
   uint16_t *ctx;
   int64_t ld_ctx;
+  // Packed rows (nullable): sequence b's rows start at seq_start[b] and only
+  // its kv_len[b] rows exist (queries and keys past it are neither read nor
+  // written).
+  const int32_t *seq_start = nullptr;
 };
 hipError_t attention(const AttnArgs &a, hipStream_t s);
 

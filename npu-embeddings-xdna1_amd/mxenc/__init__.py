@@ -111,6 +111,7 @@ SIGNATURES = {
     "mx_encoder_vit": (_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
     "mx_encoder_whisper": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "mx_encoder_set_timing": (_int, [_vp, _int]),
+    "mx_encoder_set_packing": (_int, [_vp, _int]),
     "mx_encoder_timings": (_int, [_vp, ctypes.POINTER(Timings)]),
     "mx_npue_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "mx_npue_close": (None, [_vp]),
@@ -532,6 +533,9 @@ class Encoder:
 
     def whisper(self, mel, B, hidden):
         check(lib().mx_encoder_whisper(self.handle, self.ctx.stream, _p(mel), B, _p(hidden)))
+
+    def set_packing(self, on):
+        check(lib().mx_encoder_set_packing(self.handle, int(on)))
 
     def set_timing(self, on):
         check(lib().mx_encoder_set_timing(self.handle, int(on)))

@@ -1,0 +1,94 @@
+"""Token packing in mx_encoder_embed: only the rows before each sequence's
+kv_len are computed (the padding past it is never attended as a key and never
+pooled), and the pooled output must be the padded computation's bit for bit
+-- on the bge-base benchmark workload itself, on mean pooling, on masks with
+holes, on fully masked and one-token sequences, under RoPE + gated FFN and on
+the int8 datapath."""
+import numpy as np
+import pytest
+
+import mxenc
+from mxenc import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = mxenc.Context(0)
+    yield c
+    c.close()
+
+
+def _embed(ctx, enc, ids, am, packing):
+    B, S = ids.shape
+    enc.set_packing(packing)
+    out = ctx.empty((B, enc.desc.hidden), np.float32)
+    enc.embed(ctx.put(ids), ctx.put(am), B, S, out)
+    return out.host()
+
+
+def _same(a, b):
+    return np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_bge_base_workload_packed_equals_padded(ctx):
+    """The benchmark's own batch (64 x 512, lengths U[64, 512], CLS pooling)."""
+    m = synth.make_model("bge_base")
+    ids, am, lens = synth.make_text_inputs(m)
+    enc = mxenc.Encoder(ctx, m)
+    packed = _embed(ctx, enc, ids, am, True)
+    padded = _embed(ctx, enc, ids, am, False)
+    enc.close()
+    assert _same(packed, padded)
+    assert lens.sum() < 0.7 * ids.size  # the padding that packing skips
+
+
+def test_mean_pooling_holes_and_edge_lengths(ctx):
+    m = synth.make_model("minilm", layers=3, ln_random=True)
+    ids, am, _ = synth.make_text_inputs(m, batch=9, seq=128)
+    am[1, 3] = 0.0          # a hole inside the sequence: masked key, not pooled
+    am[1, 10:12] = 0.0
+    am[2] = 0.0             # fully masked: kv_len = S, attends uniformly
+    am[3] = 0.0
+    am[3, 0] = 1.0          # a single token
+    am[4] = 1.0             # full length
+    enc = mxenc.Encoder(ctx, m)
+    packed = _embed(ctx, enc, ids, am, True)
+    padded = _embed(ctx, enc, ids, am, False)
+    enc.close()
+    assert _same(packed, padded)
+
+
+@pytest.mark.parametrize("name", ["nomic", "gte"])
+def test_rope_gated_packed_equals_padded(ctx, name):
+    """RoPE rotates a packed row by its own position (row_pos), not by its
+    packed index."""
+    m = synth.make_model(name, layers=2, ln_random=True)
+    ids, am, _ = synth.make_text_inputs(m, batch=7, seq=192)
+    enc = mxenc.Encoder(ctx, m)
+    packed = _embed(ctx, enc, ids, am, True)
+    padded = _embed(ctx, enc, ids, am, False)
+    enc.close()
+    assert _same(packed, padded)
+
+
+def test_int8_packed_equals_padded(ctx):
+    m = synth.make_model("bge_base", layers=3)
+    ids, am, _ = synth.make_text_inputs(m, batch=16, seq=512)
+    enc = mxenc.Encoder(ctx, m, int8=synth.quantise_model(m))
+    packed = _embed(ctx, enc, ids, am, True)
+    padded = _embed(ctx, enc, ids, am, False)
+    enc.close()
+    assert _same(packed, padded)
+
+
+def test_packing_then_a_longer_sequence(ctx):
+    """Workspaces regrow when the sequence grows at a fixed batch (mask,
+    positions and packed rows)."""
+    m = synth.make_model("minilm", layers=2)
+    enc = mxenc.Encoder(ctx, m)
+    for S in (64, 128, 256):
+        ids, am, _ = synth.make_text_inputs(m, batch=4, seq=S)
+        assert _same(_embed(ctx, enc, ids, am, True), _embed(ctx, enc, ids, am, False))
+    enc.close()
