@@ -10,7 +10,10 @@ bge-base geometry at batch 64 x seq 512 by default. The embed path packs each
 sequence's rows before its kv_len (the padding past it is never attended and
 never pooled; the pooled output is the padded computation's bit for bit);
 the same steps are also timed padded, as EmbedService::chunk computes them,
-and reported beside (--padded makes the padded run the headline). Weights are random-init
+and reported beside (--padded makes the padded run the headline). The
+steps are split over --lanes concurrent lanes (default 2: the reference's
+--pipeline lanes, EmbedService::embed's workers), each an encoder clone on its
+own stream; the one-lane rate is reported beside. Weights are random-init
 (N(0, 0.02), Q scale folded, bf16), inputs synthetic; see mxenc/synth.py.
 
 Prints one JSON line: sequences/s, the GEMM family's MFMA roofline (HIP event
@@ -115,6 +118,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="bge_base")
+    ap.add_argument("--lanes", type=int, default=2,
+                    help="BERT configs: concurrent lanes (the reference's --pipeline), each "
+                         "an encoder clone on its own stream and host thread with its own "
+                         "copy of the batch in HBM; the timed steps are split over them")
     ap.add_argument("--padded", action="store_true",
                     help="the headline computes every padded row (token packing off)")
     ap.add_argument("--int8", action="store_true",
@@ -159,13 +166,22 @@ def main():
     ctx = mxenc.Context(0)
     enc = mxenc.Encoder(ctx, m, int8=synth.quantise_model(m) if args.int8 else None)
     packing = kind == "bert" and not args.padded
+    lanes = max(1, args.lanes) if kind == "bert" else 1
+    lane_ctx, lane_enc, lane_step = [ctx], [enc], []
     if kind == "bert":
         ids, am, lens = synth.make_text_inputs(m)
         B, S = ids.shape
-        enc.set_packing(packing)
-        d_ids, d_am = ctx.put(ids), ctx.put(am)
-        out = ctx.empty((B, m["hidden"]), np.float32)
-        step = lambda: enc.embed(d_ids, d_am, B, S, out)  # noqa: E731
+        for _ in range(lanes - 1):
+            c = mxenc.Context(0)
+            lane_ctx.append(c)
+            lane_enc.append(enc.clone(c))
+        for c, e in zip(lane_ctx, lane_enc):
+            e.set_packing(packing)
+            d_ids, d_am = c.put(ids), c.put(am)
+            out = c.empty((B, m["hidden"]), np.float32)
+            lane_step.append(lambda e=e, d_ids=d_ids, d_am=d_am, out=out:
+                             e.embed(d_ids, d_am, B, S, out))
+        step = lane_step[0]
         unit = "sequences/s"
     elif kind == "vit":
         B, S = m["batch"], m["seq"]
@@ -182,35 +198,64 @@ def main():
     print(f"bench: {args.config} B={B} S={S} L={m['layers']} on {ctx.props.arch.decode()} "
           f"({ctx.props.compute_units} CUs)", file=sys.stderr, flush=True)
 
-    for _ in range(args.warmup):
-        step()
-    ctx.sync()
+    for st in lane_step or [step]:
+        for _ in range(args.warmup):
+            st()
+    for c in lane_ctx:
+        c.sync()
+
+    def timed(n_lanes):
+        """Wall time of args.steps steps split over the first n_lanes lanes, each
+        lane's steps issued by its own host thread (every embed call waits for
+        its stream at the end, as chunk() returns pooled rows)."""
+        import threading
+        per = [args.steps // n_lanes + (1 if i < args.steps % n_lanes else 0)
+               for i in range(n_lanes)]
+        sts = lane_step[:n_lanes] if lane_step else [step]
+
+        def work(i):
+            for _ in range(per[i]):
+                sts[i]()
+        for c in lane_ctx:
+            c.sync()
+        t0 = time.perf_counter()
+        if n_lanes == 1:
+            work(0)
+        else:
+            th = [threading.Thread(target=work, args=(i,)) for i in range(n_lanes)]
+            for t in th:
+                t.start()
+            for t in th:
+                t.join()
+        for c in lane_ctx:
+            c.sync()
+        return time.perf_counter() - t0
 
     # Timed region: throughput without per-launch events.
     enc.set_timing(False)
-    ctx.sync()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    ctx.sync()
-    dt = time.perf_counter() - t0
+    dt = timed(lanes)
     seq_s = args.steps * B / dt
     print(f"bench: {args.steps} steps in {dt*1e3:.1f} ms -> {seq_s:.1f} {unit}"
-          f"{' (token packing)' if packing else ''}", file=sys.stderr, flush=True)
+          f"{' (token packing)' if packing else ''}, {lanes} lane(s)", file=sys.stderr,
+          flush=True)
+    one_lane = None
+    if lanes > 1:
+        odt = timed(1)
+        one_lane = {"value": args.steps * B / odt, "ms_per_step": odt / args.steps * 1e3}
+        print(f"bench: one lane {one_lane['value']:.1f} {unit} "
+              f"({one_lane['ms_per_step']:.2f} ms/step)", file=sys.stderr, flush=True)
     padded = None
     if packing:
         # The same steps with every padded row computed (EmbedService::chunk).
-        enc.set_packing(False)
+        for e in lane_enc:
+            e.set_packing(False)
         step()
         ctx.sync()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        ctx.sync()
-        pdt = time.perf_counter() - t0
-        enc.set_packing(True)
+        pdt = timed(lanes)
+        for e in lane_enc:
+            e.set_packing(True)
         padded = {"value": args.steps * B / pdt, "ms_per_step": pdt / args.steps * 1e3,
-                  "rows_per_step": B * S}
+                  "rows_per_step": B * S, "lanes": lanes}
         print(f"bench: padded {padded['value']:.1f} {unit} ({padded['ms_per_step']:.2f} ms/step)",
               file=sys.stderr, flush=True)
 
@@ -318,12 +363,18 @@ def main():
         "attention": {"achieved_tflops": attn_tflops, "frac": attn_tflops / BF16_PEAK_TFLOPS,
                       "ms_per_step": tot["attn_ms"] / args.steps},
         "layernorm_ms_per_step": tot["ln_ms"] / args.steps,
+        "lanes": lanes,
+        "one_lane": one_lane,
         "token_packing": {"on": packing, "rows_per_step": M, "padded_rows_per_step": B * S,
                           "padded": padded} if kind == "bert" else None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+    for e in lane_enc[1:]:
+        e.close()
     enc.close()
+    for c in lane_ctx[1:]:
+        c.close()
     ctx.close()
 
 

@@ -514,6 +514,16 @@ class Encoder:
         self.handle = h.value
         return self
 
+    def clone(self, ctx):
+        """mx_encoder_clone: a lane on ctx's stream with this encoder's weights
+        (borrowed) and a workspace of its own; close it before the parent."""
+        c = Encoder.__new__(Encoder)
+        c.ctx, c.m, c.desc = ctx, self.m, self.desc
+        h = _vp()
+        check(lib().mx_encoder_clone(self.handle, ctypes.byref(h)))
+        c.handle = h.value
+        return c
+
     def set(self, name, arr):
         a = np.ascontiguousarray(arr)
         check(lib().mx_encoder_set(self.handle, name.encode(), a.ctypes.data,
