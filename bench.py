@@ -122,6 +122,8 @@ def main():
                     help="BERT configs: concurrent lanes (the reference's --pipeline), each "
                          "an encoder clone on its own stream and host thread with its own "
                          "copy of the batch in HBM; the timed steps are split over them")
+    ap.add_argument("--no-padded-rate", action="store_true",
+                    help="do not time the padded comparison (profiling runs)")
     ap.add_argument("--padded", action="store_true",
                     help="the headline computes every padded row (token packing off)")
     ap.add_argument("--int8", action="store_true",
@@ -245,7 +247,7 @@ def main():
         print(f"bench: one lane {one_lane['value']:.1f} {unit} "
               f"({one_lane['ms_per_step']:.2f} ms/step)", file=sys.stderr, flush=True)
     padded = None
-    if packing:
+    if packing and not args.no_padded_rate:
         # The same steps with every padded row computed (EmbedService::chunk).
         for e in lane_enc:
             e.set_packing(False)

@@ -64,6 +64,16 @@ hipError_t gemm(const GemmArgs &a, hipStream_t s);
 // 2: 128x256, 3: 128x128) and the resident blocks of a persistent launch.
 int gemm_lds_tile(int64_t M, int64_t N);
 int cu_count();
+// Blocks of a persistent launch over ntiles tiles with `grid` resident: at
+// most one per tile, rounded up to a whole number per XCD (a multiple of 8)
+// so the kernel's XCD-chunked tile order applies even when the tiles do not
+// fill the chip -- consecutive tiles share an A row-panel in one XCD's L2
+// instead of landing on eight different L2s. Surplus blocks exit at once.
+inline int persistent_grid(int ntiles, int grid) {
+  int g = ntiles < grid ? ntiles : grid;
+  if (g >= 16 && (g & 7)) g = (g + 7) & ~7;
+  return g;
+}
 
 // int8 W8A8 (k_gemm_i8.hip): C[M,N] = epi(fma(float(Aq @ Wq^T) * a_scale[m],
 // wscale[n], bias[n])) (+ residual), or the raw int32 product (c_dtype 2).
