@@ -66,10 +66,11 @@
 // runs of four consecutive columns.
 //
 // Epilogue. Per 32 x 32 accumulator block a wave adds the bias (dequantises),
-// applies the activation, writes the fp32 block to its private LDS staging
-// area (rows padded by 16 bytes) and reads it back row-major, so every global
-// store (and residual load) of a wave covers whole 128-byte (fp32) or 64-byte
-// (bf16) row segments instead of 16-byte pieces of 32 rows.
+// applies the activation, writes the block to its private LDS staging area
+// (packed bf16 in swizzled 64-byte rows for a bf16 C, else fp32 rows padded
+// by 16 bytes) and reads it back row-major, so every global store (and
+// residual load) of a wave covers whole 128-byte (fp32) or 64-byte (bf16) row
+// segments instead of 16-byte pieces of 32 rows.
 //
 // Requirements (the launchers check them; bf16 shapes outside them go to
 // k_gemm.hip's kernel): K a multiple of the slab depth and at least NS slabs,
@@ -155,6 +156,30 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
   return ((uint64_t)hi << 32) | lo;
+}
+
+// Wait until this wave's loads of the next slab have landed: at most the
+// loads of the `later` slabs issued after it (LOADS each) may stay in flight,
+// plus `extra` younger operations (the stores of an epilogue issued after that
+// slab's loads). vmcnt counts loads and stores in issue order.
+template <int LOADS, int NS, int EXTRA>
+__device__ __forceinline__ void wait_slab(int ahead, bool extra) {
+  if (ahead >= NS - 2) {
+    if (extra)
+      wait_vmcnt<LOADS *(NS - 2) + EXTRA>();
+    else
+      wait_vmcnt<LOADS *(NS - 2)>();
+  } else if (NS > 3 && ahead == NS - 3) {
+    if (extra)
+      wait_vmcnt<(NS > 3 ? LOADS * (NS - 3) : 0) + EXTRA>();
+    else
+      wait_vmcnt<(NS > 3 ? LOADS * (NS - 3) : 0)>();
+  } else {
+    if (extra)
+      wait_vmcnt<EXTRA>();
+    else
+      wait_vmcnt<0>();
+  }
 }
 
 // The datapath's MFMA, fragment and accumulator types.
@@ -366,7 +391,14 @@ __device__ __forceinline__ void gemm_lds_body(
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int cl = wn * Cfg::WN + j * 32;  // tile-local first column
-        // acc layout -> fp32 staging rows (lane li's row, columns 8q + 4g + e)
+        // acc layout -> staging rows (lane li's row, columns 8q + 4g + e).
+        // bf16 C without a residual stages packed bf16 (2 KB per block): lane
+        // (li, g) writes its four columns 8q + 4g .. +3 of row li as 8 bytes,
+        // 16-byte chunk q of the 64-byte row stored at q ^ ((li >> 2) & 3), so
+        // the writes of 16 rows and the reads of 4 rows x 4 chunks each cover
+        // all 64 banks once. Everything else stages fp32 rows (the residual is
+        // added before the one rounding).
+        constexpr bool STG_BF = CBF && !RES;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           float4 v;
@@ -394,10 +426,30 @@ __device__ __forceinline__ void gemm_lds_body(
             v.z = gemm_epilogue(acc[j][i][q * 4 + 2] + b.z, EPI);
             v.w = gemm_epilogue(acc[j][i][q * 4 + 3] + b.w, EPI);
           }
-          *(float4 *)(stg + li * STG_ROWB + (q * 8 + g * 4) * 4) = v;
+          if (STG_BF) {
+            const uint2 w = make_uint2(pack_bf2_hw(v.x, v.y), pack_bf2_hw(v.z, v.w));
+            *(uint2 *)(stg + li * 64 + ((q ^ ((li >> 2) & 3)) * 16 + g * 8)) = w;
+          } else {
+            *(float4 *)(stg + li * STG_ROWB + (q * 8 + g * 4) * 4) = v;
+          }
         }
         asm volatile("" ::: "memory");
-        if (CBF) {
+        if (STG_BF) {
+          // 8 bf16 per lane; 4 lanes per 32-column row.
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int row = r * 16 + (lane >> 2), c = lane & 3;
+            const uint4 w = *(const uint4 *)(stg + row * 64 + ((c ^ ((row >> 2) & 3)) * 16));
+            const int grow = rbase + row, gcol = n0 + cl + c * 8;
+            if (grow < M && gcol < N) {
+              const int64_t off = (int64_t)grow * ldc + gcol;
+              if (gcol + 8 <= N)
+                *(uint4 *)((uint16_t *)C + off) = w;
+              else  // N % 8 == 4: four columns left
+                *(uint2 *)((uint16_t *)C + off) = make_uint2(w.x, w.y);
+            }
+          }
+        } else if (CBF) {
           // 8 fp32 per lane -> 16 bytes of bf16; 4 lanes per 32-column row.
 #pragma unroll
           for (int r = 0; r < 2; ++r) {
@@ -468,6 +520,16 @@ __device__ __forceinline__ void gemm_lds_body(
   asm volatile("" ::: "memory");
   read_set(0, pos0, fa0, fb0);
 
+  // An epilogue issues EPI_STORES global stores per wave (one per staged row
+  // group of each 32 x 32 block) when its tile lies wholly inside C, where
+  // every store is taken. Those stores are younger than the loads of the next
+  // NS - 1 slabs, so the waits for those slabs leave them in flight instead of
+  // stalling the next tile on the previous one's write acknowledgements. An
+  // edge tile (or a residual epilogue, whose loads the compiler waits on)
+  // keeps the exact wait.
+  constexpr int EPI_STORES = RES ? 0 : (CBF ? 2 : 4) * TM * TN;
+  static_assert(Cfg::LOADS_HI * (NS - 2) + EPI_STORES < 64, "vmcnt holds at most 63");
+  int epi_left = 0;
   int ep_kt = 0, ep_ti = 0;  // tile and depth of slab s
   for (int s = 0; s < nslab; ++s) {
     // First half of slab s; its second half is read meanwhile.
@@ -478,20 +540,12 @@ __device__ __forceinline__ void gemm_lds_body(
     // loads of slab s + 1 (the slabs issued after it, at most NS - 2, may stay
     // in flight), then meet: slab s + 1 is in LDS and slot s % NS is free.
     const int ahead = nslab - 2 - s;
-    const bool hi = wave < Cfg::NHI;
-    if (ahead >= NS - 2) {
-      if (hi)
-        wait_vmcnt<Cfg::LOADS_HI *(NS - 2)>();
-      else
-        wait_vmcnt<Cfg::LOADS_LO *(NS - 2)>();
-    } else if (NS > 3 && ahead == NS - 3) {
-      if (hi)
-        wait_vmcnt<(NS > 3 ? Cfg::LOADS_HI * (NS - 3) : 0)>();
-      else
-        wait_vmcnt<(NS > 3 ? Cfg::LOADS_LO * (NS - 3) : 0)>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    const bool stores_young = EPI_STORES > 0 && epi_left > 0;
+    if (wave < Cfg::NHI)
+      wait_slab<Cfg::LOADS_HI, NS, EPI_STORES>(ahead, stores_young);
+    else
+      wait_slab<Cfg::LOADS_LO, NS, EPI_STORES>(ahead, stores_young);
+    if (epi_left > 0) --epi_left;
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -521,6 +575,11 @@ __device__ __forceinline__ void gemm_lds_body(
     }
     if (++ep_kt == nk) {
       ep_kt = 0;
+      {
+        int m0, n0;
+        tile_origin(ep_ti, m0, n0);
+        epi_left = (m0 + BM <= M && n0 + BN <= N) ? NS - 1 : 0;
+      }
       epilogue(ep_ti++);
 #pragma unroll
       for (int j = 0; j < TN; ++j)

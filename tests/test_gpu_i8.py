@@ -86,6 +86,22 @@ def test_gemm_i8_raw_is_the_exact_integer_product(ctx, M, K, N):
     mxenc.check(mxenc.lib().mx_release_weight(ctx.handle, slot))
 
 
+@pytest.mark.parametrize("M,K,N", [(32768, 768, 768), (20000, 768, 2304)])
+def test_gemm_i8_raw_multi_tile_per_block(ctx, M, K, N):
+    """More tiles than CUs: each persistent block runs several tiles, and the
+    slab waits after an epilogue leave its stores in flight -- any slab read
+    before its loads landed would show as a wrong integer."""
+    rng = np.random.default_rng(M + N)
+    A, W = _i8(rng, (M, K)), _i8(rng, (K, N))
+    slot = mxenc.stage_weight_i8(ctx, W, np.ones(N, np.float32), np.ones(K, np.float32))
+    C = ctx.empty((M, N), np.int32)
+    mxenc.gemm_i8(ctx, ctx.put(A), None, M, K, K, slot, None, mxenc.MX_EPI_NONE, None, C, N)
+    got = C.host()
+    want = A.astype(np.float64) @ W.astype(np.float64)  # exact: |sum| < 2^31
+    assert np.array_equal(got, want.astype(np.int32))
+    mxenc.check(mxenc.lib().mx_release_weight(ctx.handle, slot))
+
+
 @pytest.mark.parametrize("M,K,N,bias", [(1000, 768, 2304, True), (4096, 3072, 768, True),
                                         (257, 512, 68, False)])
 def test_gemm_i8_dequant_bit_exact(ctx, orc, M, K, N, bias):
