@@ -43,7 +43,8 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
                                                   const int32_t *__restrict__ kv_len,
                                                   uint16_t *__restrict__ ctx, int64_t ldo,
                                                   int n_qblk, int force_logits,
-                                                  const int32_t *__restrict__ seq_start) {
+                                                  const int32_t *__restrict__ seq_start,
+                                                  const int32_t *__restrict__ order) {
   constexpr int KS = HD + 8;   // K row stride in LDS (elements)
   constexpr int VS = BKV + 4;  // Vt row stride in LDS (elements)
   constexpr int KCH = BKV * HD / 8 / 256;  // 16-byte K chunks per thread (1 or 2)
@@ -56,10 +57,22 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
   __shared__ float sM[2][BKV];
   __shared__ int sF[2];  // 1 if the staged tile has a nonzero mask entry
 
+  // Block -> (sequence, query block, head). With an order (sequences by
+  // decreasing kv_len), the blocks of the longest sequences are dispatched
+  // first and the short ones fill in behind them; otherwise sequence-major.
   const int blk = blockIdx.x;
-  const int qb = blk % n_qblk;
-  const int bh = blk / n_qblk;
-  const int h = bh % H, b = bh / H;
+  int qb, h, b;
+  if (order) {
+    h = blk % H;
+    const int t = blk / H;
+    qb = t % n_qblk;
+    b = order[t / n_qblk];
+  } else {
+    qb = blk % n_qblk;
+    const int bh = blk / n_qblk;
+    h = bh % H;
+    b = bh / H;
+  }
   const int d = H * HD;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, li = lane & 31;
@@ -152,12 +165,21 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
   float m_run = -INFINITY, l_run = 0.0f;
 
   const int ntile = (kvl + BKV - 1) / BKV;
+  // A wave whose 32 queries all lie past the sequence's rows (the last query
+  // block of a packed sequence) only helps stage K/V and meets the barriers;
+  // its SIMD time goes to the other blocks on the CU.
+  const bool live = qb * BQ + wave * 32 < lim;
   gload(0);
   sstore(0);
   __syncthreads();
   for (int t = 0; t < ntile; ++t) {
     const int cur = t & 1;
     if (t + 1 < ntile) gload(t + 1);
+    if (!live) {
+      if (t + 1 < ntile) sstore(cur ^ 1);
+      __syncthreads();
+      continue;
+    }
 
     // S^T for the two 32-key halves of the tile.
     f32x16 sc[2];
@@ -269,11 +291,11 @@ hipError_t attention(const AttnArgs &a, hipStream_t s) {
   if (a.hd == 64)
     attn_fwd_k<64><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
                                                    a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
-                                                   force_logits, a.seq_start);
+                                                   force_logits, a.seq_start, a.order);
   else if (a.hd == 32)
     attn_fwd_k<32><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
                                                    a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
-                                                   force_logits, a.seq_start);
+                                                   force_logits, a.seq_start, a.order);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -409,15 +409,36 @@ __global__ __launch_bounds__(256) void mask_k(const float *__restrict__ am, int6
 // exclusive scan of kv_len, seq_start[B] the packed row count; packed row
 // seq_start[b] + s is dense row b*S + s, and row_pos records its position s.
 
-__global__ void pack_plan_k(const int32_t *__restrict__ kv_len, int64_t B,
-                            int32_t *__restrict__ seq_start) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int32_t acc = 0;
-  for (int64_t b = 0; b < B; ++b) {
-    seq_start[b] = acc;
-    acc += kv_len[b];
+// One block: seq_start (thread 0, an exclusive prefix sum of kv_len) and the
+// attention launch order -- the sequence indices by decreasing kv_len, ties by
+// index: order[rank(b)] = b with rank(b) = #{b' : kv_len[b'] > kv_len[b], or
+// equal and b' < b}, a permutation by construction. Past ORDER_MAX_B sequences
+// the quadratic ranking is skipped and the order is the identity.
+constexpr int64_t ORDER_MAX_B = 8192;
+__global__ __launch_bounds__(256) void pack_plan_k(const int32_t *__restrict__ kv_len, int64_t B,
+                                                   int32_t *__restrict__ seq_start,
+                                                   int32_t *__restrict__ order) {
+  if (threadIdx.x == 0) {
+    int32_t acc = 0;
+    for (int64_t b = 0; b < B; ++b) {
+      seq_start[b] = acc;
+      acc += kv_len[b];
+    }
+    seq_start[B] = acc;
   }
-  seq_start[B] = acc;
+  if (!order) return;
+  for (int64_t b = threadIdx.x; b < B; b += blockDim.x) {
+    int64_t rank = b;
+    if (B <= ORDER_MAX_B) {
+      const int32_t lb = kv_len[b];
+      rank = 0;
+      for (int64_t o = 0; o < B; ++o) {
+        const int32_t lo = kv_len[o];
+        rank += (lo > lb) || (lo == lb && o < b);
+      }
+    }
+    order[rank] = (int32_t)b;
+  }
 }
 
 __global__ __launch_bounds__(256) void embed_sum_packed_k(
@@ -645,8 +666,9 @@ hipError_t pool_rows(const float *h, const float *am, int64_t B, int64_t S, int6
   return hipGetLastError();
 }
 
-hipError_t pack_plan(const int32_t *kv_len, int64_t B, int32_t *seq_start, hipStream_t s) {
-  pack_plan_k<<<1, 64, 0, s>>>(kv_len, B, seq_start);
+hipError_t pack_plan(const int32_t *kv_len, int64_t B, int32_t *seq_start, int32_t *order,
+                     hipStream_t s) {
+  pack_plan_k<<<1, 256, 0, s>>>(kv_len, B, seq_start, order);
   return hipGetLastError();
 }
 

@@ -22,7 +22,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_i8_k(
 
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, int OUT>
 hipError_t launch_t(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, true>;
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, true, OUT == 1 && !RES>;
   auto kern = gemm_i8_k<BM, BN, WGM, WGN, NS, EPI, RES, OUT>;
   static bool attr_set = false;
   if (!attr_set) {

@@ -22,7 +22,7 @@ namespace mxk {
 
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF>
 hipError_t gemm_lds_launch_t(const GemmArgs &a, int grid, hipStream_t s) {
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, false>;
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, false, CBF && !RES>;
   auto kern = gemm_lds_k<BM, BN, WGM, WGN, NS, EPI, RES, CBF>;
   static bool attr_set = false;
   if (!attr_set) {

@@ -91,9 +91,10 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int ROWB = 64;       // bytes of K per LDS slab row
 constexpr int STG_ROWB = 144;  // staging row: 32 fp32 + 16 bytes of padding
-constexpr int STG_WAVE = 32 * STG_ROWB;
 
-template <int BM, int BN, int WGM, int WGN, int NS, bool I8>
+// SBF: the epilogue stages packed bf16 (a bf16 C without a residual), 2 KB per
+// wave; otherwise fp32 rows, 4.5 KB per wave.
+template <int BM, int BN, int WGM, int WGN, int NS, bool I8, bool SBF>
 struct LdsCfg {
   static constexpr int NW = WGM * WGN;                // waves
   static constexpr int NT = NW * 64;                  // threads
@@ -111,6 +112,7 @@ struct LdsCfg {
   static constexpr int NHI = PIECES % NW == 0 ? NW : PIECES % NW;
   static constexpr int BIAS_PER_WAVE = BN / NW;        // floats each wave's bias piece moves
   static constexpr int ROWS_PER_WAVE = BM / NW;        // a_scale rows each wave moves
+  static constexpr int STG_WAVE = SBF ? 32 * 64 : 32 * STG_ROWB;
   static constexpr int STG_OFF = NS * SLOT;
   static constexpr int BIAS_OFF = STG_OFF + NW * STG_WAVE;
   static constexpr int WS_OFF = BIAS_OFF + 2 * BN * 4;  // int8: wscale, two parities
@@ -212,7 +214,8 @@ __device__ __forceinline__ void gemm_lds_body(
     const float *__restrict__ bias, const float *residual, void *C, int64_t ldc, int tiles_m,
     int tiles_n, const float *__restrict__ a_scale, const float *__restrict__ wscale,
     uint8_t *smem) {
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, I8>;
+  constexpr bool STG_BF = CBF && !RES;
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, I8, STG_BF>;
   using PT = Path<I8>;
   typedef typename PT::frag frag_t;
   typedef typename PT::acc acc_t;
@@ -382,7 +385,7 @@ __device__ __forceinline__ void gemm_lds_body(
     const float *bl = (const float *)(smem + Cfg::BIAS_OFF + (ti & 1) * BN * 4);
     const float *wsl = (const float *)(smem + Cfg::WS_OFF + (ti & 1) * BN * 4);
     const float *sal = (const float *)(smem + Cfg::SA_OFF + (ti & 1) * BM * 4);
-    uint8_t *stg = smem + Cfg::STG_OFF + wave * STG_WAVE;
+    uint8_t *stg = smem + Cfg::STG_OFF + wave * Cfg::STG_WAVE;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int rbase = m0 + wm * Cfg::WM + i * 32;
@@ -398,7 +401,6 @@ __device__ __forceinline__ void gemm_lds_body(
         // the writes of 16 rows and the reads of 4 rows x 4 chunks each cover
         // all 64 banks once. Everything else stages fp32 rows (the residual is
         // added before the one rounding).
-        constexpr bool STG_BF = CBF && !RES;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           float4 v;

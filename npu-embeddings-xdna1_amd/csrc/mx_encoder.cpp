@@ -85,6 +85,10 @@ struct mx_encoder {
   int32_t *kv_len = nullptr;
   // Token packing (embed): seq_start [B + 1] and each packed row's position.
   bool packing = true;
+  // The last packed plan read back (seq_start[0..B]) and its sum of squared
+  // lengths: the attention work of a packed pass.
+  std::vector<int32_t> plan_host;
+  double packed_sq = 0.0;
   int32_t *seq_start = nullptr, *row_pos = nullptr;
   // timing
   bool timing = false;
@@ -172,7 +176,8 @@ int ensure_mask_ws(mx_encoder *enc, int64_t B, int64_t rows) {
     enc->ws_batch = enc->ws_mask_rows = 0;
     int rc = dev_alloc((void **)&enc->add_mask, nr * 4, "workspace mask");
     if (!rc) rc = dev_alloc((void **)&enc->kv_len, nb * 4, "workspace kv_len");
-    if (!rc) rc = dev_alloc((void **)&enc->seq_start, (nb + 1) * 4, "workspace seq_start");
+    // seq_start [B + 1], then attention's launch order [B].
+    if (!rc) rc = dev_alloc((void **)&enc->seq_start, (2 * nb + 1) * 4, "workspace seq_start");
     if (!rc) rc = dev_alloc((void **)&enc->row_pos, nr * 4, "workspace row_pos");
     if (rc) return rc;
     enc->ws_batch = nb;
@@ -299,21 +304,25 @@ int glu_l(mx_encoder *enc, mx_stream *s, int64_t M) {
                      enc->desc.gated_ffn);
 }
 
-int attn_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, const float *mask,
-           const int32_t *kv_len, const int32_t *seq_start = nullptr) {
-  Bracket br(enc, s->stream, CAT_ATTN);
-  const int64_t d = enc->desc.hidden;
-  enc->attn_flop += 4.0 * B * enc->desc.heads * (double)S * S * enc->desc.head_dim;
-  return attention_checked(s, enc->qkv, 3 * d, B, S, enc->desc.heads, enc->desc.head_dim,
-                           enc->desc.attn_scale, mask, kv_len, enc->ctxb, d, seq_start);
-}
-
 // The rows one pass runs over: M = B*S dense rows, or the packed rows of
-// token packing (seq_start / row_pos non-null, M = seq_start[B]).
+// token packing (seq_start / row_pos non-null, M = seq_start[B]); order
+// (nullable) is attention's launch order, longest sequence first.
 struct Rows {
   int64_t M;
-  const int32_t *seq_start = nullptr, *row_pos = nullptr;
+  const int32_t *seq_start = nullptr, *row_pos = nullptr, *order = nullptr;
 };
+
+int attn_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, const float *mask,
+           const int32_t *kv_len, const Rows *rows = nullptr) {
+  Bracket br(enc, s->stream, CAT_ATTN);
+  const int64_t d = enc->desc.hidden;
+  // Packed rows: each sequence attends over its own kv_len rows only.
+  const double sq = rows && rows->seq_start ? enc->packed_sq : (double)B * S * S;
+  enc->attn_flop += 4.0 * enc->desc.heads * sq * enc->desc.head_dim;
+  return attention_checked(s, enc->qkv, 3 * d, B, S, enc->desc.heads, enc->desc.head_dim,
+                           enc->desc.attn_scale, mask, kv_len, enc->ctxb, d,
+                           rows ? rows->seq_start : nullptr, rows ? rows->order : nullptr);
+}
 
 // One GEMM site of a layer on the encoder's datapath: bf16 A (A_bf) times
 // the bf16 panel, or the quantised A in xq/sa times the int8 operand.
@@ -352,7 +361,7 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
     rc = site_gemm(enc, s, w, SITE_QKV, enc->xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->qkv,
                    MX_BF16);
     if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S, M, rows.row_pos);
-    if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, rows.seq_start);
+    if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, &rows);
     if (!rc && enc->i8) rc = quant_l(enc, s, enc->ctxb, M, d, w.ias[SITE_AO]);
     if (!rc)
       rc = site_gemm(enc, s, w, SITE_AO, enc->ctxb, M, d, d, MX_EPI_NONE, nullptr, enc->proj,
@@ -914,23 +923,36 @@ int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids, const fl
   {
     Bracket br(enc, s->stream, CAT_OTHER);
     hipError_t e = mxk::mask_build(attn_mask, B, S, enc->add_mask, enc->kv_len, s->stream);
+    // The plan: seq_start and attention's launch order (both layouts use the
+    // order; kv_len differs per sequence either way).
+    int32_t *order = enc->seq_start + B + 1;
+    if (e == hipSuccess) e = mxk::pack_plan(enc->kv_len, B, enc->seq_start, order, s->stream);
     if (e == hipSuccess && enc->packing) {
       // Token packing: the packed row count is needed on the host for the
       // launches, so the plan is read back (one small copy per batch).
       int32_t total = 0;
-      e = mxk::pack_plan(enc->kv_len, B, enc->seq_start, s->stream);
+      enc->plan_host.resize(static_cast<size_t>(B + 1));
       if (e == hipSuccess)
-        e = hipMemcpyAsync(&total, enc->seq_start + B, sizeof total, hipMemcpyDeviceToHost,
-                           s->stream);
+        e = hipMemcpyAsync(enc->plan_host.data(), enc->seq_start, (B + 1) * sizeof(int32_t),
+                           hipMemcpyDeviceToHost, s->stream);
       if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+      if (e == hipSuccess) {
+        total = enc->plan_host[B];
+        enc->packed_sq = 0.0;
+        for (int64_t b = 0; b < B; ++b) {
+          const double L = enc->plan_host[b + 1] - enc->plan_host[b];
+          enc->packed_sq += L * L;
+        }
+      }
       if (e == hipSuccess)
         e = mxk::embed_sum_packed(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab,
                                   enc->pos, enc->type, enc->kv_len, enc->seq_start, enc->emb,
                                   enc->row_pos, s->err_dev, s->stream);
-      rows = Rows{total, enc->seq_start, enc->row_pos};
+      rows = Rows{total, enc->seq_start, enc->row_pos, order};
     } else if (e == hipSuccess) {
       e = mxk::embed_sum(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab, enc->pos,
                          enc->type, enc->emb, s->err_dev, s->stream);
+      rows.order = order;
     }
     if (e != hipSuccess) return hip_fail(e, "embed launch");
   }

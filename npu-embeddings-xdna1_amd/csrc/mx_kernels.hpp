@@ -28,9 +28,12 @@ hipError_t pool_rows(const float *h, const float *attn_mask, int64_t B, int64_t 
                      int cls, int l2, float *out, int *err, hipStream_t s,
                      const int32_t *seq_start = nullptr);
 // Token packing: seq_start[0..B] = exclusive scan of kv_len (seq_start[B] =
-// packed rows); the embedding sum of the rows s < kv_len[b] into packed row
-// seq_start[b] + s, with row_pos[packed row] = s.
-hipError_t pack_plan(const int32_t *kv_len, int64_t B, int32_t *seq_start, hipStream_t s);
+// packed rows) and, when order is non-null, order[0..B) = the sequence
+// indices by decreasing kv_len (attention's launch order); the embedding sum
+// of the rows s < kv_len[b] into packed row seq_start[b] + s, with
+// row_pos[packed row] = s.
+hipError_t pack_plan(const int32_t *kv_len, int64_t B, int32_t *seq_start, int32_t *order,
+                     hipStream_t s);
 hipError_t embed_sum_packed(const int32_t *ids, int64_t B, int64_t S, int64_t d,
                             const float *word, int64_t vocab, const float *pos,
                             const float *type0, const int32_t *kv_len, const int32_t *seq_start,
@@ -140,6 +143,9 @@ struct AttnArgs {
   // its kv_len[b] rows exist (queries and keys past it are neither read nor
   // written).
   const int32_t *seq_start = nullptr;
+  // Launch order (nullable): the B sequence indices, longest kv_len first;
+  // the blocks of order[0] are dispatched first.
+  const int32_t *order = nullptr;
 };
 hipError_t attention(const AttnArgs &a, hipStream_t s);
 
