@@ -38,20 +38,23 @@ HBM_PEAK_GBS = 8000.0
 
 
 def kernel_name(plan, epi, res, cbf, i8=False):
-    """The rocprof name of the GEMM instantiation a plan from mx_gemm_plan runs,
-    e.g. lds_128x256x32_w64x64_ns4_persistent -> gemm_lds_k<128, 256, 2, 4, 4, ...>
-    (gemm_i8_k<...> on the int8 datapath, whose tiles are the same)."""
+    """The rocprof name of the GEMM instantiation a plan from mx_gemm_plan_for
+    runs, e.g. lds_256x256x64_w64x128_ns2_persistent (bf16) ->
+    gemm_lds_k<256, 256, 4, 2, 2, epi, res, cbf, 128>; the last argument is the
+    slab row in bytes (slab K times the element size). gemm_i8_k<...> on the
+    int8 datapath."""
     if not plan.startswith("lds_"):
         return "gemm_bf16_k<128, 128, 64, 64, 64>"
     tile, wave, ns = plan.split("_")[1:4]
-    bm, bn, _ = (int(x) for x in tile.split("x"))
+    bm, bn, bk = (int(x) for x in tile.split("x"))
     wm, wn = (int(x) for x in wave[1:].split("x"))
+    rb = bk * (1 if i8 else 2)
     b = lambda v: "true" if v else "false"  # noqa: E731
     if i8:
         return (f"gemm_i8_k<{bm}, {bn}, {bm // wm}, {bn // wn}, {int(ns[2:])}, {epi}, {b(res)}, "
-                f"{1 if cbf else 0}>")
+                f"{1 if cbf else 0}, {rb}>")
     return (f"gemm_lds_k<{bm}, {bn}, {bm // wm}, {bn // wn}, {int(ns[2:])}, {epi}, {b(res)}, "
-            f"{b(cbf)}>")
+            f"{b(cbf)}, {rb}>")
 
 
 def workload_name(config, m):
@@ -306,7 +309,8 @@ def main():
                  ("ffn_up", (M, f, d, 2, False, True)), ("ffn_down", (M, d, f, 0, True, False))]
     groups = {}
     for i, (sname, (mm, nn, kk, epi, res, cbf)) in enumerate(sites):
-        plan = mxenc.lib().mx_gemm_plan(mm, nn, kk).decode()
+        plan = mxenc.lib().mx_gemm_plan_for(mm, nn, kk, mxenc.MX_BF16 if cbf else mxenc.MX_F32,
+                                            int(res), int(args.int8)).decode()
         kname = kernel_name(plan, epi, res, cbf, args.int8)
         g = groups.setdefault(kname, {"ms": 0.0, "flop": 0.0, "n": 0, "sites": []})
         g["ms"] += site_ms[i]

@@ -143,6 +143,13 @@ int mx_gemm_wt(mx_stream *s, const uint16_t *A, int64_t M, int64_t K,
  * vector-aligned. */
 const char *mx_gemm_plan(int64_t M, int64_t N, int64_t K);
 
+/* The plan for a C of c_dtype (MX_F32 / MX_BF16), with (residual != 0) or
+ * without a residual, on the bf16 (int8 = 0, mx_gemm) or int8 (int8 = 1,
+ * mx_gemm_i8) datapath: "lds_<BM>x<BN>x<slab K>_w<wave tile>_ns<slots>_..."
+ * (no counterpart in the reference). */
+const char *mx_gemm_plan_for(int64_t M, int64_t N, int64_t K, int c_dtype, int residual,
+                             int int8);
+
 /* attn (+softm fused): replaces the host qk/softmax_cpu/av triple
  * (bert_encoder.cpp:995-1135, :481-530), BertEncoder::attention_npu /
  * NpuAttention::run (runtime/src/whisper/attention_npu.cpp:177) and

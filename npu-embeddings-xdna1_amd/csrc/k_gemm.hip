@@ -171,6 +171,7 @@ namespace mxk {
 // access; the register-staged kernel above serves the rest.
 template <int BM, int BN, int WGM, int WGN, int NS>
 hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s);
+hipError_t gemm_lds_deep_launch(const GemmArgs &a, int grid, hipStream_t s);
 
 namespace {
 
@@ -179,8 +180,13 @@ enum GemmPath {
   PATH_LDS_256x256,
   PATH_LDS_256x192,
   PATH_LDS_128x256,
-  PATH_LDS_128x128
+  PATH_LDS_128x128,
+  PATH_LDS_256x256_DEEP
 };
+
+// The 256 x 256 tile on 128-byte slabs: a bf16 C without a residual, K a
+// multiple of 64.
+bool deep_ok(const GemmArgs &a) { return a.c_bf16 && !a.residual && a.K % 64 == 0; }
 
 bool lds_path_ok(const GemmArgs &a) {
   const uintptr_t c = (uintptr_t)a.C;
@@ -193,7 +199,9 @@ GemmPath pick(const GemmArgs &a) {
   if (!lds_path_ok(a)) return PATH_STAGED;
   static const GemmPath paths[] = {PATH_LDS_256x256, PATH_LDS_256x192, PATH_LDS_128x256,
                                    PATH_LDS_128x128};
-  return paths[gemm_lds_tile(a.M, a.N)];
+  const bool deep = deep_ok(a);
+  const int t = gemm_lds_tile(a.M, a.N, deep);
+  return t == 0 && deep ? PATH_LDS_256x256_DEEP : paths[t];
 }
 
 }  // namespace
@@ -202,16 +210,17 @@ GemmPath pick(const GemmArgs &a) {
 // last round costs a whole one) times the tile's area over its relative
 // throughput per unit area, measured on MI355X on the encoder's GEMM shapes
 // when every tile count is a whole number of rounds (256 x 256: 1.0, 256 x
-// 192: 0.88, 128 x 256: 0.86, 128 x 128: 0.65). The 256 x 192 tile wins
-// where N = 768 leaves 256 x 256 tiles at 1.5 rounds; small problems take
-// the small tiles that spread over the most CUs.
-int gemm_lds_tile(int64_t M, int64_t N) {
+// 192: 0.88, 128 x 256: 0.86, 128 x 128: 0.65; the 256 x 256 tile on
+// 128-byte slabs: 1.1). The 256 x 192 tile wins where N = 768 leaves 256 x
+// 256 tiles at 1.5 rounds; small problems take the small tiles that spread
+// over the most CUs.
+int gemm_lds_tile(int64_t M, int64_t N, bool deep) {
   struct Cand {
     int bm, bn;
     double eff;
   };
-  static const Cand cands[] = {{256, 256, 1.0}, {256, 192, 0.88}, {128, 256, 0.86},
-                               {128, 128, 0.65}};
+  const Cand cands[] = {{256, 256, deep ? 1.1 : 1.0}, {256, 192, 0.88}, {128, 256, 0.86},
+                        {128, 128, 0.65}};
   const int64_t G = cu_count();
   int best = 3;
   double best_t = 0.0;
@@ -243,8 +252,27 @@ int cu_count() {
 }
 
 
-const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
+const char *gemm_plan_name(int64_t M, int64_t N, int64_t K, bool c_bf16, bool residual,
+                           bool i8) {
   static const float aligned_probe[4] __attribute__((aligned(16))) = {0, 0, 0, 0};
+  if (i8) {
+    // The int8 kernels are the same tiles with slabs of 64 (or, deep, 128) int8.
+    GemmI8Args a{};
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.c_dtype = c_bf16 ? 1 : 0;
+    a.residual = residual ? aligned_probe : nullptr;
+    const bool deep = gemm_i8_deep(a);
+    switch (gemm_lds_tile(M, N, deep)) {
+      case 0:
+        return deep ? "lds_256x256x128_w64x128_ns2_persistent"
+                    : "lds_256x256x64_w128x64_ns3_persistent";
+      case 1: return "lds_256x192x64_w64x96_ns4_persistent";
+      case 2: return "lds_128x256x64_w64x64_ns4_persistent";
+      default: return "lds_128x128x64_w64x64_ns4_persistent";
+    }
+  }
   GemmArgs a{};
   a.M = M;
   a.N = N;
@@ -252,8 +280,11 @@ const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
   a.lda = K;
   a.ldc = N;
   a.bias = aligned_probe;
+  a.residual = residual ? aligned_probe : nullptr;
   a.C = (void *)aligned_probe;
+  a.c_bf16 = c_bf16 ? 1 : 0;
   switch (pick(a)) {
+    case PATH_LDS_256x256_DEEP: return "lds_256x256x64_w64x128_ns2_persistent";
     case PATH_LDS_256x256: return "lds_256x256x32_w128x64_ns3_persistent";
     case PATH_LDS_256x192: return "lds_256x192x32_w64x96_ns4_persistent";
     case PATH_LDS_128x256: return "lds_128x256x32_w64x64_ns4_persistent";
@@ -262,8 +293,13 @@ const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
   }
 }
 
+const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
+  return gemm_plan_name(M, N, K, false, false, false);
+}
+
 hipError_t gemm(const GemmArgs &a, hipStream_t s) {
   switch (pick(a)) {
+    case PATH_LDS_256x256_DEEP: return gemm_lds_deep_launch(a, cu_count(), s);
     case PATH_LDS_256x256: return gemm_lds_launch<256, 256, 2, 4, 3>(a, cu_count(), s);
     case PATH_LDS_256x192: return gemm_lds_launch<256, 192, 4, 2, 4>(a, cu_count(), s);
     case PATH_LDS_128x256: return gemm_lds_launch<128, 256, 2, 4, 4>(a, cu_count(), s);

@@ -8,22 +8,22 @@ using namespace mxlds;
 
 namespace {
 
-// OUT: 0 fp32 C, 1 bf16 C, 2 raw int32 C.
-template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, int OUT>
+// OUT: 0 fp32 C, 1 bf16 C, 2 raw int32 C. RB: bytes (= int8 K) per slab row.
+template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, int OUT, int RB>
 __global__ __launch_bounds__(WGM *WGN * 64) void gemm_i8_k(
     const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wt, int M, int N,
     int K, const float *__restrict__ a_scale, const float *__restrict__ wscale,
     const float *__restrict__ bias, const float *residual, void *C, int64_t ldc, int tiles_m,
     int tiles_n) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  gemm_lds_body<BM, BN, WGM, WGN, NS, EPI, RES, OUT == 1, true, OUT == 2>(
+  gemm_lds_body<BM, BN, WGM, WGN, NS, EPI, RES, OUT == 1, true, OUT == 2, RB>(
       A, lda, Wt, M, N, K, bias, residual, C, ldc, tiles_m, tiles_n, a_scale, wscale, smem);
 }
 
-template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, int OUT>
+template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, int OUT, int RB = 64>
 hipError_t launch_t(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, true, OUT == 1 && !RES>;
-  auto kern = gemm_i8_k<BM, BN, WGM, WGN, NS, EPI, RES, OUT>;
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, true, OUT == 1 && !RES, RB>;
+  auto kern = gemm_i8_k<BM, BN, WGM, WGN, NS, EPI, RES, OUT, RB>;
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(
@@ -57,14 +57,30 @@ hipError_t launch(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
+// The 256 x 256 tile on 128-byte slabs (128 int8 of K, two slots): a bf16 C
+// without a residual only.
+hipError_t launch_deep(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
+  switch (a.epilogue) {
+    case 0: return launch_t<256, 256, 4, 2, 2, 0, false, 1, 128>(a, grid, s);
+    case 1: return launch_t<256, 256, 4, 2, 2, 1, false, 1, 128>(a, grid, s);
+    case 2: return launch_t<256, 256, 4, 2, 2, 2, false, 1, 128>(a, grid, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
 
 namespace mxk {
 
+bool gemm_i8_deep(const GemmI8Args &a) {
+  return a.c_dtype == 1 && !a.residual && a.K % 128 == 0 && a.K >= 256;
+}
+
 hipError_t gemm_i8(const GemmI8Args &a, hipStream_t s) {
   const int grid = cu_count();
-  switch (gemm_lds_tile(a.M, a.N)) {
-    case 0: return launch<256, 256, 2, 4, 3>(a, grid, s);
+  const bool deep = gemm_i8_deep(a);
+  switch (gemm_lds_tile(a.M, a.N, deep)) {
+    case 0: return deep ? launch_deep(a, grid, s) : launch<256, 256, 2, 4, 3>(a, grid, s);
     case 1: return launch<256, 192, 4, 2, 4>(a, grid, s);
     case 2: return launch<128, 256, 2, 4, 4>(a, grid, s);
     default: return launch<128, 128, 2, 2, 4>(a, grid, s);

@@ -1,18 +1,20 @@
 // k_gemm_lds.hip -- the bf16 instantiations of the persistent LDS-pipelined
-// GEMM (the kernel body and its design are in k_gemm_lds.hpp).
+// GEMM (the kernel body and its design are in k_gemm_lds.hpp): 64-byte slabs
+// (32 K) for every tile and epilogue, and the 256 x 256 tile with 128-byte
+// slabs (64 K, two slots) for a bf16 C without a residual.
 #include "k_gemm_lds.hpp"
 
 using namespace mxlds;
 
 namespace {
 
-template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF>
+template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF, int RB>
 __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
     const uint16_t *__restrict__ A, int64_t lda, const uint16_t *__restrict__ Wt, int M, int N,
     int K, const float *__restrict__ bias, const float *residual, void *C, int64_t ldc,
     int tiles_m, int tiles_n) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  gemm_lds_body<BM, BN, WGM, WGN, NS, EPI, RES, CBF, false, false>(
+  gemm_lds_body<BM, BN, WGM, WGN, NS, EPI, RES, CBF, false, false, RB>(
       A, lda, Wt, M, N, K, bias, residual, C, ldc, tiles_m, tiles_n, nullptr, nullptr, smem);
 }
 
@@ -20,10 +22,10 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
 
 namespace mxk {
 
-template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF>
+template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF, int RB = 64>
 hipError_t gemm_lds_launch_t(const GemmArgs &a, int grid, hipStream_t s) {
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, false, CBF && !RES>;
-  auto kern = gemm_lds_k<BM, BN, WGM, WGN, NS, EPI, RES, CBF>;
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, false, CBF && !RES, RB>;
+  auto kern = gemm_lds_k<BM, BN, WGM, WGN, NS, EPI, RES, CBF, RB>;
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(
@@ -57,6 +59,18 @@ hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s) {
   MX_LDS_EPI(2)
 #undef MX_LDS_EPI
   return hipErrorInvalidValue;
+}
+
+// The 256 x 256 tile on 128-byte slabs: a bf16 C without a residual only
+// (the packed-bf16 staging is what leaves LDS room for two 64 KB slots).
+hipError_t gemm_lds_deep_launch(const GemmArgs &a, int grid, hipStream_t s) {
+  if (!a.c_bf16 || a.residual) return hipErrorInvalidValue;
+  switch (a.epilogue) {
+    case 0: return gemm_lds_launch_t<256, 256, 4, 2, 2, 0, false, true, 128>(a, grid, s);
+    case 1: return gemm_lds_launch_t<256, 256, 4, 2, 2, 1, false, true, 128>(a, grid, s);
+    case 2: return gemm_lds_launch_t<256, 256, 4, 2, 2, 2, false, true, 128>(a, grid, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template hipError_t gemm_lds_launch<256, 256, 2, 4, 3>(const GemmArgs &, int, hipStream_t);

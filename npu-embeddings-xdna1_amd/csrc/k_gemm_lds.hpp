@@ -89,22 +89,25 @@ using namespace mxd;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int ROWB = 64;       // bytes of K per LDS slab row
 constexpr int STG_ROWB = 144;  // staging row: 32 fp32 + 16 bytes of padding
 
 // SBF: the epilogue stages packed bf16 (a bf16 C without a residual), 2 KB per
-// wave; otherwise fp32 rows, 4.5 KB per wave.
-template <int BM, int BN, int WGM, int WGN, int NS, bool I8, bool SBF>
+// wave; otherwise fp32 rows, 4.5 KB per wave. RB: bytes of K per slab row, 64
+// or 128.
+template <int BM, int BN, int WGM, int WGN, int NS, bool I8, bool SBF, int RB = 64>
 struct LdsCfg {
   static constexpr int NW = WGM * WGN;                // waves
   static constexpr int NT = NW * 64;                  // threads
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
   static constexpr int TM = WM / 32, TN = WN / 32;    // 32x32 MFMA tiles per wave
   static constexpr int ESZ = I8 ? 1 : 2;              // operand element bytes
-  static constexpr int BKE = ROWB / ESZ;              // K elements per slab
-  static constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB;
+  static constexpr int BKE = RB / ESZ;                // K elements per slab
+  static constexpr int KSTEPS = RB / 32;              // MFMA k-steps (32 bytes of K) per slab
+  static constexpr int PR = 1024 / RB;                // slab rows per 1 KB piece
+  static constexpr int CPR = RB / 16;                 // 16-byte chunks per slab row
+  static constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB;
   static constexpr int SLOT = A_BYTES + B_BYTES;
-  // A slab is PIECES 1 KB wave loads of 16 rows each, A's first; wave w
+  // A slab is PIECES 1 KB wave loads of PR rows each, A's first; wave w
   // issues pieces w, w + NW, ...: LOADS_HI of them if w < NHI, else LOADS_LO
   // (a 256 x 192 slab is 28 pieces: four waves issue 4, four issue 3).
   static constexpr int A_PIECES = A_BYTES / 1024, PIECES = (A_BYTES + B_BYTES) / 1024;
@@ -123,8 +126,19 @@ struct LdsCfg {
   static_assert(BIAS_PER_WAVE % 4 == 0 && BIAS_PER_WAVE <= 256, "bias piece: 16-byte lanes");
   static_assert(ROWS_PER_WAVE <= 64, "a_scale piece: one row per lane");
   static_assert(LDS <= 160 * 1024, "gfx950 LDS is 160 KB");
-  static_assert(NS >= 3 && LOADS_HI * (NS - 2) < 64, "vmcnt holds at most 63");
+  static_assert(RB == 64 || RB == 128, "slab rows of 64 or 128 bytes");
+  static_assert(NS >= 2 && LOADS_HI * (NS - 2) < 64, "vmcnt holds at most 63");
 };
+
+// Position of logical 16-byte chunk c in slab row r (an involution in c).
+// Sixteen lanes of a ds_read_b128 phase read rows r..r+15 at one logical
+// chunk; a row of RB bytes spans RB/4 banks, so row r starts at bank
+// 16 * (r % 4) (RB = 64) or 32 * (r % 2) (RB = 128), and the XOR spreads the
+// sixteen reads over all 64 banks.
+template <int RB>
+__device__ __forceinline__ int chunk_pos(int c, int r) {
+  return RB == 64 ? c ^ ((r >> 2) & 3) : c ^ ((r >> 1) & 7);
+}
 
 // s_waitcnt vmcnt(N), other counters untouched.
 template <int N>
@@ -208,14 +222,14 @@ struct Path<true> {
 // (else fp32); I8: the int8 datapath; RAW (int8 only): store the int32
 // accumulators, no bias, scales or activation.
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF, bool I8,
-          bool RAW>
+          bool RAW, int RB = 64>
 __device__ __forceinline__ void gemm_lds_body(
     const void *__restrict__ A, int64_t lda, const void *__restrict__ Wt, int M, int N, int K,
     const float *__restrict__ bias, const float *residual, void *C, int64_t ldc, int tiles_m,
     int tiles_n, const float *__restrict__ a_scale, const float *__restrict__ wscale,
     uint8_t *smem) {
   constexpr bool STG_BF = CBF && !RES;
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, I8, STG_BF>;
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, I8, STG_BF, RB>;
   using PT = Path<I8>;
   typedef typename PT::frag frag_t;
   typedef typename PT::acc acc_t;
@@ -248,10 +262,10 @@ __device__ __forceinline__ void gemm_lds_body(
   const int wm = wave / WGN, wn = wave - wm * WGN;
   const int li = lane & 31, g = lane >> 5;
 
-  // Load addressing: lane fills row lrow of a 16-row window, logical chunk
-  // lchunk (swizzled); rows are clamped in bounds.
-  const int lrow = lane >> 2;
-  const int lchunk = (lane & 3) ^ ((lrow >> 2) & 3);
+  // Load addressing: lane fills position lpos of row lrow of a PR-row piece,
+  // i.e. it fetches the logical chunk stored there; rows are clamped in
+  // bounds.
+  const int lrow = lane / Cfg::CPR, lpos = lane % Cfg::CPR;
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
   const uint8_t *Ab = (const uint8_t *)A;
   const uint8_t *Wb = (const uint8_t *)Wt;
@@ -266,28 +280,39 @@ __device__ __forceinline__ void gemm_lds_body(
   };
   tile_origin(0, is_m0, is_n0);
   // Per issue tile: each piece's per-lane byte offset from its operand's tile
-  // origin (rows clamped in bounds), and the two origins as scalars.
+  // origin (rows clamped in bounds), and the two origins as scalars. When the
+  // waves split A's pieces evenly (SPLIT), load k of every wave is an A piece
+  // iff k < A_PIECES / NW, known at compile time, and only the two origins
+  // are kept; otherwise each load keeps its own.
+  constexpr bool SPLIT = Cfg::A_PIECES % Cfg::NW == 0;
   uint32_t poff[Cfg::LOADS_HI];
   uint64_t pbase[Cfg::LOADS_HI];
+  uint64_t abase = 0, bbase = 0;
+  auto is_a = [&](int k) {
+    return SPLIT ? k < Cfg::A_PIECES / Cfg::NW : wave + Cfg::NW * k < Cfg::A_PIECES;
+  };
   auto set_tile = [&](int m0, int n0) {
 #pragma unroll
     for (int k = 0; k < Cfg::LOADS_HI; ++k) {
       const int p = wave + Cfg::NW * k;
-      if (p < Cfg::A_PIECES) {
-        int r = m0 + p * 16 + lrow;
+      if (is_a(k)) {
+        const int tr = p * Cfg::PR + lrow;  // slab row within A's part
+        int r = m0 + tr;
         r = (r < M ? r : M - 1) - m0;
-        poff[k] = (uint32_t)(r * lda * ESZ + lchunk * 16);
+        poff[k] = (uint32_t)(r * lda * ESZ + chunk_pos<RB>(lpos, tr) * 16);
       } else {
-        int r = n0 + (p - Cfg::A_PIECES) * 16 + lrow;
+        const int tr = (p - Cfg::A_PIECES) * Cfg::PR + lrow;  // within W's part
+        int r = n0 + tr;
         r = (r < N ? r : N - 1) - n0;
-        poff[k] = (uint32_t)((int64_t)r * K * ESZ + lchunk * 16);
+        poff[k] = (uint32_t)((int64_t)r * K * ESZ + chunk_pos<RB>(lpos, tr) * 16);
       }
     }
-    const uint64_t abase = uniform64((uint64_t)(uintptr_t)(Ab + (int64_t)m0 * lda * ESZ));
-    const uint64_t bbase = uniform64((uint64_t)(uintptr_t)(Wb + (int64_t)n0 * K * ESZ));
+    abase = uniform64((uint64_t)(uintptr_t)(Ab + (int64_t)m0 * lda * ESZ));
+    bbase = uniform64((uint64_t)(uintptr_t)(Wb + (int64_t)n0 * K * ESZ));
+    if (!SPLIT) {
 #pragma unroll
-    for (int k = 0; k < Cfg::LOADS_HI; ++k)
-      pbase[k] = wave + Cfg::NW * k < Cfg::A_PIECES ? abase : bbase;
+      for (int k = 0; k < Cfg::LOADS_HI; ++k) pbase[k] = is_a(k) ? abase : bbase;
+    }
   };
   set_tile(is_m0, is_n0);
   // Issue the loads of slab is_s, then advance the cursor.
@@ -300,7 +325,8 @@ __device__ __forceinline__ void gemm_lds_body(
     for (int k = 0; k < Cfg::LOADS_HI; ++k) {
       const int p = wave + Cfg::NW * k;  // wave-uniform
       if (k < Cfg::LOADS_LO || p < Cfg::PIECES)
-        dma16s(pbase[k] + is_kb, poff[k], slot + (uint32_t)(p * 1024));
+        dma16s((SPLIT ? (is_a(k) ? abase : bbase) : pbase[k]) + is_kb, poff[k],
+               slot + (uint32_t)(p * 1024));
     }
     // Epilogue vectors, on a tile's first slab: lanes 0 .. BIAS_PER_WAVE/4 - 1
     // move 16 bytes each of the columns from n0 + wave * BIAS_PER_WAVE (clamped
@@ -326,7 +352,7 @@ __device__ __forceinline__ void gemm_lds_body(
       }
     }
     is_slot = is_slot + Cfg::SLOT == NS * Cfg::SLOT ? 0 : is_slot + Cfg::SLOT;
-    is_kb += ROWB;
+    is_kb += RB;
     if (++is_kt == nk) {
       is_kt = 0;
       is_kb = 0;
@@ -346,20 +372,34 @@ __device__ __forceinline__ void gemm_lds_body(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0;
 
-  // Fragment addressing: lane (row li, k-half g) reads logical chunk 2*kk + g
-  // of its row, at its swizzled position.
-  const int swz = (li >> 2) & 3;  // (row >> 2) & 3 with row = 32*x + li
-  const int pos0 = ((0 + g) ^ swz) * 16, pos1 = ((2 + g) ^ swz) * 16;
-  const int rowA = (wm * Cfg::WM + li) * ROWB, rowB = (wn * Cfg::WN + li) * ROWB;
+  // Fragment addressing: at k-step kk lane (row li, k-half g) reads logical
+  // chunk 2*kk + g of its row, at its swizzled position (rows 32*x + li all
+  // share li's swizzle).
+  constexpr int KS = Cfg::KSTEPS;
+  static_assert(KS % 2 == 0, "the last k-step of a slab is in set 1");
+  int pos[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) pos[kk] = chunk_pos<RB>(2 * kk + g, li) * 16;
+  const int rowA = (wm * Cfg::WM + li) * RB, rowB = (wn * Cfg::WN + li) * RB;
 
   frag_t fa0[TM], fb0[TN], fa1[TM], fb1[TN];
-  auto read_set = [&](int s, int pos, frag_t *fa, frag_t *fb) {
-    const uint8_t *slot = smem + (s % NS) * Cfg::SLOT;
+  // Reads in the order the MFMAs consume them: fb[0], fa[0..TM), fb[1..TN);
+  // read x of that order for x in [x0, x1).
+  auto read_part = [&](uint32_t soff, int pos, frag_t *fa, frag_t *fb, int x0, int x1) {
+    const uint8_t *slot = smem + soff;
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-      fb[j] = *(const frag_t *)(slot + Cfg::A_BYTES + rowB + j * 32 * ROWB + pos);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) fa[i] = *(const frag_t *)(slot + rowA + i * 32 * ROWB + pos);
+    for (int x = 0; x < TM + TN; ++x) {
+      if (x < x0 || x >= x1) continue;
+      if (x == 0)
+        fb[0] = *(const frag_t *)(slot + Cfg::A_BYTES + rowB + pos);
+      else if (x <= TM)
+        fa[x - 1] = *(const frag_t *)(slot + rowA + (x - 1) * 32 * RB + pos);
+      else
+        fb[x - TM] = *(const frag_t *)(slot + Cfg::A_BYTES + rowB + (x - TM) * 32 * RB + pos);
+    }
+  };
+  auto read_set = [&](uint32_t soff, int pos, frag_t *fa, frag_t *fb) {
+    read_part(soff, pos, fa, fb, 0, TM + TN);
   };
   auto mfma_set = [&](const frag_t *fa, const frag_t *fb) {
 #pragma unroll
@@ -513,14 +553,14 @@ __device__ __forceinline__ void gemm_lds_body(
     }
   };
 
-  // Prologue: slabs 0 .. NS-1 in flight; slab 0's first half into set 0.
+  // Prologue: slabs 0 .. NS-1 in flight; k-step 0 of slab 0 into set 0.
 #pragma unroll
   for (int s = 0; s < NS; ++s)
     if (s < nslab) issue();
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  read_set(0, pos0, fa0, fb0);
+  read_set(0, pos[0], fa0, fb0);
 
   // An epilogue issues EPI_STORES global stores per wave (one per staged row
   // group of each 32 x 32 block) when its tile lies wholly inside C, where
@@ -531,32 +571,59 @@ __device__ __forceinline__ void gemm_lds_body(
   // keeps the exact wait.
   constexpr int EPI_STORES = RES ? 0 : (CBF ? 2 : 4) * TM * TN;
   static_assert(Cfg::LOADS_HI * (NS - 2) + EPI_STORES < 64, "vmcnt holds at most 63");
+  constexpr bool SAME_LOADS = Cfg::LOADS_HI == Cfg::LOADS_LO;
   int epi_left = 0;
   int ep_kt = 0, ep_ti = 0;  // tile and depth of slab s
+  uint32_t rd_slot = 0;      // byte offset of slab s's slot
   for (int s = 0; s < nslab; ++s) {
-    // First half of slab s; its second half is read meanwhile.
-    mfma_set(fa0, fb0);
-    read_set(s, pos1, fa1, fb1);
-    interleave();
+    // k-steps 0 .. KS-2 of slab s: each one's MFMAs run while the next
+    // k-step's fragments are read into the other set.
+#pragma unroll
+    for (int kk = 0; kk + 1 < KS; ++kk) {
+      if (kk % 2 == 0) {
+        mfma_set(fa0, fb0);
+        read_set(rd_slot, pos[kk + 1], fa1, fb1);
+      } else {
+        mfma_set(fa1, fb1);
+        read_set(rd_slot, pos[kk + 1], fa0, fb0);
+      }
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+    }
     // Every read of slab s is now issued. Wait for them and for this wave's
     // loads of slab s + 1 (the slabs issued after it, at most NS - 2, may stay
     // in flight), then meet: slab s + 1 is in LDS and slot s % NS is free.
+    const uint32_t nx_slot = rd_slot + Cfg::SLOT == NS * Cfg::SLOT ? 0 : rd_slot + Cfg::SLOT;
     const int ahead = nslab - 2 - s;
     const bool stores_young = EPI_STORES > 0 && epi_left > 0;
-    if (wave < Cfg::NHI)
+    if (ahead >= NS - 2 && !stores_young) {
+      if (SAME_LOADS || wave < Cfg::NHI)
+        wait_vmcnt<Cfg::LOADS_HI *(NS - 2)>();
+      else
+        wait_vmcnt<Cfg::LOADS_LO *(NS - 2)>();
+    } else if (SAME_LOADS || wave < Cfg::NHI) {
       wait_slab<Cfg::LOADS_HI, NS, EPI_STORES>(ahead, stores_young);
-    else
+    } else {
       wait_slab<Cfg::LOADS_LO, NS, EPI_STORES>(ahead, stores_young);
+    }
     if (epi_left > 0) --epi_left;
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    // Second half of slab s; the first half of slab s + 1 is read meanwhile
-    // (after the last slab, slab s again: in bounds, unused). The loads of
-    // slab s + NS are issued after the first MFMAs, which keep the matrix
-    // pipe busy while the scalar unit addresses them.
+    // The last k-step of slab s (set 1: KS is even); k-step 0 of slab s + 1
+    // is read meanwhile, in consumption order (after the last slab, slab s
+    // again: in bounds, unused): the first TM reads beside the j = 0 MFMAs,
+    // the rest after the loads of slab s + NS are issued -- those keep the
+    // matrix pipe busy while the scalar unit addresses the loads.
+    const uint32_t rs = s + 1 < nslab ? nx_slot : rd_slot;
 #pragma unroll
     for (int i = 0; i < TM; ++i) acc[0][i] = PT::mfma(fb1[0], fa1[i], acc[0][i]);
+    read_part(rs, pos[0], fa0, fb0, 0, TM);
+#pragma unroll
+    for (int x = 0; x < TM; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (s + NS < nslab) issue();  // slab s + NS
     __builtin_amdgcn_sched_barrier(0);
@@ -564,9 +631,9 @@ __device__ __forceinline__ void gemm_lds_body(
     for (int j = 1; j < TN; ++j)
 #pragma unroll
       for (int i = 0; i < TM; ++i) acc[j][i] = PT::mfma(fb1[j], fa1[i], acc[j][i]);
-    read_set(s + 1 < nslab ? s + 1 : s, pos0, fa0, fb0);
+    read_part(rs, pos[0], fa0, fb0, TM, TM + TN);
     {
-      constexpr int NM = TM * (TN - 1), NR = TM + TN, NP = NM < NR ? NM : NR;
+      constexpr int NM = TM * (TN - 1), NR = TN, NP = NM < NR ? NM : NR;
 #pragma unroll
       for (int x = 0; x < NP; ++x) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -575,6 +642,7 @@ __device__ __forceinline__ void gemm_lds_body(
       if (NM > NP) __builtin_amdgcn_sched_group_barrier(0x008, NM - NP, 0);
       if (NR > NP) __builtin_amdgcn_sched_group_barrier(0x100, NR - NP, 0);
     }
+    rd_slot = nx_slot;
     if (++ep_kt == nk) {
       ep_kt = 0;
       {

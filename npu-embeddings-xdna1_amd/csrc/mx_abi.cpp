@@ -482,6 +482,11 @@ const char *mx_gemm_plan(int64_t M, int64_t N, int64_t K) {
   return mxk::gemm_config_name(M, N, K);
 }
 
+const char *mx_gemm_plan_for(int64_t M, int64_t N, int64_t K, int c_dtype, int residual,
+                             int int8) {
+  return mxk::gemm_plan_name(M, N, K, c_dtype == MX_BF16, residual != 0, int8 != 0);
+}
+
 int mx_attention(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
                  int64_t H, int64_t hd, float scale, const float *add_mask,
                  const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx) {

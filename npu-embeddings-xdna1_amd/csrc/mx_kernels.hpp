@@ -64,8 +64,9 @@ struct GemmArgs {
 hipError_t gemm(const GemmArgs &a, hipStream_t s);
 
 // The LDS-pipelined kernel's tile for an M x N product (0: 256x256, 1: 256x192,
-// 2: 128x256, 3: 128x128) and the resident blocks of a persistent launch.
-int gemm_lds_tile(int64_t M, int64_t N);
+// 2: 128x256, 3: 128x128; deep: the 256 x 256 tile would run on 128-byte
+// slabs) and the resident blocks of a persistent launch.
+int gemm_lds_tile(int64_t M, int64_t N, bool deep);
 int cu_count();
 // Blocks of a persistent launch over ntiles tiles with `grid` resident: at
 // most one per tile, rounded up to a whole number per XCD (a multiple of 8)
@@ -97,6 +98,8 @@ struct GemmI8Args {
   int64_t ldc;
 };
 hipError_t gemm_i8(const GemmI8Args &a, hipStream_t s);
+// Whether the 256 x 256 tile runs on 128-byte slabs for this call.
+bool gemm_i8_deep(const GemmI8Args &a);
 
 // quantise_a_int8 over rows of K (k_quant.hip): a fp32 or bf16 (row stride
 // lda), ias [K] -> q int8 (row stride ldq) and a_scale [rows]. K % 4 == 0,
@@ -127,7 +130,12 @@ hipError_t untile_panel(const uint16_t *panel, int64_t K, int64_t N, int tile_k,
                         int mac_s, int mac_t, uint16_t *wt, hipStream_t s);
 hipError_t untile_panel_i8(const int8_t *panel, int64_t K, int64_t N, int tile_k, int tile_n,
                            int mac_s, int mac_t, int8_t *wt, hipStream_t s);
-// Tile configuration the launcher would pick (for tests and reports).
+// The plan the launcher would pick (for tests and reports): tile, slab depth
+// in K elements, wave tile and ring slots, e.g.
+// "lds_256x256x64_w64x128_ns2_persistent". gemm_config_name is the bf16
+// datapath's plan for an fp32 C without a residual.
+const char *gemm_plan_name(int64_t M, int64_t N, int64_t K, bool c_bf16, bool residual,
+                           bool i8);
 const char *gemm_config_name(int64_t M, int64_t N, int64_t K);
 
 struct AttnArgs {

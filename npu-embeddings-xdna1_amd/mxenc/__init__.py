@@ -87,6 +87,7 @@ SIGNATURES = {
     "mx_gemm_wt": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp, _int,
                           _i64]),
     "mx_gemm_plan": (ctypes.c_char_p, [_i64, _i64, _i64]),
+    "mx_gemm_plan_for": (ctypes.c_char_p, [_i64, _i64, _i64, _int, _int, _int]),
     "mx_attention": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp,
                             _vp, _i64]),
     "mx_softmax_rows": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _i64, _int]),

@@ -136,6 +136,38 @@ def test_gemm_i8_dequant_bit_exact(ctx, orc, M, K, N, bias):
     mxenc.check(mxenc.lib().mx_release_weight(ctx.handle, slot))
 
 
+@pytest.mark.parametrize("K,epi", [(1024, mxenc.MX_EPI_NONE), (384, mxenc.MX_EPI_GELU_POLY)])
+def test_gemm_i8_deep_tile_bit_exact(ctx, orc, K, epi):
+    """The 256 x 256 tile on 128-byte slabs (bf16 C, no residual, K % 128 ==
+    0; K = 384 is an odd number of slabs): dequantise_c (and the activation)
+    fused, bit-identical to the host forms, on a subset of rows (rows are
+    independent): the first and last 256 and 256 random ones."""
+    M, N = 8000, 2048
+    assert mxenc.lib().mx_gemm_plan_for(M, N, K, mxenc.MX_BF16, 0, 1).decode().startswith(
+        "lds_256x256x128")
+    rng = np.random.default_rng(K)
+    A, W = _i8(rng, (M, K)), _i8(rng, (K, N))
+    sa = rng.uniform(1e-4, 1e-2, M).astype(np.float32)
+    ws = rng.uniform(1e-4, 1e-2, N).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    slot = mxenc.stage_weight_i8(ctx, W, ws, np.ones(K, np.float32))
+    C = ctx.empty((M, N), np.uint16)
+    mxenc.gemm_i8(ctx, ctx.put(A), ctx.put(sa), M, K, K, slot, ctx.put(b), epi, None, C, N)
+    got = C.host()
+    rows = np.unique(np.concatenate([np.arange(256), np.arange(M - 256, M),
+                                     rng.integers(0, M, 256)]))
+    Ar = np.ascontiguousarray(A[rows])
+    c32 = np.zeros((rows.size, N), np.int32)
+    orc.orc_gemm_i8(P(Ar), rows.size, K, P(W), N, P(c32))
+    want = np.zeros((rows.size, N), np.float32)
+    sar = np.ascontiguousarray(sa[rows])
+    orc.orc_dequantise_c(P(c32), rows.size, N, P(sar), P(ws), P(b), P(want))
+    if epi == mxenc.MX_EPI_GELU_POLY:
+        orc.orc_gelu_poly_inplace(P(want), want.size)
+    assert np.array_equal(got[rows], mxenc.to_bf16_bits(want))
+    mxenc.check(mxenc.lib().mx_release_weight(ctx.handle, slot))
+
+
 def test_gemm_i8_gelu_epilogue_is_dequant_act(ctx, orc):
     """FFN up on the int8 design: dequantise, bias, then the host's gelu8 --
     the first half of dequant_act_quant (host_kernels.hpp:405-500), bit for bit."""

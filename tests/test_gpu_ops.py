@@ -304,7 +304,14 @@ GEMM_PATHS = [
     (16000, 768, 1532, mxenc.MX_EPI_GELU_ERF, np.float32, True, "lds_256x192"),  # ragged M, N
     (4096, 384, 1536, mxenc.MX_EPI_GELU_POLY, np.uint16, False, "lds_128x256"),  # MiniLM FFN-up
     (1000, 1280, 3840, mxenc.MX_EPI_GELU_ERF, np.float32, True, "lds_128x128"),  # ragged M
-    (777, 512, 1004, mxenc.MX_EPI_GELU_ERF, np.uint16, False, "lds_128x128"),   # ragged M, N
+    # bf16 C rows of 1004 are not 16-byte multiples: the register-staged kernel
+    (777, 512, 1004, mxenc.MX_EPI_GELU_ERF, np.uint16, False, "staged_"),      # ragged M, N
+    (777, 512, 1000, mxenc.MX_EPI_GELU_ERF, np.uint16, False, "lds_128x128"),   # ragged M, N
+    # the 256 x 256 tile on 128-byte slabs (bf16 C, no residual, K % 64 == 0)
+    (17455, 768, 2304, mxenc.MX_EPI_NONE, np.uint16, False, "lds_256x256x64"),  # packed QKV
+    (17455, 3072, 768, mxenc.MX_EPI_NONE, np.uint16, False, "lds_256x256x64"),  # FFN-down
+    (8000, 1024, 2000, mxenc.MX_EPI_GELU_ERF, np.uint16, False, "lds_256x256x64"),  # ragged
+    (8000, 192, 2048, mxenc.MX_EPI_GELU_POLY, np.uint16, False, "lds_256x256x64"),  # 3 slabs
 ]
 
 
@@ -313,7 +320,8 @@ def test_gemm_kernel_paths(ctx, orc, M, K, N, epi, cdt, res, plan):
     """Each GEMM kernel configuration at a size that selects it, checked on a
     subset of rows (rows are independent) against the oracle's gemm_nt with
     the same epilogue: the first and last 128 rows and 128 random ones."""
-    assert mxenc.lib().mx_gemm_plan(M, N, K).decode().startswith(plan)
+    cdtype = mxenc.MX_BF16 if cdt == np.uint16 else mxenc.MX_F32
+    assert mxenc.lib().mx_gemm_plan_for(M, N, K, cdtype, int(res), 0).decode().startswith(plan)
     rng = np.random.default_rng(M + K + N)
     A = to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
     W = to_bf16_bits((rng.standard_normal((K, N)) * 0.05).astype(np.float32))
