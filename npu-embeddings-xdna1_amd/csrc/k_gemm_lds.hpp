@@ -19,7 +19,9 @@
 // themselves (the design's C before dequantisation).
 //
 // Grid. One block per CU walks a list of BM x BN output tiles; its slabs
-// (64 bytes of K per row: 32 bf16 or 64 int8) form one sequence across tile
+// (RB = 64 or 128 bytes of K per row: 32 or 64 bf16, 64 or 128 int8; 128-byte
+// rows make every load request a whole 128-byte line and halve the barriers
+// per K, and need two 64 KB slots for a 256 x 256 tile) form one sequence across tile
 // boundaries, so the ring keeps loading the next tile's first slabs while the
 // current tile drains: no per-tile prologue latency, no block relaunch.
 // Workgroups go round-robin over the 8 XCDs, so the blocks of XCD x
@@ -45,21 +47,23 @@
 // they are on chip for the epilogue without a compiler-tracked load; the
 // waits do not count those loads, which only makes them stricter.
 //
-// Fragments. Two register sets, one per 32-byte half of a slab; each half's
-// MFMAs run while the other set is read from LDS (one ds_read after each of
-// the first MFMAs, pinned by sched_group_barrier). The barrier sits between
-// the halves, when every read of the current slab has been issued.
+// Fragments. A slab is RB/32 k-steps of 32 bytes of K. Two register sets
+// alternate: each k-step's MFMAs run while the next k-step is read from LDS
+// into the other set (in the order the MFMAs consume it, one ds_read after
+// each of the first MFMAs, pinned by sched_group_barrier). The barrier sits
+// before the slab's last k-step, when every read of the slab has been issued.
 //
-// LDS image. A slab is rows of 64 bytes = four 16-byte chunks. gfx950
+// LDS image. A slab is rows of RB bytes = RB/16 16-byte chunks. gfx950
 // serves a ds_read_b128 sixteen lanes (256 bytes, all 64 banks) per cycle; the
 // sixteen lanes of one phase read rows r..r+15 at the same logical chunk.
-// Chunk c of row r is stored at position c ^ ((r >> 2) & 3) of its row, which
+// Chunk c of row r is stored at position chunk_pos(c, r) of its row, which
 // puts those sixteen 16-byte reads in sixteen different bank groups. The
 // direct load writes lane l's 16 bytes at LDS offset 16*l of its 1 KB window,
 // so the swizzle is applied to the GLOBAL address each lane fetches: lane l
-// fills row l/4, position l%4, i.e. logical chunk (l%4) ^ (((l/4) >> 2) & 3).
-// A lane's MFMA operand is one 16-byte chunk (8 bf16 or 16 int8), read at the
-// same chunk index for A and W, so both operands pair the same K values.
+// fills row l/(RB/16), position l%(RB/16), i.e. the logical chunk that
+// chunk_pos maps there. A lane's MFMA operand is one 16-byte chunk (8 bf16 or
+// 16 int8), read at the same chunk index for A and W, so both operands pair
+// the same K values.
 //
 // Operand roles. The MFMA's first operand is the W tile and its second the A
 // tile, so the 32x32 accumulator holds C^T: each lane owns one row of C and
