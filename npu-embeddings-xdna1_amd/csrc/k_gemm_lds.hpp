@@ -422,8 +422,94 @@ __device__ __forceinline__ void gemm_lds_body(
     __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
   };
 
+  // The epilogue of a bf16 C without a residual, block by block (k = j * TM
+  // + i): each column block's bias (and wscale) is read once for its TM row
+  // blocks; a block goes through the bias (dequantisation), the activation and
+  // the bf16 narrowing in registers, then crosses the wave's 2 KB staging
+  // area. The round trips are software-pipelined: block k is written right
+  // after block k - 1's read-back is issued (a wave's LDS operations execute
+  // in order, so the write cannot overtake the read), and only block k - 1's
+  // global stores wait for its read-back, while block k's arithmetic runs
+  // under it.
+  auto epilogue_bf = [&](int ti) {
+    int m0, n0;
+    tile_origin(ti, m0, n0);
+    const float *bl = (const float *)(smem + Cfg::BIAS_OFF + (ti & 1) * BN * 4);
+    const float *wsl = (const float *)(smem + Cfg::WS_OFF + (ti & 1) * BN * 4);
+    const float *sal = (const float *)(smem + Cfg::SA_OFF + (ti & 1) * BM * 4);
+    uint8_t *stg = smem + Cfg::STG_OFF + wave * Cfg::STG_WAVE;
+    // Staging: lane (li, g) writes its 8 bytes of chunk q of row li at
+    // position q ^ ((li >> 2) & 3); lane l reads chunk c = l & 3 of rows
+    // r * 16 + l / 4, 16 bytes each, and stores them.
+    auto store = [&](int k, const uint4 *w) {
+      const int j = k / TM, i = k % TM;
+      const int rbase = m0 + wm * Cfg::WM + i * 32;
+      const int cl = wn * Cfg::WN + j * 32;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int row = r * 16 + (lane >> 2), c = lane & 3;
+        const int grow = rbase + row, gcol = n0 + cl + c * 8;
+        if (grow < M && gcol < N) {
+          const int64_t off = (int64_t)grow * ldc + gcol;
+          if (gcol + 8 <= N)
+            *(uint4 *)((uint16_t *)C + off) = w[r];
+          else  // N % 8 == 4: four columns left
+            *(uint2 *)((uint16_t *)C + off) = make_uint2(w[r].x, w[r].y);
+        }
+      }
+    };
+    float4 b[4], w[4];
+    uint4 wv[2];
+#pragma unroll
+    for (int k = 0; k < TM * TN; ++k) {
+      const int j = k / TM, i = k % TM;
+      if (i == 0) {
+        const int cl = wn * Cfg::WN + j * 32;  // tile-local first column
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          b[q] = has_bias ? *(const float4 *)(bl + cl + q * 8 + g * 4)
+                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          if (I8) w[q] = *(const float4 *)(wsl + cl + q * 8 + g * 4);
+        }
+      }
+      const float sa = I8 ? sal[wm * Cfg::WM + i * 32 + li] : 0.0f;
+      uint32_t pk[8];  // columns 8q + 4g + 2h, +1 of row li: pk[2q + h]
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float bb[4] = {b[q].x, b[q].y, b[q].z, b[q].w};
+        const float ww[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (I8)
+            v[e] = gemm_epilogue(
+                __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + e], sa), ww[e], bb[e]), EPI);
+          else
+            v[e] = gemm_epilogue((float)acc[j][i][q * 4 + e] + bb[e], EPI);
+        }
+        pk[2 * q] = pack_bf2_hw(v[0], v[1]);
+        pk[2 * q + 1] = pack_bf2_hw(v[2], v[3]);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *(uint2 *)(stg + li * 64 + ((q ^ ((li >> 2) & 3)) * 16 + g * 8)) =
+            make_uint2(pk[2 * q], pk[2 * q + 1]);
+      if (k > 0) store(k - 1, wv);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int row = r * 16 + (lane >> 2), c = lane & 3;
+        wv[r] = *(const uint4 *)(stg + row * 64 + ((c ^ ((row >> 2) & 3)) * 16));
+      }
+    }
+    store(TM * TN - 1, wv);
+  };
+
   // The epilogue of this block's ti-th tile.
   auto epilogue = [&](int ti) {
+    if constexpr (CBF && !RES) {
+      epilogue_bf(ti);
+      return;
+    }
     int m0, n0;
     tile_origin(ti, m0, n0);
     const float *bl = (const float *)(smem + Cfg::BIAS_OFF + (ti & 1) * BN * 4);
