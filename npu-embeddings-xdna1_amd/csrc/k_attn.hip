@@ -1,6 +1,10 @@
 // k_attn.hip -- fused masked attention on gfx950 MFMA: QK^T, additive-mask
 // softmax and PV in one pass per (sequence, head, 128-query tile); the score
-// matrix never reaches HBM.
+// matrix never reaches HBM. Two kernels share the design below: attn_dma_k
+// (head_dim 64: K, V and the mask reach LDS by direct loads through a ring of
+// slots, and V^T is read with the transposing ds_read_b64_tr_b16) and
+// attn_fwd_k (head_dim 32, or a qkv too long for 32-bit row offsets: K and V
+// staged through registers, V transposed on the way into LDS).
 //
 // Each of the 4 waves owns 32 queries and computes the TRANSPOSED score tile
 // S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (keys on rows, queries on
@@ -279,6 +283,272 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
   }
 }
 
+
+// ---- head_dim 64: K, V and the mask through a ring of LDS slots ----------------
+//
+// The same block and wave roles and the same softmax as attn_fwd_k, with the
+// key tiles staged differently: K, V and the tile's mask row go global -> LDS
+// by direct loads (global_load_lds_dwordx4 / _dword, issued from inline
+// assembly so the compiler adds no waits) into a ring of NSL slots, NSL - 1
+// tiles ahead, and V stays row-major in LDS: the PV operand V^T is read with
+// ds_read_b64_tr_b16, which hands each lane of a 16-lane group one column of
+// the 4 x 16 bf16 block the group addresses (lane j of the group receives
+// element j % 4 of group lane 4e + j / 4's 8 bytes, e = 0..3). No registers
+// hold K or V in flight and no VALU transposes them.
+//
+// LDS rows are 128 bytes (64 bf16); 16-byte chunk c of row r is stored at
+// c ^ ((r >> 1) & 7) for K (sixteen ds_read_b128 rows r..r+15 hit sixteen
+// bank groups) and at c ^ ((r & 2) << 1) for V (the 32 lanes of a
+// ds_read_b64_tr_b16 phase read rows k0..k0+3 of two 16-column groups: row
+// parity picks a 32-bank half, the XOR separates rows k0 and k0 + 2). Rows
+// past the sequence's last are fetched from that last row (in bounds) and
+// carry probability 0.
+constexpr int NSL = 3;
+
+__device__ __forceinline__ void dma16o(uint64_t base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff),
+               "s"(base)
+               : "memory");
+}
+__device__ __forceinline__ void dma4o(uint64_t base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff),
+               "s"(base)
+               : "memory");
+}
+__device__ __forceinline__ uint64_t uni64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict__ qkv,
+                                                   int64_t ldq, int S, int H, float scale_log2e,
+                                                   const float *__restrict__ add_mask,
+                                                   const int32_t *__restrict__ kv_len,
+                                                   uint16_t *__restrict__ ctx, int64_t ldo,
+                                                   int n_qblk, int force_logits,
+                                                   const int32_t *__restrict__ seq_start,
+                                                   const int32_t *__restrict__ order) {
+  constexpr int HD = 64, NKK = HD / 16, NHT = HD / 32;
+  constexpr int ROWB = HD * 2, TILE = BKV * ROWB;  // 128-byte rows, 8 KB per operand tile
+  constexpr int SLOT = 2 * TILE + BKV * 4;         // K, V, mask row
+  __shared__ __attribute__((aligned(1024))) uint8_t sm[NSL * SLOT];
+
+  const int blk = blockIdx.x;
+  int qb, h, b;
+  if (order) {
+    h = blk % H;
+    const int t = blk / H;
+    qb = t % n_qblk;
+    b = order[t / n_qblk];
+  } else {
+    qb = blk % n_qblk;
+    const int bh = blk / n_qblk;
+    h = bh % H;
+    b = bh / H;
+  }
+  const int d = H * HD;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, li = lane & 31;
+  int kvl = kv_len ? kv_len[b] : S;
+  kvl = kvl < 1 ? 1 : (kvl > S ? S : kvl);
+  const int64_t row0 = seq_start ? (int64_t)seq_start[b] : (int64_t)b * S;
+  const int lim = seq_start ? kvl : S;
+  if (qb * BQ >= lim) return;
+  const uint16_t *base = qkv + row0 * ldq;
+  const bool live = qb * BQ + wave * 32 < lim;
+
+  // Q fragments (B operand of S^T = K Q^T), waited for before the loop.
+  const int q = qb * BQ + wave * 32 + li;
+  bf16x8 qf[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (q < lim) v = *(const uint4 *)(base + (int64_t)q * ldq + h * HD + kk * 16 + g * 8);
+    qf[kk] = __builtin_bit_cast(bf16x8, v);
+  }
+  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]));
+
+  // Key tile t -> slot t % NSL: wave w moves K rows and V rows 8p .. 8p + 7
+  // for pieces p = w and w + 4 (1 KB each: lane l fills row 8p + l / 8,
+  // position l % 8); wave 0 also the tile's 64 mask entries.
+  const uint64_t kb64 = uni64((uint64_t)(uintptr_t)(base + d + h * HD));
+  const uint64_t vb64 = uni64((uint64_t)(uintptr_t)(base + 2 * d + h * HD));
+  const uint64_t mb64 = add_mask ? uni64((uint64_t)(uintptr_t)(add_mask + (int64_t)b * S)) : 0;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)sm;
+  const uint32_t rowbytes = (uint32_t)(ldq * 2);
+  const int prow = lane >> 3, ppos = lane & 7;
+  auto issue = [&](int t) {
+    const uint32_t slot = lds0 + (uint32_t)((t % NSL) * SLOT);
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const int p = wave + 4 * x;
+      const int row = p * 8 + prow;
+      int key = t * BKV + row;
+      key = key < lim ? key : lim - 1;
+      const uint32_t roff = (uint32_t)key * rowbytes;
+      dma16o(kb64, roff + (uint32_t)((ppos ^ ((row >> 1) & 7)) * 16), slot + p * 1024);
+      dma16o(vb64, roff + (uint32_t)((ppos ^ ((row & 2) << 1)) * 16), slot + TILE + p * 1024);
+    }
+    if (wave == 0 && add_mask) {
+      int key = t * BKV + lane;
+      key = key < S ? key : S - 1;
+      dma4o(mb64, (uint32_t)key * 4, slot + 2 * TILE);
+    }
+  };
+  // This wave's loads of one tile complete in issue order; the wait for tile
+  // t leaves tile t + 1's (issued after it) in flight.
+  const bool mwave = wave == 0 && add_mask != nullptr;
+  auto wait_next = [&](bool one_more_in_flight) {
+    if (one_more_in_flight) {
+      if (mwave)
+        vm_wait<5>();
+      else
+        vm_wait<4>();
+    } else {
+      vm_wait<0>();
+    }
+  };
+
+  f32x16 o[NHT];
+#pragma unroll
+  for (int t = 0; t < NHT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  // Fixed per-lane LDS offsets: K fragment rows sub * 32 + li, chunk 2kk + g;
+  // the V^T transposed reads (group G = lane / 16, e, qq below).
+  const int swk = (li >> 1) & 7;
+  const int G = lane >> 4, e4 = (lane & 15) >> 2, qq = lane & 3;
+  const int swv = ((e4 >> 1) & 1);  // (row & 2) << 1 with row = 16ch + 4(G >> 1) + e4, as 0/1
+  const int vrow = 4 * (G >> 1) + e4;
+
+  const int ntile = (kvl + BKV - 1) / BKV;
+  issue(0);
+  if (ntile > 1) issue(1);
+  wait_next(ntile > 1);
+  __syncthreads();
+  for (int t = 0; t < ntile; ++t) {
+    if (t + 2 < ntile) issue(t + 2);
+    const uint8_t *sl = sm + (t % NSL) * SLOT;
+    if (live) {
+      f32x16 sc[2];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[sub][r] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+          const bf16x8 kf = *(const bf16x8 *)(sl + (sub * 32 + li) * ROWB +
+                                              (((2 * kk + g) ^ swk) * 16));
+          sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sc[sub], 0, 0, 0);
+        }
+      }
+      // The tile needs logits (mask added, keys past kv_len at -inf) if it
+      // reaches past kv_len or has a nonzero mask entry.
+      const float *smk = (const float *)(sl + 2 * TILE);
+      bool masked = (t + 1) * BKV > kvl || force_logits;
+      if (add_mask) masked = masked || __ballot(smk[lane] != 0.0f) != 0;
+      float mx = -INFINITY, cc;
+      if (masked) {
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = sub * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
+            const float mv = t * BKV + key < kvl
+                                 ? (add_mask ? smk[key] * 1.4426950408889634f : 0.0f)
+                                 : -INFINITY;
+            const float v = __builtin_fmaf(sc[sub][r], scale_log2e, mv);
+            sc[sub][r] = v;
+            mx = fmaxf(mx, v);
+          }
+        cc = 1.0f;
+      } else {
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[sub][r]);
+        mx *= scale_log2e;
+        cc = scale_log2e;
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      if (mx > m_run + 8.0f) {
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mx);
+        m_run = mx;
+        l_run *= alpha;
+#pragma unroll
+        for (int ht = 0; ht < NHT; ++ht)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[ht][r] *= alpha;
+      }
+      bf16x8 pk[4];
+      float ps = 0.0f;
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch) {
+        const int sub = ch >> 1, c = ch & 1;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[sub][c * 8 + jj], cc, -m_run));
+          ps += p;
+          pk[ch][jj] = (__bf16)p;
+        }
+      }
+      l_run += ps;
+      // O^T += V^T P^T: lane (hd row li, half g) needs keys 16ch + 4g + 0..3
+      // and 16ch + 8 + 4g + 0..3 of its hd column; group G of the transposed
+      // read covers hd columns 32ht + 16(G & 1) + 0..15 and keys
+      // 16ch + 4(G >> 1) + 0..3 (+ 8), its lane 4e + qq addressing row
+      // 16ch + 4(G >> 1) + e, columns 32ht + 16(G & 1) + 4qq .. + 3.
+      const uint8_t *vs = sl + TILE;
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch) {
+#pragma unroll
+        for (int ht = 0; ht < NHT; ++ht) {
+          const int chunk = ((4 * ht) ^ (4 * swv)) + 2 * (G & 1) + (qq >> 1);
+          const uint8_t *a = vs + (16 * ch + vrow) * ROWB + chunk * 16 + (qq & 1) * 8;
+          const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4s *)(uintptr_t)(uint32_t)(uintptr_t)a);
+          const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4s *)(uintptr_t)(uint32_t)(uintptr_t)(a + 8 * ROWB));
+          const short vv8 __attribute__((ext_vector_type(8))) = {lo[0], lo[1], lo[2], lo[3],
+                                                                   hi[0], hi[1], hi[2], hi[3]};
+          o[ht] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vv8),
+                                                          pk[ch], o[ht], 0, 0, 0);
+        }
+      }
+    }
+    // Tile t + 1 in LDS (tile t + 2's loads may stay in flight), then meet:
+    // every read of slot t % NSL is done before iteration t + 1 refills it.
+    if (t + 1 < ntile) wait_next(t + 2 < ntile);
+    __syncthreads();
+  }
+
+  const float l = l_run + __shfl_xor(l_run, 32);
+  const float inv = 1.0f / l;
+  if (q < lim) {
+    uint16_t *dst = ctx + (row0 + q) * ldo + h * HD;
+#pragma unroll
+    for (int ht = 0; ht < NHT; ++ht)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int hd0 = ht * 32 + r4 * 8 + g * 4;
+        uint2 w;
+        w.x = pack_bf2(o[ht][r4 * 4 + 0] * inv, o[ht][r4 * 4 + 1] * inv);
+        w.y = pack_bf2(o[ht][r4 * 4 + 2] * inv, o[ht][r4 * 4 + 3] * inv);
+        *(uint2 *)(dst + hd0) = w;
+      }
+  }
+}
+
 }  // namespace
 
 namespace mxk {
@@ -288,7 +558,11 @@ hipError_t attention(const AttnArgs &a, hipStream_t s) {
   const int64_t blocks = a.B * a.H * n_qblk;
   const float sl2e = a.scale * 1.4426950408889634f;
   const int force_logits = a.scale > 0.0f ? 0 : 1;  // raw-score max needs scale > 0
-  if (a.hd == 64)
+  if (a.hd == 64 && (int64_t)a.S * a.ld_qkv * 2 < ((int64_t)1 << 31))
+    attn_dma_k<<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
+                                               a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
+                                               force_logits, a.seq_start, a.order);
+  else if (a.hd == 64)
     attn_fwd_k<64><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
                                                    a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
                                                    force_logits, a.seq_start, a.order);

@@ -423,6 +423,34 @@ def test_attention_unmasked_odd_lengths(ctx, orc, B, S, H, scale):
     assert np.max(np.abs(got - want)) < 2e-2 * np.max(np.abs(want))
 
 
+@pytest.mark.parametrize("with_mask", [False, True])
+def test_attention_kvlen_holes_and_additive_mask(ctx, orc, with_mask):
+    """kv_len cutting mid-tile with and without a mask row; with a mask, holes
+    (-1e30) inside the sequence and finite additive values (-3, +0.5), which
+    send every tile through the logits path."""
+    B, S, H, hd = 3, 320, 4, 64  # S % 8 == 0: the oracle's masked qk/softmax/av form
+    rng = np.random.default_rng(31 + with_mask)
+    d = H * hd
+    qkv = to_bf16_bits(rng.standard_normal((B * S, 3 * d)).astype(np.float32))
+    lens = np.array([300, 77, 129], np.int32)
+    mask = np.zeros((B, S), np.float32)
+    for b, n in enumerate(lens):
+        mask[b, n:] = -1e30
+    if with_mask:
+        mask[0, 5:9] = -1e30
+        mask[1, 64] = -3.0
+        mask[2, 1:100:7] = 0.5
+    want = _attn_ref(orc, qkv, B, S, H, hd, mask)
+    dq, dk = ctx.put(qkv), ctx.put(lens)
+    out = ctx.empty((B * S, d), np.uint16)
+    mxenc.attention(ctx, dq, 3 * d, B, S, H, hd, 1.0, ctx.put(mask) if with_mask else None, dk,
+                    out, d)
+    got = from_bf16_bits(out.host())
+    err = np.abs(got - want)
+    assert np.max(err) < 2e-2 * np.max(np.abs(want)), np.max(err)
+    assert np.mean(err) < 2e-3
+
+
 def test_attention_fully_masked_row_is_uniform(ctx):
     """All keys masked with -1e30: the host softmax gives every key the same
     weight; so does the kernel (kv_len = S, finite mask)."""
