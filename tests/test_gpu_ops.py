@@ -451,6 +451,25 @@ def test_attention_kvlen_holes_and_additive_mask(ctx, orc, with_mask):
     assert np.mean(err) < 2e-3
 
 
+def test_attention_row_strides_bit_exact(ctx):
+    """QKV rows wider than 3*d (a row stride of 3*d + 8) and a ctx stride of
+    d + 4 give the same bits as the dense layout (head_dim 64 and 32)."""
+    for hd in (64, 32):
+        B, S, H = 2, 200, 3
+        d = H * hd
+        rng = np.random.default_rng(hd)
+        qkv = to_bf16_bits(rng.standard_normal((B * S, 3 * d)).astype(np.float32))
+        wide = np.zeros((B * S, 3 * d + 8), np.uint16)
+        wide[:, :3 * d] = qkv
+        lens = np.array([200, 61], np.int32)
+        dk = ctx.put(lens)
+        out = ctx.empty((B * S, d), np.uint16)
+        mxenc.attention(ctx, ctx.put(qkv), 3 * d, B, S, H, hd, 0.125, None, dk, out, d)
+        out2 = ctx.empty((B * S, d + 4), np.uint16)
+        mxenc.attention(ctx, ctx.put(wide), 3 * d + 8, B, S, H, hd, 0.125, None, dk, out2, d + 4)
+        assert np.array_equal(out.host(), out2.host()[:, :d])
+
+
 def test_attention_fully_masked_row_is_uniform(ctx):
     """All keys masked with -1e30: the host softmax gives every key the same
     weight; so does the kernel (kv_len = S, finite mask)."""
