@@ -504,10 +504,92 @@ __device__ __forceinline__ void gemm_lds_body(
     store(TM * TN - 1, wv);
   };
 
+  // The epilogue of an fp32 C with a residual (C = epi(A W + b) + R, R may be
+  // C itself), block by block (k = i * TN + j): block k + 1's residual rows
+  // are loaded while block k goes through the bias (dequantisation), the
+  // activation and the fp32 staging, so the loads' latency is paid once per
+  // tile instead of once per block. Rows of different blocks are disjoint, so
+  // loading block k + 1's residual before storing block k is exact also in
+  // place.
+  auto epilogue_res = [&](int ti) {
+    int m0, n0;
+    tile_origin(ti, m0, n0);
+    const float *bl = (const float *)(smem + Cfg::BIAS_OFF + (ti & 1) * BN * 4);
+    const float *wsl = (const float *)(smem + Cfg::WS_OFF + (ti & 1) * BN * 4);
+    const float *sal = (const float *)(smem + Cfg::SA_OFF + (ti & 1) * BM * 4);
+    uint8_t *stg = smem + Cfg::STG_OFF + wave * Cfg::STG_WAVE;
+    // Lane l handles 4 columns (l % 8) * 4 of rows r * 8 + l / 8, r = 0..3.
+    auto load_res = [&](int k, float4 *rv) {
+      const int i = k / TN, j = k % TN;
+      const int rbase = m0 + wm * Cfg::WM + i * 32;
+      const int cl = wn * Cfg::WN + j * 32;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int grow = rbase + r * 8 + (lane >> 3), gcol = n0 + cl + (lane & 7) * 4;
+        rv[r] = grow < M && gcol < N ? *(const float4 *)(residual + (int64_t)grow * ldc + gcol)
+                                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    };
+    float4 rcur[4], rnext[4];
+    load_res(0, rcur);
+#pragma unroll
+    for (int k = 0; k < TM * TN; ++k) {
+      const int i = k / TN, j = k % TN;
+      if (k + 1 < TM * TN) load_res(k + 1, rnext);
+      const int rbase = m0 + wm * Cfg::WM + i * 32;
+      const int cl = wn * Cfg::WN + j * 32;
+      const float sa = I8 ? sal[wm * Cfg::WM + i * 32 + li] : 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 b = has_bias ? *(const float4 *)(bl + cl + q * 8 + g * 4)
+                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 v;
+        if (I8) {
+          const float4 w = *(const float4 *)(wsl + cl + q * 8 + g * 4);
+          v.x = gemm_epilogue(
+              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 0], sa), w.x, b.x), EPI);
+          v.y = gemm_epilogue(
+              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 1], sa), w.y, b.y), EPI);
+          v.z = gemm_epilogue(
+              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 2], sa), w.z, b.z), EPI);
+          v.w = gemm_epilogue(
+              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 3], sa), w.w, b.w), EPI);
+        } else {
+          v.x = gemm_epilogue(acc[j][i][q * 4 + 0] + b.x, EPI);
+          v.y = gemm_epilogue(acc[j][i][q * 4 + 1] + b.y, EPI);
+          v.z = gemm_epilogue(acc[j][i][q * 4 + 2] + b.z, EPI);
+          v.w = gemm_epilogue(acc[j][i][q * 4 + 3] + b.w, EPI);
+        }
+        *(float4 *)(stg + li * STG_ROWB + (q * 8 + g * 4) * 4) = v;
+      }
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = r * 8 + (lane >> 3), c4 = (lane & 7) * 4;
+        float4 x = *(const float4 *)(stg + row * STG_ROWB + c4 * 4);
+        const int grow = rbase + row, gcol = n0 + cl + c4;
+        if (grow < M && gcol < N) {
+          x.x += rcur[r].x;
+          x.y += rcur[r].y;
+          x.z += rcur[r].z;
+          x.w += rcur[r].w;
+          *(float4 *)((float *)C + (int64_t)grow * ldc + gcol) = x;
+        }
+      }
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rcur[r] = rnext[r];
+    }
+  };
+
   // The epilogue of this block's ti-th tile.
   auto epilogue = [&](int ti) {
     if constexpr (CBF && !RES) {
       epilogue_bf(ti);
+      return;
+    }
+    if constexpr (RES && !CBF) {
+      epilogue_res(ti);
       return;
     }
     int m0, n0;
