@@ -1,10 +1,10 @@
 // k_attn.hip -- fused masked attention on gfx950 MFMA: QK^T, additive-mask
 // softmax and PV in one pass per (sequence, head, 128-query tile); the score
 // matrix never reaches HBM. Two kernels share the design below: attn_dma_k
-// (head_dim 64: K, V and the mask reach LDS by direct loads through a ring of
-// slots, and V^T is read with the transposing ds_read_b64_tr_b16) and
-// attn_fwd_k (head_dim 32, or a qkv too long for 32-bit row offsets: K and V
-// staged through registers, V transposed on the way into LDS).
+// (K, V and the mask reach LDS by direct loads through a ring of slots, and
+// V^T is read with the transposing ds_read_b64_tr_b16) and attn_fwd_k (a qkv
+// too long for 32-bit row offsets: K and V staged through registers, V
+// transposed on the way into LDS).
 //
 // Each of the 4 waves owns 32 queries and computes the TRANSPOSED score tile
 // S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (keys on rows, queries on
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
 }
 
 
-// ---- head_dim 64: K, V and the mask through a ring of LDS slots ----------------
+// ---- K, V and the mask through a ring of LDS slots ------------------------------
 //
 // The same block and wave roles and the same softmax as attn_fwd_k, with the
 // key tiles staged differently: K, V and the tile's mask row go global -> LDS
@@ -296,13 +296,15 @@ __global__ __launch_bounds__(256, 3) void attn_fwd_k(const uint16_t *__restrict_
 // element j % 4 of group lane 4e + j / 4's 8 bytes, e = 0..3). No registers
 // hold K or V in flight and no VALU transposes them.
 //
-// LDS rows are 128 bytes (64 bf16); 16-byte chunk c of row r is stored at
-// c ^ ((r >> 1) & 7) for K (sixteen ds_read_b128 rows r..r+15 hit sixteen
-// bank groups) and at c ^ ((r & 2) << 1) for V (the 32 lanes of a
-// ds_read_b64_tr_b16 phase read rows k0..k0+3 of two 16-column groups: row
-// parity picks a 32-bank half, the XOR separates rows k0 and k0 + 2). Rows
-// past the sequence's last are fetched from that last row (in bounds) and
-// carry probability 0.
+// LDS rows are head_dim bf16: 128 bytes (head_dim 64) or 64 bytes (32).
+// 16-byte chunk c of K row r is stored at c ^ ((r >> 1) & 7) (128-byte rows)
+// or c ^ ((r >> 2) & 3) (64-byte rows), so sixteen ds_read_b128 rows r..r+15
+// hit sixteen bank groups. V chunks of 128-byte rows are stored at
+// c ^ ((r & 2) << 1): the 32 lanes of a ds_read_b64_tr_b16 phase read rows
+// k0..k0+3 of two 16-column groups, row parity picks a 32-bank half and the
+// XOR separates rows k0 and k0 + 2; 64-byte rows k0..k0+3 already start in
+// four different 16-bank quarters. Rows past the sequence's last are fetched
+// from that last row (in bounds) and carry probability 0.
 constexpr int NSL = 3;
 
 __device__ __forceinline__ void dma16o(uint64_t base, uint32_t voff, uint32_t lds) {
@@ -327,6 +329,7 @@ __device__ __forceinline__ void vm_wait() {
 
 typedef short v4s __attribute__((ext_vector_type(4)));
 
+template <int HD>
 __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict__ qkv,
                                                    int64_t ldq, int S, int H, float scale_log2e,
                                                    const float *__restrict__ add_mask,
@@ -335,9 +338,13 @@ __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict_
                                                    int n_qblk, int force_logits,
                                                    const int32_t *__restrict__ seq_start,
                                                    const int32_t *__restrict__ order) {
-  constexpr int HD = 64, NKK = HD / 16, NHT = HD / 32;
-  constexpr int ROWB = HD * 2, TILE = BKV * ROWB;  // 128-byte rows, 8 KB per operand tile
+  constexpr int NKK = HD / 16, NHT = HD / 32;
+  constexpr int ROWB = HD * 2, TILE = BKV * ROWB;  // bytes per row and per operand tile
   constexpr int SLOT = 2 * TILE + BKV * 4;         // K, V, mask row
+  constexpr int CPR = ROWB / 16, PR = 1024 / ROWB;  // chunks per row, rows per 1 KB piece
+  constexpr int NP = TILE / 1024 / 4;               // pieces per wave and operand (2 or 1)
+  constexpr int LOADS = 2 * NP;                     // this wave's K and V loads per tile
+  static_assert(HD == 64 || HD == 32, "head_dim 64 or 32");
   __shared__ __attribute__((aligned(1024))) uint8_t sm[NSL * SLOT];
 
   const int blk = blockIdx.x;
@@ -374,7 +381,8 @@ __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict_
     if (q < lim) v = *(const uint4 *)(base + (int64_t)q * ldq + h * HD + kk * 16 + g * 8);
     qf[kk] = __builtin_bit_cast(bf16x8, v);
   }
-  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]));
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) asm volatile("" ::"v"(qf[kk]));
 
   // Key tile t -> slot t % NSL: wave w moves K rows and V rows 8p .. 8p + 7
   // for pieces p = w and w + 4 (1 KB each: lane l fills row 8p + l / 8,
@@ -384,18 +392,20 @@ __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict_
   const uint64_t mb64 = add_mask ? uni64((uint64_t)(uintptr_t)(add_mask + (int64_t)b * S)) : 0;
   const uint32_t lds0 = (uint32_t)(uintptr_t)sm;
   const uint32_t rowbytes = (uint32_t)(ldq * 2);
-  const int prow = lane >> 3, ppos = lane & 7;
+  const int prow = lane / CPR, ppos = lane % CPR;
+  auto swz_k = [](int r) { return HD == 64 ? (r >> 1) & 7 : (r >> 2) & 3; };
+  auto swz_v = [](int r) { return HD == 64 ? (r & 2) << 1 : 0; };
   auto issue = [&](int t) {
     const uint32_t slot = lds0 + (uint32_t)((t % NSL) * SLOT);
 #pragma unroll
-    for (int x = 0; x < 2; ++x) {
+    for (int x = 0; x < NP; ++x) {
       const int p = wave + 4 * x;
-      const int row = p * 8 + prow;
+      const int row = p * PR + prow;
       int key = t * BKV + row;
       key = key < lim ? key : lim - 1;
       const uint32_t roff = (uint32_t)key * rowbytes;
-      dma16o(kb64, roff + (uint32_t)((ppos ^ ((row >> 1) & 7)) * 16), slot + p * 1024);
-      dma16o(vb64, roff + (uint32_t)((ppos ^ ((row & 2) << 1)) * 16), slot + TILE + p * 1024);
+      dma16o(kb64, roff + (uint32_t)((ppos ^ swz_k(row)) * 16), slot + p * 1024);
+      dma16o(vb64, roff + (uint32_t)((ppos ^ swz_v(row)) * 16), slot + TILE + p * 1024);
     }
     if (wave == 0 && add_mask) {
       int key = t * BKV + lane;
@@ -409,9 +419,9 @@ __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict_
   auto wait_next = [&](bool one_more_in_flight) {
     if (one_more_in_flight) {
       if (mwave)
-        vm_wait<5>();
+        vm_wait<LOADS + 1>();
       else
-        vm_wait<4>();
+        vm_wait<LOADS>();
     } else {
       vm_wait<0>();
     }
@@ -426,9 +436,10 @@ __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict_
 
   // Fixed per-lane LDS offsets: K fragment rows sub * 32 + li, chunk 2kk + g;
   // the V^T transposed reads (group G = lane / 16, e, qq below).
-  const int swk = (li >> 1) & 7;
+  const int swk = swz_k(li);  // rows sub * 32 + li share li's swizzle
   const int G = lane >> 4, e4 = (lane & 15) >> 2, qq = lane & 3;
-  const int swv = ((e4 >> 1) & 1);  // (row & 2) << 1 with row = 16ch + 4(G >> 1) + e4, as 0/1
+  // swz_v(16ch + 4(G >> 1) + e4) = swz_v(e4), as a multiple of 4 chunks
+  const int swv = swz_v(e4) >> 2;
   const int vrow = 4 * (G >> 1) + e4;
 
   const int ntile = (kvl + BKV - 1) / BKV;
@@ -558,10 +569,17 @@ hipError_t attention(const AttnArgs &a, hipStream_t s) {
   const int64_t blocks = a.B * a.H * n_qblk;
   const float sl2e = a.scale * 1.4426950408889634f;
   const int force_logits = a.scale > 0.0f ? 0 : 1;  // raw-score max needs scale > 0
-  if (a.hd == 64 && (int64_t)a.S * a.ld_qkv * 2 < ((int64_t)1 << 31))
-    attn_dma_k<<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
-                                               a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
-                                               force_logits, a.seq_start, a.order);
+  // The direct-load kernel addresses K/V rows by 32-bit byte offsets from the
+  // sequence's first row.
+  const bool off32 = (int64_t)a.S * a.ld_qkv * 2 < ((int64_t)1 << 31);
+  if (a.hd == 64 && off32)
+    attn_dma_k<64><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
+                                                   a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
+                                                   force_logits, a.seq_start, a.order);
+  else if (a.hd == 32 && off32)
+    attn_dma_k<32><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
+                                                   a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
+                                                   force_logits, a.seq_start, a.order);
   else if (a.hd == 64)
     attn_fwd_k<64><<<(unsigned)blocks, 256, 0, s>>>(a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e,
                                                    a.add_mask, a.kv_len, a.ctx, a.ld_ctx, n_qblk,
