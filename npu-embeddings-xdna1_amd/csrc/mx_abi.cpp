@@ -165,6 +165,9 @@ int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t
     return fail(MX_E_INVALID, "attention: qkv row stride " + std::to_string(ld_qkv) +
                                   " cannot hold Q|K|V of " + std::to_string(H * hd) +
                                   " each, or is not a multiple of 8");
+  if (ld_qkv >= ((int64_t)1 << 24))
+    return fail(MX_E_UNSUPPORTED, "attention: qkv row stride " + std::to_string(ld_qkv) +
+                                      " (a 64-key tile is addressed by 32-bit offsets: < 2^24)");
   if (ld_ctx < H * hd || ld_ctx % 4)
     return fail(MX_E_INVALID, "attention: ctx row stride too small or not a multiple of 4");
   if (!aligned(qkv, 16) || !aligned(ctx, 8))
