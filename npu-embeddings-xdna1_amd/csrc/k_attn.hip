@@ -203,11 +203,17 @@ __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict_
     if (t + 2 < ntile) issue(t + 2);
     const uint8_t *sl = sm + (t % NSL) * SLOT;
     if (live) {
+      // The tile's second 32 keys all at or past kv_len (the last tile of a
+      // sequence whose length is <= 32 past a multiple of 64): their scores,
+      // probabilities and PV products are skipped -- each would be exp2(-inf)
+      // = 0.
+      const bool h1 = t * BKV + 32 < kvl;
       f32x16 sc[2];
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[sub][r] = 0.0f;
+        if (sub == 1 && !h1) continue;
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
           const bf16x8 kf = *(const bf16x8 *)(sl + (sub * 32 + li) * ROWB +
@@ -223,7 +229,8 @@ __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict_
       float mx = -INFINITY, cc;
       if (masked) {
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
+        for (int sub = 0; sub < 2; ++sub) {
+          if (sub == 1 && !h1) continue;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = sub * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
@@ -234,6 +241,7 @@ __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict_
             sc[sub][r] = v;
             mx = fmaxf(mx, v);
           }
+        }
         cc = 1.0f;
       } else {
 #pragma unroll
@@ -258,6 +266,7 @@ __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict_
 #pragma unroll
       for (int ch = 0; ch < 4; ++ch) {
         const int sub = ch >> 1, c = ch & 1;
+        if (sub == 1 && !h1) continue;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
           const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[sub][c * 8 + jj], cc, -m_run));
@@ -274,6 +283,7 @@ __global__ __launch_bounds__(256, 3) void attn_dma_k(const uint16_t *__restrict_
       const uint8_t *vs = sl + TILE;
 #pragma unroll
       for (int ch = 0; ch < 4; ++ch) {
+        if (ch >= 2 && !h1) continue;
 #pragma unroll
         for (int ht = 0; ht < NHT; ++ht) {
           const int chunk = ((4 * ht) ^ (4 * swv)) + 2 * (G & 1) + (qq >> 1);
