@@ -184,9 +184,11 @@ enum GemmPath {
   PATH_LDS_256x256_DEEP
 };
 
-// The 256 x 256 tile on 128-byte slabs: a bf16 C without a residual, K a
-// multiple of 64.
-bool deep_ok(const GemmArgs &a) { return a.c_bf16 && !a.residual && a.K % 64 == 0; }
+// The 256 x 256 tile on 128-byte slabs: a bf16 C without a residual or an
+// fp32 C with one, K a multiple of 64.
+bool deep_ok(const GemmArgs &a) {
+  return ((a.c_bf16 && !a.residual) || (!a.c_bf16 && a.residual)) && a.K % 64 == 0;
+}
 
 bool lds_path_ok(const GemmArgs &a) {
   const uintptr_t c = (uintptr_t)a.C;

@@ -22,7 +22,7 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_i8_k(
 
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, int OUT, int RB = 64>
 hipError_t launch_t(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, true, OUT == 1 && !RES, RB>;
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, true, stg_kind(OUT == 1, RES), RB>;
   auto kern = gemm_i8_k<BM, BN, WGM, WGN, NS, EPI, RES, OUT, RB>;
   static bool attr_set = false;
   if (!attr_set) {
@@ -58,20 +58,25 @@ hipError_t launch(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
 }
 
 // The 256 x 256 tile on 128-byte slabs (128 int8 of K, two slots): a bf16 C
-// without a residual only.
+// without a residual.
 hipError_t launch_deep(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
-  switch (a.epilogue) {
-    case 0: return launch_t<256, 256, 4, 2, 2, 0, false, 1, 128>(a, grid, s);
-    case 1: return launch_t<256, 256, 4, 2, 2, 1, false, 1, 128>(a, grid, s);
-    case 2: return launch_t<256, 256, 4, 2, 2, 2, false, 1, 128>(a, grid, s);
-    default: return hipErrorInvalidValue;
+  if (a.c_dtype == 1 && !a.residual) {
+    switch (a.epilogue) {
+      case 0: return launch_t<256, 256, 4, 2, 2, 0, false, 1, 128>(a, grid, s);
+      case 1: return launch_t<256, 256, 4, 2, 2, 1, false, 1, 128>(a, grid, s);
+      case 2: return launch_t<256, 256, 4, 2, 2, 2, false, 1, 128>(a, grid, s);
+      default: return hipErrorInvalidValue;
+    }
   }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
 
 namespace mxk {
 
+// (An fp32 C with a residual stays on 64-byte slabs on this datapath: with the
+// dequantisation vectors its 128-byte-slab form spills registers.)
 bool gemm_i8_deep(const GemmI8Args &a) {
   return a.c_dtype == 1 && !a.residual && a.K % 128 == 0 && a.K >= 256;
 }

@@ -1,7 +1,8 @@
 // k_gemm_lds.hip -- the bf16 instantiations of the persistent LDS-pipelined
 // GEMM (the kernel body and its design are in k_gemm_lds.hpp): 64-byte slabs
 // (32 K) for every tile and epilogue, and the 256 x 256 tile with 128-byte
-// slabs (64 K, two slots) for a bf16 C without a residual.
+// slabs (64 K, two slots) for a bf16 C without a residual or an fp32 C with
+// one.
 #include "k_gemm_lds.hpp"
 
 using namespace mxlds;
@@ -24,7 +25,7 @@ namespace mxk {
 
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF, int RB = 64>
 hipError_t gemm_lds_launch_t(const GemmArgs &a, int grid, hipStream_t s) {
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, false, CBF && !RES, RB>;
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, false, stg_kind(CBF, RES), RB>;
   auto kern = gemm_lds_k<BM, BN, WGM, WGN, NS, EPI, RES, CBF, RB>;
   static bool attr_set = false;
   if (!attr_set) {
@@ -61,16 +62,27 @@ hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-// The 256 x 256 tile on 128-byte slabs: a bf16 C without a residual only
-// (the packed-bf16 staging is what leaves LDS room for two 64 KB slots).
+// The 256 x 256 tile on 128-byte slabs: a bf16 C without a residual or an
+// fp32 C with one (their compact staging is what leaves LDS room for two 64 KB
+// slots).
 hipError_t gemm_lds_deep_launch(const GemmArgs &a, int grid, hipStream_t s) {
-  if (!a.c_bf16 || a.residual) return hipErrorInvalidValue;
-  switch (a.epilogue) {
-    case 0: return gemm_lds_launch_t<256, 256, 4, 2, 2, 0, false, true, 128>(a, grid, s);
-    case 1: return gemm_lds_launch_t<256, 256, 4, 2, 2, 1, false, true, 128>(a, grid, s);
-    case 2: return gemm_lds_launch_t<256, 256, 4, 2, 2, 2, false, true, 128>(a, grid, s);
-    default: return hipErrorInvalidValue;
+  if (a.c_bf16 && !a.residual) {
+    switch (a.epilogue) {
+      case 0: return gemm_lds_launch_t<256, 256, 4, 2, 2, 0, false, true, 128>(a, grid, s);
+      case 1: return gemm_lds_launch_t<256, 256, 4, 2, 2, 1, false, true, 128>(a, grid, s);
+      case 2: return gemm_lds_launch_t<256, 256, 4, 2, 2, 2, false, true, 128>(a, grid, s);
+      default: return hipErrorInvalidValue;
+    }
   }
+  if (!a.c_bf16 && a.residual) {
+    switch (a.epilogue) {
+      case 0: return gemm_lds_launch_t<256, 256, 4, 2, 2, 0, true, false, 128>(a, grid, s);
+      case 1: return gemm_lds_launch_t<256, 256, 4, 2, 2, 1, true, false, 128>(a, grid, s);
+      case 2: return gemm_lds_launch_t<256, 256, 4, 2, 2, 2, true, false, 128>(a, grid, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  return hipErrorInvalidValue;
 }
 
 template hipError_t gemm_lds_launch<256, 256, 2, 4, 3>(const GemmArgs &, int, hipStream_t);

@@ -95,10 +95,13 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int STG_ROWB = 144;  // staging row: 32 fp32 + 16 bytes of padding
 
-// SBF: the epilogue stages packed bf16 (a bf16 C without a residual), 2 KB per
-// wave; otherwise fp32 rows, 4.5 KB per wave. RB: bytes of K per slab row, 64
-// or 128.
-template <int BM, int BN, int WGM, int WGN, int NS, bool I8, bool SBF, int RB = 64>
+// The epilogue's staging per wave (stg_kind): 1 packed bf16 32-row blocks (a
+// bf16 C without a residual), 2 KB; 2 fp32 16-row half blocks (an fp32 C with
+// a residual), 2.25 KB; 0 fp32 32-row blocks (the rest), 4.5 KB. RB: bytes of
+// K per slab row, 64 or 128.
+constexpr int stg_kind(bool cbf, bool res) { return cbf && !res ? 1 : (res && !cbf ? 2 : 0); }
+
+template <int BM, int BN, int WGM, int WGN, int NS, bool I8, int STG, int RB = 64>
 struct LdsCfg {
   static constexpr int NW = WGM * WGN;                // waves
   static constexpr int NT = NW * 64;                  // threads
@@ -119,7 +122,7 @@ struct LdsCfg {
   static constexpr int NHI = PIECES % NW == 0 ? NW : PIECES % NW;
   static constexpr int BIAS_PER_WAVE = BN / NW;        // floats each wave's bias piece moves
   static constexpr int ROWS_PER_WAVE = BM / NW;        // a_scale rows each wave moves
-  static constexpr int STG_WAVE = SBF ? 32 * 64 : 32 * STG_ROWB;
+  static constexpr int STG_WAVE = STG == 1 ? 32 * 64 : (STG == 2 ? 16 : 32) * STG_ROWB;
   static constexpr int STG_OFF = NS * SLOT;
   static constexpr int BIAS_OFF = STG_OFF + NW * STG_WAVE;
   static constexpr int WS_OFF = BIAS_OFF + 2 * BN * 4;  // int8: wscale, two parities
@@ -233,7 +236,7 @@ __device__ __forceinline__ void gemm_lds_body(
     int tiles_n, const float *__restrict__ a_scale, const float *__restrict__ wscale,
     uint8_t *smem) {
   constexpr bool STG_BF = CBF && !RES;
-  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, I8, STG_BF, RB>;
+  using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, I8, stg_kind(CBF, RES), RB>;
   using PT = Path<I8>;
   typedef typename PT::frag frag_t;
   typedef typename PT::acc acc_t;
@@ -505,12 +508,13 @@ __device__ __forceinline__ void gemm_lds_body(
   };
 
   // The epilogue of an fp32 C with a residual (C = epi(A W + b) + R, R may be
-  // C itself), block by block (k = i * TN + j): block k + 1's residual rows
-  // are loaded while block k goes through the bias (dequantisation), the
-  // activation and the fp32 staging, so the loads' latency is paid once per
-  // tile instead of once per block. Rows of different blocks are disjoint, so
-  // loading block k + 1's residual before storing block k is exact also in
-  // place.
+  // C itself), block by block (k = i * TN + j), each block staged as two
+  // 16-row halves (2.25 KB per wave, which leaves LDS for two 64 KB slots):
+  // block k + 1's residual rows are loaded while block k goes through the
+  // bias (dequantisation), the activation and the staging, so the loads'
+  // latency is paid once per tile instead of once per block. Rows of
+  // different blocks are disjoint, so loading block k + 1's residual before
+  // storing block k is exact also in place.
   auto epilogue_res = [&](int ti) {
     int m0, n0;
     tile_origin(ti, m0, n0);
@@ -518,17 +522,22 @@ __device__ __forceinline__ void gemm_lds_body(
     const float *wsl = (const float *)(smem + Cfg::WS_OFF + (ti & 1) * BN * 4);
     const float *sal = (const float *)(smem + Cfg::SA_OFF + (ti & 1) * BM * 4);
     uint8_t *stg = smem + Cfg::STG_OFF + wave * Cfg::STG_WAVE;
-    // Lane l handles 4 columns (l % 8) * 4 of rows r * 8 + l / 8, r = 0..3.
+    // Half h of a block: lane l reads (and stores) row 16h + l / 4, columns
+    // (l % 4) * 8 + 4 * part .. + 3, part = 0, 1.
     auto load_res = [&](int k, float4 *rv) {
       const int i = k / TN, j = k % TN;
       const int rbase = m0 + wm * Cfg::WM + i * 32;
       const int cl = wn * Cfg::WN + j * 32;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int grow = rbase + r * 8 + (lane >> 3), gcol = n0 + cl + (lane & 7) * 4;
-        rv[r] = grow < M && gcol < N ? *(const float4 *)(residual + (int64_t)grow * ldc + gcol)
-                                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      }
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          const int grow = rbase + h * 16 + (lane >> 2);
+          const int gcol = n0 + cl + (lane & 3) * 8 + part * 4;
+          rv[h * 2 + part] = grow < M && gcol < N
+                                 ? *(const float4 *)(residual + (int64_t)grow * ldc + gcol)
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
     };
     float4 rcur[4], rnext[4];
     load_res(0, rcur);
@@ -539,6 +548,7 @@ __device__ __forceinline__ void gemm_lds_body(
       const int rbase = m0 + wm * Cfg::WM + i * 32;
       const int cl = wn * Cfg::WN + j * 32;
       const float sa = I8 ? sal[wm * Cfg::WM + i * 32 + li] : 0.0f;
+      float4 vq[4];  // columns 8q + 4g .. + 3 of row li
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float4 b = has_bias ? *(const float4 *)(bl + cl + q * 8 + g * 4)
@@ -560,23 +570,32 @@ __device__ __forceinline__ void gemm_lds_body(
           v.z = gemm_epilogue(acc[j][i][q * 4 + 2] + b.z, EPI);
           v.w = gemm_epilogue(acc[j][i][q * 4 + 3] + b.w, EPI);
         }
-        *(float4 *)(stg + li * STG_ROWB + (q * 8 + g * 4) * 4) = v;
+        vq[q] = v;
       }
-      asm volatile("" ::: "memory");
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = r * 8 + (lane >> 3), c4 = (lane & 7) * 4;
-        float4 x = *(const float4 *)(stg + row * STG_ROWB + c4 * 4);
-        const int grow = rbase + row, gcol = n0 + cl + c4;
-        if (grow < M && gcol < N) {
-          x.x += rcur[r].x;
-          x.y += rcur[r].y;
-          x.z += rcur[r].z;
-          x.w += rcur[r].w;
-          *(float4 *)((float *)C + (int64_t)grow * ldc + gcol) = x;
+      for (int h = 0; h < 2; ++h) {
+        if ((li >> 4) == h) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *(float4 *)(stg + (li & 15) * STG_ROWB + (q * 8 + g * 4) * 4) = vq[q];
         }
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          const int row = lane >> 2, c4 = (lane & 3) * 8 + part * 4;
+          float4 x = *(const float4 *)(stg + row * STG_ROWB + c4 * 4);
+          const int grow = rbase + h * 16 + row, gcol = n0 + cl + c4;
+          if (grow < M && gcol < N) {
+            const float4 r = rcur[h * 2 + part];
+            x.x += r.x;
+            x.y += r.y;
+            x.z += r.z;
+            x.w += r.w;
+            *(float4 *)((float *)C + (int64_t)grow * ldc + gcol) = x;
+          }
+        }
+        asm volatile("" ::: "memory");
       }
-      asm volatile("" ::: "memory");
 #pragma unroll
       for (int r = 0; r < 4; ++r) rcur[r] = rnext[r];
     }

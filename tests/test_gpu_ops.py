@@ -312,6 +312,10 @@ GEMM_PATHS = [
     (17455, 3072, 768, mxenc.MX_EPI_NONE, np.uint16, False, "lds_256x256x64"),  # FFN-down
     (8000, 1024, 2000, mxenc.MX_EPI_GELU_ERF, np.uint16, False, "lds_256x256x64"),  # ragged
     (8000, 192, 2048, mxenc.MX_EPI_GELU_POLY, np.uint16, False, "lds_256x256x64"),  # 3 slabs
+    # ... and an fp32 C with a residual (the pre-LN stacks; half-block staging)
+    (50432, 768, 768, mxenc.MX_EPI_NONE, np.float32, True, "lds_256x256x64"),  # ViT attn-out
+    (12000, 5120, 1280, mxenc.MX_EPI_NONE, np.float32, True, "lds_256x256x64"),  # Whisper down
+    (8000, 1024, 2000, mxenc.MX_EPI_GELU_POLY, np.float32, True, "lds_256x256x64"),  # ragged
 ]
 
 
