@@ -132,6 +132,9 @@ def main():
     ap.add_argument("--int8", action="store_true",
                     help="the W8A8 datapath (BERT configs): int8 operands by the packer's "
                          "scheme over the same random weights")
+    ap.add_argument("--no-fusion", action="store_true",
+                    help="gated-FFN configs: FFN-up then the separate gated pass, instead of "
+                         "the activation fused into FFN-up's epilogue")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=16)
     ap.add_argument("--calibrate", action="store_true",
@@ -182,6 +185,7 @@ def main():
             lane_enc.append(enc.clone(c))
         for c, e in zip(lane_ctx, lane_enc):
             e.set_packing(packing)
+            e.set_fusion(not args.no_fusion)
             d_ids, d_am = c.put(ids), c.put(am)
             out = c.empty((B, m["hidden"]), np.float32)
             lane_step.append(lambda e=e, d_ids=d_ids, d_am=d_am, out=out:

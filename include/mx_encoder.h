@@ -415,6 +415,14 @@ int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids,
  * per batch. mx_encoder_run always computes every row (it returns them all). */
 int mx_encoder_set_packing(mx_encoder *enc, int on);
 
+/* The gated FFN (swiglu_cpu, bert_encoder.cpp:582-627) fused into FFN-up's
+ * GEMM epilogue (on by default): FFN-up's operand is kept a second time with
+ * its lo and hi rows interleaved, and the GEMM writes lo * act(hi) directly,
+ * the [M, 2f] intermediate never reaching memory. The output is the unfused
+ * GEMM-then-glu pair's, bit for bit; off runs that pair. No counterpart in
+ * the reference, whose host path runs the two steps. */
+int mx_encoder_set_fusion(mx_encoder *enc, int on);
+
 /* VitEncoder::run + head_matvec (runtime/src/vit/encoder.cpp:222-431,
  * runtime/src/vit/head.cpp:16-49), every step on the GPU: pixels fp32
  * [B, 3, image, image] (device) -> im2col patch rows (c, ky, kx order) -> patch

@@ -202,7 +202,8 @@ GemmPath pick(const GemmArgs &a) {
   static const GemmPath paths[] = {PATH_LDS_256x256, PATH_LDS_256x192, PATH_LDS_128x256,
                                    PATH_LDS_128x128};
   const bool deep = deep_ok(a);
-  const int t = gemm_lds_tile(a.M, a.N, deep);
+  int t = gemm_lds_tile(a.M, a.N, deep);
+  if (t == 1 && a.epilogue >= EPI_GLU_SILU) t = 0;  // 96-column waves cannot pair blocks
   return t == 0 && deep ? PATH_LDS_256x256_DEEP : paths[t];
 }
 
@@ -300,7 +301,10 @@ const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
 }
 
 hipError_t gemm(const GemmArgs &a, hipStream_t s) {
-  switch (pick(a)) {
+  const GemmPath p = pick(a);
+  // The fused gated FFN exists only on the LDS-pipelined kernel.
+  if (a.epilogue >= EPI_GLU_SILU && (p == PATH_STAGED || a.N % 64)) return hipErrorInvalidValue;
+  switch (p) {
     case PATH_LDS_256x256_DEEP: return gemm_lds_deep_launch(a, cu_count(), s);
     case PATH_LDS_256x256: return gemm_lds_launch<256, 256, 2, 4, 3>(a, cu_count(), s);
     case PATH_LDS_256x192: return gemm_lds_launch<256, 192, 4, 2, 4>(a, cu_count(), s);

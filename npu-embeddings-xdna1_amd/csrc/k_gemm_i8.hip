@@ -42,6 +42,18 @@ hipError_t launch_t(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
 template <int BM, int BN, int WGM, int WGN, int NS>
 hipError_t launch(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
   if (a.c_dtype == 2) return launch_t<BM, BN, WGM, WGN, NS, 0, false, 2>(a, grid, s);
+  if (a.epilogue >= mxk::EPI_GLU_SILU) {
+    // The fused gated FFN pairs a wave's column blocks: an even number of
+    // them, a bf16 C.
+    if constexpr ((BN / WGN) % 64 == 0) {
+      if (a.c_dtype != 1 || a.residual) return hipErrorInvalidValue;
+      if (a.epilogue == mxk::EPI_GLU_SILU)
+        return launch_t<BM, BN, WGM, WGN, NS, mxk::EPI_GLU_SILU, false, 1>(a, grid, s);
+      if (a.epilogue == mxk::EPI_GLU_GELU)
+        return launch_t<BM, BN, WGM, WGN, NS, mxk::EPI_GLU_GELU, false, 1>(a, grid, s);
+    }
+    return hipErrorInvalidValue;
+  }
 #define MX_I8_EPI(E)                                                                 \
   if (a.epilogue == E) {                                                             \
     if (a.residual)                                                                  \
@@ -65,6 +77,10 @@ hipError_t launch_deep(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
       case 0: return launch_t<256, 256, 4, 2, 2, 0, false, 1, 128>(a, grid, s);
       case 1: return launch_t<256, 256, 4, 2, 2, 1, false, 1, 128>(a, grid, s);
       case 2: return launch_t<256, 256, 4, 2, 2, 2, false, 1, 128>(a, grid, s);
+      case mxk::EPI_GLU_SILU:
+        return launch_t<256, 256, 4, 2, 2, mxk::EPI_GLU_SILU, false, 1, 128>(a, grid, s);
+      case mxk::EPI_GLU_GELU:
+        return launch_t<256, 256, 4, 2, 2, mxk::EPI_GLU_GELU, false, 1, 128>(a, grid, s);
       default: return hipErrorInvalidValue;
     }
   }
@@ -84,7 +100,9 @@ bool gemm_i8_deep(const GemmI8Args &a) {
 hipError_t gemm_i8(const GemmI8Args &a, hipStream_t s) {
   const int grid = cu_count();
   const bool deep = gemm_i8_deep(a);
-  switch (gemm_lds_tile(a.M, a.N, deep)) {
+  int t = gemm_lds_tile(a.M, a.N, deep);
+  if (t == 1 && a.epilogue >= EPI_GLU_SILU) t = 0;  // 96-column waves cannot pair blocks
+  switch (t) {
     case 0: return deep ? launch_deep(a, grid, s) : launch<256, 256, 2, 4, 3>(a, grid, s);
     case 1: return launch<256, 192, 4, 2, 4>(a, grid, s);
     case 2: return launch<128, 256, 2, 4, 4>(a, grid, s);

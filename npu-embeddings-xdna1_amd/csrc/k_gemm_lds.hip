@@ -47,6 +47,18 @@ hipError_t gemm_lds_launch_t(const GemmArgs &a, int grid, hipStream_t s) {
 // (one per CU).
 template <int BM, int BN, int WGM, int WGN, int NS>
 hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s) {
+  if (a.epilogue >= EPI_GLU_SILU) {
+    // The fused gated FFN pairs a wave's column blocks: an even number of
+    // them, a bf16 C.
+    if constexpr ((BN / WGN) % 64 == 0) {
+      if (!a.c_bf16 || a.residual) return hipErrorInvalidValue;
+      if (a.epilogue == EPI_GLU_SILU)
+        return gemm_lds_launch_t<BM, BN, WGM, WGN, NS, EPI_GLU_SILU, false, true>(a, grid, s);
+      if (a.epilogue == EPI_GLU_GELU)
+        return gemm_lds_launch_t<BM, BN, WGM, WGN, NS, EPI_GLU_GELU, false, true>(a, grid, s);
+    }
+    return hipErrorInvalidValue;
+  }
 #define MX_LDS_EPI(E)                                                                        \
   if (a.epilogue == E) {                                                                     \
     if (a.residual)                                                                          \
@@ -62,15 +74,19 @@ hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-// The 256 x 256 tile on 128-byte slabs: a bf16 C without a residual or an
-// fp32 C with one (their compact staging is what leaves LDS room for two 64 KB
-// slots).
+// The 256 x 256 tile on 128-byte slabs: a bf16 C without a residual (the
+// fused gated FFN included) or an fp32 C with one (their compact staging is
+// what leaves LDS room for two 64 KB slots).
 hipError_t gemm_lds_deep_launch(const GemmArgs &a, int grid, hipStream_t s) {
   if (a.c_bf16 && !a.residual) {
     switch (a.epilogue) {
       case 0: return gemm_lds_launch_t<256, 256, 4, 2, 2, 0, false, true, 128>(a, grid, s);
       case 1: return gemm_lds_launch_t<256, 256, 4, 2, 2, 1, false, true, 128>(a, grid, s);
       case 2: return gemm_lds_launch_t<256, 256, 4, 2, 2, 2, false, true, 128>(a, grid, s);
+      case EPI_GLU_SILU:
+        return gemm_lds_launch_t<256, 256, 4, 2, 2, EPI_GLU_SILU, false, true, 128>(a, grid, s);
+      case EPI_GLU_GELU:
+        return gemm_lds_launch_t<256, 256, 4, 2, 2, EPI_GLU_GELU, false, true, 128>(a, grid, s);
       default: return hipErrorInvalidValue;
     }
   }

@@ -243,6 +243,13 @@ __device__ __forceinline__ void gemm_lds_body(
   static_assert(I8 || !RAW, "RAW is the int8 datapath's");
   static_assert(!RAW || (EPI == 0 && !RES && !CBF), "RAW stores the accumulators as they are");
   constexpr int TM = Cfg::TM, TN = Cfg::TN, ESZ = Cfg::ESZ;
+  // EPI 8 / 9: the gated FFN fused (GLU), C = lo * act(hi) in bf16 (act 1
+  // SiLU, 2 exact-erf GELU), Wt's rows interleaved in groups of 16 (8 lo, 8
+  // hi): each 32-column accumulator block gives 16 columns of C.
+  constexpr bool GLU = EPI >= 8;
+  constexpr int GACT = EPI - 7, EPA = GLU ? 0 : EPI;
+  static_assert(!GLU || (EPI <= 9 && CBF && !RES && !RAW), "GLU: bf16 C, no residual");
+  static_assert(!GLU || TN % 2 == 0, "GLU pairs a wave's column blocks");
   // The bf16 kernel always has a bias (the launcher routes others away); the
   // int8 kernel takes it as optional.
   const bool has_bias = !RAW && (!I8 || bias != nullptr);
@@ -441,57 +448,101 @@ __device__ __forceinline__ void gemm_lds_body(
     const float *wsl = (const float *)(smem + Cfg::WS_OFF + (ti & 1) * BN * 4);
     const float *sal = (const float *)(smem + Cfg::SA_OFF + (ti & 1) * BM * 4);
     uint8_t *stg = smem + Cfg::STG_OFF + wave * Cfg::STG_WAVE;
+    // C's columns per accumulator column (GLU: half).
+    constexpr int CD = GLU ? 2 : 1;
+    const int NC = N / CD;
     // Staging: lane (li, g) writes its 8 bytes of chunk q of row li at
     // position q ^ ((li >> 2) & 3); lane l reads chunk c = l & 3 of rows
-    // r * 16 + l / 4, 16 bytes each, and stores them.
+    // r * 16 + l / 4, 16 bytes each, and stores them. Block k covers C's
+    // columns [cl, cl + 32) of row block i (GLU: column blocks 2j and 2j + 1
+    // of the accumulators).
     auto store = [&](int k, const uint4 *w) {
       const int j = k / TM, i = k % TM;
       const int rbase = m0 + wm * Cfg::WM + i * 32;
-      const int cl = wn * Cfg::WN + j * 32;
+      const int cl = (n0 + wn * Cfg::WN) / CD + j * 32;
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const int row = r * 16 + (lane >> 2), c = lane & 3;
-        const int grow = rbase + row, gcol = n0 + cl + c * 8;
-        if (grow < M && gcol < N) {
+        const int grow = rbase + row, gcol = cl + c * 8;
+        if (grow < M && gcol < NC) {
           const int64_t off = (int64_t)grow * ldc + gcol;
-          if (gcol + 8 <= N)
+          if (gcol + 8 <= NC)
             *(uint4 *)((uint16_t *)C + off) = w[r];
           else  // N % 8 == 4: four columns left
             *(uint2 *)((uint16_t *)C + off) = make_uint2(w[r].x, w[r].y);
         }
       }
     };
+    // The epilogue's value of accumulator (j, i) element q * 4 + e: the bias
+    // (dequantisation) added, before the activation.
+    auto pre = [&](int j, int i, int q, int e, float bb, float ww, float sa) {
+      if (I8)
+        return __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + e], sa), ww, bb);
+      return (float)acc[j][i][q * 4 + e] + bb;
+    };
     float4 b[4], w[4];
     uint4 wv[2];
+    constexpr int NB = TM * TN / CD;  // staged blocks
 #pragma unroll
-    for (int k = 0; k < TM * TN; ++k) {
+    for (int k = 0; k < NB; ++k) {
       const int j = k / TM, i = k % TM;
-      if (i == 0) {
-        const int cl = wn * Cfg::WN + j * 32;  // tile-local first column
+      uint32_t pk[8];  // columns 8q + 4g + 2h, +1 of row li: pk[2q + h]
+      if constexpr (GLU) {
+        // Columns 16u + e (lo) and 16u + 8 + e (hi) of accumulator block
+        // 2j + jj give C's column 8(2jj + u) + e: each pair rounds to bf16 as
+        // the unfused GEMM's C does, then lo * act(hi) rounds once more.
+        const float sa = I8 ? sal[wm * Cfg::WM + i * 32 + li] : 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const int ja = 2 * j + jj;
+          const int cl = wn * Cfg::WN + ja * 32;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            b[q] = has_bias ? *(const float4 *)(bl + cl + q * 8 + g * 4)
+                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (I8) w[q] = *(const float4 *)(wsl + cl + q * 8 + g * 4);
+          }
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const float bl4[4] = {b[2 * u].x, b[2 * u].y, b[2 * u].z, b[2 * u].w};
+            const float bh4[4] = {b[2 * u + 1].x, b[2 * u + 1].y, b[2 * u + 1].z,
+                                  b[2 * u + 1].w};
+            const float wl4[4] = {w[2 * u].x, w[2 * u].y, w[2 * u].z, w[2 * u].w};
+            const float wh4[4] = {w[2 * u + 1].x, w[2 * u + 1].y, w[2 * u + 1].z,
+                                  w[2 * u + 1].w};
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t h = pack_bf2_hw(pre(ja, i, 2 * u, e, bl4[e], wl4[e], sa),
+                                             pre(ja, i, 2 * u + 1, e, bh4[e], wh4[e], sa));
+              o[e] = bf2f(h & 0xFFFFu) * glu_act<GACT>(bf2f(h >> 16));
+            }
+            pk[2 * (2 * jj + u)] = pack_bf2(o[0], o[1]);
+            pk[2 * (2 * jj + u) + 1] = pack_bf2(o[2], o[3]);
+          }
+        }
+      } else {
+        if (i == 0) {
+          const int cl = wn * Cfg::WN + j * 32;  // tile-local first column
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            b[q] = has_bias ? *(const float4 *)(bl + cl + q * 8 + g * 4)
+                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (I8) w[q] = *(const float4 *)(wsl + cl + q * 8 + g * 4);
+          }
+        }
+        const float sa = I8 ? sal[wm * Cfg::WM + i * 32 + li] : 0.0f;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          b[q] = has_bias ? *(const float4 *)(bl + cl + q * 8 + g * 4)
-                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          if (I8) w[q] = *(const float4 *)(wsl + cl + q * 8 + g * 4);
-        }
-      }
-      const float sa = I8 ? sal[wm * Cfg::WM + i * 32 + li] : 0.0f;
-      uint32_t pk[8];  // columns 8q + 4g + 2h, +1 of row li: pk[2q + h]
+          const float bb[4] = {b[q].x, b[q].y, b[q].z, b[q].w};
+          const float ww[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
+          float v[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float bb[4] = {b[q].x, b[q].y, b[q].z, b[q].w};
-        const float ww[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (I8)
-            v[e] = gemm_epilogue(
-                __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + e], sa), ww[e], bb[e]), EPI);
-          else
-            v[e] = gemm_epilogue((float)acc[j][i][q * 4 + e] + bb[e], EPI);
+          for (int e = 0; e < 4; ++e)
+            v[e] = gemm_epilogue(pre(j, i, q, e, bb[e], ww[e], sa), EPA);
+          pk[2 * q] = pack_bf2_hw(v[0], v[1]);
+          pk[2 * q + 1] = pack_bf2_hw(v[2], v[3]);
         }
-        pk[2 * q] = pack_bf2_hw(v[0], v[1]);
-        pk[2 * q + 1] = pack_bf2_hw(v[2], v[3]);
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -504,7 +555,7 @@ __device__ __forceinline__ void gemm_lds_body(
         wv[r] = *(const uint4 *)(stg + row * 64 + ((c ^ ((row >> 2) & 3)) * 16));
       }
     }
-    store(TM * TN - 1, wv);
+    store(NB - 1, wv);
   };
 
   // The epilogue of an fp32 C with a residual (C = epi(A W + b) + R, R may be
@@ -760,7 +811,7 @@ __device__ __forceinline__ void gemm_lds_body(
   // stalling the next tile on the previous one's write acknowledgements. An
   // edge tile (or a residual epilogue, whose loads the compiler waits on)
   // keeps the exact wait.
-  constexpr int EPI_STORES = RES ? 0 : (CBF ? 2 : 4) * TM * TN;
+  constexpr int EPI_STORES = RES ? 0 : (GLU ? 1 : CBF ? 2 : 4) * TM * TN;
   static_assert(Cfg::LOADS_HI * (NS - 2) + EPI_STORES < 64, "vmcnt holds at most 63");
   constexpr bool SAME_LOADS = Cfg::LOADS_HI == Cfg::LOADS_LO;
   int epi_left = 0;

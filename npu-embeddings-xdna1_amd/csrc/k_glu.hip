@@ -13,7 +13,10 @@
 // glu_k: swiglu_cpu (bert_encoder.cpp:582-627): FFN-up's [rows, 2f] output as
 // lo | hi halves -> [rows, f] = lo * act(hi), act SiLU with the host's
 // exp2 polynomial and -120 argument floor (x / (1 + 2^max(-x log2e, -120))),
-// or exact-erf GELU. Four consecutive outputs per thread.
+// or exact-erf GELU. Four consecutive outputs per thread. The encoder fuses
+// this pass into FFN-up's GEMM epilogue where it can (k_gemm_lds.hpp, GLU),
+// over FFN-up's operands put in glu_interleave_k's row order once; the
+// product and its roundings are the same (glu_act).
 #include "mx_common.hpp"
 #include "mx_kernels.hpp"
 
@@ -58,12 +61,6 @@ __global__ __launch_bounds__(256) void rope_qkv_k(uint16_t *__restrict__ qkv, in
   }
 }
 
-__device__ __forceinline__ float silu_host(float x) {
-  float a = -x * 1.4426950408889634f;
-  a = a < -120.0f ? -120.0f : a;
-  return x / (1.0f + exp2_poly(a));
-}
-
 __device__ __forceinline__ float4 load4(const void *p, bool bf, int64_t off) {
   if (bf) {
     const uint2 u = *(const uint2 *)((const uint16_t *)p + off);
@@ -81,17 +78,10 @@ __global__ __launch_bounds__(256) void glu_k(const void *__restrict__ in, void *
     const int64_t r = i / q4, j = (i - r * q4) * 4;
     const float4 lo = load4(in, IN_BF, r * 2 * f + j), hi = load4(in, IN_BF, r * 2 * f + f + j);
     float4 o;
-    if (ACT == 1) {
-      o.x = lo.x * silu_host(hi.x);
-      o.y = lo.y * silu_host(hi.y);
-      o.z = lo.z * silu_host(hi.z);
-      o.w = lo.w * silu_host(hi.w);
-    } else {
-      o.x = lo.x * gelu_erf(hi.x);
-      o.y = lo.y * gelu_erf(hi.y);
-      o.z = lo.z * gelu_erf(hi.z);
-      o.w = lo.w * gelu_erf(hi.w);
-    }
+    o.x = lo.x * glu_act<ACT>(hi.x);
+    o.y = lo.y * glu_act<ACT>(hi.y);
+    o.z = lo.z * glu_act<ACT>(hi.z);
+    o.w = lo.w * glu_act<ACT>(hi.w);
     const int64_t oo = r * f + j;
     if (OUT_BF)
       *(uint2 *)((uint16_t *)out + oo) = make_uint2(pack_bf2(o.x, o.y), pack_bf2(o.z, o.w));
@@ -100,9 +90,29 @@ __global__ __launch_bounds__(256) void glu_k(const void *__restrict__ in, void *
   }
 }
 
+// Row n of dst = row orig(n) of src, in groups of 16: the first 8 from the lo
+// half (rows 8G ..), the next 8 the matching rows of the hi half (f + 8G ..).
+// One block per row, 4-byte words.
+__global__ __launch_bounds__(256) void glu_interleave_k(const uint32_t *__restrict__ src,
+                                                        uint32_t *__restrict__ dst, int64_t f,
+                                                        int64_t words) {
+  const int64_t n = blockIdx.x, G = n >> 4, r = n & 15;
+  const int64_t orig = r < 8 ? 8 * G + r : f + 8 * G + (r - 8);
+  for (int64_t w = threadIdx.x; w < words; w += blockDim.x)
+    dst[n * words + w] = src[orig * words + w];
+}
+
 }  // namespace
 
 namespace mxk {
+
+hipError_t glu_interleave(const void *src, void *dst, int64_t f, int64_t row_bytes,
+                          hipStream_t s) {
+  if (f <= 0 || f % 8 || row_bytes <= 0 || row_bytes % 4) return hipErrorInvalidValue;
+  glu_interleave_k<<<(unsigned)(2 * f), 256, 0, s>>>((const uint32_t *)src, (uint32_t *)dst, f,
+                                                     row_bytes / 4);
+  return hipGetLastError();
+}
 
 hipError_t rope_qkv(uint16_t *qkv, int64_t ld, int64_t rows, int S, int H, int hd,
                     const float *cos_t, const float *sin_t, hipStream_t s,

@@ -94,6 +94,27 @@ __device__ __forceinline__ float exp2_poly(float x) {
   return p * __uint_as_float((uint32_t)(k + 127) << 23);
 }
 
+// swiglu_cpu's SiLU (bert_encoder.cpp:582-627): x / (1 + 2^max(-x log2e,
+// -120)) with the exp2 polynomial above, each operation rounded on its own as
+// the host's AVX2 form is (no multiply-add contraction of the polynomial's
+// last product into the 1 + ...).
+__device__ __forceinline__ float silu_host(float x) {
+#pragma clang fp contract(off)
+  float a = -x * 1.4426950408889634f;
+  a = a < -120.0f ? -120.0f : a;
+  return x / (1.0f + exp2_poly(a));
+}
+
+// The gated FFN's activation of the gate half: 1 SiLU, 2 exact-erf GELU.
+// Contraction is off here too, so the GELU form rounds alike wherever it is
+// inlined (the gated-FFN pass and the GEMM epilogue that fuses it).
+template <int ACT>
+__device__ __forceinline__ float glu_act(float hi) {
+#pragma clang fp contract(off)
+  if (ACT == 1) return silu_host(hi);
+  return 0.5f * hi * (1.0f + erff(hi * 0.70710678118654752440f));
+}
+
 // The AIE exp2_poly (kernels/exp2_poly.h:35-65): the same table, each Horner
 // step a rounded multiply then a rounded add (no FMA).
 __device__ __forceinline__ float exp2_poly_aie(float x) {

@@ -52,6 +52,13 @@ struct LayerW {
   int8_t *wq[4] = {nullptr, nullptr, nullptr, nullptr};
   float *ws[4] = {nullptr, nullptr, nullptr, nullptr};
   float *ias[4] = {nullptr, nullptr, nullptr, nullptr};
+  // The gated FFN fused into FFN-up's epilogue: FFN-up's operand (bf16 or
+  // int8), bias and wscale with their 2f rows in glu_interleave's order,
+  // built from the tensors of weight generation glu_gen.
+  uint16_t *wg = nullptr;
+  int8_t *wqg = nullptr;
+  float *bg = nullptr, *wsg = nullptr;
+  uint64_t glu_gen = 0;
 };
 
 enum Cat { CAT_GEMM = 0, CAT_ATTN = 1, CAT_LN = 2, CAT_OTHER = 3 };
@@ -64,6 +71,10 @@ struct mx_encoder {
   mx_ctx *ctx = nullptr;
   mx_encoder_desc desc{};
   bool owns_weights = true;  // false for a lane clone, which borrows its parent's
+  // Bumped by every tensor set: the fused gated FFN's interleaved copies are
+  // current while their glu_gen equals it.
+  uint64_t wgen = 1;
+  bool fuse_glu = true;  // the gated FFN in FFN-up's epilogue where it can run
   std::vector<LayerW> layers;
   float *emb_ln[2] = {nullptr, nullptr};
   float *fin_ln[2] = {nullptr, nullptr};
@@ -304,6 +315,80 @@ int glu_l(mx_encoder *enc, mx_stream *s, int64_t M) {
                      enc->desc.gated_ffn);
 }
 
+// Whether FFN-up can carry the gated FFN in its epilogue: whole 64-row
+// groups of the interleaved operand (f % 32 == 0) on the LDS-pipelined kernel
+// (bf16: K a multiple of 32, at least 128; the int8 GEMM always is).
+bool glu_fusable(const mx_encoder *enc) {
+  const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
+  return enc->desc.gated_ffn != MX_GATED_NONE && f % 32 == 0 &&
+         (enc->i8 || (d % 32 == 0 && d >= 128));
+}
+
+// The interleaved FFN-up copies of every layer, when stale (owning encoder
+// only; a clone runs the copies it was cloned with, or the unfused pair).
+int ensure_glu_operands(mx_encoder *enc) {
+  if (!enc->owns_weights || !enc->fuse_glu || !glu_fusable(enc)) return MX_OK;
+  const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
+  bool synced = false;
+  for (LayerW &w : enc->layers) {
+    if (w.glu_gen == enc->wgen) continue;
+    if (!synced) {  // the source tensors may still be in flight
+      const int rc = use_device(enc->ctx);
+      if (rc) return rc;
+      const hipError_t e = hipDeviceSynchronize();
+      if (e != hipSuccess) return hip_fail(e, "gated FFN interleave");
+      synced = true;
+    }
+    free_dev(w.wg);
+    free_dev(w.wqg);
+    free_dev(w.bg);
+    free_dev(w.wsg);
+    w.glu_gen = 0;
+    int rc = dev_alloc((void **)&w.bg, 2 * f * 4, "gated FFN-up bias");
+    hipError_t e = rc ? hipSuccess : mxk::glu_interleave(w.b[SITE_UP], w.bg, f, 4, nullptr);
+    if (!rc && e == hipSuccess) {
+      if (enc->i8) {
+        rc = dev_alloc((void **)&w.wqg, 2 * f * d, "gated FFN-up operand");
+        if (!rc) rc = dev_alloc((void **)&w.wsg, 2 * f * 4, "gated FFN-up wscale");
+        if (!rc) e = mxk::glu_interleave(w.wq[SITE_UP], w.wqg, f, d, nullptr);
+        if (!rc && e == hipSuccess) e = mxk::glu_interleave(w.ws[SITE_UP], w.wsg, f, 4, nullptr);
+      } else {
+        rc = dev_alloc((void **)&w.wg, 2 * f * d * 2, "gated FFN-up operand");
+        if (!rc) e = mxk::glu_interleave(w.w[SITE_UP], w.wg, f, d * 2, nullptr);
+      }
+    }
+    if (rc) return rc;
+    if (e != hipSuccess) return hip_fail(e, "gated FFN interleave");
+  }
+  if (synced) {
+    const hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(e, "gated FFN interleave");
+    for (LayerW &w : enc->layers) w.glu_gen = enc->wgen;
+  }
+  return MX_OK;
+}
+
+// FFN-up with the gated FFN fused: the layer's interleaved operand, C =
+// enc->glu [M, f] bf16, the same values as the GEMM into enc->up and glu_l.
+int gemm_glu_l(mx_encoder *enc, mx_stream *s, const LayerW &w, int64_t M) {
+  Bracket br(enc, s->stream, CAT_GEMM + 16 * SITE_UP);
+  const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
+  enc->gemm_flop += 2.0 * M * 2 * f * d;
+  enc->site_flop[SITE_UP] += 2.0 * M * 2 * f * d;
+  const int epi =
+      enc->desc.gated_ffn == MX_GATED_SILU ? mxk::EPI_GLU_SILU : mxk::EPI_GLU_GELU;
+  hipError_t e;
+  if (enc->i8) {
+    const mxk::GemmI8Args a{enc->xq, d,       w.wqg,   M, 2 * f, d,   enc->sa,
+                            w.wsg,   w.bg,    epi,     nullptr,  enc->glu, 1, f};
+    e = mxk::gemm_i8(a, s->stream);
+  } else {
+    const mxk::GemmArgs a{enc->xb, d, w.wg, M, 2 * f, d, w.bg, epi, nullptr, enc->glu, 1, f};
+    e = mxk::gemm(a, s->stream);
+  }
+  return e == hipSuccess ? MX_OK : hip_fail(e, "gemm launch (FFN-up with the gated FFN)");
+}
+
 // The rows one pass runs over: M = B*S dense rows, or the packed rows of
 // token packing (seq_start / row_pos non-null, M = seq_start[B]); order
 // (nullable) is attention's launch order, longest sequence first.
@@ -358,6 +443,8 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
                  enc->layers[0].ias[SITE_QKV]);
   for (size_t l = 0; !rc && l < L; ++l) {
     const LayerW &w = enc->layers[l];
+    const bool fused = gated && enc->fuse_glu && glu_fusable(enc) && w.glu_gen == enc->wgen &&
+                       (enc->i8 ? w.wqg && w.wsg : w.wg != nullptr) && w.bg;
     rc = site_gemm(enc, s, w, SITE_QKV, enc->xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->qkv,
                    MX_BF16);
     if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S, M, rows.row_pos);
@@ -368,10 +455,14 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
                      MX_BF16);
     if (!rc)
       rc = site_ln(enc, s, x, enc->proj, MX_BF16, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
-    if (!rc)
-      rc = site_gemm(enc, s, w, SITE_UP, enc->xb, M, d, fu, gated ? MX_EPI_NONE : epi, nullptr,
-                     enc->up, MX_BF16);
-    if (!rc && gated) rc = glu_l(enc, s, M);
+    if (!rc && fused) {
+      rc = gemm_glu_l(enc, s, w, M);
+    } else {
+      if (!rc)
+        rc = site_gemm(enc, s, w, SITE_UP, enc->xb, M, d, fu, gated ? MX_EPI_NONE : epi,
+                       nullptr, enc->up, MX_BF16);
+      if (!rc && gated) rc = glu_l(enc, s, M);
+    }
     if (!rc && enc->i8) rc = quant_l(enc, s, act, M, f, w.ias[SITE_DOWN]);
     if (!rc)
       rc = site_gemm(enc, s, w, SITE_DOWN, act, M, f, d, MX_EPI_NONE, nullptr, enc->proj,
@@ -570,6 +661,10 @@ void mx_encoder_destroy(mx_encoder *enc) {
         for (auto &p : l.wq) free_dev(p);
         for (auto &p : l.ws) free_dev(p);
         for (auto &p : l.ias) free_dev(p);
+        free_dev(l.wg);
+        free_dev(l.wqg);
+        free_dev(l.bg);
+        free_dev(l.wsg);
       }
       for (auto &p : enc->emb_ln) free_dev(p);
       for (auto &p : enc->fin_ln) free_dev(p);
@@ -631,6 +726,8 @@ int mx_encoder_clone(mx_encoder *enc, mx_encoder **out) {
   c->desc = enc->desc;
   c->owns_weights = false;
   c->layers = enc->layers;
+  c->wgen = enc->wgen;
+  c->fuse_glu = enc->fuse_glu;
   c->i8 = enc->i8;
   c->rope_inv = enc->rope_inv;
   c->packing = enc->packing;
@@ -660,6 +757,7 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
   if (!enc->owns_weights)
     return fail(MX_E_STATE, "encoder_set: a lane clone borrows its parent's weights; set them "
                             "on the parent");
+  ++enc->wgen;
   int rc = use_device(enc->ctx);
   if (rc) return rc;
   const std::string name(name_c);
@@ -882,7 +980,7 @@ int mx_encoder_ready(mx_encoder *enc) {
     return fail(MX_E_STATE, "encoder: RoPE without a frequency set -- a positive rope_theta or "
                             "rope.inv_freq is needed");
   enc->i8 = i8;
-  return MX_OK;
+  return ensure_glu_operands(enc);
 }
 
 int mx_encoder_run(mx_encoder *enc, mx_stream *s, float *x_io, const float *add_mask,
@@ -1072,6 +1170,13 @@ int mx_encoder_set_packing(mx_encoder *enc, int on) {
   return MX_OK;
 }
 
+int mx_encoder_set_fusion(mx_encoder *enc, int on) {
+  clear_error();
+  if (!enc) return fail(MX_E_INVALID, "encoder_set_fusion: null encoder");
+  enc->fuse_glu = on != 0;
+  return MX_OK;
+}
+
 int mx_encoder_set_timing(mx_encoder *enc, int on) {
   if (!enc) return fail(MX_E_INVALID, "encoder_set_timing: null encoder");
   enc->timing = on != 0;
@@ -1123,6 +1228,7 @@ int mx_encoder_set_panel(mx_encoder *enc, const char *name_c, const uint16_t *pa
   if (!enc || !name_c || !panel) return fail(MX_E_INVALID, "encoder_set_panel: null argument");
   if (!enc->owns_weights)
     return fail(MX_E_STATE, "encoder_set_panel: a lane clone borrows its parent's weights");
+  ++enc->wgen;
   const std::string name(name_c);
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
   uint16_t **dst = nullptr;
@@ -1381,6 +1487,7 @@ int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
                                              std::to_string(Ns[i]) + "] one wanted"));
       }
       LayerW &w = enc->layers[static_cast<size_t>(L)];
+      ++enc->wgen;
       free_dev(w.w[i]);
       free_dev(w.wq[i]);
       free_dev(w.ws[i]);

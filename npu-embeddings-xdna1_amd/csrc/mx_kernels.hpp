@@ -63,6 +63,18 @@ struct GemmArgs {
 };
 hipError_t gemm(const GemmArgs &a, hipStream_t s);
 
+// Internal epilogues beyond mx_epilogue (bf16 C, no residual, on both
+// datapaths): the gated FFN fused into FFN-up. The GEMM's N = 2f rows of Wt
+// (and the bias, wscale) come in glu_interleave's order -- groups of 16, the
+// first 8 from the lo half, the next 8 the matching rows of the hi half -- and
+// C is [M, f] = lo * act(hi), each product of the two bf16-rounded GEMM
+// outputs, as the GEMM followed by glu() computes it. f % 32 == 0.
+constexpr int EPI_GLU_SILU = 8, EPI_GLU_GELU = 9;
+// Wt [2f, row_bytes] (or a [2f] vector, row_bytes 4) -> the interleaved row
+// order above. row_bytes % 4 == 0.
+hipError_t glu_interleave(const void *src, void *dst, int64_t f, int64_t row_bytes,
+                          hipStream_t s);
+
 // The LDS-pipelined kernel's tile for an M x N product (0: 256x256, 1: 256x192,
 // 2: 128x256, 3: 128x128; deep: the 256 x 256 tile would run on 128-byte
 // slabs) and the resident blocks of a persistent launch.

@@ -113,6 +113,7 @@ SIGNATURES = {
     "mx_encoder_whisper": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "mx_encoder_set_timing": (_int, [_vp, _int]),
     "mx_encoder_set_packing": (_int, [_vp, _int]),
+    "mx_encoder_set_fusion": (_int, [_vp, _int]),
     "mx_encoder_timings": (_int, [_vp, ctypes.POINTER(Timings)]),
     "mx_npue_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "mx_npue_close": (None, [_vp]),
@@ -547,6 +548,9 @@ class Encoder:
 
     def set_packing(self, on):
         check(lib().mx_encoder_set_packing(self.handle, int(on)))
+
+    def set_fusion(self, on):
+        check(lib().mx_encoder_set_fusion(self.handle, int(on)))
 
     def set_timing(self, on):
         check(lib().mx_encoder_set_timing(self.handle, int(on)))

@@ -179,3 +179,68 @@ def test_nomic_int8_stack(ctx, orc):
     enc.close()
     _check_i8_parity(got, _oracle_embed(orc, m, ids, am, q8),
                      _oracle_embed(orc, _dequantised(m, q8), ids, am), "nomic int8")
+
+
+# (arch, int8 datapath, model overrides, B, S): the row counts put FFN-up's
+# fused kernel on each tile -- 128 rows: 128 x 128; 1000: 128 x 256; 2048: the
+# 256 x 256 tile (on 128-byte slabs, or on 64-byte slabs for a hidden width
+# that is not a multiple of 64 (bf16) or 128 (int8)).
+FUSED_CASES = [
+    ("nomic", False, {}, 4, 512),
+    ("gte", False, {}, 2, 64),
+    ("gte", False, {}, 2, 500),
+    ("nomic", False, dict(hidden=288, heads=9, head_dim=32), 4, 512),
+    ("nomic", True, {}, 4, 512),
+    ("gte", True, {}, 2, 64),
+    ("nomic", True, {}, 2, 500),
+    ("gte", True, dict(hidden=448, heads=7, head_dim=64), 4, 512),
+]
+
+
+@pytest.mark.parametrize("name,int8,over,B,S", FUSED_CASES)
+def test_fused_glu_is_bitwise_the_unfused_pair(ctx, name, int8, over, B, S):
+    """FFN-up with lo * act(hi) in its epilogue (the default) against the
+    GEMM into the [M, 2f] intermediate followed by the gated-FFN pass: every
+    row of the hidden state equal bit for bit, on both datapaths; then a new
+    FFN-up bias reaches the fused path (its interleaved copies are rebuilt)."""
+    m = synth.make_model(name, layers=2, ln_random=True, **over)
+    d = m["hidden"]
+    enc = mxenc.Encoder(ctx, m, int8=synth.quantise_model(m) if int8 else None)
+    x = np.random.default_rng(B * S).standard_normal((B * S, d)).astype(np.float32)
+
+    def run(fused):
+        enc.set_fusion(fused)
+        dx = ctx.put(x)
+        enc.run(dx, None, None, B, S)
+        return dx.host()
+
+    try:
+        a, b = run(True), run(False)
+        assert np.isfinite(a).all()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        rng = np.random.default_rng(5)
+        enc.set("layer.1.ffn_up.bias",
+                rng.standard_normal(2 * m["ffn"]).astype(np.float32) * 0.5)
+        c, e = run(True), run(False)
+        assert np.array_equal(c.view(np.uint32), e.view(np.uint32))
+        assert not np.array_equal(c.view(np.uint32), a.view(np.uint32))
+    finally:
+        enc.close()
+
+
+def test_fused_glu_lane_clone_is_bitwise_its_parent(ctx):
+    """A lane clone runs the parent's interleaved operands: the same rows."""
+    m = synth.make_model("nomic", layers=2, ln_random=True)
+    enc = mxenc.Encoder(ctx, m)
+    lane = enc.clone(ctx)
+    x = np.random.default_rng(3).standard_normal((1024, m["hidden"])).astype(np.float32)
+    outs = []
+    try:
+        for e in (enc, lane):
+            dx = ctx.put(x)
+            e.run(dx, None, None, 2, 512)
+            outs.append(dx.host())
+        assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    finally:
+        lane.close()
+        enc.close()
