@@ -467,13 +467,20 @@ __global__ __launch_bounds__(256) void embed_sum_packed_k(
 
 // ---- pooling (app_state.hpp:335-374), bit-exact with the host form ----------
 
-__global__ __launch_bounds__(256) void pool_k(const float *__restrict__ h,
-                                              const float *__restrict__ am, int64_t S,
-                                              int64_t d, int cls, int l2, float *out,
-                                              int *err, const int32_t *__restrict__ seq_start) {
+// One block per sequence, one column per thread (d <= 1024; a thread takes
+// every blockDim-th column beyond). Each column's sum runs over s in order, in
+// double, as the host's does; the rows' loads are issued POOL_U at a time
+// ahead of their adds (the mask row is uniform, so its test branches the
+// whole block alike), which keeps the in-order chain from waiting on one load
+// per row. Every thread forms the float denominator itself, in the same order.
+constexpr int POOL_U = 16;
+
+__global__ __launch_bounds__(1024) void pool_k(const float *__restrict__ h,
+                                               const float *__restrict__ am, int64_t S,
+                                               int64_t d, int cls, int l2, float *out,
+                                               int *err, const int32_t *__restrict__ seq_start) {
   extern __shared__ double acc[];
   __shared__ double nrm_s;
-  __shared__ float denom_s;
   const int64_t b = blockIdx.x;
   const float *amb = am + b * S;
   // Packed rows: the loop below reads row s only where the mask is nonzero,
@@ -487,27 +494,39 @@ __global__ __launch_bounds__(256) void pool_k(const float *__restrict__ h,
     }
     for (int64_t c = threadIdx.x; c < d; c += blockDim.x) acc[c] = (double)hb[c];
   } else {
-    if (threadIdx.x == 0) {
-      float den = 0.0f;
-      for (int64_t s = 0; s < S; ++s) den += amb[s];
-      denom_s = den > 1e-9f ? den : 1e-9f;
-    }
-    __syncthreads();
     for (int64_t c = threadIdx.x; c < d; c += blockDim.x) {
       double a = 0.0;
-      for (int64_t s = 0; s < S; ++s) {
-        const float m = amb[s];
-        if (m == 0.0f) continue;
-        a += (double)(__fmul_rn(hb[s * d + c], m));
+      float den = 0.0f;
+      for (int64_t s0 = 0; s0 < S; s0 += POOL_U) {
+        float m[POOL_U], v[POOL_U];
+#pragma unroll
+        for (int u = 0; u < POOL_U; ++u) {
+          m[u] = s0 + u < S ? amb[s0 + u] : 0.0f;
+          v[u] = m[u] != 0.0f ? hb[(s0 + u) * d + c] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < POOL_U; ++u) {
+          if (s0 + u < S) den += m[u];
+          if (m[u] != 0.0f) a += (double)(__fmul_rn(v[u], m[u]));
+        }
       }
-      acc[c] = a / (double)denom_s;
+      acc[c] = a / (double)(den > 1e-9f ? den : 1e-9f);
     }
   }
   __syncthreads();
   if (l2) {
     if (threadIdx.x == 0) {
+      // In column order, POOL_U values read ahead of their FMAs.
       double n = 0.0;
-      for (int64_t c = 0; c < d; ++c) n = __builtin_fma(acc[c], acc[c], n);
+      int64_t c0 = 0;
+      for (; c0 + POOL_U <= d; c0 += POOL_U) {
+        double x[POOL_U];
+#pragma unroll
+        for (int u = 0; u < POOL_U; ++u) x[u] = acc[c0 + u];
+#pragma unroll
+        for (int u = 0; u < POOL_U; ++u) n = __builtin_fma(x[u], x[u], n);
+      }
+      for (; c0 < d; ++c0) n = __builtin_fma(acc[c0], acc[c0], n);
       nrm_s = sqrt(n > 1e-24 ? n : 1e-24);
     }
     __syncthreads();
@@ -661,8 +680,9 @@ hipError_t mask_build(const float *am, int64_t B, int64_t S, float *add_mask, in
 
 hipError_t pool_rows(const float *h, const float *am, int64_t B, int64_t S, int64_t d, int cls,
                      int l2, float *out, int *err, hipStream_t s, const int32_t *seq_start) {
-  pool_k<<<(unsigned)B, 256, (size_t)d * sizeof(double), s>>>(h, am, S, d, cls, l2, out, err,
-                                                              seq_start);
+  const int nt = d >= 1024 ? 1024 : (int)((d + 63) / 64 * 64);
+  pool_k<<<(unsigned)B, nt, (size_t)d * sizeof(double), s>>>(h, am, S, d, cls, l2, out, err,
+                                                             seq_start);
   return hipGetLastError();
 }
 

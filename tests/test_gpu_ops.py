@@ -522,6 +522,28 @@ def test_embed_sum_mask_kvlen_bit_exact(ctx, orc, golden_dir):
                                    d_t.p, emb.p, None, None))
 
 
+@pytest.mark.parametrize("B,S,d", [(5, 77, 1100), (3, 130, 100), (64, 512, 768)])
+def test_pool_rows_mean_bit_exact_random(ctx, orc, B, S, d):
+    """Mean pooling in double, in row order, over values spread across 2^-20 ..
+    2^20 (so a reordered sum would differ), a weighted mask with holes, a
+    sequence with no kept row (denominator 1e-9), S and d not multiples of the
+    kernel's read-ahead, and d beyond one column per thread."""
+    rng = np.random.default_rng(S)
+    h = (rng.standard_normal((B, S, d)) *
+         np.exp2(rng.integers(-20, 20, (B, S, d)))).astype(np.float32)
+    am = ((rng.random((B, S)) < 0.7) *
+          rng.choice([1.0, 0.5, 3.0], (B, S))).astype(np.float32)
+    am[0] = 0
+    L = mxenc.lib()
+    dh, dam = ctx.put(h), ctx.put(am)
+    out = ctx.empty((B, d), np.float32)
+    for l2 in (0, 1):
+        want = np.empty((B, d), np.float32)
+        assert orc.orc_pool_rows(P(h), P(am), B, S, d, 0, l2, P(want)) == 0
+        mxenc.check(L.mx_pool_rows(ctx.stream, dh.p, dam.p, B, S, d, 0, l2, out.p))
+        assert np.array_equal(out.host().view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("cls", [0, 1])
 def test_pool_rows_bit_exact_on_reference_goldens(ctx, orc, golden_dir, cls):
     if cls:
