@@ -467,13 +467,16 @@ __global__ __launch_bounds__(256) void embed_sum_packed_k(
 
 // ---- pooling (app_state.hpp:335-374), bit-exact with the host form ----------
 
-// One block per sequence, one column per thread (d <= 1024; a thread takes
-// every blockDim-th column beyond). Each column's sum runs over s in order, in
-// double, as the host's does; the rows' loads are issued POOL_U at a time
-// ahead of their adds (the mask row is uniform, so its test branches the
-// whole block alike), which keeps the in-order chain from waiting on one load
-// per row. Every thread forms the float denominator itself, in the same order.
-constexpr int POOL_U = 16;
+// One block per sequence, one column per thread (d <= 1024; beyond, the
+// threads take the columns in rounds). Each column's sum runs over s in
+// order, in double, as the host's does. The mask row reaches LDS a chunk at a
+// time; the rows' loads are issued POOL_U at a time ahead of their adds (a
+// masked row's load reads the buffer's first element instead, and its term
+// is an exact +0.0: the running sum starts at +0.0 and can never be -0.0, so
+// adding it is the host's skip), which keeps the in-order chain from waiting
+// on one load per row. Every thread forms the float denominator itself, in
+// the same order.
+constexpr int POOL_U = 16, POOL_CH = 1024;
 
 __global__ __launch_bounds__(1024) void pool_k(const float *__restrict__ h,
                                                const float *__restrict__ am, int64_t S,
@@ -481,6 +484,7 @@ __global__ __launch_bounds__(1024) void pool_k(const float *__restrict__ h,
                                                int *err, const int32_t *__restrict__ seq_start) {
   extern __shared__ double acc[];
   __shared__ double nrm_s;
+  __shared__ __align__(16) float msk[POOL_CH];
   const int64_t b = blockIdx.x;
   const float *amb = am + b * S;
   // Packed rows: the loop below reads row s only where the mask is nonzero,
@@ -494,23 +498,41 @@ __global__ __launch_bounds__(1024) void pool_k(const float *__restrict__ h,
     }
     for (int64_t c = threadIdx.x; c < d; c += blockDim.x) acc[c] = (double)hb[c];
   } else {
-    for (int64_t c = threadIdx.x; c < d; c += blockDim.x) {
+    const int64_t rounds = (d + blockDim.x - 1) / blockDim.x;
+    for (int64_t rd = 0; rd < rounds; ++rd) {
+      const int64_t c = rd * blockDim.x + threadIdx.x;
+      const bool live = c < d;
       double a = 0.0;
       float den = 0.0f;
-      for (int64_t s0 = 0; s0 < S; s0 += POOL_U) {
-        float m[POOL_U], v[POOL_U];
+      for (int64_t sb = 0; sb < S; sb += POOL_CH) {
+        const int n = (int)(S - sb < POOL_CH ? S - sb : POOL_CH);
+        __syncthreads();
+        for (int i = threadIdx.x; i < n; i += blockDim.x) msk[i] = amb[sb + i];
+        __syncthreads();
+        for (int i0 = 0; i0 < n; i0 += POOL_U) {
+          float m[POOL_U], v[POOL_U];
 #pragma unroll
-        for (int u = 0; u < POOL_U; ++u) {
-          m[u] = s0 + u < S ? amb[s0 + u] : 0.0f;
-          v[u] = m[u] != 0.0f ? hb[(s0 + u) * d + c] : 0.0f;
-        }
+          for (int q = 0; q < POOL_U / 4; ++q) {  // in bounds: POOL_CH % POOL_U == 0
+            const float4 x = *(const float4 *)(msk + i0 + 4 * q);
+            m[4 * q] = x.x;
+            m[4 * q + 1] = x.y;
+            m[4 * q + 2] = x.z;
+            m[4 * q + 3] = x.w;
+          }
 #pragma unroll
-        for (int u = 0; u < POOL_U; ++u) {
-          if (s0 + u < S) den += m[u];
-          if (m[u] != 0.0f) a += (double)(__fmul_rn(v[u], m[u]));
+          for (int u = 0; u < POOL_U; ++u) {
+            m[u] = i0 + u < n ? m[u] : 0.0f;
+            const float *p = live && m[u] != 0.0f ? hb + (sb + i0 + u) * d + c : h;
+            v[u] = *p;
+          }
+#pragma unroll
+          for (int u = 0; u < POOL_U; ++u) {
+            if (i0 + u < n) den += m[u];
+            a += m[u] != 0.0f ? (double)(__fmul_rn(v[u], m[u])) : 0.0;
+          }
         }
       }
-      acc[c] = a / (double)(den > 1e-9f ? den : 1e-9f);
+      if (live) acc[c] = a / (double)(den > 1e-9f ? den : 1e-9f);
     }
   }
   __syncthreads();
