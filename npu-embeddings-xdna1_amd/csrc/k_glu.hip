@@ -7,8 +7,8 @@
 // head the pairs (j, j + hd/2) rotate by the table's angle:
 //   o1 = x1*c - x2*s,  o2 = x2*c + x1*s
 // each product rounded as the host's AVX2 form (no fused multiply-add), the
-// result narrowed once to bf16. One block per row; each thread moves two
-// adjacent pairs (4-byte bf16 loads of x1 and x2, 8-byte table loads).
+// result narrowed once to bf16. Each thread moves four adjacent pairs (two
+// when head_dim % 8 != 0 or the rows are not 8-byte aligned).
 //
 // glu_k: swiglu_cpu (bert_encoder.cpp:582-627): FFN-up's [rows, 2f] output as
 // lo | hi halves -> [rows, f] = lo * act(hi), act SiLU with the host's
@@ -32,32 +32,64 @@ using namespace mxd;
 
 namespace {
 
+// PAIRS adjacent pairs per thread (4: 8-byte loads of x1 and x2 and 16-byte
+// table loads, for head_dim % 8 == 0; else 2), threads over (row, unit) flat.
+template <int PAIRS>
 __global__ __launch_bounds__(256) void rope_qkv_k(uint16_t *__restrict__ qkv, int64_t ld,
-                                                  int S, int H, int hd,
+                                                  int64_t rows, int S, int H, int hd,
                                                   const float *__restrict__ cos_t,
                                                   const float *__restrict__ sin_t,
                                                   const int32_t *__restrict__ row_pos) {
-  const int64_t row = blockIdx.x;
-  const int s = row_pos ? row_pos[row] : (int)(row % S), half = hd / 2, d = H * hd;
-  const int per_head = half / 2;  // thread units (two pairs) per head
+  const int half = hd / 2, d = H * hd;
+  const int per_head = half / PAIRS;  // thread units per head
   const int units = 2 * H * per_head;
-  uint16_t *base = qkv + row * ld;
-  const float *cs = cos_t + (int64_t)s * hd, *sn = sin_t + (int64_t)s * hd;
-  for (int u = threadIdx.x; u < units; u += blockDim.x) {
+  const int64_t total = rows * units;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = t / units;
+    const int u = (int)(t - row * units);
+    const int s = row_pos ? row_pos[row] : (int)(row % S);
     const int which = u / (H * per_head);  // 0: Q, 1: K
     const int rem = u - which * H * per_head;
-    const int h = rem / per_head, j = (rem - h * per_head) * 2;
-    uint16_t *v = base + which * d + h * hd;
-    const uint32_t p1 = *(const uint32_t *)(v + j), p2 = *(const uint32_t *)(v + j + half);
-    const float2 c = *(const float2 *)(cs + j), si = *(const float2 *)(sn + j);
-    const float a0 = bf2f(p1 & 0xFFFFu), a1 = bf2f(p1 >> 16);
-    const float b0 = bf2f(p2 & 0xFFFFu), b1 = bf2f(p2 >> 16);
-    const float o10 = a0 * c.x - b0 * si.x;
-    const float o11 = a1 * c.y - b1 * si.y;
-    const float o20 = b0 * c.x + a0 * si.x;
-    const float o21 = b1 * c.y + a1 * si.y;
-    *(uint32_t *)(v + j) = pack_bf2(o10, o11);
-    *(uint32_t *)(v + j + half) = pack_bf2(o20, o21);
+    const int h = rem / per_head, j = (rem - h * per_head) * PAIRS;
+    uint16_t *v = qkv + row * ld + which * d + h * hd;
+    const float *cs = cos_t + (int64_t)s * hd + j, *sn = sin_t + (int64_t)s * hd + j;
+    float a[PAIRS], b[PAIRS], c[PAIRS], si[PAIRS];
+    if constexpr (PAIRS == 4) {
+      const uint2 p1 = *(const uint2 *)(v + j), p2 = *(const uint2 *)(v + j + half);
+      const float4 c4 = *(const float4 *)cs, s4 = *(const float4 *)sn;
+      const uint32_t w1[2] = {p1.x, p1.y}, w2[2] = {p2.x, p2.y};
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        a[2 * k] = bf2f(w1[k] & 0xFFFFu);
+        a[2 * k + 1] = bf2f(w1[k] >> 16);
+        b[2 * k] = bf2f(w2[k] & 0xFFFFu);
+        b[2 * k + 1] = bf2f(w2[k] >> 16);
+      }
+      c[0] = c4.x, c[1] = c4.y, c[2] = c4.z, c[3] = c4.w;
+      si[0] = s4.x, si[1] = s4.y, si[2] = s4.z, si[3] = s4.w;
+    } else {
+      const uint32_t p1 = *(const uint32_t *)(v + j), p2 = *(const uint32_t *)(v + j + half);
+      const float2 c2 = *(const float2 *)cs, s2 = *(const float2 *)sn;
+      a[0] = bf2f(p1 & 0xFFFFu), a[1] = bf2f(p1 >> 16);
+      b[0] = bf2f(p2 & 0xFFFFu), b[1] = bf2f(p2 >> 16);
+      c[0] = c2.x, c[1] = c2.y;
+      si[0] = s2.x, si[1] = s2.y;
+    }
+    uint32_t o1[PAIRS / 2], o2[PAIRS / 2];
+#pragma unroll
+    for (int k = 0; k < PAIRS / 2; ++k) {
+      const int e = 2 * k;
+      o1[k] = pack_bf2(a[e] * c[e] - b[e] * si[e], a[e + 1] * c[e + 1] - b[e + 1] * si[e + 1]);
+      o2[k] = pack_bf2(b[e] * c[e] + a[e] * si[e], b[e + 1] * c[e + 1] + a[e + 1] * si[e + 1]);
+    }
+    if constexpr (PAIRS == 4) {
+      *(uint2 *)(v + j) = make_uint2(o1[0], o1[1]);
+      *(uint2 *)(v + j + half) = make_uint2(o2[0], o2[1]);
+    } else {
+      *(uint32_t *)(v + j) = o1[0];
+      *(uint32_t *)(v + j + half) = o2[0];
+    }
   }
 }
 
@@ -117,7 +149,17 @@ hipError_t glu_interleave(const void *src, void *dst, int64_t f, int64_t row_byt
 hipError_t rope_qkv(uint16_t *qkv, int64_t ld, int64_t rows, int S, int H, int hd,
                     const float *cos_t, const float *sin_t, hipStream_t s,
                     const int32_t *row_pos) {
-  rope_qkv_k<<<(unsigned)rows, 256, 0, s>>>(qkv, ld, S, H, hd, cos_t, sin_t, row_pos);
+  // Four pairs where their 8- and 16-byte accesses are aligned.
+  const bool wide = hd % 8 == 0 && ld % 4 == 0 && (uintptr_t)qkv % 8 == 0 &&
+                    (uintptr_t)cos_t % 16 == 0 && (uintptr_t)sin_t % 16 == 0;
+  const int pairs = wide ? 4 : 2;
+  const int64_t total = rows * (2 * H * (hd / 2 / pairs));
+  int64_t g = (total + 255) / 256;
+  if (g > 65536) g = 65536;
+  if (pairs == 4)
+    rope_qkv_k<4><<<(unsigned)g, 256, 0, s>>>(qkv, ld, rows, S, H, hd, cos_t, sin_t, row_pos);
+  else
+    rope_qkv_k<2><<<(unsigned)g, 256, 0, s>>>(qkv, ld, rows, S, H, hd, cos_t, sin_t, row_pos);
   return hipGetLastError();
 }
 

@@ -35,11 +35,14 @@ def test_rope_tables_match_oracle(orc):
         assert np.array_equal(c0, c1) and np.array_equal(s0, s1)
 
 
-@pytest.mark.parametrize("B,S,H,hd", [(3, 77, 12, 64), (2, 128, 12, 32)])
-def test_rope_qkv_bit_exact(ctx, orc, B, S, H, hd):
+@pytest.mark.parametrize("B,S,H,hd,pad", [(3, 77, 12, 64, 0), (2, 128, 12, 32, 0),
+                                          (2, 50, 3, 36, 0), (2, 77, 12, 64, 2)])
+def test_rope_qkv_bit_exact(ctx, orc, B, S, H, hd, pad):
     """On bf16 values the GPU rotates with the host's operations (products
     rounded, no fused multiply-add) and narrows once: bit for bit the oracle's
-    rotation of the same values, narrowed by to_bf16."""
+    rotation of the same values, narrowed by to_bf16. Four pairs per thread,
+    and two where head_dim % 8 != 0 or a row stride (3d + pad) leaves rows
+    only 4-byte aligned; the padding columns stay untouched."""
     rng = np.random.default_rng(S)
     d = H * hd
     qkv = mxenc.from_bf16_bits(mxenc.to_bf16_bits(
@@ -47,10 +50,13 @@ def test_rope_qkv_bit_exact(ctx, orc, B, S, H, hd):
     c, s = mxenc.rope_tables(S, hd, 1000.0)
     want = qkv.copy()
     orc.orc_rope_qkv(P(want), B * S, S, H, hd, P(c), P(s))
-    dq = ctx.put(mxenc.to_bf16_bits(qkv))
-    mxenc.rope_qkv(ctx, dq, 3 * d, B, S, H, hd, ctx.put(c), ctx.put(s))
+    bits = np.full((B * S, 3 * d + pad), 0x1234, np.uint16)
+    bits[:, :3 * d] = mxenc.to_bf16_bits(qkv)
+    dq = ctx.put(bits)
+    mxenc.rope_qkv(ctx, dq, 3 * d + pad, B, S, H, hd, ctx.put(c), ctx.put(s))
     got = dq.host()
-    assert np.array_equal(got, mxenc.to_bf16_bits(want))
+    assert np.array_equal(got[:, :3 * d], mxenc.to_bf16_bits(want))
+    assert (got[:, 3 * d:] == 0x1234).all()
 
 
 @pytest.mark.parametrize("act", [mxenc.MX_GATED_SILU, mxenc.MX_GATED_GELU_ERF])
