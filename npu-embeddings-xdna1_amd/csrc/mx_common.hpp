@@ -71,10 +71,30 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
 }
 
-// The GEMM epilogue activation (mx_epilogue): 0 none, 1 gelu_poly, 2 gelu_erf.
+// Exact-erf GELU for the GEMM epilogues, where it runs while the matrix pipe
+// idles: erfc(z), z = |x|/sqrt2, by Abramowitz & Stegun 7.1.26 (|error| <=
+// 1.5e-7, the method of the reference's accelerator kernel, gelu_erf.cc:60-65)
+// with the hardware reciprocal and exp2, about half the instructions of erff.
+// Formed from erfc, GELU(x) = x - x erfc(z) / 2 for x >= 0 and x erfc(z) / 2
+// below, so the negative side keeps its relative accuracy instead of
+// cancelling in 1 + erf. +inf gives +inf; -inf and NaN give NaN, as the host's
+// 0.5 x (1 + erf(x / sqrt2)) does.
+__device__ __forceinline__ float gelu_erf_epi(float v) {
+  const float z = fabsf(v) * 0.70710678118654752440f;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, z, 1.0f));
+  float p = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  p = __builtin_fmaf(p, t, 1.421413741f);
+  p = __builtin_fmaf(p, t, -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.254829592f);
+  const float erfc = p * t * __builtin_amdgcn_exp2f(-(z * z) * 1.4426950408889634f);
+  const float h = 0.5f * v * erfc;
+  return v >= 0.0f ? (erfc == 0.0f ? v : v - h) : h;
+}
+
+// The GEMM epilogue activation (mx_epilogue): 0 none, 1 gelu_poly, 2 GELU erf.
 __device__ __forceinline__ float gemm_epilogue(float v, int epi) {
   if (epi == 1) return gelu_poly(v);
-  if (epi == 2) return gelu_erf(v);
+  if (epi == 2) return gelu_erf_epi(v);
   return v;
 }
 
