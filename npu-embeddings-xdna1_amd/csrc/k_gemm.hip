@@ -172,6 +172,7 @@ namespace mxk {
 template <int BM, int BN, int WGM, int WGN, int NS>
 hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s);
 hipError_t gemm_lds_deep_launch(const GemmArgs &a, int grid, hipStream_t s);
+hipError_t gemm_lds_128_deep_launch(const GemmArgs &a, int grid, hipStream_t s);
 
 namespace {
 
@@ -181,7 +182,8 @@ enum GemmPath {
   PATH_LDS_256x192,
   PATH_LDS_128x256,
   PATH_LDS_128x128,
-  PATH_LDS_256x256_DEEP
+  PATH_LDS_256x256_DEEP,
+  PATH_LDS_128x128_DEEP
 };
 
 // The 256 x 256 tile on 128-byte slabs: a bf16 C without a residual or an
@@ -204,7 +206,9 @@ GemmPath pick(const GemmArgs &a) {
   const bool deep = deep_ok(a);
   int t = gemm_lds_tile(a.M, a.N, deep);
   if (t == 1 && a.epilogue >= EPI_GLU_SILU) t = 0;  // 96-column waves cannot pair blocks
-  return t == 0 && deep ? PATH_LDS_256x256_DEEP : paths[t];
+  if (t == 0 && deep) return PATH_LDS_256x256_DEEP;
+  if (t == 3 && deep && a.c_bf16 && !a.residual) return PATH_LDS_128x128_DEEP;
+  return paths[t];
 }
 
 }  // namespace
@@ -288,6 +292,7 @@ const char *gemm_plan_name(int64_t M, int64_t N, int64_t K, bool c_bf16, bool re
   a.c_bf16 = c_bf16 ? 1 : 0;
   switch (pick(a)) {
     case PATH_LDS_256x256_DEEP: return "lds_256x256x64_w64x128_ns2_persistent";
+    case PATH_LDS_128x128_DEEP: return "lds_128x128x64_w64x64_ns2_persistent";
     case PATH_LDS_256x256: return "lds_256x256x32_w128x64_ns3_persistent";
     case PATH_LDS_256x192: return "lds_256x192x32_w64x96_ns4_persistent";
     case PATH_LDS_128x256: return "lds_128x256x32_w64x64_ns4_persistent";
@@ -306,6 +311,7 @@ hipError_t gemm(const GemmArgs &a, hipStream_t s) {
   if (a.epilogue >= EPI_GLU_SILU && (p == PATH_STAGED || a.N % 64)) return hipErrorInvalidValue;
   switch (p) {
     case PATH_LDS_256x256_DEEP: return gemm_lds_deep_launch(a, cu_count(), s);
+    case PATH_LDS_128x128_DEEP: return gemm_lds_128_deep_launch(a, cu_count(), s);
     case PATH_LDS_256x256: return gemm_lds_launch<256, 256, 2, 4, 3>(a, cu_count(), s);
     case PATH_LDS_256x192: return gemm_lds_launch<256, 192, 4, 2, 4>(a, cu_count(), s);
     case PATH_LDS_128x256: return gemm_lds_launch<128, 256, 2, 4, 4>(a, cu_count(), s);

@@ -101,6 +101,23 @@ hipError_t gemm_lds_deep_launch(const GemmArgs &a, int grid, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
+// The 128 x 128 tile on 128-byte slabs (two 32 KB slots: the LDS of the
+// 64-byte form's four, half the barriers per K) for a bf16 C without a
+// residual.
+hipError_t gemm_lds_128_deep_launch(const GemmArgs &a, int grid, hipStream_t s) {
+  if (!a.c_bf16 || a.residual) return hipErrorInvalidValue;
+  switch (a.epilogue) {
+    case 0: return gemm_lds_launch_t<128, 128, 2, 2, 2, 0, false, true, 128>(a, grid, s);
+    case 1: return gemm_lds_launch_t<128, 128, 2, 2, 2, 1, false, true, 128>(a, grid, s);
+    case 2: return gemm_lds_launch_t<128, 128, 2, 2, 2, 2, false, true, 128>(a, grid, s);
+    case EPI_GLU_SILU:
+      return gemm_lds_launch_t<128, 128, 2, 2, 2, EPI_GLU_SILU, false, true, 128>(a, grid, s);
+    case EPI_GLU_GELU:
+      return gemm_lds_launch_t<128, 128, 2, 2, 2, EPI_GLU_GELU, false, true, 128>(a, grid, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template hipError_t gemm_lds_launch<256, 256, 2, 4, 3>(const GemmArgs &, int, hipStream_t);
 template hipError_t gemm_lds_launch<128, 256, 2, 4, 4>(const GemmArgs &, int, hipStream_t);
 template hipError_t gemm_lds_launch<128, 128, 2, 2, 4>(const GemmArgs &, int, hipStream_t);
