@@ -200,8 +200,10 @@ int mx_narrow_i32_bf16(mx_stream *s, const int32_t *in, uint16_t *out, int64_t n
  * sum and mask (runtime/src/server/embed_service.cpp:29-64) and
  * app::pool_rows (common/app_state.hpp:335-374).
  * embed_sum: emb[b*S+s] = word[ids] + pos[s] + type0 (fp32, left to right);
- * add_mask = m > 0 ? 0 : -1e30; kv_len[b] = 1 + last s with m > 0 (S when the
- * whole row is masked, which attends uniformly like the reference). Every
+ * add_mask = m > 0 ? 0 : -1e30; kv_len[b] = 1 + last s with m != 0 (every
+ * row pool_rows weights, negative weights included; keys before it with
+ * m <= 0 are masked), or S when no m > 0 (the row attends uniformly like the
+ * reference's all -1e30 row). Every
  * output nullable except emb. Ids outside [0, vocab) are refused by the
  * kernel (MX_E_DATA after the stream drains). */
 int mx_embed_sum(mx_stream *s, const int32_t *ids, const float *attn_mask,
@@ -527,17 +529,28 @@ int mx_encoder_set_panel(mx_encoder *enc, const char *name, const uint16_t *pane
                          int64_t mac_s, int64_t mac_t);
 /* setup_encoder for a BERT container (run_setup.hpp:483-877 with
  * app::set_model_shape, app_state.hpp:380-620, and BertEncoder::stage_all,
- * bert_encoder.cpp:40-160): arch "bert_abs_gelu_postln" only (RoPE and gated
- * FFNs are refused by name); geometry from num_layers / hidden / num_heads /
- * head_dim / intermediate / max_seq_len; pooling "cls" or "mean";
- * l2_normalize (default true); LayerNorm eps 1e-12 and the polynomial GELU
- * (gelu_cpu), as BertEncoder hard-codes them. Every tensor is set from the
- * mapping: pre-tiled BF16 GEMM operands through mx_encoder_set_panel, and an
- * --int8 pack's pre-tiled I8 operands with their .wscale/.asmooth through the
- * int8 staging of mx_stage_weight_panel_i8 (the int4 pack's I4 nibbles are
- * refused by name). A "host" container (F32 row-major operands) is refused
- * for the GEMM, as the reference refuses --npu-ops gemm on one
- * (bert_encoder.cpp:79-87). The encoder is ready on MX_OK. */
+ * bert_encoder.cpp:40-160). Three archs load:
+ *  - "bert_abs_gelu_postln": absolute positions; a plain FFN, or a gated one
+ *    when the config says gated_ffn true;
+ *  - "nomic_bert_rope_swiglu": needs position_embedding_type "rope",
+ *    gated_ffn true, swiglu_halves "fc11_up|fc12_gate" and a positive
+ *    rope_theta;
+ *  - "gte_new_rope_geglu": needs position_embedding_type "rope", gated_ffn
+ *    true, glu_halves beginning "up_first|gate_second", rope_inv_freq (an
+ *    array of head_dim/2 numbers) and an activation key.
+ * Any other arch is refused by name. A gated container's gate activation is
+ * its "activation" key ("silu" or "gelu", the exact erf form; missing means
+ * silu except on gte; anything else is refused). Geometry from num_layers /
+ * hidden / num_heads / head_dim / intermediate / max_seq_len; pooling "cls"
+ * or "mean"; l2_normalize (default true); LayerNorm eps 1e-12 and the
+ * polynomial GELU of a plain FFN (gelu_cpu), as BertEncoder hard-codes them.
+ * Every tensor is set from the mapping: pre-tiled BF16 GEMM operands through
+ * mx_encoder_set_panel, and an --int8 pack's pre-tiled I8 operands with their
+ * .wscale/.asmooth through the int8 staging of mx_stage_weight_panel_i8 (the
+ * int4 pack's I4 nibbles are refused by name). A "host" container (F32
+ * row-major operands) is refused for the GEMM, as the reference refuses
+ * --npu-ops gemm on one (bert_encoder.cpp:79-87). The encoder is ready on
+ * MX_OK. */
 int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out);
 
 #ifdef __cplusplus

@@ -386,21 +386,28 @@ __global__ __launch_bounds__(256) void embed_sum_k(const int32_t *__restrict__ i
   for (int64_t c = lane; c < d; c += 64) emb[r * d + c] = (wv[c] + pv[c]) + type0[c];
 }
 
+// kv_len[b] = 1 + the last position with m != 0: every row pooling reads
+// (pool_rows weights every row with m != 0, negative ones included) and every
+// key attention can weight (m > 0) lies before it. A row with no m > 0 attends
+// uniformly over all S keys, as the reference's all -1e30 row does, so it
+// keeps S.
 __global__ __launch_bounds__(256) void mask_k(const float *__restrict__ am, int64_t S,
                                               float *add_mask, int32_t *kv_len) {
-  __shared__ int last;
-  if (threadIdx.x == 0) last = 0;
+  __shared__ int last_pos, last_nz;
+  if (threadIdx.x == 0) last_pos = last_nz = 0;
   __syncthreads();
   const int64_t b = blockIdx.x;
-  int mine = 0;
+  int pos = 0, nz = 0;
   for (int64_t s = threadIdx.x; s < S; s += blockDim.x) {
     const float m = am[b * S + s];
     if (add_mask) add_mask[b * S + s] = m > 0.0f ? 0.0f : -1.0e30f;
-    if (m > 0.0f) mine = (int)s + 1;
+    if (m > 0.0f) pos = (int)s + 1;
+    if (m != 0.0f) nz = (int)s + 1;
   }
-  atomicMax(&last, mine);
+  atomicMax(&last_pos, pos);
+  atomicMax(&last_nz, nz);
   __syncthreads();
-  if (threadIdx.x == 0 && kv_len) kv_len[b] = last > 0 ? last : (int32_t)S;
+  if (threadIdx.x == 0 && kv_len) kv_len[b] = last_pos > 0 ? last_nz : (int32_t)S;
 }
 
 // ---- token packing: only the rows pooling can see ---------------------------

@@ -195,6 +195,7 @@ bool deep_ok(const GemmArgs &a) {
 bool lds_path_ok(const GemmArgs &a) {
   const uintptr_t c = (uintptr_t)a.C;
   return a.K % 32 == 0 && a.K >= 128 && a.N % 4 == 0 && a.lda % 8 == 0 && a.bias &&
+         lds_offsets_fit(a.lda, a.K, 2) &&
          a.ldc % (a.c_bf16 ? 8 : 4) == 0 && c % 16 == 0 && (uintptr_t)a.bias % 16 == 0 &&
          (!a.residual || (uintptr_t)a.residual % 16 == 0);
 }

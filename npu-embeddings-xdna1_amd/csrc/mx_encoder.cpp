@@ -27,6 +27,7 @@
 
 #include <cctype>
 #include <cstring>
+#include <mutex>
 #include <set>
 #include <string>
 #include <vector>
@@ -71,6 +72,13 @@ struct mx_encoder {
   mx_ctx *ctx = nullptr;
   mx_encoder_desc desc{};
   bool owns_weights = true;  // false for a lane clone, which borrows its parent's
+  // Lane clones borrow the owner's weight pointers. While any clone is alive
+  // the owner's weights neither change (set / set_panel refuse) nor go away:
+  // destroying the owner first frees only its workspace and leaves the rest
+  // to the last clone's destroy. Guarded by g_clone_mu.
+  mx_encoder *owner = nullptr;  // a clone's owner
+  int live_clones = 0;          // an owner's clones not yet destroyed
+  bool orphaned = false;        // an owner destroyed while clones were alive
   // Bumped by every tensor set: the fused gated FFN's interleaved copies are
   // current while their glu_gen equals it.
   uint64_t wgen = 1;
@@ -119,6 +127,8 @@ struct mx_encoder {
 };
 
 namespace {
+
+std::mutex g_clone_mu;
 
 template <typename T>
 void free_dev(T *&p) {
@@ -594,6 +604,82 @@ int stage_i8_panel(mx_ctx *ctx, const int8_t *kn, int64_t K, int64_t N, int8_t *
   return MX_OK;
 }
 
+void free_weights(mx_encoder *enc) {
+  for (auto &l : enc->layers) {
+    for (auto &p : l.w) free_dev(p);
+    for (auto &p : l.b) free_dev(p);
+    for (auto &p : l.ln) free_dev(p);
+    for (auto &p : l.wq) free_dev(p);
+    for (auto &p : l.ws) free_dev(p);
+    for (auto &p : l.ias) free_dev(p);
+    free_dev(l.wg);
+    free_dev(l.wqg);
+    free_dev(l.bg);
+    free_dev(l.wsg);
+  }
+  for (auto &p : enc->emb_ln) free_dev(p);
+  for (auto &p : enc->fin_ln) free_dev(p);
+  free_dev(enc->word);
+  free_dev(enc->pos);
+  free_dev(enc->type);
+  free_dev(enc->patch_w);
+  free_dev(enc->head_w);
+  free_dev(enc->patch_b);
+  free_dev(enc->head_b);
+  for (auto &p : enc->conv_w) free_dev(p);
+  for (auto &p : enc->conv_b) free_dev(p);
+  free_dev(enc->cls_tok);
+  free_dev(enc->front_pos);
+}
+
+void free_workspace(mx_encoder *enc) {
+  free_dev(enc->xb);
+  free_dev(enc->qkv);
+  free_dev(enc->ctxb);
+  free_dev(enc->up);
+  free_dev(enc->proj);
+  free_dev(enc->emb);
+  free_dev(enc->xq);
+  free_dev(enc->sa);
+  free_dev(enc->glu);
+  free_dev(enc->rope_cos);
+  free_dev(enc->rope_sin);
+  free_dev(enc->add_mask);
+  free_dev(enc->kv_len);
+  free_dev(enc->seq_start);
+  free_dev(enc->row_pos);
+  free_dev(enc->f_rows);
+  free_dev(enc->f_cls);
+  free_dev(enc->f_mel);
+  free_dev(enc->f_out1);
+  free_dev(enc->f_patch);
+  free_dev(enc->f_x);
+  for (auto ev : enc->events) (void)hipEventDestroy(ev);
+  enc->events.clear();
+  enc->ev_cat.clear();
+  for (auto &ev : enc->ev_all)
+    if (ev) {
+      (void)hipEventDestroy(ev);
+      ev = nullptr;
+    }
+  enc->ws_rows = enc->ws_batch = enc->ws_mask_rows = enc->fw_batch = 0;
+  enc->rope_rows = 0;
+}
+
+// The refusal of a weight change on an owner whose clones still borrow them.
+int refuse_if_cloned(const mx_encoder *enc, const char *what) {
+  int n = 0;
+  {
+    std::lock_guard<std::mutex> lk(g_clone_mu);
+    n = enc->live_clones;
+  }
+  if (n > 0)
+    return fail(MX_E_STATE, std::string(what) + ": " + std::to_string(n) +
+                                " lane clone(s) borrow this encoder's weights; destroy them "
+                                "before changing the weights");
+  return MX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -652,60 +738,28 @@ int mx_encoder_create(mx_ctx *ctx, const mx_encoder_desc *desc, mx_encoder **out
 
 void mx_encoder_destroy(mx_encoder *enc) {
   if (!enc) return;
-  if (use_device(enc->ctx) == MX_OK) {
-    if (enc->owns_weights) {
-      for (auto &l : enc->layers) {
-        for (auto &p : l.w) free_dev(p);
-        for (auto &p : l.b) free_dev(p);
-        for (auto &p : l.ln) free_dev(p);
-        for (auto &p : l.wq) free_dev(p);
-        for (auto &p : l.ws) free_dev(p);
-        for (auto &p : l.ias) free_dev(p);
-        free_dev(l.wg);
-        free_dev(l.wqg);
-        free_dev(l.bg);
-        free_dev(l.wsg);
-      }
-      for (auto &p : enc->emb_ln) free_dev(p);
-      for (auto &p : enc->fin_ln) free_dev(p);
-      free_dev(enc->word);
-      free_dev(enc->pos);
-      free_dev(enc->type);
-      free_dev(enc->patch_w);
-      free_dev(enc->head_w);
-      free_dev(enc->patch_b);
-      free_dev(enc->head_b);
-      for (auto &p : enc->conv_w) free_dev(p);
-      for (auto &p : enc->conv_b) free_dev(p);
-      free_dev(enc->cls_tok);
-      free_dev(enc->front_pos);
+  // An owner with live clones keeps its weights (the clones read them) until
+  // the last clone goes; a clone's destroy may be that moment.
+  mx_encoder *orphan = nullptr;
+  bool keep_weights = false;
+  {
+    std::lock_guard<std::mutex> lk(g_clone_mu);
+    if (enc->owns_weights && enc->live_clones > 0) {
+      enc->orphaned = true;
+      keep_weights = true;
+    } else if (enc->owner && --enc->owner->live_clones == 0 && enc->owner->orphaned) {
+      orphan = enc->owner;
     }
-    free_dev(enc->xb);
-    free_dev(enc->qkv);
-    free_dev(enc->ctxb);
-    free_dev(enc->up);
-    free_dev(enc->proj);
-    free_dev(enc->emb);
-    free_dev(enc->xq);
-    free_dev(enc->sa);
-    free_dev(enc->glu);
-    free_dev(enc->rope_cos);
-    free_dev(enc->rope_sin);
-    free_dev(enc->add_mask);
-    free_dev(enc->kv_len);
-    free_dev(enc->seq_start);
-    free_dev(enc->row_pos);
-    free_dev(enc->f_rows);
-    free_dev(enc->f_cls);
-    free_dev(enc->f_mel);
-    free_dev(enc->f_out1);
-    free_dev(enc->f_patch);
-    free_dev(enc->f_x);
-    for (auto ev : enc->events) (void)hipEventDestroy(ev);
-    for (auto ev : enc->ev_all)
-      if (ev) (void)hipEventDestroy(ev);
   }
-  delete enc;
+  if (use_device(enc->ctx) == MX_OK) {
+    free_workspace(enc);
+    if (!keep_weights && enc->owns_weights) free_weights(enc);
+  }
+  if (!keep_weights) delete enc;
+  if (orphan) {
+    if (use_device(orphan->ctx) == MX_OK) free_weights(orphan);
+    delete orphan;
+  }
 }
 
 }  // extern "C"
@@ -725,6 +779,12 @@ int mx_encoder_clone(mx_encoder *enc, mx_encoder **out) {
   c->ctx = enc->ctx;
   c->desc = enc->desc;
   c->owns_weights = false;
+  {
+    std::lock_guard<std::mutex> lk(g_clone_mu);
+    // A clone of a clone borrows from the same owner.
+    c->owner = enc->owns_weights ? enc : enc->owner;
+    ++c->owner->live_clones;
+  }
   c->layers = enc->layers;
   c->wgen = enc->wgen;
   c->fuse_glu = enc->fuse_glu;
@@ -757,6 +817,7 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
   if (!enc->owns_weights)
     return fail(MX_E_STATE, "encoder_set: a lane clone borrows its parent's weights; set them "
                             "on the parent");
+  if (int r = refuse_if_cloned(enc, "encoder_set")) return r;
   ++enc->wgen;
   int rc = use_device(enc->ctx);
   if (rc) return rc;
@@ -1228,6 +1289,7 @@ int mx_encoder_set_panel(mx_encoder *enc, const char *name_c, const uint16_t *pa
   if (!enc || !name_c || !panel) return fail(MX_E_INVALID, "encoder_set_panel: null argument");
   if (!enc->owns_weights)
     return fail(MX_E_STATE, "encoder_set_panel: a lane clone borrows its parent's weights");
+  if (int r = refuse_if_cloned(enc, "encoder_set_panel")) return r;
   ++enc->wgen;
   const std::string name(name_c);
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
@@ -1355,6 +1417,11 @@ int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
         p = e;
       }
     }
+  }
+  // The gated activation is read for every gated container, whatever its
+  // arch (set_model_shape, app_state.hpp:534-553): a missing key means SiLU
+  // except on gte, whose containers must carry it; an unknown value refuses.
+  if (gated != MX_GATED_NONE) {
     std::string act;
     if (!npue_config(f, "activation", act)) {
       if (gte)

@@ -102,6 +102,12 @@ int gemm_i8_checked(mx_stream *s, const int8_t *A, const float *a_scale, int64_t
                     int64_t lda, const int8_t *Wt, const float *wscale, int64_t N,
                     const float *bias, int epilogue, const float *residual, void *C,
                     int c_dtype, int64_t ldc) {
+  // The 32-bit row offsets come first: a shape the kernel cannot address is
+  // refused whatever else is wrong with the call.
+  if (!mxk::lds_offsets_fit(lda, K, 1))
+    return fail(MX_E_UNSUPPORTED, "gemm_i8: lda " + std::to_string(lda) + " / K " +
+                                      std::to_string(K) + " -- the int8 GEMM addresses a tile's "
+                                      "rows by 32-bit byte offsets (lda and K below 2^24)");
   if (!s) return fail(MX_E_INVALID, "gemm_i8: null stream");
   if (!A || !Wt || !C) return fail(MX_E_INVALID, "gemm_i8: null A, weight or C");
   if (M <= 0 || N <= 0 || K <= 0) return fail(MX_E_INVALID, "gemm_i8: zero dimension");

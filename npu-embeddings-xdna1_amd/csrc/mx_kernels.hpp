@@ -90,6 +90,14 @@ inline int persistent_grid(int ntiles, int grid) {
   if (g >= 16 && (g & 7)) g = (g + 7) & ~7;
   return g;
 }
+// The LDS-pipelined kernel addresses a lane's operand row within a tile as a
+// 32-bit byte offset from the tile origin: row r (< 256) of A at r * lda * esz
+// and of Wt at r * K * esz, plus at most 128 bytes of K. Both must stay below
+// 2^32, i.e. lda * esz and K * esz below 2^24.
+inline bool lds_offsets_fit(int64_t lda, int64_t K, int esz) {
+  const int64_t lim = (int64_t)1 << 24;
+  return lda * esz < lim && K * esz < lim;
+}
 
 // int8 W8A8 (k_gemm_i8.hip): C[M,N] = epi(fma(float(Aq @ Wq^T) * a_scale[m],
 // wscale[n], bias[n])) (+ residual), or the raw int32 product (c_dtype 2).

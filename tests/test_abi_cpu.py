@@ -93,3 +93,22 @@ def test_no_silent_cpu_fallback(L):
                        timeout=120)
     rc = int(r.stdout.split()[0])
     assert rc != 0
+
+
+def test_gemm_rows_beyond_32bit_offsets_leave_the_lds_kernel(L):
+    """The LDS-pipelined GEMM addresses a tile's rows by 32-bit byte offsets
+    (row < 256 times lda or K, times the element size). A bf16 call whose
+    lda or K reaches 2^23 elements goes to the register-staged kernel (64-bit
+    indexing); an int8 call whose lda or K reaches 2^24 is refused by name
+    before anything is launched."""
+    plan = lambda K: L.mx_gemm_plan_for(1024, 1024, K, mxenc.MX_BF16, 0, 0).decode()  # noqa: E731
+    assert plan((1 << 23) - 64).startswith("lds_")
+    assert plan(1 << 23).startswith("staged_")
+    # (s, A, a_scale, M, K, lda, Wt, wscale, N, bias, epilogue, residual, C, c_dtype, ldc)
+    args = [None, None, None, 1024, 1024, 1 << 24, None, None, 1024, None, 0, None, None,
+            mxenc.MX_BF16, 1024]
+    assert L.mx_gemm_i8_wt(*args) == -3
+    msg = L.mx_last_error().decode()
+    assert "32-bit byte offsets" in msg and "2^24" in msg
+    args[5] = 1024  # in range: the next refusal is the missing stream
+    assert L.mx_gemm_i8_wt(*args) == -1 and "null stream" in L.mx_last_error().decode()

@@ -139,3 +139,46 @@ def test_encoder_from_npue_refuses_int4_mixed_and_missing_tensors(tmp_path, ctx)
     with pytest.raises(mxenc.MxError, match="no tensor named layer.0.ln2.bias"):
         mxenc.Encoder.from_npue(ctx, f)
     f.close()
+
+
+@pytest.mark.parametrize("act,gated", [("gelu", mxenc.MX_GATED_GELU_ERF), (None, mxenc.MX_GATED_SILU)])
+def test_gated_bert_container_reads_its_activation(tmp_path, ctx, act, gated):
+    """A gated FFN on the plain BERT arch (absolute positions) takes its gate
+    activation from the container's 'activation' key, SiLU when the key is
+    missing, as set_model_shape reads it for every gated arch but gemma."""
+    m = dict(synth.make_model("gte", layers=2, ln_random=True))
+    m["rope"] = False
+    m.pop("rope_inv_freq", None)
+    m["gated"] = gated
+    extra = {"gated_ffn": True}
+    c = nw.bert_container(m, 64, 64, (8, 8), extra_config=extra)
+    if act is None:
+        c.config.pop("activation", None)
+    else:
+        c.config["activation"] = act
+    path = str(tmp_path / "gated.npue")
+    c.write(path)
+    f = mxenc.Npue(path)
+    a_enc = mxenc.Encoder.from_npue(ctx, f)
+    b_enc = mxenc.Encoder(ctx, m)
+    ids, am, _ = synth.make_text_inputs(m, batch=4, seq=128)
+    a = gpu_embed(ctx, a_enc, ids, am)
+    b = gpu_embed(ctx, b_enc, ids, am)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    a_enc.close()
+    b_enc.close()
+    f.close()
+
+
+def test_gated_bert_container_unknown_activation_refused(tmp_path, ctx):
+    m = dict(synth.make_model("gte", layers=1))
+    m["rope"] = False
+    m.pop("rope_inv_freq", None)
+    c = nw.bert_container(m, 64, 64, (8, 8), extra_config={"gated_ffn": True,
+                                                           "activation": "relu"})
+    path = str(tmp_path / "relu.npue")
+    c.write(path)
+    f = mxenc.Npue(path)
+    with pytest.raises(mxenc.MxError, match="unknown gated-FFN activation 'relu'"):
+        mxenc.Encoder.from_npue(ctx, f)
+    f.close()

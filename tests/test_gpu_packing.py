@@ -53,6 +53,13 @@ def test_mean_pooling_holes_and_edge_lengths(ctx):
     am[3] = 0.0
     am[3, 0] = 1.0          # a single token
     am[4] = 1.0             # full length
+    # negative weights past the last positive one: masked keys, but pooled
+    # (pool_rows weights every row with m != 0), so packing keeps their rows
+    am[5, 40:] = 0.0
+    am[5, 45] = -0.5
+    am[5, 60] = -1.0
+    am[6] = 0.0             # no positive weight at all: uniform attention
+    am[6, 7] = -1.0
     enc = mxenc.Encoder(ctx, m)
     packed = _embed(ctx, enc, ids, am, True)
     padded = _embed(ctx, enc, ids, am, False)

@@ -78,3 +78,35 @@ def test_service_and_clone_refusals(ctx, enc):
     rc = mxenc.lib().mx_encoder_set(h.value, b"layer.0.ln1.bias", a.ctypes.data, mxenc.MX_F32, 8)
     assert rc == -4 and b"borrows" in mxenc.lib().mx_last_error()
     mxenc.lib().mx_encoder_destroy(h.value)
+
+
+def test_clone_pins_the_owners_weights(ctx, model):
+    """While a lane clone is alive its owner refuses weight changes by name
+    (the clone reads the owner's device tensors); destroying the owner first
+    leaves the clone running on the same weights, and the last clone's
+    destroy frees them."""
+    import ctypes
+    ids, am, _ = synth.make_text_inputs(model, batch=6)
+    owner = mxenc.Encoder(ctx, model)
+    want = gpu_embed(ctx, owner, ids, am)
+    lane = owner.clone(ctx)
+    ln = np.zeros(model["hidden"], np.float32)
+    rc = mxenc.lib().mx_encoder_set(owner.handle, b"layer.0.ln1.bias", ln.ctypes.data,
+                                    mxenc.MX_F32, ln.size)
+    assert rc == -4 and b"lane clone(s) borrow" in mxenc.lib().mx_last_error()
+    h = ctypes.c_void_p()
+    mxenc.check(mxenc.lib().mx_encoder_clone(lane.handle, ctypes.byref(h)))  # clone of a clone
+    rc = mxenc.lib().mx_encoder_set(owner.handle, b"layer.0.ln1.bias", ln.ctypes.data,
+                                    mxenc.MX_F32, ln.size)
+    assert rc == -4 and b"2 lane clone(s)" in mxenc.lib().mx_last_error()
+    mxenc.lib().mx_encoder_destroy(h.value)
+    owner.close()  # the weights stay: the lane still borrows them
+    got = gpu_embed(ctx, lane, ids, am)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    lane.close()
+    # an owner whose clones are gone takes weight changes again
+    owner = mxenc.Encoder(ctx, model)
+    lane = owner.clone(ctx)
+    lane.close()
+    owner.set("layer.0.ln1.bias", ln)
+    owner.close()
