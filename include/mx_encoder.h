@@ -237,6 +237,25 @@ int mx_stage_weight_i8(mx_ctx *ctx, const int8_t *kn_host, const float *wscale_h
 int mx_stage_weight_panel_i8(mx_ctx *ctx, const int8_t *panel_host, const float *wscale_host,
                              const float *asmooth_host, int64_t K, int64_t N, int64_t tile_k,
                              int64_t tile_n, int64_t mac_s, int64_t mac_t, int *slot);
+/* The same from a container's I4 operand (int4 storage over the int8
+ * datapath; npue::gemm_b_panel's I4 branch, common/int4_panel.hpp:77-246):
+ * packed_host holds K * N / 2 bytes of the block_panel run, two values per
+ * byte (element f in nibble f % 2 of byte f / 2, low nibble first), gscale_host
+ * the .gscale sidecar F32 [ceil(K / g), N] with g = int4_group (0: g = K).
+ * Each nibble t (sign-extended) becomes q = clip(rint(t * gscale[k / g][n]),
+ * -127, 127) on the GPU -- the int8 panel an I8 container carries -- which is
+ * then staged as mx_stage_weight_panel_i8 stages it. Refusals as the
+ * reference's: an odd nibble count, no tiling, int4_group < 0. */
+int mx_stage_weight_panel_i4(mx_ctx *ctx, const uint8_t *packed_host, const float *gscale_host,
+                             int64_t int4_group, const float *wscale_host,
+                             const float *asmooth_host, int64_t K, int64_t N, int64_t tile_k,
+                             int64_t tile_n, int64_t mac_s, int64_t mac_t, int *slot);
+/* The widening alone, device to device on stream s: the I4 run (K * N / 2
+ * bytes) and gscale in, the int8 run of the same tiling out (K * N bytes,
+ * the bytes gemm_b_panel hands Design::stage, int4_panel.hpp:183-246). */
+int mx_widen_panel_i4(mx_stream *s, const uint8_t *packed, const float *gscale,
+                      int64_t int4_group, int64_t K, int64_t N, int64_t tile_k, int64_t tile_n,
+                      int64_t mac_s, int64_t mac_t, int8_t *out);
 /* The device vectors of a staged int8 operand: wscale [N] and ias [K] (the
  * ias to quantise this GEMM's A with). */
 int mx_weight_i8_scales(mx_ctx *ctx, int slot, const float **wscale, const float **ias);
@@ -546,8 +565,9 @@ int mx_encoder_set_panel(mx_encoder *enc, const char *name, const uint16_t *pane
  * polynomial GELU of a plain FFN (gelu_cpu), as BertEncoder hard-codes them.
  * Every tensor is set from the mapping: pre-tiled BF16 GEMM operands through
  * mx_encoder_set_panel, and an --int8 pack's pre-tiled I8 operands with their
- * .wscale/.asmooth through the int8 staging of mx_stage_weight_panel_i8 (the
- * int4 pack's I4 nibbles are refused by name). A "host" container (F32
+ * .wscale/.asmooth through the int8 staging of mx_stage_weight_panel_i8, and
+ * an --int4 pack's I4 operands (with .gscale and config int4_group) widened
+ * on the GPU and staged likewise (mx_stage_weight_panel_i4). A "host" container (F32
  * row-major operands) is refused for the GEMM, as the reference refuses
  * --npu-ops gemm on one (bert_encoder.cpp:79-87). The encoder is ready on
  * MX_OK. */

@@ -2,8 +2,9 @@
 
     python npu-embeddings-xdna1_amd/build.py [--jobs N]
 
-Every source under csrc/ is compiled with hipcc for gfx950 only and linked
-into _build/libmx_encoder.so beside this file. Packed-fp32 instructions are
+Every library source under csrc/ is compiled with hipcc for gfx950 only and
+linked into _build/libmx_encoder.so beside this file; csrc/probe_mfma_clock.hip
+becomes the measurement program _build/probe_mfma_clock. Packed-fp32 instructions are
 disabled for all device code (-packed-fp32-ops); hipcc's host pass warns that
 it does not know that feature, which is harmless.
 """
@@ -59,7 +60,23 @@ def build(jobs=None, verbose=False):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
+    build_probe()
     return LIB
+
+
+PROBE = os.path.join(OUT, "probe_mfma_clock")
+
+
+def build_probe():
+    """The clock / MFMA / LDS measurement program (csrc/probe_mfma_clock.hip),
+    a standalone executable beside the library."""
+    cmd = [HIPCC] + [f for f in FLAGS if f != "-fPIC"] + [
+        os.path.join(CSRC, "probe_mfma_clock.hip"), "-o", PROBE + ".tmp"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("hipcc failed on probe_mfma_clock.hip:\n" + r.stdout + r.stderr)
+    os.replace(PROBE + ".tmp", PROBE)
+    return PROBE
 
 
 if __name__ == "__main__":

@@ -1509,30 +1509,38 @@ int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
       if (!t.logical.empty() && t.logical != t.padded)
         return refuse(fail(MX_E_INVALID, n + ": logical and padded shapes differ; the GEMM "
                                              "needs them equal (repack)"));
-      if (t.dtype == "I4")
-        return refuse(fail(MX_E_UNSUPPORTED, n + ": I4 operand -- the int4 container's nibble "
-                                             "widening is not built in this backend"));
-      const bool i8 = t.dtype == "I8";
+      // I4 is storage over the int8 datapath (common/int4_panel.hpp): the
+      // nibbles are widened to the int8 panel on the GPU, then staged as I8.
+      const bool i4 = t.dtype == "I4";
+      const bool i8 = t.dtype == "I8" || i4;
       if ((t.dtype != "BF16" && !i8) || !t.block_panel)
         return refuse(fail(MX_E_INVALID, n + ": " + t.dtype + " without a block_panel "
-                                             "layout; a pre-tiled BF16 or I8 operand is wanted"));
+                                             "layout; a pre-tiled BF16, I8 or I4 operand is "
+                                             "wanted"));
       const int64_t K = t.padded[0], N = t.padded[1];
-      if (t.nbytes != static_cast<uint64_t>(K * N * (i8 ? 1 : 2)))
+      if (i4 && (K * N) % 2)
+        return refuse(fail(MX_E_INVALID, n + ": I4 payload of [" + std::to_string(K) + "," +
+                                             std::to_string(N) + "] holds an odd number of "
+                                             "nibbles; two int4 values make a byte"));
+      const uint64_t want = static_cast<uint64_t>(i4 ? K * N / 2 : K * N * (i8 ? 1 : 2));
+      if (t.nbytes != want)
         return refuse(fail(MX_E_INVALID, n + ": " + std::to_string(t.nbytes) + " bytes for a [" +
                                              std::to_string(K) + "," + std::to_string(N) +
-                                             "] " + (i8 ? "int8" : "bf16") + " operand"));
+                                             "] " + (i4 ? "int4" : i8 ? "int8" : "bf16") +
+                                             " operand (" + std::to_string(want) + " wanted)"));
       if (!i8) {
         rc = mx_encoder_set_panel(enc, n.c_str(), static_cast<const uint16_t *>(t.data), K, N,
                                   t.tile_k, t.tile_n, t.mac_s, t.mac_t);
         if (rc) return refuse(rc);
         continue;
       }
-      // An int8 design's operand (tools/lib/gemm_i8.py's scheme): the panel,
-      // its per-column .wscale and per-row .asmooth, all from the mapping.
+      // An int8 design's operand (tools/lib/gemm_i8.py's scheme; gemm_i4.py's
+      // for I4): the panel, its per-column .wscale and per-row .asmooth, all
+      // from the mapping.
       const TensorRecView ws = npue_tensor(f, n + ".wscale");
       const TensorRecView sm = npue_tensor(f, n + ".asmooth");
       if (!ws.found || !sm.found)
-        return refuse(fail(MX_E_INVALID, n + ": an I8 operand without its " +
+        return refuse(fail(MX_E_INVALID, n + ": an " + t.dtype + " operand without its " +
                                              (ws.found ? ".asmooth" : ".wscale") +
                                              " -- the container is not a complete int8 pack"));
       if (ws.dtype != "F32" || sm.dtype != "F32" || ws.nbytes != static_cast<uint64_t>(N * 4) ||
@@ -1540,9 +1548,44 @@ int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
         return refuse(fail(MX_E_INVALID, n + ": .wscale must be F32 [" + std::to_string(N) +
                                              "] and .asmooth F32 [" + std::to_string(K) + "]"));
       I8Operand op;
-      rc = stage_i8(ctx, static_cast<const int8_t *>(t.data), static_cast<const float *>(ws.data),
-                    static_cast<const float *>(sm.data), K, N, t.tile_k, t.tile_n, t.mac_s,
-                    t.mac_t, &op);
+      if (i4) {
+        // The group size is config, checked against the sidecar's height
+        // (int4_panel.hpp:127-173).
+        std::string gtext;
+        if (!npue_config(f, "int4_group", gtext))
+          return refuse(fail(MX_E_INVALID, n + ": I4 payload, but the container states no "
+                                               "int4_group -- the group size says which rows "
+                                               "of K share a scale"));
+        int64_t group = 0;
+        if ((rc = cfg_int("int4_group", group))) return refuse(rc);
+        if (group < 0)
+          return refuse(fail(MX_E_INVALID, n + ": config int4_group is " +
+                                               std::to_string(group) + "; rows per group must "
+                                               "be >= 0, where 0 means one group over the "
+                                               "whole K"));
+        const int64_t g = group == 0 ? K : group, G = (K + g - 1) / g;
+        const TensorRecView gs = npue_tensor(f, n + ".gscale");
+        if (!gs.found)
+          return refuse(fail(MX_E_INVALID, n + ": I4 payload but no " + n + ".gscale in the "
+                                               "container -- the group scale is the only thing "
+                                               "that puts a nibble back in units of .wscale"));
+        if (gs.dtype != "F32" || gs.padded.size() != 2 || gs.padded[0] != G ||
+            gs.padded[1] != N || gs.nbytes != static_cast<uint64_t>(G * N * 4))
+          return refuse(fail(MX_E_INVALID, n + ".gscale is " + gs.dtype + " with " +
+                                               std::to_string(gs.nbytes) + " bytes but "
+                                               "int4_group=" + std::to_string(group) +
+                                               " over K=" + std::to_string(K) + " needs F32 [" +
+                                               std::to_string(G) + "," + std::to_string(N) +
+                                               "]"));
+        rc = stage_i4(ctx, static_cast<const uint8_t *>(t.data),
+                      static_cast<const float *>(gs.data), group,
+                      static_cast<const float *>(ws.data), static_cast<const float *>(sm.data), K,
+                      N, t.tile_k, t.tile_n, t.mac_s, t.mac_t, &op);
+      } else {
+        rc = stage_i8(ctx, static_cast<const int8_t *>(t.data),
+                      static_cast<const float *>(ws.data), static_cast<const float *>(sm.data), K,
+                      N, t.tile_k, t.tile_n, t.mac_s, t.mac_t, &op);
+      }
       if (rc) return refuse(rc);
       const int64_t d = enc->desc.hidden, fw = enc->desc.ffn;
       const int64_t Ks[4] = {d, d, d, fw}, Ns[4] = {3 * d, d, gated ? 2 * fw : fw, d};

@@ -98,6 +98,91 @@ int stage_i8(mx_ctx *ctx, const int8_t *kn_host, const float *wscale_host,
   return MX_OK;
 }
 
+// The checks gemm_b_panel makes of an I4 operand before it widens it
+// (int4_panel.hpp:87-173): a two-dimensional [K, N] with an even number of
+// nibbles, a block_panel tiling, int4_group >= 0 (0: one group over K) and a
+// gscale of ceil(K / group) rows.
+int check_i4(const std::string &what, int64_t K, int64_t N, int64_t group, int64_t tile_k,
+             int64_t tile_n, int64_t mac_s, int64_t mac_t) {
+  if (K <= 0 || N <= 0 || (K * N) % 2)
+    return fail(MX_E_INVALID, what + ": I4 payload of [" + std::to_string(K) + "," +
+                                  std::to_string(N) + "] holds an odd number of nibbles; two "
+                                  "int4 values make a byte");
+  int rc = check_panel(what, K, N, tile_k, tile_n, mac_s, mac_t);
+  if (rc) return rc;
+  if (group < 0)
+    return fail(MX_E_INVALID, what + ": int4_group is " + std::to_string(group) +
+                                  "; rows per group must be >= 0, where 0 means one group over "
+                                  "the whole K");
+  return MX_OK;
+}
+
+int stage_i4(mx_ctx *ctx, const uint8_t *packed_host, const float *gscale_host, int64_t group,
+             const float *wscale_host, const float *asmooth_host, int64_t K, int64_t N,
+             int64_t tile_k, int64_t tile_n, int64_t mac_s, int64_t mac_t, I8Operand *out) {
+  if (!packed_host || !gscale_host || !wscale_host || !asmooth_host)
+    return fail(MX_E_INVALID, "stage_weight_panel_i4: null payload, gscale, wscale or asmooth");
+  int rc = check_i4("stage_weight_panel_i4", K, N, group, tile_k, tile_n, mac_s, mac_t);
+  if (rc) return rc;
+  if (K % 16)
+    return fail(MX_E_INVALID, "stage_weight_panel_i4: K = " + std::to_string(K) +
+                                  " is not a multiple of 16 (the int8 GEMM reads K in "
+                                  "16-byte chunks)");
+  rc = use_device(ctx);
+  if (rc) return rc;
+  const int64_t g = group == 0 ? K : group, G = (K + g - 1) / g;
+  uint8_t *packed = nullptr;
+  float *gs = nullptr;
+  int8_t *tiled = nullptr;
+  rc = upload(packed_host, static_cast<size_t>(K * N / 2), &packed,
+              "stage_weight_panel_i4: payload");
+  if (!rc) rc = upload(gscale_host, static_cast<size_t>(G * N), &gs,
+                       "stage_weight_panel_i4: gscale");
+  if (!rc) {
+    void *p = nullptr;
+    const hipError_t e = hipMalloc(&p, static_cast<size_t>(K) * N);
+    if (e != hipSuccess) rc = hip_fail(e, "stage_weight_panel_i4: hipMalloc");
+    tiled = static_cast<int8_t *>(p);
+  }
+  if (!rc) {
+    hipError_t e = mxk::widen_i4_panel(packed, K, N, (int)tile_k, (int)tile_n, (int)mac_s,
+                                       (int)mac_t, gs, g, tiled, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) rc = hip_fail(e, "stage_weight_panel_i4: widen");
+  }
+  if (packed) (void)hipFree(packed);
+  if (gs) (void)hipFree(gs);
+  // The widened run is exactly an I8 container's run: the scales as
+  // stage_i8 stages them (1/asmooth once, in fp32), the run untiled into the
+  // [N, K] panel.
+  I8Operand op;
+  if (!rc) {
+    std::vector<float> ias(static_cast<size_t>(K));
+    for (int64_t k = 0; k < K; ++k) ias[k] = 1.0f / asmooth_host[k];
+    rc = upload(wscale_host, static_cast<size_t>(N), &op.wscale,
+                "stage_weight_panel_i4: wscale");
+    if (!rc) rc = upload(ias.data(), ias.size(), &op.ias, "stage_weight_panel_i4: asmooth");
+  }
+  if (!rc) {
+    void *wq = nullptr;
+    hipError_t e = hipMalloc(&wq, static_cast<size_t>(K) * N);
+    if (e == hipSuccess) {
+      op.wq = static_cast<int8_t *>(wq);
+      e = mxk::untile_panel_i8(tiled, K, N, (int)tile_k, (int)tile_n, (int)mac_s, (int)mac_t,
+                               op.wq, nullptr);
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) rc = hip_fail(e, "stage_weight_panel_i4: untile");
+  }
+  if (tiled) (void)hipFree(tiled);
+  if (rc) {
+    free_i8(op);
+    return rc;
+  }
+  *out = op;
+  return MX_OK;
+}
+
 int gemm_i8_checked(mx_stream *s, const int8_t *A, const float *a_scale, int64_t M, int64_t K,
                     int64_t lda, const int8_t *Wt, const float *wscale, int64_t N,
                     const float *bias, int epilogue, const float *residual, void *C,
@@ -267,6 +352,33 @@ int mx_stage_weight_panel_i8(mx_ctx *ctx, const int8_t *panel_host, const float 
                           mac_s, mac_t, &op);
   if (rc) return rc;
   return push_slot(ctx, op, K, N, slot);
+}
+
+int mx_stage_weight_panel_i4(mx_ctx *ctx, const uint8_t *packed_host, const float *gscale_host,
+                             int64_t int4_group, const float *wscale_host,
+                             const float *asmooth_host, int64_t K, int64_t N, int64_t tile_k,
+                             int64_t tile_n, int64_t mac_s, int64_t mac_t, int *slot) {
+  clear_error();
+  if (!ctx || !slot) return fail(MX_E_INVALID, "mx_stage_weight_panel_i4: null argument");
+  I8Operand op;
+  const int rc = stage_i4(ctx, packed_host, gscale_host, int4_group, wscale_host, asmooth_host,
+                          K, N, tile_k, tile_n, mac_s, mac_t, &op);
+  if (rc) return rc;
+  return push_slot(ctx, op, K, N, slot);
+}
+
+int mx_widen_panel_i4(mx_stream *s, const uint8_t *packed, const float *gscale,
+                      int64_t int4_group, int64_t K, int64_t N, int64_t tile_k, int64_t tile_n,
+                      int64_t mac_s, int64_t mac_t, int8_t *out) {
+  clear_error();
+  if (!s || !packed || !gscale || !out)
+    return fail(MX_E_INVALID, "mx_widen_panel_i4: null argument");
+  int rc = check_i4("mx_widen_panel_i4", K, N, int4_group, tile_k, tile_n, mac_s, mac_t);
+  if (rc) return rc;
+  const hipError_t e = mxk::widen_i4_panel(packed, K, N, (int)tile_k, (int)tile_n, (int)mac_s,
+                                           (int)mac_t, gscale, int4_group == 0 ? K : int4_group,
+                                           out, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "mx_widen_panel_i4");
 }
 
 int mx_weight_i8_scales(mx_ctx *ctx, int slot, const float **wscale, const float **ias) {

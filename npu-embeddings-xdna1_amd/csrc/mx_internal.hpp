@@ -68,6 +68,15 @@ int stage_i8(mx_ctx *ctx, const int8_t *kn_host, const float *wscale_host,
              const float *asmooth_host, int64_t K, int64_t N, int64_t tile_k, int64_t tile_n,
              int64_t mac_s, int64_t mac_t, I8Operand *out);
 void free_i8(I8Operand &op);
+// The same from a container's I4 run (K * N / 2 bytes) and its .gscale
+// ([ceil(K / group), N], group 0 = K): widened on the GPU to the int8 run of
+// the same tiling (gemm_b_panel's I4 branch, int4_panel.hpp:77-246), then
+// staged as an I8 operand.
+int check_i4(const std::string &what, int64_t K, int64_t N, int64_t group, int64_t tile_k,
+             int64_t tile_n, int64_t mac_s, int64_t mac_t);
+int stage_i4(mx_ctx *ctx, const uint8_t *packed_host, const float *gscale_host, int64_t group,
+             const float *wscale_host, const float *asmooth_host, int64_t K, int64_t N,
+             int64_t tile_k, int64_t tile_n, int64_t mac_s, int64_t mac_t, I8Operand *out);
 int gemm_i8_checked(mx_stream *s, const int8_t *A, const float *a_scale, int64_t M, int64_t K,
                     int64_t lda, const int8_t *Wt, const float *wscale, int64_t N,
                     const float *bias, int epilogue, const float *residual, void *C,

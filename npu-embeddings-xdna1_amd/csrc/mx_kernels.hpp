@@ -150,6 +150,12 @@ hipError_t untile_panel(const uint16_t *panel, int64_t K, int64_t N, int tile_k,
                         int mac_s, int mac_t, uint16_t *wt, hipStream_t s);
 hipError_t untile_panel_i8(const int8_t *panel, int64_t K, int64_t N, int tile_k, int tile_n,
                            int mac_s, int mac_t, int8_t *wt, hipStream_t s);
+// An I4 container run (K * N / 2 bytes, two values per byte, low nibble
+// first) -> the int8 run of the same tiling, each value widened by its
+// group's gscale ([ceil(K / group), N] fp32): int4_panel.hpp:183-246.
+hipError_t widen_i4_panel(const uint8_t *packed, int64_t K, int64_t N, int tile_k, int tile_n,
+                          int mac_s, int mac_t, const float *gscale, int64_t group, int8_t *out,
+                          hipStream_t s);
 // The plan the launcher would pick (for tests and reports): tile, slab depth
 // in K elements, wave tile and ring slots, e.g.
 // "lds_256x256x64_w64x128_ns2_persistent". gemm_config_name is the bf16

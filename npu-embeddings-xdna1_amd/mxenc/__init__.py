@@ -133,6 +133,9 @@ SIGNATURES = {
     "mx_stage_weight_i8": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, ctypes.POINTER(_int)]),
     "mx_stage_weight_panel_i8": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                         ctypes.POINTER(_int)]),
+    "mx_stage_weight_panel_i4": (_int, [_vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
+                                        _i64, _i64, ctypes.POINTER(_int)]),
+    "mx_widen_panel_i4": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "mx_weight_i8_scales": (_int, [_vp, _int, ctypes.POINTER(_vp), ctypes.POINTER(_vp)]),
     "mx_quantise_a_int8": (_int, [_vp, _vp, _int, _i64, _i64, _vp, _vp, _vp]),
     "mx_gemm_i8": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp, _int, _vp, _vp, _int,
@@ -330,6 +333,13 @@ def gemm_i8(ctx, A, a_scale, M, K, lda, slot, bias, epilogue, residual, C, ldc):
     cd = _np_dtype_code(np.empty(0, C.dtype))
     check(lib().mx_gemm_i8(ctx.stream, _p(A), _p(a_scale), M, K, lda, slot, _p(bias), epilogue,
                            _p(residual), _p(C), cd, ldc))
+
+
+def widen_panel_i4(ctx, packed, gscale, int4_group, K, N, tile_k, tile_n, mac_s, mac_t, out):
+    """The I4 run (device, K*N/2 bytes) and .gscale (device) -> the int8 run of
+    the same tiling (device, K*N bytes)."""
+    check(lib().mx_widen_panel_i4(ctx.stream, _p(packed), _p(gscale), int4_group, K, N, tile_k,
+                                  tile_n, mac_s, mac_t, _p(out)))
 
 
 def gemm_i8_wt(ctx, A, a_scale, M, K, lda, Wt, wscale, N, bias, epilogue, residual, C, ldc):

@@ -190,6 +190,30 @@ def quantise_weights(w_kn, asmooth=None):
     return q, s
 
 
+def quantise_weights_i4(w_kn, asmooth=None, group=32):
+    """The reference packer's int4 operand scheme (tools/lib/gemm_i4.py:23-140):
+    W' = W * asmooth[:, None]; the int8 column scale s8 = max_k |W'| / 127
+    (1 for an all-zero column), kept as .wscale; per group g of `group` rows
+    (0: one group over K) and column, s4 = max |W'| / 7 (1 when zero), the
+    nibble t = rint(W' / s4) clipped to [-7, 7], and .gscale = s4 / s8.
+    Returns (t int8 [K, N], s8 fp32 [N], gscale fp32 [ceil(K / group), N])."""
+    w = np.asarray(w_kn, np.float32)
+    if asmooth is not None:
+        w = w * np.asarray(asmooth, np.float32)[:, None]
+    K, N = w.shape
+    g = int(group or K)
+    s8 = (np.abs(w).max(axis=0) / np.float32(127.0)).astype(np.float32)
+    s8 = np.where(s8 > 0, s8, np.float32(1.0)).astype(np.float32)
+    G = -(-K // g)
+    padded = np.zeros((G * g, N), np.float32)
+    padded[:K] = w
+    blocks = padded.reshape(G, g, N)
+    s4 = (np.abs(blocks).max(axis=1) / np.float32(7.0)).astype(np.float32)
+    s4 = np.where(s4 > 0, s4, np.float32(1.0)).astype(np.float32)
+    t = np.rint(blocks / s4[:, None, :]).clip(-7, 7).astype(np.int8).reshape(G * g, N)[:K]
+    return np.ascontiguousarray(t), s8, (s4 / s8[None, :]).astype(np.float32)
+
+
 GEMM_KEYS = ("w_qkv", "w_ao", "w_up", "w_down")
 
 
@@ -210,4 +234,21 @@ def quantise_model(m, seed=SEED + 7, smooth=(0.5, 2.0)):
         qs, ss = zip(*[quantise_weights(W[l], sm[l]) for l in range(L)])
         out.append((np.ascontiguousarray(np.stack(qs)), np.ascontiguousarray(np.stack(ss)),
                     np.ascontiguousarray(sm)))
+    return out
+
+
+def quantise_model_i4(m, group=32, seed=SEED + 7, smooth=(0.5, 2.0)):
+    """The int4 operands of a synthetic encoder, as an --int4 pack carries them:
+    per GEMM site (t [L, K, N] int8 in [-7, 7], wscale [L, N], gscale
+    [L, ceil(K / group), N], asmooth [L, K]); sites as quantise_model."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for key in GEMM_KEYS:
+        W = m[key]
+        L, K, _ = W.shape
+        sm = (np.ones((L, K), np.float32) if smooth is None else
+              rng.uniform(smooth[0], smooth[1], (L, K)).astype(np.float32))
+        ts, ss, gs = zip(*[quantise_weights_i4(W[l], sm[l], group) for l in range(L)])
+        out.append((np.ascontiguousarray(np.stack(ts)), np.ascontiguousarray(np.stack(ss)),
+                    np.ascontiguousarray(np.stack(gs)), np.ascontiguousarray(sm)))
     return out

@@ -307,6 +307,20 @@ void orc_bert_run_i8(const orc_encoder *m, const orc_i8_operands *q, float *x_io
 int orc_untile_b_panel(const uint16_t *panel, int64_t K, int64_t N, int64_t tile_k,
                        int64_t tile_n, int64_t mac_s, int64_t mac_t, uint16_t *kn);
 
+/* int4 storage over the int8 datapath: npue::gemm_b_panel's I4 branch
+ * (common/int4_panel.hpp:77-246). packed holds K * N / 2 bytes of the
+ * container's flat run (two values per byte, even index in the low nibble);
+ * gscale is F32 [ceil(K / g), N], g = int4_group (0: g = K). Writes the int8
+ * run of the same tiling: out[f] = clip(nearbyint(t * gscale[k / g][n]),
+ * -127, 127) for the sign-extended nibble t of element f at (k, n). Returns 0,
+ * or -1 for a shape gemm_b_panel refuses (odd nibble count, a tiling that does
+ * not divide, int4_group < 0). Pinned bit-exact against oracle/_ref's
+ * gemm_b_panel reading the same container, and against the packer's
+ * arithmetic written as numpy (tools/lib/npue.py fold_i4, :394-430). */
+int orc_widen_i4_panel(const uint8_t *packed, int64_t K, int64_t N, int64_t tile_k,
+                       int64_t tile_n, int64_t mac_s, int64_t mac_t, const float *gscale,
+                       int64_t int4_group, int8_t *out);
+
 #ifdef __cplusplus
 }
 #endif

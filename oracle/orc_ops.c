@@ -430,6 +430,45 @@ int orc_untile_b_panel(const uint16_t *panel, int64_t K, int64_t N, int64_t tile
   return 0;
 }
 
+/* npue::gemm_b_panel's I4 branch (common/int4_panel.hpp:183-246): walk the
+ * flat run's six axes (k-block, n-block, row group, column group, row, column)
+ * so each element's (k, n) is known; element f is nibble f % 2 (low first) of
+ * byte f / 2, sign-extended; q = clip(nearbyint(t * gscale[k / g][n]), +-127)
+ * stays at flat index f. */
+int orc_widen_i4_panel(const uint8_t *packed, int64_t K, int64_t N, int64_t tile_k,
+                       int64_t tile_n, int64_t mac_s, int64_t mac_t, const float *gscale,
+                       int64_t int4_group, int8_t *out) {
+  if (K <= 0 || N <= 0 || (K * N) % 2 || tile_k <= 0 || tile_n <= 0 || mac_s <= 0 ||
+      mac_t <= 0 || int4_group < 0)
+    return -1;
+  if (K % tile_k || N % tile_n || tile_k % mac_s || tile_n % mac_t) return -1;
+  const int64_t g = int4_group == 0 ? K : int4_group;
+  const int64_t kblocks = K / tile_k, nblocks = N / tile_n;
+  const int64_t rows = tile_k / mac_s, cols = tile_n / mac_t;
+  int64_t f = 0;
+  for (int64_t bk = 0; bk < kblocks; ++bk)
+    for (int64_t bn = 0; bn < nblocks; ++bn)
+      for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+          for (int64_t si = 0; si < mac_s; ++si) {
+            const int64_t k = bk * tile_k + r * mac_s + si;
+            const float *grow = gscale + (k / g) * N;
+            for (int64_t ti = 0; ti < mac_t; ++ti, ++f) {
+              const int64_t n = bn * tile_n + c * mac_t + ti;
+              const uint8_t b = packed[f >> 1];
+              const int nv = (f & 1) ? (int)(b >> 4) : (int)(b & 0x0F);
+              const float t = (float)(nv > 7 ? nv - 16 : nv);
+              float q = nearbyintf(t * grow[n]);
+              if (q > 127.0f)
+                q = 127.0f;
+              else if (q < -127.0f)
+                q = -127.0f;
+              out[f] = (int8_t)q;
+            }
+          }
+  return 0;
+}
+
 /* ---- int8 W8A8 (host_kernels.hpp:263-320, 529-600) ------------------------ */
 typedef struct {
   const float *a, *ias;

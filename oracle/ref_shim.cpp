@@ -114,6 +114,23 @@ long long ref_npue_host_b_kn(const char *path, const char *name, float *out, lon
   }
 }
 
+// npue::gemm_b_panel(File(path), name, a_elem_bytes): the bytes Design::stage
+// receives (an I4 payload widened to int8, int4_panel.hpp) into out (cap
+// bytes); their count, or -1 when the reference refuses.
+long long ref_npue_gemm_b_panel(const char *path, const char *name, long long a_elem_bytes,
+                                void *out, long long cap, char *err, size_t len) {
+  try {
+    npue::File f(path);
+    const npue::Panel p = npue::gemm_b_panel(f, name, static_cast<size_t>(a_elem_bytes));
+    if (static_cast<long long>(p.bytes.bytes) > cap) return -2;
+    std::memcpy(out, p.bytes.data, p.bytes.bytes);
+    return static_cast<long long>(p.bytes.bytes);
+  } catch (const std::exception &e) {
+    put_err(e, err, len);
+    return -1;
+  }
+}
+
 // File::config_string(key) into buf; its length, or -1.
 long long ref_npue_config(const char *path, const char *key, char *buf, size_t buflen,
                           char *err, size_t len) {

@@ -44,6 +44,16 @@ def tile_panel(kn, tile_k, tile_n, mac_s, mac_t):
     return np.ascontiguousarray(x.transpose(0, 3, 1, 4, 2, 5)).reshape(-1)
 
 
+def pack_i4(flat):
+    """int4 values (int8 in [-8, 7]) -> bytes, two per byte, even index in the
+    low nibble (tools/lib/npue.py:347-374)."""
+    f = np.ascontiguousarray(flat, np.int8).reshape(-1)
+    assert f.size % 2 == 0
+    lo = (f[0::2].astype(np.int16) & 0x0F).astype(np.uint8)
+    hi = (f[1::2].astype(np.int16) & 0x0F).astype(np.uint8)
+    return (lo | (hi << 4)).astype(np.uint8)
+
+
 def panel_layout(tile_k, tile_n, mac_s, mac_t, dtype="BF16"):
     return {"kind": "block_panel", "tile_k": tile_k, "tile_n": tile_n, "order": "k,n,kt,nt",
             "inner": "s,t", "mac_s": mac_s, "mac_t": mac_t, "dtype": dtype}
@@ -99,6 +109,21 @@ class Container:
         self.add_f32(name + ".wscale", wscale, "quant_scale")
         self.add_f32(name + ".asmooth", asmooth, "quant_smooth")
 
+    def add_gemm_i4(self, name, t_kn, wscale, gscale, asmooth, tile_k, tile_n, mac_s, mac_t):
+        """An --int4 pack's operand (tools/lib/gemm_i4.py:23-140): the int4 values
+        t [K, N] in [-8, 7] pre-tiled in the I8 layout's order and packed two per
+        byte, low nibble first (tools/lib/npue.py pack_i4, :347-374), as dtype
+        "I4"; then .wscale [N], .gscale [G, N] and .asmooth [K]."""
+        t_kn = np.asarray(t_kn, np.int8)
+        K, N = t_kn.shape
+        assert int(t_kn.min(initial=0)) >= -8 and int(t_kn.max(initial=0)) <= 7
+        flat = tile_panel(t_kn, tile_k, tile_n, mac_s, mac_t)
+        self.add(name, pack_i4(flat), "I4", "gemm_b", [K, N],
+                 layout=panel_layout(tile_k, tile_n, mac_s, mac_t, dtype="I8"))
+        self.add_f32(name + ".wscale", wscale, "quant_scale")
+        self.add_f32(name + ".gscale", gscale, "quant_group")
+        self.add_f32(name + ".asmooth", asmooth, "quant_smooth")
+
     def write(self, path, version=1, magic=b"NPUE", data_align=ALIGN, raw_json=None,
               trailing=b""):
         """raw_json (bytes) replaces the directory; trailing bytes are appended
@@ -121,11 +146,13 @@ class Container:
 
 
 def bert_container(m, tile_k=64, tile_n=64, mac=(8, 8), arch="bert_abs_gelu_postln",
-                   pooling=None, extra_config=None, int8=None):
+                   pooling=None, extra_config=None, int8=None, int4=None, int4_group=32):
     """A BERT container of a synthetic model dict (mxenc.synth.make_model):
     the packer's tensor names, roles and config keys
     (tools/pack/pack_npue.py:2630-2760). int8: the model's int8 operands
-    (mxenc.synth.quantise_model) -- the container is then an --int8 pack."""
+    (mxenc.synth.quantise_model) -- the container is then an --int8 pack; int4:
+    its int4 operands (mxenc.synth.quantise_model_i4 at int4_group rows per
+    group) -- an --int4 pack."""
     d, f, L = m["hidden"], m["ffn"], m["layers"]
     cfg = {"arch": arch, "source_repo": "synthetic/bert", "source_sha256": "0" * 64,
            "num_layers": L, "num_heads": m["heads"], "hidden": d, "head_dim": m["head_dim"],
@@ -134,7 +161,7 @@ def bert_container(m, tile_k=64, tile_n=64, mac=(8, 8), arch="bert_abs_gelu_post
            "pooling": pooling or ("cls" if m.get("cls_pool") else "mean"),
            "l2_normalize": True, "activation": "gelu_erf_exact", "gemm_layout": "pretiled_bf16",
            "tile_k": tile_k, "tile_n": tile_n, "mac_s": mac[0], "mac_t": mac[1],
-           "a_dtype": "i8" if int8 else "bf16",
+           "a_dtype": "i8" if (int8 or int4) else "bf16",
            "fusions": {"qkv_fused": True, "transposed_to_kn": True,
                        "qk_scale_folded_into_q": True}}
     if m.get("rope"):
@@ -148,6 +175,8 @@ def bert_container(m, tile_k=64, tile_n=64, mac=(8, 8), arch="bert_abs_gelu_post
         else:
             cfg.update({"swiglu_halves": "fc11_up|fc12_gate", "rope_theta": m["rope_theta"],
                         "activation": "silu"})
+    if int4:
+        cfg["int4_group"] = int4_group
     cfg.update(extra_config or {})
     c = Container(cfg)
     c.add_f32("embeddings.word", m["word"], "embedding")
@@ -159,7 +188,11 @@ def bert_container(m, tile_k=64, tile_n=64, mac=(8, 8), arch="bert_abs_gelu_post
              ("ffn_up", "w_up", "b_up"), ("ffn_down", "w_down", "b_down")]
     for l in range(L):
         for i, (n, w, b) in enumerate(names):
-            if int8:
+            if int4:
+                t, ws, gs, sm = int4[i]
+                c.add_gemm_i4(f"layer.{l}.{n}", t[l], ws[l], gs[l], sm[l], tile_k, tile_n,
+                              mac[0], mac[1])
+            elif int8:
                 q, ws, sm = int8[i]
                 c.add_gemm_i8(f"layer.{l}.{n}", q[l], ws[l], sm[l], tile_k, tile_n, mac[0],
                               mac[1])

@@ -87,6 +87,8 @@ def load():
         "orc_head_matvec": (None, [_vp, _vp, _vp, _c_i64, _c_i64, _vp]),
         "orc_untile_b_panel": (ctypes.c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                               _c_i64, _vp]),
+        "orc_widen_i4_panel": (ctypes.c_int, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                              _c_i64, _vp, _c_i64, _vp]),
         "orc_quantise_a_int8": (None, [_vp, _c_i64, _c_i64, _vp, _vp, _vp]),
         "orc_gemm_i8": (None, [_vp, _c_i64, _c_i64, _vp, _c_i64, _vp]),
         "orc_dequantise_c": (None, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
@@ -123,6 +125,9 @@ def load_ref():
         "ref_npue_host_b_kn": (ctypes.c_longlong, [ctypes.c_char_p, ctypes.c_char_p, _vp,
                                                    ctypes.c_longlong, ctypes.c_char_p,
                                                    ctypes.c_size_t]),
+        "ref_npue_gemm_b_panel": (ctypes.c_longlong, [ctypes.c_char_p, ctypes.c_char_p,
+                                                      ctypes.c_longlong, _vp, ctypes.c_longlong,
+                                                      ctypes.c_char_p, ctypes.c_size_t]),
         "ref_npue_config": (ctypes.c_longlong, [ctypes.c_char_p, ctypes.c_char_p,
                                                 ctypes.c_char_p, ctypes.c_size_t,
                                                 ctypes.c_char_p, ctypes.c_size_t]),

@@ -13,6 +13,7 @@ import npue_writer as nw
 from mxenc import synth
 from orc import P
 from test_gpu_encoder import COS_MIN, cosines, gpu_embed, oracle_embed
+from test_npue_cpu import I4_CASES, _fold_i4_numpy, _i4_operand
 
 pytestmark = pytest.mark.gpu
 
@@ -107,16 +108,16 @@ def test_encoder_from_npue_refusals(tmp_path, ctx, over, why):
     f.close()
 
 
-def test_encoder_from_npue_refuses_int4_mixed_and_missing_tensors(tmp_path, ctx):
+def test_encoder_from_npue_refuses_short_i4_mixed_and_missing_tensors(tmp_path, ctx):
     m = synth.make_model("minilm", layers=1)
     c = nw.bert_container(m, 64, 64, (8, 8))
     for e in c.entries:
         if e["name"] == "layer.0.attn_out":
-            e["dtype"] = "I4"
+            e["dtype"] = "I4"  # bf16-sized bytes under an I4 tag
     path = str(tmp_path / "i4.npue")
     c.write(path)
     f = mxenc.Npue(path)
-    with pytest.raises(mxenc.MxError, match="I4 operand"):
+    with pytest.raises(mxenc.MxError, match="int4 operand"):
         mxenc.Encoder.from_npue(ctx, f)
     f.close()
     # an int8 operand among bf16 ones: one datapath per stack
@@ -182,3 +183,97 @@ def test_gated_bert_container_unknown_activation_refused(tmp_path, ctx):
     with pytest.raises(mxenc.MxError, match="unknown gated-FFN activation 'relu'"):
         mxenc.Encoder.from_npue(ctx, f)
     f.close()
+
+
+# ---- int4 storage over the int8 datapath (common/int4_panel.hpp) --------------------
+
+I4_GPU_CASES = I4_CASES + [
+    (768, 2304, 64, 48, 8, 4, 32),   # bge-base QKV operand
+    (3072, 768, 64, 64, 8, 8, 0),    # bge-base FFN-down, one group over K
+]
+
+
+@pytest.mark.parametrize("K,N,tk,tn,s,t,group", I4_GPU_CASES)
+def test_widen_panel_i4_is_the_oracle_widening(ctx, orc, K, N, tk, tn, s, t, group):
+    """mx_widen_panel_i4 on the GPU and the oracle (pinned to the reference's
+    gemm_b_panel) widen the same stored bytes to identical int8 runs: ties
+    to even, clipping at +-127, groups straddling the sub-tile rows."""
+    tv, gs = _i4_operand(K, N, group, K * N + group + 1)
+    packed = nw.pack_i4(nw.tile_panel(tv, tk, tn, s, t))
+    want = np.zeros(K * N, np.int8)
+    assert orc.orc_widen_i4_panel(P(packed), K, N, tk, tn, s, t, P(gs), group, P(want)) == 0
+    out = ctx.empty((K * N,), np.int8)
+    mxenc.widen_panel_i4(ctx, ctx.put(packed), ctx.put(gs), group, K, N, tk, tn, s, t, out)
+    assert np.array_equal(out.host(), want)
+
+
+def test_widen_panel_i4_refusals(ctx):
+    buf = ctx.empty((64 * 64,), np.uint8)
+    gs = ctx.empty((64 * 64,), np.float32)
+    out = ctx.empty((64 * 64,), np.int8)
+    with pytest.raises(mxenc.MxError, match="odd number of nibbles"):
+        mxenc.widen_panel_i4(ctx, buf, gs, 0, 63, 1, 63, 1, 1, 1, out)
+    with pytest.raises(mxenc.MxError, match="must be >= 0"):
+        mxenc.widen_panel_i4(ctx, buf, gs, -1, 64, 64, 64, 64, 8, 8, out)
+    with pytest.raises(mxenc.MxError, match="does not tile"):
+        mxenc.widen_panel_i4(ctx, buf, gs, 0, 64, 64, 48, 64, 8, 8, out)
+
+
+@pytest.mark.parametrize("group", [32, 0])
+def test_i4_container_is_bitwise_its_widened_i8_container(tmp_path, ctx, group):
+    """An --int4 pack (I4 nibbles, .gscale, config int4_group) loaded by
+    mx_encoder_from_npue embeds bit for bit what the --int8 pack holding the
+    widened panels (the packer's fold, pinned to gemm_b_panel) embeds: int4 is
+    storage over the int8 datapath, and nothing downstream of the widening
+    differs."""
+    m = synth.make_model("minilm", layers=2, ln_random=True)
+    q4 = synth.quantise_model_i4(m, group=group)
+    q8 = []
+    for t, ws, gs, sm in q4:
+        q8.append((np.stack([_fold_i4_numpy(t[l], gs[l], group) for l in range(t.shape[0])]),
+                   ws, sm))
+    p4, p8 = str(tmp_path / "m4.npue"), str(tmp_path / "m8.npue")
+    nw.bert_container(m, 64, 48, (8, 4), int4=q4, int4_group=group).write(p4)
+    nw.bert_container(m, 64, 48, (8, 4), int8=q8).write(p8)
+    f4, f8 = mxenc.Npue(p4), mxenc.Npue(p8)
+    e4, e8 = mxenc.Encoder.from_npue(ctx, f4), mxenc.Encoder.from_npue(ctx, f8)
+    ids, am, _ = synth.make_text_inputs(m, batch=8)
+    a, b = gpu_embed(ctx, e4, ids, am), gpu_embed(ctx, e8, ids, am)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.all(np.isfinite(a))
+    e4.close()
+    e8.close()
+    f4.close()
+    f8.close()
+
+
+def test_i4_container_refusals(tmp_path, ctx):
+    """The loader refuses an int4 pack as gemm_b_panel does (int4_panel.hpp:
+    127-173): no int4_group, a negative one, no .gscale, a .gscale whose rows
+    do not match the group size."""
+    m = synth.make_model("minilm", layers=1)
+    q4 = synth.quantise_model_i4(m, group=32)
+
+    def load(c, name):
+        path = str(tmp_path / name)
+        c.write(path)
+        f = mxenc.Npue(path)
+        try:
+            mxenc.Encoder.from_npue(ctx, f).close()
+        finally:
+            f.close()
+
+    c = nw.bert_container(m, 64, 64, (8, 8), int4=q4)
+    del c.config["int4_group"]
+    with pytest.raises(mxenc.MxError, match="states no int4_group"):
+        load(c, "nogroup.npue")
+    c = nw.bert_container(m, 64, 64, (8, 8), int4=q4, int4_group=-4)
+    with pytest.raises(mxenc.MxError, match="must be >= 0"):
+        load(c, "neg.npue")
+    c = nw.bert_container(m, 64, 64, (8, 8), int4=q4)
+    c.entries = [e for e in c.entries if e["name"] != "layer.0.qkv.gscale"]
+    with pytest.raises(mxenc.MxError, match="no layer.0.qkv.gscale"):
+        load(c, "nogs.npue")
+    c = nw.bert_container(m, 64, 64, (8, 8), int4=q4, int4_group=16)
+    with pytest.raises(mxenc.MxError, match="gscale is F32"):
+        load(c, "rows.npue")

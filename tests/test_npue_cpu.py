@@ -193,3 +193,100 @@ def test_reader_refuses_malformed_directories(tmp_path, raw, why):
 def test_missing_file_is_refused_by_name(tmp_path):
     with pytest.raises(mxenc.MxError, match="cannot open"):
         mxenc.Npue(str(tmp_path / "nope.npue"))
+
+
+# ---- int4 storage over the int8 datapath (common/int4_panel.hpp) --------------------
+
+I4_CASES = [  # (K, N, tile_k, tile_n, mac_s, mac_t, int4_group)
+    (128, 96, 64, 48, 8, 4, 32),
+    (128, 96, 64, 48, 8, 4, 0),    # one group over the whole K
+    (96, 64, 32, 32, 4, 8, 24),    # groups straddle mac_s runs: per-row group index
+    (64, 128, 64, 64, 8, 8, 7),    # a group size no tiling divides; ceil(K/g) rows
+    (16, 24, 8, 8, 2, 4, 16),
+]
+
+
+def _i4_operand(K, N, group, seed):
+    """int4 values over the full [-8, 7] range and a gscale with exact
+    half-integer products (1.5, 2.5: ties for rint to break to even) beside
+    random ones, some large enough to clip at +-127."""
+    rng = np.random.default_rng(seed)
+    t = rng.integers(-8, 8, (K, N)).astype(np.int8)
+    G = -(-K // (group or K))
+    gs = rng.uniform(0.5, 20.0, (G, N)).astype(np.float32)
+    gs[:, ::3] = 1.5
+    gs[:, 1::7] = 2.5
+    gs[:, 2::11] = 40.0  # |t| * 40 > 127 for |t| >= 4: clipped
+    return t, gs
+
+
+def _fold_i4_numpy(t, gs, group):
+    """The packer's arithmetic (tools/lib/npue.py fold_i4, :394-430) on the
+    logical [K, N] panel: clip(rint(t * gscale[k // g]), -127, 127)."""
+    K = t.shape[0]
+    row = np.arange(K) // int(group or K)
+    return np.clip(np.rint(t.astype(np.float32) * gs[row, :]), -127, 127).astype(np.int8)
+
+
+def test_i4_nibble_order_hand_worked(orc):
+    """Two bytes, four values: element 0 in byte 0's low nibble, element 1 in
+    its high nibble; 0xF is -1 and 0x8 is -8 after sign extension."""
+    packed = np.array([0x8F, 0x71], np.uint8)  # elements -1, -8, 1, 7
+    out = np.zeros(4, np.int8)
+    gs = np.ones((1, 2), np.float32)  # [2, 2] operand, one group, one 2 x 2 tile of 1 x 2
+    assert orc.orc_widen_i4_panel(P(packed), 2, 2, 2, 2, 1, 2, P(gs), 0, P(out)) == 0
+    assert list(out) == [-1, -8, 1, 7]
+    assert list(nw.pack_i4(np.array([-1, -8, 1, 7], np.int8))) == [0x8F, 0x71]
+
+
+@pytest.mark.parametrize("K,N,tk,tn,s,t,group", I4_CASES)
+def test_widen_i4_matches_reference_gemm_b_panel(tmp_path, orc, ref, K, N, tk, tn, s, t, group):
+    """The reference's npue::gemm_b_panel widens the I4 operand of a written
+    container; the oracle widens the same stored bytes: identical int8 runs,
+    and equal to the packer's fold of the logical panel, tiled."""
+    tv, gs = _i4_operand(K, N, group, K * N + group)
+    c = nw.Container({"arch": "bert_abs_gelu_postln", "int4_group": group})
+    c.add_gemm_i4("layer.0.qkv", tv, np.ones(N, np.float32), gs, np.ones(K, np.float32),
+                  tk, tn, s, t)
+    path = str(tmp_path / "i4.npue")
+    c.write(path)
+    want = np.zeros(K * N, np.int8)
+    err = ctypes.create_string_buffer(512)
+    n = ref.ref_npue_gemm_b_panel(path.encode(), b"layer.0.qkv", 1, P(want), want.size, err, 512)
+    assert n == K * N, err.value
+    stored = np.frombuffer(mxenc.Npue(path).bytes("layer.0.qkv"), np.uint8)
+    assert stored.size == K * N // 2
+    mine = np.zeros(K * N, np.int8)
+    assert orc.orc_widen_i4_panel(P(np.ascontiguousarray(stored)), K, N, tk, tn, s, t, P(gs),
+                                  group, P(mine)) == 0
+    assert np.array_equal(mine, want)
+    assert np.array_equal(mine, nw.tile_panel(_fold_i4_numpy(tv, gs, group), tk, tn, s, t))
+    # the ties broke to even and the large factors clipped
+    assert np.any(np.abs(mine) == 127)
+
+
+def test_widen_i4_refuses_what_gemm_b_panel_refuses(tmp_path, orc, ref):
+    buf = np.zeros(64 * 64, np.uint8)
+    gs = np.ones((64, 64), np.float32)
+    out = np.zeros(64 * 64, np.int8)
+    for args in [(64, 64, 48, 64, 8, 8, 0), (64, 64, 64, 64, 6, 8, 0), (63, 1, 63, 1, 1, 1, 0),
+                 (64, 64, 64, 64, 8, 8, -1), (0, 64, 64, 64, 8, 8, 0)]:
+        assert orc.orc_widen_i4_panel(P(buf), *args[:6], P(gs), args[6], P(out)) == -1
+    # the reference's refusals of an I4 container the loader must also refuse
+    tv, g = _i4_operand(64, 32, 32, 5)
+    cases = {
+        "no int4_group": ({"arch": "x"}, g, "int4_group"),
+        "negative group": ({"arch": "x", "int4_group": -2}, g, "must be >= 0"),
+        "gscale rows": ({"arch": "x", "int4_group": 16}, g, ".gscale"),
+    }
+    for what, (cfg, gsc, why) in cases.items():
+        c = nw.Container(cfg)
+        c.add_gemm_i4("w", tv, np.ones(32, np.float32), gsc, np.ones(64, np.float32),
+                      32, 32, 8, 8)
+        path = str(tmp_path / "r.npue")
+        c.write(path)
+        err = ctypes.create_string_buffer(512)
+        wbuf = np.zeros(64 * 32, np.int8)
+        assert ref.ref_npue_gemm_b_panel(path.encode(), b"w", 1, P(wbuf), wbuf.size, err,
+                                         512) == -1, what
+        assert why in err.value.decode(), (what, err.value)
