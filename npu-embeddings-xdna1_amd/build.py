@@ -29,7 +29,7 @@ FLAGS = [
 ]
 SOURCES = ["k_gemm_lds.hip", "k_gemm_i8.hip", "k_elem.hip", "k_gemm.hip", "k_attn.hip",
            "k_front.hip", "k_panel.hip", "k_quant.hip", "k_glu.hip", "mx_abi.cpp", "mx_i8.cpp",
-           "mx_encoder.cpp", "mx_npue.cpp", "mx_service.cpp"]
+           "mx_encoder.cpp", "mx_npue.cpp", "mx_service.cpp", "mx_host.cpp"]
 
 
 def _compile(src):
@@ -61,7 +61,26 @@ def build(jobs=None, verbose=False):
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
     build_probe()
+    build_abi_check()
     return LIB
+
+
+ABI_CHECK = os.path.join(OUT, "abi_check")
+
+
+def build_abi_check():
+    """tests/abi_cxx/abi_check.cpp: a C++17 caller of include/mx_gpu_backend.hpp,
+    compiled by the host compiler (no HIP) and linked to the library, as the
+    reference runtime would build against it."""
+    src = os.path.join(HERE, "..", "tests", "abi_cxx", "abi_check.cpp")
+    cmd = [os.environ.get("CXX", "g++"), "-std=c++17", "-O2", "-Wall", "-Wextra", "-Werror",
+           "-I", os.path.join(HERE, "..", "include"), src, "-o", ABI_CHECK + ".tmp", "-L", OUT,
+           "-lmx_encoder", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("g++ failed on abi_check.cpp:\n" + r.stdout + r.stderr)
+    os.replace(ABI_CHECK + ".tmp", ABI_CHECK)
+    return ABI_CHECK
 
 
 PROBE = os.path.join(OUT, "probe_mfma_clock")
@@ -69,9 +88,10 @@ PROBE = os.path.join(OUT, "probe_mfma_clock")
 
 def build_probe():
     """The clock / MFMA / LDS measurement program (csrc/probe_mfma_clock.hip),
-    a standalone executable beside the library."""
+    an executable beside the library that also calls it through the C ABI."""
     cmd = [HIPCC] + [f for f in FLAGS if f != "-fPIC"] + [
-        os.path.join(CSRC, "probe_mfma_clock.hip"), "-o", PROBE + ".tmp"]
+        os.path.join(CSRC, "probe_mfma_clock.hip"), "-o", PROBE + ".tmp", "-L", OUT,
+        "-lmx_encoder", "-Wl,-rpath,$ORIGIN"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("hipcc failed on probe_mfma_clock.hip:\n" + r.stdout + r.stderr)

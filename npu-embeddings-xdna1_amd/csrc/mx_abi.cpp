@@ -1,5 +1,6 @@
-// mx_abi.cpp -- the C ABI: device, streams, memory, weight staging, the
-// per-op entry points (validated, refused by name) and the placement registry.
+// mx_abi.cpp -- the C ABI: device, streams, memory, weight staging and the
+// per-op entry points (validated, refused by name). The error state and the
+// placement registry are host-only code in mx_host.cpp.
 #include "mx_internal.hpp"
 #include "mx_kernels.hpp"
 
@@ -11,16 +12,6 @@
 #include <sstream>
 
 namespace mx {
-
-static thread_local std::string t_err;
-
-void set_error(const std::string &msg) { t_err = msg; }
-void clear_error() { t_err.clear(); }
-
-int fail(int code, const std::string &msg) {
-  set_error(msg);
-  return code;
-}
 
 int hip_fail(hipError_t e, const char *what) {
   return fail(MX_E_DEVICE, std::string(what) + ": " + hipGetErrorName(e) + " (" +
@@ -251,47 +242,11 @@ int take_data_error(mx_stream *s, int *flags) {
   return MX_OK;
 }
 
-// ---- placement registry ---------------------------------------------------
-
-struct OpCode {
-  const char *code;
-  const char *long_name;
-};
-
-// The reference's codes, in its table order (npu_ops_flag.hpp:105-142).
-static const OpCode kOps[] = {
-    {"gemm", "the per-layer GEMMs"},
-    {"gelu", "GELU"},
-    {"layn", "LayerNorm"},
-    {"softm", "softmax"},
-    {"conv", "conv1d (Whisper's audio front end)"},
-    {"attn", "attention (QK^T, softmax, softmax.V fused)"},
-    {"mproj", "Whisper's mel filter bank, as a GEMM"},
-    {"fft", "Whisper's 400-point transform, as a GEMM"},
-    {"logit", "the vocabulary projection, as a GEMM"},
-};
-
-static std::mutex g_ops_mu;
-static std::set<std::string> g_ops;
-
-static std::string codes_joined() {
-  std::string s;
-  for (const auto &o : kOps) {
-    if (!s.empty()) s += ", ";
-    s += o.code;
-  }
-  return s;
-}
-
 }  // namespace mx
 
 using namespace mx;
 
 extern "C" {
-
-const char *mx_last_error(void) { return t_err.c_str(); }
-
-int mx_version(void) { return 1; }
 
 int mx_create(int device, mx_ctx **out) {
   clear_error();
@@ -641,77 +596,4 @@ int mx_pool_rows(mx_stream *s, const float *h, const float *attn_mask, int64_t B
   return MX_OK;
 }
 
-int mx_ops_parse(const char *list) {
-  clear_error();
-  if (!list) return fail(MX_E_INVALID, "--npu-ops: null list");
-  std::set<std::string> out;
-  std::string item;
-  auto commit = [&]() -> bool {
-    std::string code;
-    for (char c : item)
-      if (!std::isspace(static_cast<unsigned char>(c))) code.push_back(c);
-    item.clear();
-    if (code.empty()) return true;
-    bool known = false;
-    for (const auto &o : kOps) known = known || code == o.code;
-    if (!known) {
-      set_error("--npu-ops: '" + code + "' is not an op this build knows. Valid codes: [" +
-                codes_joined() +
-                "]. Nothing listed means no op is placed on the accelerator.");
-      return false;
-    }
-    out.insert(code);
-    return true;
-  };
-  for (const char *p = list; *p; ++p) {
-    if (*p == ',') {
-      if (!commit()) return MX_E_INVALID;
-      continue;
-    }
-    item.push_back(*p);
-  }
-  if (!commit()) return MX_E_INVALID;
-  std::lock_guard<std::mutex> lk(g_ops_mu);
-  g_ops = out;
-  return MX_OK;
-}
-
-int mx_op_on_gpu(const char *code) {
-  if (!code) return 0;
-  std::lock_guard<std::mutex> lk(g_ops_mu);
-  return g_ops.count(code) ? 1 : 0;
-}
-
-const char *mx_op_codes(void) {
-  static const std::string s = codes_joined();
-  return s.c_str();
-}
-
-int mx_ops_check_flag(const char *flag) {
-  clear_error();
-  if (!flag) return MX_OK;
-  static const std::pair<const char *, const char *> removed[] = {
-      {"--npu-eltwise", "--npu-ops gelu,layn,softm"},
-      {"--host-gelu", "--npu-ops without gelu"},
-      {"--host-ln", "--npu-ops without layn"},
-      {"--host-sm", "--npu-ops without softm"},
-      {"--npu-extra-ops", "--npu-ops"},
-  };
-  for (const auto &r : removed)
-    if (std::strcmp(flag, r.first) == 0)
-      return fail(MX_E_INVALID, std::string(r.first) +
-                                    " is gone: one flag now says which ops go on the "
-                                    "accelerator, and an op is on the host when it is NOT "
-                                    "listed. Use " +
-                                    r.second + ".");
-  return MX_OK;
-}
-
 }  // extern "C"
-
-namespace mx {
-std::set<std::string> placed_ops() {
-  std::lock_guard<std::mutex> lk(g_ops_mu);
-  return g_ops;
-}
-}  // namespace mx

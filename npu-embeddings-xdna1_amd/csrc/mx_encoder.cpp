@@ -32,10 +32,6 @@
 #include <string>
 #include <vector>
 
-namespace mx {
-std::set<std::string> placed_ops();
-}
-
 using namespace mx;
 
 namespace mx {
@@ -693,6 +689,13 @@ int mx_encoder_create(mx_ctx *ctx, const mx_encoder_desc *desc, mx_encoder **out
     return fail(MX_E_INVALID, "encoder_create: unknown arch " + std::to_string(d.arch));
   if (d.layers <= 0 || d.hidden <= 0 || d.heads <= 0 || d.head_dim <= 0 || d.ffn <= 0)
     return fail(MX_E_INVALID, "encoder_create: zero dimension");
+  // Geometry may come from a container's config: bound it before anything is
+  // sized from it (every product below then fits in 64 bits).
+  if (d.layers > 4096 || d.hidden > 65536 || d.heads > 4096 || d.ffn > 1048576 ||
+      d.vocab < 0 || d.vocab > (1 << 24) || d.max_pos < 0 || d.max_pos > (1 << 20))
+    return fail(MX_E_INVALID, "encoder_create: geometry beyond this backend's bounds "
+                              "(layers <= 4096, hidden <= 65536, heads <= 4096, ffn <= 2^20, "
+                              "vocab <= 2^24, max_seq_len <= 2^20)");
   if (d.heads * d.head_dim != d.hidden)
     return fail(MX_E_INVALID, "encoder_create: " + std::to_string(d.heads) + " heads x " +
                                   std::to_string(d.head_dim) + " is not hidden " +
@@ -1506,6 +1509,12 @@ int mx_encoder_from_npue(mx_ctx *ctx, const mx_npue *f, mx_encoder **out) {
       if (!t.found) return refuse(fail(MX_E_INVALID, ".npue: no tensor named " + n));
       if (t.padded.size() != 2)
         return refuse(fail(MX_E_INVALID, n + ": GEMM operand is not two-dimensional"));
+      // Shapes come from the file: bound them before any product is formed.
+      if (t.padded[0] <= 0 || t.padded[1] <= 0 || t.padded[0] > (1 << 20) ||
+          t.padded[1] > (1 << 20))
+        return refuse(fail(MX_E_INVALID, n + ": a [" + std::to_string(t.padded[0]) + "," +
+                                             std::to_string(t.padded[1]) + "] GEMM operand; "
+                                             "each dimension must lie in [1, 2^20]"));
       if (!t.logical.empty() && t.logical != t.padded)
         return refuse(fail(MX_E_INVALID, n + ": logical and padded shapes differ; the GEMM "
                                              "needs them equal (repack)"));

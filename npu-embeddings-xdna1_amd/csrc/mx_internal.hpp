@@ -8,14 +8,10 @@
 #include <string>
 #include <vector>
 
-#include "../../include/mx_encoder.h"
+#include "mx_host.hpp"
 
 namespace mx {
 
-// Thread-local last error, set by every failing entry point.
-void set_error(const std::string &msg);
-void clear_error();
-int fail(int code, const std::string &msg);
 int hip_fail(hipError_t e, const char *what);
 
 struct WeightSlot {
@@ -103,17 +99,6 @@ int take_data_error(mx_stream *s, int *flags);
 mx_ctx *encoder_ctx(const mx_encoder *enc);
 int64_t encoder_hidden(const mx_encoder *enc);
 
-// A container tensor as the loaders use it (mx_npue.cpp).
-struct TensorRecView {
-  bool found = false, has_layout = false, block_panel = false;
-  std::string dtype;
-  std::vector<int64_t> padded, logical;
-  int64_t tile_k = 0, tile_n = 0, mac_s = 0, mac_t = 0;
-  const void *data = nullptr;
-  uint64_t nbytes = 0;
-};
-const TensorRecView npue_tensor(const mx_npue *f, const std::string &name);
-bool npue_config(const mx_npue *f, const std::string &key, std::string &out);
 // Check a block_panel tiling of a [K, N] operand; MX_OK or a refusal naming it.
 int check_panel(const std::string &what, int64_t K, int64_t N, int64_t tile_k, int64_t tile_n,
                 int64_t mac_s, int64_t mac_t);

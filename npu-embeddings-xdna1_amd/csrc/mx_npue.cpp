@@ -27,7 +27,7 @@
 #include <string>
 #include <vector>
 
-#include "mx_internal.hpp"
+#include "mx_host.hpp"
 
 namespace {
 
@@ -48,10 +48,15 @@ struct TensorRec {
 };
 
 // Recursive-descent reader over the directory text. Every method advances
-// `i` past what it consumed; errors carry the byte position.
+// `i` past what it consumed; errors carry the byte position. Objects and
+// arrays nest at most kMaxDepth deep (the packer writes four levels), so a
+// crafted directory cannot exhaust the stack.
+constexpr int kMaxDepth = 64;
+
 struct Json {
   const std::string &s;
   size_t i = 0;
+  int depth = 0;
   std::string err;
 
   explicit Json(const std::string &text) : s(text) {}
@@ -172,24 +177,30 @@ struct Json {
     const size_t b = i;
     if (i >= s.size()) return fail("expected a value");
     std::string tmp;
+    if ((s[i] == '{' || s[i] == '[') && depth >= kMaxDepth)
+      return fail("objects and arrays nested deeper than " + std::to_string(kMaxDepth));
     if (s[i] == '"') {
       if (!string(tmp)) return false;
     } else if (s[i] == '{') {
       ++i;
+      ++depth;
       if (!peek('}')) {
         do {
           if (!string(tmp) || !eat(':') || !value()) return false;
         } while (peek(',') && (++i, true));
       }
       if (!eat('}')) return false;
+      --depth;
     } else if (s[i] == '[') {
       ++i;
+      ++depth;
       if (!peek(']')) {
         do {
           if (!value()) return false;
         } while (peek(',') && (++i, true));
       }
       if (!eat(']')) return false;
+      --depth;
     } else if (!scalar(tmp)) {
       return false;
     }

@@ -112,3 +112,16 @@ def test_gemm_rows_beyond_32bit_offsets_leave_the_lds_kernel(L):
     assert "32-bit byte offsets" in msg and "2^24" in msg
     args[5] = 1024  # in range: the next refusal is the missing stream
     assert L.mx_gemm_i8_wt(*args) == -1 and "null stream" in L.mx_last_error().decode()
+
+
+def test_cxx_caller_refusal_paths():
+    """A C++17 program built by the host compiler against include/
+    (mx_gpu_backend.hpp over mx_encoder.h) and linked to the library runs the
+    registry, reader and null-argument refusals through the wrapper, each as
+    std::runtime_error("gpu: ...") naming its reason."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(mxenc.LIB_PATH), "abi_check")
+    assert os.path.exists(exe), "build() builds the C++ caller beside the library"
+    r = subprocess.run([exe, "cpu"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and r.stdout.strip() == "cpu ok", r.stdout + r.stderr

@@ -277,3 +277,32 @@ def test_i4_container_refusals(tmp_path, ctx):
     c = nw.bert_container(m, 64, 64, (8, 8), int4=q4, int4_group=16)
     with pytest.raises(mxenc.MxError, match="gscale is F32"):
         load(c, "rows.npue")
+
+
+def test_cxx_caller_embeds_what_the_binding_embeds(tmp_path, ctx):
+    """The C++17 caller (tests/abi_cxx/abi_check.cpp over include/
+    mx_gpu_backend.hpp, built by the host compiler and linked to the library)
+    loads a container and embeds a batch in a process of its own; its pooled
+    rows are bit for bit the ctypes binding's."""
+    import os
+    import subprocess
+    m = synth.make_model("minilm", layers=2, ln_random=True)
+    path = str(tmp_path / "m.npue")
+    nw.bert_container(m, 64, 48, (8, 4)).write(path)
+    ids, am, _ = synth.make_text_inputs(m, batch=6)
+    B, S = ids.shape
+    ids.tofile(str(tmp_path / "ids.bin"))
+    am.astype(np.float32).tofile(str(tmp_path / "mask.bin"))
+    exe = os.path.join(os.path.dirname(mxenc.LIB_PATH), "abi_check")
+    print("abi_check gpu: minilm 2 layers, B", B, "S", S, flush=True)
+    r = subprocess.run([exe, "gpu", path, str(tmp_path / "ids.bin"), str(tmp_path / "mask.bin"),
+                        str(B), str(S), str(tmp_path / "out.bin")], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0 and r.stdout.strip().endswith("gpu ok"), r.stdout + r.stderr
+    got = np.fromfile(str(tmp_path / "out.bin"), np.float32).reshape(B, m["hidden"])
+    f = mxenc.Npue(path)
+    enc = mxenc.Encoder.from_npue(ctx, f)
+    want = gpu_embed(ctx, enc, ids, am)
+    enc.close()
+    f.close()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
