@@ -69,24 +69,52 @@ def workload_name(config, m):
             f"{m['seq']} positions ({geo}) -> final LN")
 
 
-def cpu_baseline(name, sample_batch, threads, int8=False):
-    """The oracle's host path (the reference CPU fallback restated) over
-    `sample_batch` sequences of the same workload, all layers; int8: the
-    int8 design's host halves with the exact integer product
+def host_threads():
+    """Host threads the CPU baseline uses: the CPUs this process may run on
+    (sched_getaffinity), at most 16 -- the host CPU share of one GPU."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return max(1, min(16, n or 1))
+
+
+def physical_cores(cpus):
+    """Distinct physical cores (package, core id) under the logical CPUs
+    `cpus`, from /sys; None where the topology is not readable."""
+    seen = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(base + "core_id") as f:
+                core = f.read().strip()
+        except OSError:
+            return None
+        seen.add((pkg, core))
+    return len(seen)
+
+
+def cpu_baseline(name, sample_batch, threads, int8=False, lanes=4):
+    """The oracle's host path (the reference CPU fallback restated: embed sum,
+    every layer, pooling) timed as run_bench_or_check times it
+    (runtime/include/runtime/run_execute.hpp:436-465): one warm-up run, then
+    the timed ones. Two figures over the same `sample_batch` sequences of the
+    workload: one pool of `threads` workers over one chunk, and the
+    reference's --pipeline lanes (embed/serve default --threads 24 --pipeline
+    4, runtime/src/cli/subcommand.cpp:220,268: `lanes` concurrent chunks, each
+    lane with its own pool of threads // lanes workers, run_setup.hpp:465-477).
+    int8: the int8 design's host halves with the exact integer product
     (orc_bert_run_i8)."""
+    import threading
+
     import numpy as np
 
     import orc as orc_mod
     from mxenc import synth
 
     orc = orc_mod.load()
-    orc.orc_set_threads(threads)
     m = synth.make_model(name)
-    ids, am, _ = synth.make_text_inputs(m)
-    ids = np.ascontiguousarray(ids[:sample_batch])
-    am = np.ascontiguousarray(am[:sample_batch])
-    B, S = ids.shape
-    d = m["hidden"]
+    ids_all, am_all, _ = synth.make_text_inputs(m)
+    S, d = ids_all.shape[1], m["hidden"]
     P = orc_mod.P
     keep = []
     enc = orc_mod.encoder_struct(m, keep)
@@ -97,22 +125,56 @@ def cpu_baseline(name, sample_batch, threads, int8=False):
             ias = np.ascontiguousarray((np.float32(1.0) / sm).astype(np.float32))
             keep += [q, ws, ias]
             ops.wq[i], ops.wscale[i], ops.ias[i] = q.ctypes.data, ws.ctypes.data, ias.ctypes.data
-    emb = np.empty((B * S, d), np.float32)
-    cm = np.empty((B, S), np.float32)
-    out = np.empty((B, d), np.float32)
+
+    def chunk(lo, hi):
+        """EmbedService::chunk on the host for sequences [lo, hi)."""
+        ids = np.ascontiguousarray(ids_all[lo:hi])
+        am = np.ascontiguousarray(am_all[lo:hi])
+        B = hi - lo
+        emb = np.empty((B * S, d), np.float32)
+        cm = np.empty((B, S), np.float32)
+        out = np.empty((B, d), np.float32)
+        orc.orc_embed_sum(P(ids), P(am), B, S, d, P(m["word"]), P(m["pos"]), P(m["type"]),
+                          P(emb), P(cm))
+        if int8:
+            orc.orc_bert_run_i8(enc, ops, P(emb), P(cm), B, S, -1)
+        else:
+            orc.orc_bert_run(enc, P(emb), P(cm), B, S, -1)
+        orc.orc_pool_rows(P(emb), P(am), B, S, d, int(m["cls_pool"]), 1, P(out))
+
+    orc.orc_set_threads(threads)
+    chunk(0, 2)  # warm-up: pages the weights in, starts the pool
     t0 = time.perf_counter()
-    orc.orc_embed_sum(P(ids), P(am), B, S, d, P(m["word"]), P(m["pos"]), P(m["type"]), P(emb),
-                      P(cm))
-    if int8:
-        orc.orc_bert_run_i8(enc, ops, P(emb), P(cm), B, S, -1)
-    else:
-        orc.orc_bert_run(enc, P(emb), P(cm), B, S, -1)
-    orc.orc_pool_rows(P(emb), P(am), B, S, d, int(m["cls_pool"]), 1, P(out))
+    chunk(0, sample_batch)
     dt = time.perf_counter() - t0
-    return {"value": B / dt, "unit": "sequences/s", "cores": threads, "kind": "port",
-            "sample": f"{B} of the {m['batch']} sequences (seq {S}, {m['layers']} layers, "
-                      f"embed+run+pool) through the oracle's host path"
-                      f"{' (int8 design)' if int8 else ''}, {dt:.1f} s wall"}
+
+    per = max(1, threads // lanes)
+    cut = [sample_batch * i // lanes for i in range(lanes + 1)]
+
+    def lane(i):
+        orc.orc_lane_begin(per)
+        try:
+            chunk(cut[i], cut[i + 1])
+        finally:
+            orc.orc_lane_end()
+
+    th = [threading.Thread(target=lane, args=(i,)) for i in range(lanes)]
+    t0 = time.perf_counter()
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    ldt = time.perf_counter() - t0
+    cpus = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else []
+    return {"value": sample_batch / dt, "unit": "sequences/s", "cores": threads, "kind": "port",
+            "host": {"logical_cpus": len(cpus), "physical_cores": physical_cores(cpus),
+                     "machine_logical_cpus": os.cpu_count()},
+            "sample": f"{sample_batch} of the {m['batch']} sequences (seq {S}, every row as the "
+                      f"reference's chunk() computes them, {m['layers']} layers, embed+run+pool) "
+                      f"through the oracle's host path{' (int8 design)' if int8 else ''}, one "
+                      f"pool of {threads} threads, after a 2-sequence warm-up: {dt:.1f} s wall",
+            "lanes": {"value": sample_batch / ldt, "lanes": lanes, "threads_per_lane": per,
+                      "wall_s": ldt}}
 
 
 def main():
@@ -337,10 +399,10 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline and kind == "bert":
-        threads = min(16, os.cpu_count() or 1)
-        cpu = cpu_baseline(args.config, args.cpu_sample, threads, args.int8)
-        print(f"bench: cpu baseline {cpu['value']:.3f} seq/s ({cpu['sample']})",
-              file=sys.stderr, flush=True)
+        cpu = cpu_baseline(args.config, args.cpu_sample, host_threads(), args.int8)
+        print(f"bench: cpu baseline {cpu['value']:.3f} seq/s ({cpu['sample']}); "
+              f"{cpu['lanes']['lanes']} lanes x {cpu['lanes']['threads_per_lane']} threads: "
+              f"{cpu['lanes']['value']:.3f} seq/s", file=sys.stderr, flush=True)
 
     peak = INT8_PEAK_TOPS if args.int8 else BF16_PEAK_TFLOPS
     punit = "TOP/s" if args.int8 else "TFLOP/s"

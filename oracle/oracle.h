@@ -35,6 +35,12 @@ extern "C" {
  * independent in every op below, so the partition never changes a bit. */
 void orc_set_threads(int n);
 int orc_threads(void);
+/* A pool of n workers for the calling thread alone (one --pipeline lane,
+ * runtime/include/runtime/run_setup.hpp:465-477): until orc_lane_end, every
+ * op this thread runs uses it. Returns 0, or -1 if the thread already has
+ * one. */
+int orc_lane_begin(int n);
+void orc_lane_end(void);
 
 /* ---- bf16 -----------------------------------------------------------------
  * to_bf16: (u + 0x7FFF + ((u >> 16) & 1)) >> 16 on the fp32 bits

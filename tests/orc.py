@@ -49,6 +49,8 @@ def load():
     lib = ctypes.CDLL(ORC_SO)
     sig = {
         "orc_set_threads": (None, [ctypes.c_int]),
+        "orc_lane_begin": (ctypes.c_int, [ctypes.c_int]),
+        "orc_lane_end": (None, []),
         "orc_threads": (ctypes.c_int, []),
         "orc_to_bf16": (ctypes.c_uint16, [ctypes.c_float]),
         "orc_from_bf16": (ctypes.c_float, [ctypes.c_uint16]),
