@@ -83,11 +83,20 @@ class Container {
   Container(const Container &) = delete;
   Container &operator=(const Container &) = delete;
   const mx_npue *get() const { return f_; }
-  // File::config_string (model.cpp): the value's text; throws when absent.
+  // File::config_string (model.cpp:374-379): the value's text; throws when
+  // absent. mx_npue_config returns the value's full length, so a value longer
+  // than the first buffer is read again into one of that size.
   std::string config(const std::string &key) const {
-    char buf[4096];
-    check(mx_npue_config(f_, key.c_str(), buf, sizeof(buf)));
-    return std::string(buf);
+    std::string v(256, '\0');
+    int n = mx_npue_config(f_, key.c_str(), &v[0], v.size());
+    if (n < 0) check(n);
+    if (static_cast<size_t>(n) >= v.size()) {
+      v.assign(static_cast<size_t>(n) + 1, '\0');
+      n = mx_npue_config(f_, key.c_str(), &v[0], v.size());
+      if (n < 0) check(n);
+    }
+    v.resize(static_cast<size_t>(n));
+    return v;
   }
 
  private:

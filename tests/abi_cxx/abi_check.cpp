@@ -3,12 +3,13 @@
 // npu-embeddings-xdna1_amd/build.py), as the reference runtime would be.
 // TEST PROGRAM.
 //
-//   abi_check cpu
+//   abi_check cpu [<container.npue> <key> <value>]
 //       The paths that need no GPU: the op registry with the reference's
 //       refusals (npu_ops_flag.hpp:96-214, :238-268), the container reader's
 //       refusals (model.cpp:214-380), null-argument refusals, plan names --
 //       each failure surfacing as std::runtime_error("gpu: ...") through the
-//       wrapper. Prints "cpu ok".
+//       wrapper; with a container, its config read through the wrapper (the
+//       value of <key> must be <value>). Prints "cpu ok".
 //   abi_check gpu <container.npue> <ids.bin> <mask.bin> <B> <S> <out.bin>
 //       One embed on GPU 0: the container loaded by mxgpu::Encoder, ids int32
 //       [B, S] and the 1/0 mask fp32 [B, S] from the files, the pooled fp32
@@ -57,7 +58,7 @@ std::vector<T> read_file(const char *path, size_t count) {
   return v;
 }
 
-int run_cpu() {
+int run_cpu(const char *container, const std::string &key, const std::string &value) {
   expect(mx_version() > 0, "mx_version");
   // The registry: codes, separators, unknown codes and removed flags.
   expect(mx_ops_parse(" gemm ,attn,, softm,layn , gelu,") == MX_OK, "ops_parse list");
@@ -82,6 +83,20 @@ int run_cpu() {
                  "embed without an encoder");
   const char *plan = mx_gemm_plan_for(17455, 2304, 768, MX_BF16, 0, 0);
   expect(plan && std::strncmp(plan, "lds_", 4) == 0, "plan name");
+  // A valid container: its config values through the wrapper, a missing key
+  // refused by name.
+  if (container) {
+    mxgpu::Container c(container);
+    expect(c.config(key) == value, "config value");
+    expect(std::atoll(c.config("hidden").c_str()) > 0, "config hidden");
+    try {
+      (void)c.config("no_such_key");
+      std::printf("FAIL: a missing config key was read\n");
+      ++failures;
+    } catch (const std::runtime_error &e) {
+      expect(std::string(e.what()).find("no_such_key") != std::string::npos, "missing key");
+    }
+  }
   if (failures) return 1;
   std::printf("cpu ok\n");
   return 0;
@@ -130,7 +145,9 @@ int run_gpu(int argc, char **argv) {
 
 int main(int argc, char **argv) {
   try {
-    if (argc >= 2 && std::strcmp(argv[1], "cpu") == 0) return run_cpu();
+    if (argc >= 2 && std::strcmp(argv[1], "cpu") == 0)
+      return run_cpu(argc >= 5 ? argv[2] : nullptr, argc >= 5 ? argv[3] : "",
+                     argc >= 5 ? argv[4] : "");
     if (argc >= 2 && std::strcmp(argv[1], "gpu") == 0) return run_gpu(argc, argv);
     std::printf("usage: abi_check cpu | gpu ...\n");
     return 2;

@@ -114,14 +114,29 @@ def test_gemm_rows_beyond_32bit_offsets_leave_the_lds_kernel(L):
     assert L.mx_gemm_i8_wt(*args) == -1 and "null stream" in L.mx_last_error().decode()
 
 
-def test_cxx_caller_refusal_paths():
+def test_cxx_caller_refusal_paths(tmp_path):
     """A C++17 program built by the host compiler against include/
     (mx_gpu_backend.hpp over mx_encoder.h) and linked to the library runs the
     registry, reader and null-argument refusals through the wrapper, each as
-    std::runtime_error("gpu: ...") naming its reason."""
-    import os
+    std::runtime_error("gpu: ...") naming its reason; and reads a container's
+    config through the wrapper, a value longer than its first buffer included."""
     import subprocess
+
+    import npue_writer as nw
+    from mxenc import synth
     exe = os.path.join(os.path.dirname(mxenc.LIB_PATH), "abi_check")
     assert os.path.exists(exe), "build() builds the C++ caller beside the library"
     r = subprocess.run([exe, "cpu"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0 and r.stdout.strip() == "cpu ok", r.stdout + r.stderr
+    m = synth.make_model("minilm", layers=1, hidden=64, heads=2, head_dim=32, ffn=128, vocab=64,
+                         max_pos=16)
+    note = "n" * 3000
+    path = str(tmp_path / "m.npue")
+    nw.bert_container(m, 32, 32, (8, 8), extra_config={"note": note}).write(path)
+    for key, value in (("arch", "bert_abs_gelu_postln"), ("note", note), ("hidden", "64")):
+        r = subprocess.run([exe, "cpu", path, key, value], capture_output=True, text=True,
+                           timeout=60)
+        assert r.returncode == 0 and r.stdout.strip() == "cpu ok", (key, r.stdout + r.stderr)
+    r = subprocess.run([exe, "cpu", path, "hidden", "65"], capture_output=True, text=True,
+                       timeout=60)
+    assert r.returncode == 1 and "config value" in r.stdout
