@@ -405,7 +405,9 @@ int mx_encoder_clone(mx_encoder *enc, mx_encoder **out);
 int mx_encoder_set(mx_encoder *enc, const char *name, const void *host,
                    int dtype, int64_t count);
 /* Every tensor the architecture needs has been set: MX_OK, else MX_E_STATE
- * naming the first missing one. */
+ * naming the first missing one. Then builds what the stack derives on the
+ * device: the gated FFN's interleaved FFN-up operands and, with RoPE, the
+ * cos/sin tables for max_pos positions. */
 int mx_encoder_ready(mx_encoder *enc);
 
 /* BertEncoder::run (bert_encoder.cpp:1419-1598) with every op on the GPU,
@@ -424,6 +426,30 @@ int mx_encoder_run(mx_encoder *enc, mx_stream *s, float *x_io,
  * out [B, hidden] (device). BERT only. Synchronises s. */
 int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids,
                      const float *attn_mask, int64_t B, int64_t S, float *out);
+
+/* The static scratch of mx_encoder_embed_static: device memory that every GPU
+ * the library runs on holds from mx_create until the process ends. */
+#define MX_STATIC_SCRATCH_BYTES ((size_t)128 << 20)
+/* mx_encoder_embed without allocating: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The same inputs,
+ * output and refusals as mx_encoder_embed, bit for bit the same pooled rows;
+ * its workspace is carved from the library's static scratch
+ * (MX_STATIC_SCRATCH_BYTES per GPU) instead of the encoder's own. The
+ * workspace is, in 256-byte pieces, the mask [B, S] fp32, kv_len [B] and the
+ * plan [2B + 1] int32, then per computed row (the packed row count with
+ * token packing, else B*S) its position int32, xb / ctx / proj bf16 [hidden],
+ * qkv bf16 [3 hidden], up bf16 [ffn] (2 ffn gated, plus the gated product
+ * [ffn]), emb fp32 [hidden] and on the int8 datapath xq int8 [max(hidden,
+ * ffn)] and its scale fp32; a batch whose workspace exceeds the scratch is
+ * refused (MX_E_INVALID, naming both sizes). Also refused: timing on
+ * (its events are created on demand) and an encoder whose device tables are
+ * stale (MX_E_STATE: call mx_encoder_ready after the last tensor is set;
+ * mx_encoder_from_npue and mx_encoder_clone return ready encoders). Every
+ * call on one GPU shares that GPU's scratch: calls that overlap on one GPU,
+ * from any encoder or stream, race. Synchronises s. */
+int mx_encoder_embed_static(mx_encoder *enc, mx_stream *s, const int32_t *ids,
+                            const float *attn_mask, int64_t B, int64_t S, float *out);
 
 /* Token packing in mx_encoder_embed (on by default): the only rows of a
  * sequence that reach its pooled row are those before kv_len (every later

@@ -29,7 +29,7 @@ FLAGS = [
 ]
 SOURCES = ["k_gemm_lds.hip", "k_gemm_i8.hip", "k_elem.hip", "k_gemm.hip", "k_attn.hip",
            "k_front.hip", "k_panel.hip", "k_quant.hip", "k_glu.hip", "mx_abi.cpp", "mx_i8.cpp",
-           "mx_encoder.cpp", "mx_npue.cpp", "mx_service.cpp", "mx_host.cpp"]
+           "mx_encoder.cpp", "mx_npue.cpp", "mx_service.cpp", "mx_host.cpp", "mx_static.hip"]
 
 
 def _compile(src):

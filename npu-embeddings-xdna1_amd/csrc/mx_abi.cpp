@@ -264,6 +264,17 @@ int mx_create(int device, mx_ctx **out) {
   if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
     return fail(MX_E_UNSUPPORTED, std::string("mx_create: device is ") + p.gcnArchName +
                                       "; this backend is built for gfx950 (MI355X) only");
+  // The static scratch's address on this device (mx_encoder_embed_static),
+  // looked up once with the device current; the caller's current device is
+  // restored.
+  int prev = 0;
+  e = hipGetDevice(&prev);
+  if (e == hipSuccess) e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(e, "mx_create: hipSetDevice");
+  const int rc = static_scratch_init(device);
+  e = hipSetDevice(prev);
+  if (rc) return rc;
+  if (e != hipSuccess) return hip_fail(e, "mx_create: restoring the current device");
   auto *c = new mx_ctx();
   c->device = device;
   c->props.device = device;

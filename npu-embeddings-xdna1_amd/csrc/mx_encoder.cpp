@@ -62,6 +62,20 @@ enum Cat { CAT_GEMM = 0, CAT_ATTN = 1, CAT_LN = 2, CAT_OTHER = 3 };
 // GEMM sites of a layer, in the order of mx_timings.gemm_site_*.
 enum Site { SITE_QKV = 0, SITE_AO = 1, SITE_UP = 2, SITE_DOWN = 3 };
 
+// The device buffers one embed / run works in (the HBM layout above).
+struct Work {
+  uint16_t *xb = nullptr, *qkv = nullptr, *ctxb = nullptr, *up = nullptr;
+  uint16_t *proj = nullptr;
+  float *emb = nullptr, *add_mask = nullptr;
+  int8_t *xq = nullptr;  // int8 datapath: quantised A and its row scales
+  float *sa = nullptr;
+  uint16_t *glu = nullptr;  // gated FFN: lo * act(hi), [M, f] bf16
+  int32_t *kv_len = nullptr;
+  // token packing: seq_start [B + 1] then attention's launch order [B], and
+  // each packed row's position [M]
+  int32_t *seq_start = nullptr, *row_pos = nullptr;
+};
+
 }  // namespace
 
 struct mx_encoder {
@@ -83,28 +97,23 @@ struct mx_encoder {
   float *emb_ln[2] = {nullptr, nullptr};
   float *fin_ln[2] = {nullptr, nullptr};
   float *word = nullptr, *pos = nullptr, *type = nullptr;
-  // workspace
+  // workspace: the encoder's own (sized by ensure_ws), or for one
+  // mx_encoder_embed_static call the carved static scratch
   int64_t ws_rows = 0, ws_batch = 0, ws_mask_rows = 0;
-  uint16_t *xb = nullptr, *qkv = nullptr, *ctxb = nullptr, *up = nullptr;
-  uint16_t *proj = nullptr;
-  float *emb = nullptr, *add_mask = nullptr;
-  int8_t *xq = nullptr;  // int8 datapath: quantised A and its row scales
-  float *sa = nullptr;
-  uint16_t *glu = nullptr;  // gated FFN: lo * act(hi), [M, f] bf16
+  Work work;
   // RoPE: the frequencies when the container gives them ("rope.inv_freq"),
   // and the device cos/sin tables [rope_rows, head_dim], built on first use.
   std::vector<float> rope_inv;
   float *rope_cos = nullptr, *rope_sin = nullptr;
   int64_t rope_rows = 0;
   bool i8 = false;       // set by mx_encoder_ready: every GEMM operand is int8
-  int32_t *kv_len = nullptr;
-  // Token packing (embed): seq_start [B + 1] and each packed row's position.
+  // Token packing (embed): seq_start [B + 1] and each packed row's position
+  // (work.seq_start, work.row_pos).
   bool packing = true;
   // The last packed plan read back (seq_start[0..B]) and its sum of squared
   // lengths: the attention work of a packed pass.
   std::vector<int32_t> plan_host;
   double packed_sq = 0.0;
-  int32_t *seq_start = nullptr, *row_pos = nullptr;
   // timing
   bool timing = false;
   std::vector<hipEvent_t> events;
@@ -142,7 +151,7 @@ int ensure_mask_ws(mx_encoder *enc, int64_t B, int64_t rows);
 
 int ensure_ws(mx_encoder *enc, int64_t B, int64_t S) {
   const int64_t rows = B * S;
-  if (rows > enc->ws_rows || (enc->i8 && !enc->xq)) {
+  if (rows > enc->ws_rows || (enc->i8 && !enc->work.xq)) {
     const int64_t want = rows > enc->ws_rows ? rows : enc->ws_rows;
     return ensure_ws_rows(enc, want, B);
   }
@@ -152,28 +161,28 @@ int ensure_ws(mx_encoder *enc, int64_t B, int64_t S) {
 int ensure_ws_rows(mx_encoder *enc, int64_t rows, int64_t B) {
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
   {
-    free_dev(enc->xb);
-    free_dev(enc->qkv);
-    free_dev(enc->ctxb);
-    free_dev(enc->up);
-    free_dev(enc->proj);
-    free_dev(enc->emb);
-    free_dev(enc->xq);
-    free_dev(enc->sa);
-    free_dev(enc->glu);
+    free_dev(enc->work.xb);
+    free_dev(enc->work.qkv);
+    free_dev(enc->work.ctxb);
+    free_dev(enc->work.up);
+    free_dev(enc->work.proj);
+    free_dev(enc->work.emb);
+    free_dev(enc->work.xq);
+    free_dev(enc->work.sa);
+    free_dev(enc->work.glu);
     enc->ws_rows = 0;
     const int64_t fu = enc->desc.gated_ffn ? 2 * f : f;
-    int rc = dev_alloc((void **)&enc->xb, rows * d * 2, "workspace xb");
-    if (!rc) rc = dev_alloc((void **)&enc->qkv, rows * 3 * d * 2, "workspace qkv");
-    if (!rc) rc = dev_alloc((void **)&enc->ctxb, rows * d * 2, "workspace ctx");
-    if (!rc) rc = dev_alloc((void **)&enc->up, rows * fu * 2, "workspace up");
+    int rc = dev_alloc((void **)&enc->work.xb, rows * d * 2, "workspace xb");
+    if (!rc) rc = dev_alloc((void **)&enc->work.qkv, rows * 3 * d * 2, "workspace qkv");
+    if (!rc) rc = dev_alloc((void **)&enc->work.ctxb, rows * d * 2, "workspace ctx");
+    if (!rc) rc = dev_alloc((void **)&enc->work.up, rows * fu * 2, "workspace up");
     if (!rc && enc->desc.gated_ffn)
-      rc = dev_alloc((void **)&enc->glu, rows * f * 2, "workspace gated");
-    if (!rc) rc = dev_alloc((void **)&enc->proj, rows * d * 2, "workspace proj");
-    if (!rc) rc = dev_alloc((void **)&enc->emb, rows * d * 4, "workspace emb");
+      rc = dev_alloc((void **)&enc->work.glu, rows * f * 2, "workspace gated");
+    if (!rc) rc = dev_alloc((void **)&enc->work.proj, rows * d * 2, "workspace proj");
+    if (!rc) rc = dev_alloc((void **)&enc->work.emb, rows * d * 4, "workspace emb");
     if (!rc && enc->i8)
-      rc = dev_alloc((void **)&enc->xq, rows * (d > f ? d : f), "workspace xq");
-    if (!rc && enc->i8) rc = dev_alloc((void **)&enc->sa, rows * 4, "workspace sa");
+      rc = dev_alloc((void **)&enc->work.xq, rows * (d > f ? d : f), "workspace xq");
+    if (!rc && enc->i8) rc = dev_alloc((void **)&enc->work.sa, rows * 4, "workspace sa");
     if (rc) return rc;
     enc->ws_rows = rows;
   }
@@ -186,16 +195,16 @@ int ensure_mask_ws(mx_encoder *enc, int64_t B, int64_t rows) {
   if (B > enc->ws_batch || rows > enc->ws_mask_rows) {
     const int64_t nb = B > enc->ws_batch ? B : enc->ws_batch;
     const int64_t nr = rows > enc->ws_mask_rows ? rows : enc->ws_mask_rows;
-    free_dev(enc->add_mask);
-    free_dev(enc->kv_len);
-    free_dev(enc->seq_start);
-    free_dev(enc->row_pos);
+    free_dev(enc->work.add_mask);
+    free_dev(enc->work.kv_len);
+    free_dev(enc->work.seq_start);
+    free_dev(enc->work.row_pos);
     enc->ws_batch = enc->ws_mask_rows = 0;
-    int rc = dev_alloc((void **)&enc->add_mask, nr * 4, "workspace mask");
-    if (!rc) rc = dev_alloc((void **)&enc->kv_len, nb * 4, "workspace kv_len");
+    int rc = dev_alloc((void **)&enc->work.add_mask, nr * 4, "workspace mask");
+    if (!rc) rc = dev_alloc((void **)&enc->work.kv_len, nb * 4, "workspace kv_len");
     // seq_start [B + 1], then attention's launch order [B].
-    if (!rc) rc = dev_alloc((void **)&enc->seq_start, (2 * nb + 1) * 4, "workspace seq_start");
-    if (!rc) rc = dev_alloc((void **)&enc->row_pos, nr * 4, "workspace row_pos");
+    if (!rc) rc = dev_alloc((void **)&enc->work.seq_start, (2 * nb + 1) * 4, "workspace seq_start");
+    if (!rc) rc = dev_alloc((void **)&enc->work.row_pos, nr * 4, "workspace row_pos");
     if (rc) return rc;
     enc->ws_batch = nb;
     enc->ws_mask_rows = nr;
@@ -270,7 +279,7 @@ int gemm_i8_l(mx_encoder *enc, mx_stream *s, int site, int64_t M, int64_t K, con
   Bracket br(enc, s->stream, CAT_GEMM + 16 * site);
   enc->gemm_flop += 2.0 * M * N * K;
   enc->site_flop[site] += 2.0 * M * N * K;
-  return gemm_i8_checked(s, enc->xq, enc->sa, M, K, K, Wq, ws, N, bias, epi, resid, C, c_dtype,
+  return gemm_i8_checked(s, enc->work.xq, enc->work.sa, M, K, K, Wq, ws, N, bias, epi, resid, C, c_dtype,
                          N);
 }
 
@@ -278,13 +287,13 @@ int lnq_l(mx_encoder *enc, mx_stream *s, const float *x, const void *y, int y_dt
           const float *b, int64_t rows, float *of, const float *ias) {
   Bracket br(enc, s->stream, CAT_LN);
   return layernorm_i8_checked(s, x, y, y_dt, g, b, enc->desc.ln_eps, rows, enc->desc.hidden, of,
-                              ias, enc->xq, enc->sa);
+                              ias, enc->work.xq, enc->work.sa);
 }
 
 int quant_l(mx_encoder *enc, mx_stream *s, const uint16_t *a, int64_t rows, int64_t K,
             const float *ias) {
   Bracket br(enc, s->stream, CAT_OTHER);
-  return quantise_checked(s, a, MX_BF16, K, rows, K, ias, enc->xq, K, enc->sa);
+  return quantise_checked(s, a, MX_BF16, K, rows, K, ias, enc->work.xq, K, enc->work.sa);
 }
 
 // RoPE tables for positions [0, S), built on the host once (double angles,
@@ -311,13 +320,13 @@ int ensure_rope(mx_encoder *enc, int64_t S) {
 int rope_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, int64_t M,
            const int32_t *row_pos) {
   Bracket br(enc, s->stream, CAT_OTHER);
-  return rope_checked(s, enc->qkv, 3 * enc->desc.hidden, B, S, enc->desc.heads,
+  return rope_checked(s, enc->work.qkv, 3 * enc->desc.hidden, B, S, enc->desc.heads,
                       enc->desc.head_dim, enc->rope_cos, enc->rope_sin, M, row_pos);
 }
 
 int glu_l(mx_encoder *enc, mx_stream *s, int64_t M) {
   Bracket br(enc, s->stream, CAT_OTHER);
-  return glu_checked(s, enc->up, MX_BF16, enc->glu, MX_BF16, M, enc->desc.ffn,
+  return glu_checked(s, enc->work.up, MX_BF16, enc->work.glu, MX_BF16, M, enc->desc.ffn,
                      enc->desc.gated_ffn);
 }
 
@@ -375,7 +384,7 @@ int ensure_glu_operands(mx_encoder *enc) {
 }
 
 // FFN-up with the gated FFN fused: the layer's interleaved operand, C =
-// enc->glu [M, f] bf16, the same values as the GEMM into enc->up and glu_l.
+// enc->work.glu [M, f] bf16, the same values as the GEMM into enc->work.up and glu_l.
 int gemm_glu_l(mx_encoder *enc, mx_stream *s, const LayerW &w, int64_t M) {
   Bracket br(enc, s->stream, CAT_GEMM + 16 * SITE_UP);
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
@@ -385,11 +394,11 @@ int gemm_glu_l(mx_encoder *enc, mx_stream *s, const LayerW &w, int64_t M) {
       enc->desc.gated_ffn == MX_GATED_SILU ? mxk::EPI_GLU_SILU : mxk::EPI_GLU_GELU;
   hipError_t e;
   if (enc->i8) {
-    const mxk::GemmI8Args a{enc->xq, d,       w.wqg,   M, 2 * f, d,   enc->sa,
-                            w.wsg,   w.bg,    epi,     nullptr,  enc->glu, 1, f};
+    const mxk::GemmI8Args a{enc->work.xq, d,       w.wqg,   M, 2 * f, d,   enc->work.sa,
+                            w.wsg,   w.bg,    epi,     nullptr,  enc->work.glu, 1, f};
     e = mxk::gemm_i8(a, s->stream);
   } else {
-    const mxk::GemmArgs a{enc->xb, d, w.wg, M, 2 * f, d, w.bg, epi, nullptr, enc->glu, 1, f};
+    const mxk::GemmArgs a{enc->work.xb, d, w.wg, M, 2 * f, d, w.bg, epi, nullptr, enc->work.glu, 1, f};
     e = mxk::gemm(a, s->stream);
   }
   return e == hipSuccess ? MX_OK : hip_fail(e, "gemm launch (FFN-up with the gated FFN)");
@@ -410,8 +419,8 @@ int attn_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, const float *mas
   // Packed rows: each sequence attends over its own kv_len rows only.
   const double sq = rows && rows->seq_start ? enc->packed_sq : (double)B * S * S;
   enc->attn_flop += 4.0 * enc->desc.heads * sq * enc->desc.head_dim;
-  return attention_checked(s, enc->qkv, 3 * d, B, S, enc->desc.heads, enc->desc.head_dim,
-                           enc->desc.attn_scale, mask, kv_len, enc->ctxb, d,
+  return attention_checked(s, enc->work.qkv, 3 * d, B, S, enc->desc.heads, enc->desc.head_dim,
+                           enc->desc.attn_scale, mask, kv_len, enc->work.ctxb, d,
                            rows ? rows->seq_start : nullptr, rows ? rows->order : nullptr);
 }
 
@@ -432,7 +441,7 @@ int site_gemm(mx_encoder *enc, mx_stream *s, const LayerW &w, int site, const ui
 int site_ln(mx_encoder *enc, mx_stream *s, float *x, const void *y, int y_dt, const float *g,
             const float *b, int64_t M, float *out_f32, const float *ias_next) {
   if (enc->i8 && ias_next) return lnq_l(enc, s, x, y, y_dt, g, b, M, out_f32, ias_next);
-  return ln_l(enc, s, x, MX_F32, y, y_dt, g, b, M, out_f32, enc->i8 ? nullptr : enc->xb);
+  return ln_l(enc, s, x, MX_F32, y, y_dt, g, b, M, out_f32, enc->i8 ? nullptr : enc->work.xb);
 }
 
 int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
@@ -442,7 +451,7 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
   const size_t L = enc->layers.size();
   const bool gated = enc->desc.gated_ffn != MX_GATED_NONE;
   const int64_t fu = gated ? 2 * f : f;
-  uint16_t *act = gated ? enc->glu : enc->up;  // FFN-down's A (bf16 datapath)
+  uint16_t *act = gated ? enc->work.glu : enc->work.up;  // FFN-down's A (bf16 datapath)
   int rc = enc->desc.rope ? ensure_rope(enc, S) : MX_OK;
   if (!rc)
     rc = site_ln(enc, s, x, nullptr, MX_F32, enc->emb_ln[0], enc->emb_ln[1], M, x,
@@ -451,30 +460,30 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
     const LayerW &w = enc->layers[l];
     const bool fused = gated && enc->fuse_glu && glu_fusable(enc) && w.glu_gen == enc->wgen &&
                        (enc->i8 ? w.wqg && w.wsg : w.wg != nullptr) && w.bg;
-    rc = site_gemm(enc, s, w, SITE_QKV, enc->xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->qkv,
+    rc = site_gemm(enc, s, w, SITE_QKV, enc->work.xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->work.qkv,
                    MX_BF16);
     if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S, M, rows.row_pos);
     if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, &rows);
-    if (!rc && enc->i8) rc = quant_l(enc, s, enc->ctxb, M, d, w.ias[SITE_AO]);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.ctxb, M, d, w.ias[SITE_AO]);
     if (!rc)
-      rc = site_gemm(enc, s, w, SITE_AO, enc->ctxb, M, d, d, MX_EPI_NONE, nullptr, enc->proj,
+      rc = site_gemm(enc, s, w, SITE_AO, enc->work.ctxb, M, d, d, MX_EPI_NONE, nullptr, enc->work.proj,
                      MX_BF16);
     if (!rc)
-      rc = site_ln(enc, s, x, enc->proj, MX_BF16, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
+      rc = site_ln(enc, s, x, enc->work.proj, MX_BF16, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
     if (!rc && fused) {
       rc = gemm_glu_l(enc, s, w, M);
     } else {
       if (!rc)
-        rc = site_gemm(enc, s, w, SITE_UP, enc->xb, M, d, fu, gated ? MX_EPI_NONE : epi,
-                       nullptr, enc->up, MX_BF16);
+        rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, M, d, fu, gated ? MX_EPI_NONE : epi,
+                       nullptr, enc->work.up, MX_BF16);
       if (!rc && gated) rc = glu_l(enc, s, M);
     }
     if (!rc && enc->i8) rc = quant_l(enc, s, act, M, f, w.ias[SITE_DOWN]);
     if (!rc)
-      rc = site_gemm(enc, s, w, SITE_DOWN, act, M, f, d, MX_EPI_NONE, nullptr, enc->proj,
+      rc = site_gemm(enc, s, w, SITE_DOWN, act, M, f, d, MX_EPI_NONE, nullptr, enc->work.proj,
                      MX_BF16);
     if (!rc)
-      rc = site_ln(enc, s, x, enc->proj, MX_BF16, w.ln[2], w.ln[3], M, x,
+      rc = site_ln(enc, s, x, enc->work.proj, MX_BF16, w.ln[2], w.ln[3], M, x,
                    l + 1 < L ? enc->layers[l + 1].ias[SITE_QKV] : nullptr);
   }
   return rc;
@@ -489,15 +498,15 @@ int run_preln(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const 
     const LayerW &w = enc->layers[l];
     rc = site_ln(enc, s, x, nullptr, MX_F32, w.ln[0], w.ln[1], M, nullptr, w.ias[SITE_QKV]);
     if (!rc)
-      rc = site_gemm(enc, s, w, SITE_QKV, enc->xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->qkv,
+      rc = site_gemm(enc, s, w, SITE_QKV, enc->work.xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->work.qkv,
                      MX_BF16);
     if (!rc) rc = attn_l(enc, s, B, S, mask, kvl);
-    if (!rc && enc->i8) rc = quant_l(enc, s, enc->ctxb, M, d, w.ias[SITE_AO]);
-    if (!rc) rc = site_gemm(enc, s, w, SITE_AO, enc->ctxb, M, d, d, MX_EPI_NONE, x, x, MX_F32);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.ctxb, M, d, w.ias[SITE_AO]);
+    if (!rc) rc = site_gemm(enc, s, w, SITE_AO, enc->work.ctxb, M, d, d, MX_EPI_NONE, x, x, MX_F32);
     if (!rc) rc = site_ln(enc, s, x, nullptr, MX_F32, w.ln[2], w.ln[3], M, nullptr, w.ias[SITE_UP]);
-    if (!rc) rc = site_gemm(enc, s, w, SITE_UP, enc->xb, M, d, f, epi, nullptr, enc->up, MX_BF16);
-    if (!rc && enc->i8) rc = quant_l(enc, s, enc->up, M, f, w.ias[SITE_DOWN]);
-    if (!rc) rc = site_gemm(enc, s, w, SITE_DOWN, enc->up, M, f, d, MX_EPI_NONE, x, x, MX_F32);
+    if (!rc) rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, M, d, f, epi, nullptr, enc->work.up, MX_BF16);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.up, M, f, w.ias[SITE_DOWN]);
+    if (!rc) rc = site_gemm(enc, s, w, SITE_DOWN, enc->work.up, M, f, d, MX_EPI_NONE, x, x, MX_F32);
   }
   if (!rc) rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, enc->fin_ln[0], enc->fin_ln[1], M, x, nullptr);
   return rc;
@@ -629,21 +638,21 @@ void free_weights(mx_encoder *enc) {
 }
 
 void free_workspace(mx_encoder *enc) {
-  free_dev(enc->xb);
-  free_dev(enc->qkv);
-  free_dev(enc->ctxb);
-  free_dev(enc->up);
-  free_dev(enc->proj);
-  free_dev(enc->emb);
-  free_dev(enc->xq);
-  free_dev(enc->sa);
-  free_dev(enc->glu);
+  free_dev(enc->work.xb);
+  free_dev(enc->work.qkv);
+  free_dev(enc->work.ctxb);
+  free_dev(enc->work.up);
+  free_dev(enc->work.proj);
+  free_dev(enc->work.emb);
+  free_dev(enc->work.xq);
+  free_dev(enc->work.sa);
+  free_dev(enc->work.glu);
   free_dev(enc->rope_cos);
   free_dev(enc->rope_sin);
-  free_dev(enc->add_mask);
-  free_dev(enc->kv_len);
-  free_dev(enc->seq_start);
-  free_dev(enc->row_pos);
+  free_dev(enc->work.add_mask);
+  free_dev(enc->work.kv_len);
+  free_dev(enc->work.seq_start);
+  free_dev(enc->work.row_pos);
   free_dev(enc->f_rows);
   free_dev(enc->f_cls);
   free_dev(enc->f_mel);
@@ -809,6 +818,12 @@ int mx_encoder_clone(mx_encoder *enc, mx_encoder **out) {
   c->head_b = enc->head_b;
   c->cls_tok = enc->cls_tok;
   c->front_pos = enc->front_pos;
+  // The clone's own device tables (RoPE), so it is ready as the owner is.
+  rc = mx_encoder_ready(c);
+  if (rc) {
+    mx_encoder_destroy(c);
+    return rc;
+  }
   *out = c;
   return MX_OK;
 }
@@ -995,8 +1010,13 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
   return fail(MX_E_INVALID, "encoder_set: unknown tensor '" + name + "'");
 }
 
-int mx_encoder_ready(mx_encoder *enc) {
-  if (!enc) return fail(MX_E_INVALID, "encoder_ready: null encoder");
+}  // extern "C"
+
+namespace {
+
+// mx_encoder_ready's checks, allocating nothing: every tensor of the path
+// set, one datapath (*i8: int8), a RoPE frequency.
+int check_ready(const mx_encoder *enc, bool *i8_out) {
   // The datapath is the first operand's: bf16, or int8 (BertEncoder's
   // int8 design set). A stack mixing the two is refused by name.
   const bool i8 = !enc->layers.empty() && enc->layers[0].wq[0] != nullptr;
@@ -1043,8 +1063,212 @@ int mx_encoder_ready(mx_encoder *enc) {
   if (enc->desc.rope && enc->rope_inv.empty() && !(enc->desc.rope_theta > 0.0))
     return fail(MX_E_STATE, "encoder: RoPE without a frequency set -- a positive rope_theta or "
                             "rope.inv_freq is needed");
+  *i8_out = i8;
+  return MX_OK;
+}
+
+// Whether everything mx_encoder_ready builds on the device is current for an
+// embed of sequence length S, so that the embed allocates nothing: the
+// datapath flag, the gated FFN's interleaved operands, the RoPE tables.
+int check_prepared(const mx_encoder *enc, int64_t S) {
+  bool i8 = false;
+  const int rc = check_ready(enc, &i8);
+  if (rc) return rc;
+  const char *stale = nullptr;
+  if (i8 != enc->i8) stale = "the datapath";
+  if (!stale && enc->owns_weights && enc->fuse_glu && glu_fusable(enc))
+    for (const LayerW &w : enc->layers)
+      if (w.glu_gen != enc->wgen) stale = "the gated FFN's interleaved operands";
+  if (!stale && enc->desc.rope && enc->rope_rows < S) stale = "the RoPE tables";
+  if (stale)
+    return fail(MX_E_STATE, std::string("encoder_embed_static: ") + stale +
+                                " are not built for this call (it allocates nothing); call "
+                                "mx_encoder_ready after the last tensor is set");
+  return MX_OK;
+}
+
+// The argument checks both embeds share.
+int embed_args(const mx_encoder *enc, const mx_stream *s, const int32_t *ids,
+               const float *attn_mask, int64_t B, int64_t S, const float *out,
+               const char *what) {
+  const std::string w = what;
+  if (!enc || !s || !ids || !attn_mask || !out) return fail(MX_E_INVALID, w + ": null argument");
+  if (B <= 0 || S <= 0) return fail(MX_E_INVALID, w + ": empty batch");
+  if (enc->desc.arch != MX_ARCH_BERT)
+    return fail(MX_E_INVALID, w + ": the text path is the BERT encoder's");
+  if (!enc->word || !enc->pos || !enc->type)
+    return fail(MX_E_STATE, w + ": embeddings.word/position/token_type not set");
+  if (S > enc->desc.max_pos)
+    return fail(MX_E_INVALID, w + ": seq " + std::to_string(S) + " exceeds the " +
+                                  std::to_string(enc->desc.max_pos) + " position embeddings");
+  return MX_OK;
+}
+
+// The static scratch handed out in 256-byte aligned pieces, front to back.
+struct Carver {
+  uint8_t *base;
+  size_t cap;
+  size_t used = 0;
+  static size_t piece(int64_t bytes) { return (static_cast<size_t>(bytes) + 255) & ~size_t(255); }
+  template <typename T>
+  T *take(int64_t count) {
+    T *p = reinterpret_cast<T *>(base + used);
+    used += piece(count * static_cast<int64_t>(sizeof(T)));
+    return p;
+  }
+};
+
+// Bytes of the batch-shaped buffers (mask [B, S], kv_len [B], seq_start and
+// the launch order [2B + 1]) and of the row-shaped ones for `rows` rows
+// (row_pos and the activations of the HBM layout above), in Carver pieces.
+size_t plan_bytes(int64_t B, int64_t S) {
+  return Carver::piece(B * S * 4) + Carver::piece(B * 4) + Carver::piece((2 * B + 1) * 4);
+}
+size_t rows_bytes(const mx_encoder *enc, int64_t rows) {
+  const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
+  const bool gated = enc->desc.gated_ffn != MX_GATED_NONE;
+  size_t n = Carver::piece(rows * 4);                                  // row_pos
+  n += 3 * Carver::piece(rows * d * 2) + Carver::piece(rows * 3 * d * 2);  // xb ctx proj qkv
+  n += Carver::piece(rows * (gated ? 2 * f : f) * 2);                  // up
+  if (gated) n += Carver::piece(rows * f * 2);                         // glu
+  n += Carver::piece(rows * d * 4);                                    // emb
+  if (enc->i8) n += Carver::piece(rows * (d > f ? d : f)) + Carver::piece(rows * 4);
+  return n;
+}
+void carve_plan(Carver &c, int64_t B, int64_t S, Work &w) {
+  w.add_mask = c.take<float>(B * S);
+  w.kv_len = c.take<int32_t>(B);
+  w.seq_start = c.take<int32_t>(2 * B + 1);
+}
+void carve_rows(const mx_encoder *enc, Carver &c, int64_t rows, Work &w) {
+  const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
+  const bool gated = enc->desc.gated_ffn != MX_GATED_NONE;
+  w.row_pos = c.take<int32_t>(rows);
+  w.xb = c.take<uint16_t>(rows * d);
+  w.ctxb = c.take<uint16_t>(rows * d);
+  w.proj = c.take<uint16_t>(rows * d);
+  w.qkv = c.take<uint16_t>(rows * 3 * d);
+  w.up = c.take<uint16_t>(rows * (gated ? 2 * f : f));
+  if (gated) w.glu = c.take<uint16_t>(rows * f);
+  w.emb = c.take<float>(rows * d);
+  if (enc->i8) {
+    w.xq = c.take<int8_t>(rows * (d > f ? d : f));
+    w.sa = c.take<float>(rows);
+  }
+}
+int scratch_refusal(const mx_encoder *enc, int64_t B, int64_t S, int64_t rows, size_t need,
+                    size_t cap, bool packed) {
+  return fail(MX_E_INVALID,
+              "encoder_embed_static: " + std::to_string(B) + " x " + std::to_string(S) +
+                  (packed ? " packs to " + std::to_string(rows) + " rows" : " is " +
+                   std::to_string(rows) + " rows") + " of hidden " +
+                  std::to_string(enc->desc.hidden) + ", whose workspace needs " +
+                  std::to_string(need) + " bytes; the static scratch holds " +
+                  std::to_string(cap) + " (MX_STATIC_SCRATCH_BYTES)");
+}
+
+// EmbedService::chunk minus the tokenizer (embed_service.cpp:29-64): mask and
+// plan, embedding sum, the stack, pooling, then the data refusals. carve null:
+// the encoder's own workspace (ensure_ws sized it). carve set: every buffer
+// is carved from the static scratch -- the batch-shaped ones first, the
+// row-shaped ones once the packed row count is known -- and nothing is
+// allocated.
+int embed_body(mx_encoder *enc, mx_stream *s, const int32_t *ids, const float *attn_mask,
+               int64_t B, int64_t S, float *out, Carver *carve) {
+  if (carve) {
+    const size_t need = plan_bytes(B, S) + (enc->packing ? 0 : rows_bytes(enc, B * S));
+    if (need > carve->cap) return scratch_refusal(enc, B, S, B * S, need, carve->cap, false);
+    carve_plan(*carve, B, S, enc->work);
+    if (!enc->packing) carve_rows(enc, *carve, B * S, enc->work);
+  }
+  int rc = begin_timing(enc, s);
+  if (rc) return rc;
+  Rows rows{B * S};
+  {
+    Bracket br(enc, s->stream, CAT_OTHER);
+    hipError_t e = mxk::mask_build(attn_mask, B, S, enc->work.add_mask, enc->work.kv_len, s->stream);
+    // The plan: seq_start and attention's launch order (both layouts use the
+    // order; kv_len differs per sequence either way).
+    int32_t *order = enc->work.seq_start + B + 1;
+    if (e == hipSuccess) e = mxk::pack_plan(enc->work.kv_len, B, enc->work.seq_start, order, s->stream);
+    if (e == hipSuccess && enc->packing) {
+      // Token packing: the packed row count is needed on the host for the
+      // launches, so it is read back (one small copy per batch; the whole
+      // plan when timing, for the attention work).
+      int32_t total = 0;
+      if (carve) {
+        e = hipMemcpyAsync(&total, enc->work.seq_start + B, sizeof(int32_t),
+                           hipMemcpyDeviceToHost, s->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+        if (e != hipSuccess) return hip_fail(e, "reading the packed row count");
+        const size_t need = carve->used + rows_bytes(enc, total);
+        if (need > carve->cap) return scratch_refusal(enc, B, S, total, need, carve->cap, true);
+        carve_rows(enc, *carve, total, enc->work);
+        enc->packed_sq = 0.0;
+      } else {
+        enc->plan_host.resize(static_cast<size_t>(B + 1));
+        e = hipMemcpyAsync(enc->plan_host.data(), enc->work.seq_start, (B + 1) * sizeof(int32_t),
+                           hipMemcpyDeviceToHost, s->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+        if (e == hipSuccess) {
+          total = enc->plan_host[B];
+          enc->packed_sq = 0.0;
+          for (int64_t b = 0; b < B; ++b) {
+            const double L = enc->plan_host[b + 1] - enc->plan_host[b];
+            enc->packed_sq += L * L;
+          }
+        }
+      }
+      if (e == hipSuccess)
+        e = mxk::embed_sum_packed(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab,
+                                  enc->pos, enc->type, enc->work.kv_len, enc->work.seq_start,
+                                  enc->work.emb, enc->work.row_pos, s->err_dev, s->stream);
+      rows = Rows{total, enc->work.seq_start, enc->work.row_pos, order};
+    } else if (e == hipSuccess) {
+      e = mxk::embed_sum(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab, enc->pos,
+                         enc->type, enc->work.emb, s->err_dev, s->stream);
+      rows.order = order;
+    }
+    if (e != hipSuccess) return hip_fail(e, "embed launch");
+  }
+  rc = run_impl(enc, s, enc->work.emb, enc->work.add_mask, enc->work.kv_len, B, S, &rows);
+  if (rc) return rc;
+  {
+    Bracket br(enc, s->stream, CAT_OTHER);
+    const hipError_t e =
+        mxk::pool_rows(enc->work.emb, attn_mask, B, S, enc->desc.hidden, enc->desc.cls_pool,
+                       enc->desc.l2_normalize, out, s->err_dev, s->stream, rows.seq_start);
+    if (e != hipSuccess) return hip_fail(e, "pool launch");
+  }
+  end_timing(enc, s);
+  int flags = 0;
+  rc = take_data_error(s, &flags);
+  if (rc) return rc;
+  if (flags & 1)
+    return fail(MX_E_DATA, "encoder_embed: a token id is outside [0, " +
+                               std::to_string(enc->desc.vocab) + ")");
+  if (flags & 2) return fail(MX_E_DATA, "CLS pooling on a sequence whose first token is masked");
+  return MX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mx_encoder_ready(mx_encoder *enc) {
+  if (!enc) return fail(MX_E_INVALID, "encoder_ready: null encoder");
+  bool i8 = false;
+  int rc = check_ready(enc, &i8);
+  if (rc) return rc;
   enc->i8 = i8;
-  return ensure_glu_operands(enc);
+  rc = ensure_glu_operands(enc);
+  // The RoPE tables for every position the text path embeds (S <= max_pos),
+  // built here once so that no embed needs to allocate them.
+  if (!rc && enc->desc.rope && enc->rope_rows < enc->desc.max_pos) {
+    rc = use_device(enc->ctx);
+    if (!rc) rc = ensure_rope(enc, enc->desc.max_pos);
+  }
+  return rc;
 }
 
 int mx_encoder_run(mx_encoder *enc, mx_stream *s, float *x_io, const float *add_mask,
@@ -1066,76 +1290,35 @@ int mx_encoder_run(mx_encoder *enc, mx_stream *s, float *x_io, const float *add_
 int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids, const float *attn_mask,
                      int64_t B, int64_t S, float *out) {
   clear_error();
-  if (!enc || !s || !ids || !attn_mask || !out)
-    return fail(MX_E_INVALID, "encoder_embed: null argument");
-  if (enc->desc.arch != MX_ARCH_BERT)
-    return fail(MX_E_INVALID, "encoder_embed: the text path is the BERT encoder's");
-  if (!enc->word || !enc->pos || !enc->type)
-    return fail(MX_E_STATE, "encoder_embed: embeddings.word/position/token_type not set");
-  if (S > enc->desc.max_pos)
-    return fail(MX_E_INVALID, "encoder_embed: seq " + std::to_string(S) + " exceeds the " +
-                                  std::to_string(enc->desc.max_pos) + " position embeddings");
-  int rc = use_device(enc->ctx);
+  int rc = embed_args(enc, s, ids, attn_mask, B, S, out, "encoder_embed");
+  if (!rc) rc = use_device(enc->ctx);
   if (!rc) rc = check_placement();
   if (!rc) rc = mx_encoder_ready(enc);
   if (!rc) rc = ensure_ws(enc, B, S);
-  if (!rc) rc = begin_timing(enc, s);
   if (rc) return rc;
-  Rows rows{B * S};
-  {
-    Bracket br(enc, s->stream, CAT_OTHER);
-    hipError_t e = mxk::mask_build(attn_mask, B, S, enc->add_mask, enc->kv_len, s->stream);
-    // The plan: seq_start and attention's launch order (both layouts use the
-    // order; kv_len differs per sequence either way).
-    int32_t *order = enc->seq_start + B + 1;
-    if (e == hipSuccess) e = mxk::pack_plan(enc->kv_len, B, enc->seq_start, order, s->stream);
-    if (e == hipSuccess && enc->packing) {
-      // Token packing: the packed row count is needed on the host for the
-      // launches, so the plan is read back (one small copy per batch).
-      int32_t total = 0;
-      enc->plan_host.resize(static_cast<size_t>(B + 1));
-      if (e == hipSuccess)
-        e = hipMemcpyAsync(enc->plan_host.data(), enc->seq_start, (B + 1) * sizeof(int32_t),
-                           hipMemcpyDeviceToHost, s->stream);
-      if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
-      if (e == hipSuccess) {
-        total = enc->plan_host[B];
-        enc->packed_sq = 0.0;
-        for (int64_t b = 0; b < B; ++b) {
-          const double L = enc->plan_host[b + 1] - enc->plan_host[b];
-          enc->packed_sq += L * L;
-        }
-      }
-      if (e == hipSuccess)
-        e = mxk::embed_sum_packed(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab,
-                                  enc->pos, enc->type, enc->kv_len, enc->seq_start, enc->emb,
-                                  enc->row_pos, s->err_dev, s->stream);
-      rows = Rows{total, enc->seq_start, enc->row_pos, order};
-    } else if (e == hipSuccess) {
-      e = mxk::embed_sum(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab, enc->pos,
-                         enc->type, enc->emb, s->err_dev, s->stream);
-      rows.order = order;
-    }
-    if (e != hipSuccess) return hip_fail(e, "embed launch");
-  }
-  rc = run_impl(enc, s, enc->emb, enc->add_mask, enc->kv_len, B, S, &rows);
+  return embed_body(enc, s, ids, attn_mask, B, S, out, nullptr);
+}
+
+int mx_encoder_embed_static(mx_encoder *enc, mx_stream *s, const int32_t *ids,
+                            const float *attn_mask, int64_t B, int64_t S, float *out) {
+  clear_error();
+  int rc = embed_args(enc, s, ids, attn_mask, B, S, out, "encoder_embed_static");
   if (rc) return rc;
-  {
-    Bracket br(enc, s->stream, CAT_OTHER);
-    const hipError_t e =
-        mxk::pool_rows(enc->emb, attn_mask, B, S, enc->desc.hidden, enc->desc.cls_pool,
-                       enc->desc.l2_normalize, out, s->err_dev, s->stream, rows.seq_start);
-    if (e != hipSuccess) return hip_fail(e, "pool launch");
-  }
-  end_timing(enc, s);
-  int flags = 0;
-  rc = take_data_error(s, &flags);
+  if (enc->timing)
+    return fail(MX_E_STATE, "encoder_embed_static: timing is on (its events are created on "
+                            "demand); mx_encoder_set_timing(enc, 0) first");
+  void *scratch = nullptr;
+  rc = use_device(enc->ctx);
+  if (!rc) rc = static_scratch(enc->ctx->device, &scratch);
+  if (!rc) rc = check_placement();
+  if (!rc) rc = check_prepared(enc, S);
   if (rc) return rc;
-  if (flags & 1)
-    return fail(MX_E_DATA, "encoder_embed: a token id is outside [0, " +
-                               std::to_string(enc->desc.vocab) + ")");
-  if (flags & 2) return fail(MX_E_DATA, "CLS pooling on a sequence whose first token is masked");
-  return MX_OK;
+  Carver carve{static_cast<uint8_t *>(scratch), static_scratch_bytes()};
+  const Work own = enc->work;  // the encoder's workspace, back in place on return
+  enc->work = Work{};
+  rc = embed_body(enc, s, ids, attn_mask, B, S, out, &carve);
+  enc->work = own;
+  return rc;
 }
 
 int mx_encoder_vit(mx_encoder *enc, mx_stream *s, const float *pixels, int64_t B, float *logits,

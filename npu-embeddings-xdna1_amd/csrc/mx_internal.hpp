@@ -94,6 +94,12 @@ int glu_checked(mx_stream *s, const void *up, int up_dtype, void *out, int out_d
                 int64_t rows, int64_t f, int act);
 // Read and clear the stream's data-refusal flag (synchronises the stream).
 int take_data_error(mx_stream *s, int *flags);
+// The static device scratch of mx_encoder_embed_static (mx_static.hip): its
+// address on each device is looked up once, by mx_create with that device
+// current (static_scratch_init), and handed out by static_scratch.
+int static_scratch_init(int device);
+int static_scratch(int device, void **ptr);
+size_t static_scratch_bytes();
 
 // The context and width of an encoder (for mx_service.cpp).
 mx_ctx *encoder_ctx(const mx_encoder *enc);

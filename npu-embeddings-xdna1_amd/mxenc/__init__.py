@@ -21,6 +21,7 @@ MX_SOFTMAX_POLY, MX_SOFTMAX_EXACT, MX_SOFTMAX_AIE = 0, 1, 2
 MX_ARCH_BERT, MX_ARCH_PRELN = 0, 1
 MX_FRONT_NONE, MX_FRONT_VIT, MX_FRONT_WHISPER = 0, 1, 2
 MX_GATED_NONE, MX_GATED_SILU, MX_GATED_GELU_ERF = 0, 1, 2
+MX_STATIC_SCRATCH_BYTES = 128 << 20
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -109,6 +110,7 @@ SIGNATURES = {
     "mx_encoder_ready": (_int, [_vp]),
     "mx_encoder_run": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64]),
     "mx_encoder_embed": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "mx_encoder_embed_static": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "mx_encoder_vit": (_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
     "mx_encoder_whisper": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "mx_encoder_set_timing": (_int, [_vp, _int]),
@@ -548,6 +550,15 @@ class Encoder:
     def embed(self, ids, attn_mask, B, S, out):
         check(lib().mx_encoder_embed(self.handle, self.ctx.stream, _p(ids), _p(attn_mask), B,
                                      S, _p(out)))
+
+    def embed_static(self, ids, attn_mask, B, S, out):
+        """mx_encoder_embed_static: the same embed with its workspace carved from
+        the library's static scratch (MX_STATIC_SCRATCH_BYTES per GPU)."""
+        check(lib().mx_encoder_embed_static(self.handle, self.ctx.stream, _p(ids),
+                                            _p(attn_mask), B, S, _p(out)))
+
+    def ready(self):
+        check(lib().mx_encoder_ready(self.handle))
 
     def vit(self, pixels, B, logits, hidden=None):
         check(lib().mx_encoder_vit(self.handle, self.ctx.stream, _p(pixels), B, _p(logits),
