@@ -175,10 +175,13 @@ int ensure_ws_rows(mx_encoder *enc, int64_t rows, int64_t B) {
     int rc = dev_alloc((void **)&enc->work.xb, rows * d * 2, "workspace xb");
     if (!rc) rc = dev_alloc((void **)&enc->work.qkv, rows * 3 * d * 2, "workspace qkv");
     if (!rc) rc = dev_alloc((void **)&enc->work.ctxb, rows * d * 2, "workspace ctx");
-    if (!rc) rc = dev_alloc((void **)&enc->work.up, rows * fu * 2, "workspace up");
+    // int8: FFN-up's activation stays fp32 up to its quantiser
+    const int64_t ab = enc->i8 ? 4 : 2;
+    if (!rc) rc = dev_alloc((void **)&enc->work.up, rows * fu * ab, "workspace up");
     if (!rc && enc->desc.gated_ffn)
-      rc = dev_alloc((void **)&enc->work.glu, rows * f * 2, "workspace gated");
-    if (!rc) rc = dev_alloc((void **)&enc->work.proj, rows * d * 2, "workspace proj");
+      rc = dev_alloc((void **)&enc->work.glu, rows * f * ab, "workspace gated");
+    // int8: the attention-out / FFN-down results stay fp32 (dequantise_c's C)
+    if (!rc) rc = dev_alloc((void **)&enc->work.proj, rows * d * ab, "workspace proj");
     if (!rc) rc = dev_alloc((void **)&enc->work.emb, rows * d * 4, "workspace emb");
     if (!rc && enc->i8)
       rc = dev_alloc((void **)&enc->work.xq, rows * (d > f ? d : f), "workspace xq");
@@ -290,10 +293,10 @@ int lnq_l(mx_encoder *enc, mx_stream *s, const float *x, const void *y, int y_dt
                               ias, enc->work.xq, enc->work.sa);
 }
 
-int quant_l(mx_encoder *enc, mx_stream *s, const uint16_t *a, int64_t rows, int64_t K,
+int quant_l(mx_encoder *enc, mx_stream *s, const void *a, int a_dtype, int64_t rows, int64_t K,
             const float *ias) {
   Bracket br(enc, s->stream, CAT_OTHER);
-  return quantise_checked(s, a, MX_BF16, K, rows, K, ias, enc->work.xq, K, enc->work.sa);
+  return quantise_checked(s, a, a_dtype, K, rows, K, ias, enc->work.xq, K, enc->work.sa);
 }
 
 // RoPE tables for positions [0, S), built on the host once (double angles,
@@ -324,19 +327,21 @@ int rope_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, int64_t M,
                       enc->desc.head_dim, enc->rope_cos, enc->rope_sin, M, row_pos);
 }
 
-int glu_l(mx_encoder *enc, mx_stream *s, int64_t M) {
+int glu_l(mx_encoder *enc, mx_stream *s, int64_t M, int dtype) {
   Bracket br(enc, s->stream, CAT_OTHER);
-  return glu_checked(s, enc->work.up, MX_BF16, enc->work.glu, MX_BF16, M, enc->desc.ffn,
+  return glu_checked(s, enc->work.up, dtype, enc->work.glu, dtype, M, enc->desc.ffn,
                      enc->desc.gated_ffn);
 }
 
 // Whether FFN-up can carry the gated FFN in its epilogue: whole 64-row
-// groups of the interleaved operand (f % 32 == 0) on the LDS-pipelined kernel
-// (bf16: K a multiple of 32, at least 128; the int8 GEMM always is).
+// groups of the interleaved operand (f % 32 == 0) on the LDS-pipelined bf16
+// kernel (K a multiple of 32, at least 128). The int8 datapath keeps FFN-up's
+// activation in fp32 up to its quantiser (dequant_act_quant), which the
+// fused epilogue's bf16 C does not, so it runs the GEMM and the GLU apart.
 bool glu_fusable(const mx_encoder *enc) {
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
-  return enc->desc.gated_ffn != MX_GATED_NONE && f % 32 == 0 &&
-         (enc->i8 || (d % 32 == 0 && d >= 128));
+  return enc->desc.gated_ffn != MX_GATED_NONE && f % 32 == 0 && !enc->i8 && d % 32 == 0 &&
+         d >= 128;
 }
 
 // The interleaved FFN-up copies of every layer, when stale (owning encoder
@@ -464,26 +469,35 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
                    MX_BF16);
     if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S, M, rows.row_pos);
     if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, &rows);
-    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.ctxb, M, d, w.ias[SITE_AO]);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.ctxb, MX_BF16, M, d, w.ias[SITE_AO]);
+    // proj: bf16 (the array path's C) or, on the int8 datapath, fp32 as
+    // dequantise_c writes it (host_kernels.hpp:529-600)
+    const int pdt = enc->i8 ? MX_F32 : MX_BF16;
     if (!rc)
-      rc = site_gemm(enc, s, w, SITE_AO, enc->work.ctxb, M, d, d, MX_EPI_NONE, nullptr, enc->work.proj,
-                     MX_BF16);
-    if (!rc)
-      rc = site_ln(enc, s, x, enc->work.proj, MX_BF16, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
-    if (!rc && fused) {
+      rc = site_gemm(enc, s, w, SITE_AO, enc->work.ctxb, M, d, d, MX_EPI_NONE, nullptr,
+                     enc->work.proj, pdt);
+    if (!rc) rc = site_ln(enc, s, x, enc->work.proj, pdt, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
+    if (!rc && enc->i8) {
+      // dequant_act_quant (host_kernels.hpp:405-522, bert_encoder.cpp:811-860):
+      // FFN-up dequantised, biased and activated in fp32 (the gated halves
+      // combined in fp32), then quantised per row from those fp32 values.
+      rc = site_gemm(enc, s, w, SITE_UP, nullptr, M, d, fu, gated ? MX_EPI_NONE : epi, nullptr,
+                     enc->work.up, MX_F32);
+      if (!rc && gated) rc = glu_l(enc, s, M, MX_F32);
+      if (!rc) rc = quant_l(enc, s, act, MX_F32, M, f, w.ias[SITE_DOWN]);
+    } else if (!rc && fused) {
       rc = gemm_glu_l(enc, s, w, M);
     } else {
       if (!rc)
         rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, M, d, fu, gated ? MX_EPI_NONE : epi,
                        nullptr, enc->work.up, MX_BF16);
-      if (!rc && gated) rc = glu_l(enc, s, M);
+      if (!rc && gated) rc = glu_l(enc, s, M, MX_BF16);
     }
-    if (!rc && enc->i8) rc = quant_l(enc, s, act, M, f, w.ias[SITE_DOWN]);
     if (!rc)
       rc = site_gemm(enc, s, w, SITE_DOWN, act, M, f, d, MX_EPI_NONE, nullptr, enc->work.proj,
-                     MX_BF16);
+                     pdt);
     if (!rc)
-      rc = site_ln(enc, s, x, enc->work.proj, MX_BF16, w.ln[2], w.ln[3], M, x,
+      rc = site_ln(enc, s, x, enc->work.proj, pdt, w.ln[2], w.ln[3], M, x,
                    l + 1 < L ? enc->layers[l + 1].ias[SITE_QKV] : nullptr);
   }
   return rc;
@@ -501,11 +515,15 @@ int run_preln(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const 
       rc = site_gemm(enc, s, w, SITE_QKV, enc->work.xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->work.qkv,
                      MX_BF16);
     if (!rc) rc = attn_l(enc, s, B, S, mask, kvl);
-    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.ctxb, M, d, w.ias[SITE_AO]);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.ctxb, MX_BF16, M, d, w.ias[SITE_AO]);
     if (!rc) rc = site_gemm(enc, s, w, SITE_AO, enc->work.ctxb, M, d, d, MX_EPI_NONE, x, x, MX_F32);
     if (!rc) rc = site_ln(enc, s, x, nullptr, MX_F32, w.ln[2], w.ln[3], M, nullptr, w.ias[SITE_UP]);
-    if (!rc) rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, M, d, f, epi, nullptr, enc->work.up, MX_BF16);
-    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.up, M, f, w.ias[SITE_DOWN]);
+    // int8: FFN-up's activation in fp32 up to its quantiser, as the dequantise
+    // -> GELU -> quantise_a_int8 sequence keeps it (npu_ops.cpp:334-361)
+    if (!rc)
+      rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, M, d, f, epi, nullptr, enc->work.up,
+                     enc->i8 ? MX_F32 : MX_BF16);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.up, MX_F32, M, f, w.ias[SITE_DOWN]);
     if (!rc) rc = site_gemm(enc, s, w, SITE_DOWN, enc->work.up, M, f, d, MX_EPI_NONE, x, x, MX_F32);
   }
   if (!rc) rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, enc->fin_ln[0], enc->fin_ln[1], M, x, nullptr);
@@ -1128,9 +1146,11 @@ size_t rows_bytes(const mx_encoder *enc, int64_t rows) {
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
   const bool gated = enc->desc.gated_ffn != MX_GATED_NONE;
   size_t n = Carver::piece(rows * 4);                                  // row_pos
-  n += 3 * Carver::piece(rows * d * 2) + Carver::piece(rows * 3 * d * 2);  // xb ctx proj qkv
-  n += Carver::piece(rows * (gated ? 2 * f : f) * 2);                  // up
-  if (gated) n += Carver::piece(rows * f * 2);                         // glu
+  const int64_t ab = enc->i8 ? 4 : 2;  // int8: FFN-up's activation and proj in fp32
+  n += 2 * Carver::piece(rows * d * 2) + Carver::piece(rows * d * ab);  // xb ctx proj
+  n += Carver::piece(rows * 3 * d * 2);                                 // qkv
+  n += Carver::piece(rows * (gated ? 2 * f : f) * ab);                 // up
+  if (gated) n += Carver::piece(rows * f * ab);                        // glu
   n += Carver::piece(rows * d * 4);                                    // emb
   if (enc->i8) n += Carver::piece(rows * (d > f ? d : f)) + Carver::piece(rows * 4);
   return n;
@@ -1146,10 +1166,11 @@ void carve_rows(const mx_encoder *enc, Carver &c, int64_t rows, Work &w) {
   w.row_pos = c.take<int32_t>(rows);
   w.xb = c.take<uint16_t>(rows * d);
   w.ctxb = c.take<uint16_t>(rows * d);
-  w.proj = c.take<uint16_t>(rows * d);
+  const int64_t ab = enc->i8 ? 2 : 1;  // int8: FFN-up's activation and proj in fp32
+  w.proj = c.take<uint16_t>(rows * d * ab);
   w.qkv = c.take<uint16_t>(rows * 3 * d);
-  w.up = c.take<uint16_t>(rows * (gated ? 2 * f : f));
-  if (gated) w.glu = c.take<uint16_t>(rows * f);
+  w.up = c.take<uint16_t>(rows * (gated ? 2 * f : f) * ab);
+  if (gated) w.glu = c.take<uint16_t>(rows * f * ab);
   w.emb = c.take<float>(rows * d);
   if (enc->i8) {
     w.xq = c.take<int8_t>(rows * (d > f ? d : f));

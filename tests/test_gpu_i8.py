@@ -335,22 +335,25 @@ def _dequantised(m, q8):
 
 def _check_i8_parity(got8, host8, hostf, tag):
     """The int8 datapath's end-to-end bar. The integer product, the
-    quantisation and the dequantisation are pinned bit for bit per op (above);
-    end to end, the GPU computes attention and the activations between the
-    quantisers in bf16 where the host keeps fp32, and a value that lands on
-    the other side of an int8 rounding boundary moves by a whole step of the
-    grid. So the GPU's departure from the host int8 result is measured against
-    the int8 scheme's own error (host int8 against the host fp32 stack on the
-    dequantised operands): (1) the GPU int8 result is as accurate as the
-    host's, within 25 %; (2) GPU and host int8 differ by at most 2.5 draws of
-    that error (two independent draws of the same grid noise differ by ~2)."""
+    quantisation and the dequantisation are pinned bit for bit per op (above),
+    and between the quantisers the GPU keeps the host's fp32 where the
+    reference does (FFN-up's activation up to its quantiser, as
+    dequant_act_quant; the attention-out and FFN-down results, as
+    dequantise_c). Attention still runs on bf16 Q/K/V into a bf16 context,
+    and a value that lands on the other side of an int8 rounding boundary
+    moves by a whole step of the grid. So the GPU's departure from the host
+    int8 result is measured against the int8 scheme's own error e (host int8
+    against the host fp32 stack on the dequantised operands): (1) the GPU int8
+    result is as accurate as the host's, within 10 %; (2) GPU and host int8
+    differ by at most 1.75 e (two independent draws of the same grid noise
+    differ by ~2 e; measured on bge-base: 1.39 e)."""
     e_scheme = 1.0 - _cos(host8, hostf)
     e_gpu = 1.0 - _cos(got8, hostf)
     e_pair = 1.0 - _cos(got8, host8)
     print(f"{tag}: 1-cos gpu8~host8 {e_pair.max():.3e}, host8~fp32 {e_scheme.max():.3e}, "
           f"gpu8~fp32 {e_gpu.max():.3e}")
-    assert np.all(e_gpu <= 1.25 * e_scheme + 1e-5), (e_gpu, e_scheme)
-    assert np.all(e_pair <= 2.5 * e_scheme + 1e-5), (e_pair, e_scheme)
+    assert np.all(e_gpu <= 1.1 * e_scheme + 1e-5), (e_gpu, e_scheme)
+    assert np.all(e_pair <= 1.75 * e_scheme + 1e-5), (e_pair, e_scheme)
 
 
 def test_i8_stack_minilm_full_config(ctx, orc):

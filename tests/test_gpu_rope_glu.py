@@ -190,7 +190,9 @@ def test_nomic_int8_stack(ctx, orc):
 # (arch, int8 datapath, model overrides, B, S): the row counts put FFN-up's
 # fused kernel on each tile -- 128 rows: 128 x 128; 1000: 128 x 256; 2048: the
 # 256 x 256 tile (on 128-byte slabs, or on 64-byte slabs for a hidden width
-# that is not a multiple of 64 (bf16) or 128 (int8)).
+# that is not a multiple of 64). The int8 datapath keeps FFN-up's activation
+# in fp32 up to its quantiser (dequant_act_quant), so it always runs the GEMM
+# and the gated-FFN pass apart: its cases check the switch leaves it as it is.
 FUSED_CASES = [
     ("nomic", False, {}, 4, 512),
     ("gte", False, {}, 2, 64),
