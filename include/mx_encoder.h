@@ -184,6 +184,19 @@ int mx_layernorm(mx_stream *s, const void *x, int x_dtype, const void *y,
                  int y_dtype, const float *gamma, const float *beta, float eps,
                  int64_t rows, int64_t cols, float *out_f32, uint16_t *out_bf16);
 
+/* layn on the accelerator's own arithmetic: replaces the K2r LayerNorm kernel
+ * (kernels/layernorm.cc:65-142 built with layernorm_rne.cc:42-52's
+ * conv_even rounding) that eltwise(layn) dispatches on the array. bf16
+ * x [rows, cols] -> bf16 out (may alias x), row stride cols; 16 fp32 partial
+ * sums per pass (column j into sum j % 16, in column order) added in order,
+ * the biased variance about that mean, fast_invsqrt (the 0x5f3759df estimate
+ * and two Newton steps) of var + eps, y = (d * inv_std) * gamma + beta
+ * rounded to bf16 to nearest even, every operation rounded on its own.
+ * cols % 16 == 0 and cols <= 4096 (MX_E_UNSUPPORTED otherwise), rows <= 2^28;
+ * x, out, gamma and beta 16-byte aligned. */
+int mx_layernorm_aie(mx_stream *s, const uint16_t *x, const float *gamma, const float *beta,
+                     float eps, int64_t rows, int64_t cols, uint16_t *out);
+
 /* gelu: replaces gelu_cpu / eltwise(gelu) (bert_encoder.cpp:532-580),
  * gelu_erf_inplace (npu_ops.cpp:470-476) and NpuEltwise::gelu. Elementwise,
  * in place allowed (x == y with equal dtypes). */

@@ -94,19 +94,19 @@ __global__ void narrow_i32_scalar_k(const int32_t *__restrict__ in, uint16_t *__
 
 // gelu_erf.cc:79-145: A&S 7.1.26 erf with the AIE exp2, unfused steps.
 __device__ __forceinline__ float gelu_erf_as(float x) {
-  const float u = __fmul_rn(x, 0.70710678118654752440f);
+  const float u = mul_rn(x, 0.70710678118654752440f);
   const float au = fabsf(u);
-  const float t = __fdiv_rn(1.0f, __fadd_rn(1.0f, __fmul_rn(0.3275911f, au)));
+  const float t = __fdiv_rn(1.0f, add_rn(1.0f, mul_rn(0.3275911f, au)));
   float p = 1.061405429f;
-  p = __fadd_rn(__fmul_rn(p, t), -1.453152027f);
-  p = __fadd_rn(__fmul_rn(p, t), 1.421413741f);
-  p = __fadd_rn(__fmul_rn(p, t), -0.284496736f);
-  p = __fadd_rn(__fmul_rn(p, t), 0.254829592f);
-  float z = __fmul_rn(__fsub_rn(0.0f, __fmul_rn(u, u)), 1.4426950408889634f);
+  p = add_rn(mul_rn(p, t), -1.453152027f);
+  p = add_rn(mul_rn(p, t), 1.421413741f);
+  p = add_rn(mul_rn(p, t), -0.284496736f);
+  p = add_rn(mul_rn(p, t), 0.254829592f);
+  float z = mul_rn(sub_rn(0.0f, mul_rn(u, u)), 1.4426950408889634f);
   z = z > -125.0f ? z : -125.0f;
   const float ex = exp2_poly_aie(z);
-  const float eabs = __fsub_rn(1.0f, __fmul_rn(__fmul_rn(t, p), ex));
-  return __fadd_rn(__fmul_rn(x, 0.5f), __fmul_rn(__fmul_rn(fabsf(x), 0.5f), eabs));
+  const float eabs = sub_rn(1.0f, mul_rn(mul_rn(t, p), ex));
+  return add_rn(mul_rn(x, 0.5f), mul_rn(mul_rn(fabsf(x), 0.5f), eabs));
 }
 
 __device__ __forceinline__ float gelu_variant(float v, int variant) {
@@ -294,6 +294,85 @@ __global__ __launch_bounds__(256) void layernorm_any_k(
   }
 }
 
+// ---- LayerNorm with the accelerator kernel's arithmetic ---------------------
+// kernels/layernorm.cc:85-142 under layernorm_rne.cc's conv_even: bf16 in and
+// out; 16 fp32 partial sums per pass (column j into sum j % 16, in column
+// order), the 16 added in order; the biased variance about that mean;
+// fast_invsqrt of var + eps (the 0x5f3759df estimate and two Newton steps,
+// layernorm.cc:65-75); y = (d * inv_std) * gamma + beta narrowed to bf16 to
+// nearest even. Every product and sum rounds on its own (no FMA).
+// One wave normalises 4 rows: the rows reach LDS by 16-byte loads, lanes
+// 16r .. 16r + 15 keep row r's 16 partial sums (lane 16r + l is sum l), each
+// of them adds the 16 in order itself, and the results leave in 16-byte
+// stores. The 4 rows are in LDS before any is written, so out may alias x.
+__device__ __forceinline__ float fast_invsqrt_aie(float x) {
+  const float xhalf = mul_rn(0.5f, x);
+  int i = __float_as_int(x);
+  i = 0x5f3759df - (i >> 1);
+  float y = __int_as_float(i);
+  y = mul_rn(y, sub_rn(1.5f, mul_rn(mul_rn(xhalf, y), y)));
+  y = mul_rn(y, sub_rn(1.5f, mul_rn(mul_rn(xhalf, y), y)));
+  return y;
+}
+
+__global__ __launch_bounds__(64) void layernorm_aie_k(const uint16_t *__restrict__ x,
+                                                      const float *__restrict__ gamma,
+                                                      const float *__restrict__ beta, float eps,
+                                                      float inv_cols, int64_t rows, int cols,
+                                                      uint16_t *out) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t srow[];  // [4][cols]
+  const int lane = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * 4;
+  const int nr = rows - r0 < 4 ? (int)(rows - r0) : 4;
+  const int cpr = cols / 8;  // 16-byte chunks per row
+  for (int c = lane; c < nr * cpr; c += 64) {
+    const int r = c / cpr, k = c - r * cpr;
+    *(uint4 *)(srow + r * cols + k * 8) = *(const uint4 *)(x + (r0 + r) * cols + k * 8);
+  }
+  __syncthreads();
+  const int r = lane >> 4, l = lane & 15, lead = lane & ~15;
+  const bool live = r < nr;
+  const uint16_t *xr = srow + (live ? r : 0) * cols;
+  float acc = 0.0f;
+  if (live)
+    for (int j = l; j < cols; j += 16) acc = add_rn(acc, bf2f(xr[j]));
+  float sum = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) sum = add_rn(sum, __shfl(acc, lead + q));
+  const float mean = mul_rn(sum, inv_cols);
+  float acc2 = 0.0f;
+  if (live)
+    for (int j = l; j < cols; j += 16) {
+      const float d = sub_rn(bf2f(xr[j]), mean);
+      acc2 = add_rn(acc2, mul_rn(d, d));
+    }
+  float vs = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) vs = add_rn(vs, __shfl(acc2, lead + q));
+  const float inv_std = fast_invsqrt_aie(add_rn(mul_rn(vs, inv_cols), eps));
+  if (!live) return;
+  for (int k = l; k < cpr; k += 16) {
+    const uint4 raw = *(const uint4 *)(xr + k * 8);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    const float4 g0 = *(const float4 *)(gamma + k * 8), g1 = *(const float4 *)(gamma + k * 8 + 4);
+    const float4 b0 = *(const float4 *)(beta + k * 8), b1 = *(const float4 *)(beta + k * 8 + 4);
+    const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float y2[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float d = sub_rn(bf2f(h ? w[e] >> 16 : w[e] & 0xFFFFu), mean);
+        y2[h] = add_rn(mul_rn(mul_rn(d, inv_std), g[2 * e + h]), b[2 * e + h]);
+      }
+      o[e] = pack_bf2(y2[0], y2[1]);
+    }
+    *(uint4 *)(out + (r0 + r) * cols + k * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // ---- softmax: one wave per row, NV values per lane (cols <= 64 * NV) --------
 
 template <int NV>
@@ -340,15 +419,34 @@ __global__ __launch_bounds__(256) void softmax_wave_k(void *x, int bf, int64_t r
       } else {
         float d = v[i] - m;
         d = d > -100.0f ? d : -100.0f;
-        float a = __fmul_rn(d, 1.4426950408889634f);
+        float a = mul_rn(d, 1.4426950408889634f);
         a = a > -120.0f ? a : -120.0f;
         e = bf2f(f2bf(exp2_poly_aie(a)));
       }
-      s += e;
+      if (variant != 2) s += e;
     }
     v[i] = e;
   }
-  s = wave_sum(s);
+  if (variant == 2) {
+    // softmax.cc:115-145's 16-lane accumulator: column j into partial sum
+    // j % 16 in column order (columns l, l + 16, l + 32, l + 48 of each
+    // 64-column group sit in lanes l .. l + 48), then the 16 in order. Lanes
+    // 0 .. 15 hold the partial sums; every lane adds them itself.
+    float part = 0.0f;
+    const int l = lane & 15;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float t = __shfl(v[i], l + 16 * q);
+        if (64 * i + 16 * q + l < cols) part = add_rn(part, t);
+      }
+    s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) s = add_rn(s, __shfl(part, q));
+  } else {
+    s = wave_sum(s);
+  }
   const float inv = variant == 1 ? (s > 0.0f ? 1.0f / s : 0.0f) : 1.0f / s;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -535,7 +633,7 @@ __global__ __launch_bounds__(1024) void pool_k(const float *__restrict__ h,
 #pragma unroll
           for (int u = 0; u < POOL_U; ++u) {
             if (i0 + u < n) den += m[u];
-            a += m[u] != 0.0f ? (double)(__fmul_rn(v[u], m[u])) : 0.0;
+            a += m[u] != 0.0f ? (double)(mul_rn(v[u], m[u])) : 0.0;
           }
         }
       }
@@ -670,6 +768,16 @@ hipError_t layernorm(const void *x, int x_bf, const void *y, int y_bf, const flo
   }
   layernorm_any_k<<<(unsigned)rows, 256, 0, s>>>(x, x_bf, y, y_bf, gamma, beta, eps, rows, cols,
                                                  out_f32, out_bf16);
+  return hipGetLastError();
+}
+
+hipError_t layernorm_aie(const uint16_t *x, const float *gamma, const float *beta, float eps,
+                         int64_t rows, int64_t cols, uint16_t *out, hipStream_t s) {
+  const int64_t g = (rows + 3) / 4;
+  const size_t lds = (size_t)4 * cols * 2;
+  const float inv_cols = 1.0f / (float)cols;
+  layernorm_aie_k<<<(unsigned)g, 64, lds, s>>>(x, gamma, beta, eps, inv_cols, rows, (int)cols,
+                                               out);
   return hipGetLastError();
 }
 

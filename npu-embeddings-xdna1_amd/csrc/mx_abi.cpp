@@ -509,6 +509,25 @@ int mx_layernorm(mx_stream *s, const void *x, int x_dtype, const void *y, int y_
   return e == hipSuccess ? MX_OK : hip_fail(e, "layernorm launch");
 }
 
+int mx_layernorm_aie(mx_stream *s, const uint16_t *x, const float *gamma, const float *beta,
+                     float eps, int64_t rows, int64_t cols, uint16_t *out) {
+  clear_error();
+  if (!s || !x || !gamma || !beta || !out)
+    return fail(MX_E_INVALID, "layernorm_aie: null argument");
+  if (rows <= 0 || cols <= 0) return fail(MX_E_INVALID, "layernorm_aie: zero dimension");
+  // one 64-lane workgroup per 4 rows: at most 2^26 workgroups
+  if (rows > ((int64_t)1 << 28)) return fail(MX_E_INVALID, "layernorm_aie: more than 2^28 rows");
+  if (cols % 16 || cols > 4096)
+    return fail(MX_E_UNSUPPORTED, "layernorm_aie: cols " + std::to_string(cols) +
+                                      " is not a multiple of 16 up to 4096 (the kernel's "
+                                      "16-lane vectors)");
+  if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(MX_E_INVALID, "layernorm_aie: bad eps");
+  if (!aligned(x, 16) || !aligned(out, 16) || !aligned(gamma, 16) || !aligned(beta, 16))
+    return fail(MX_E_INVALID, "layernorm_aie: x, out, gamma and beta must be 16-byte aligned");
+  const hipError_t e = mxk::layernorm_aie(x, gamma, beta, eps, rows, cols, out, s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "layernorm_aie launch");
+}
+
 int mx_gelu(mx_stream *s, const void *x, int x_dtype, void *y, int y_dtype, int64_t n,
             int variant) {
   clear_error();

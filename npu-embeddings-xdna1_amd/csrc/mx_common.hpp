@@ -135,20 +135,38 @@ __device__ __forceinline__ float glu_act(float hi) {
   return 0.5f * hi * (1.0f + erff(hi * 0.70710678118654752440f));
 }
 
+// A rounded product, sum and difference that the compiler may not fuse into a
+// multiply-add. (HIP's __fmul_rn / __fadd_rn are plain x * y and x + y in its
+// headers, compiled under the default contraction, so a product feeding a sum
+// through them still becomes one FMA.) Contraction is off inside each; a
+// product without the contract flag is never fused.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
+
 // The AIE exp2_poly (kernels/exp2_poly.h:35-65): the same table, each Horner
 // step a rounded multiply then a rounded add (no FMA).
 __device__ __forceinline__ float exp2_poly_aie(float x) {
   const int k = (int)x;
-  const float f = __fsub_rn(x, (float)k);
+  const float f = sub_rn(x, (float)k);
   float p = 1.5483275463e-05f;
-  p = __fadd_rn(__fmul_rn(p, f), 1.5669833174e-04f);
-  p = __fadd_rn(__fmul_rn(p, f), 1.3331825236e-03f);
-  p = __fadd_rn(__fmul_rn(p, f), 9.6164605538e-03f);
-  p = __fadd_rn(__fmul_rn(p, f), 5.5504156855e-02f);
-  p = __fadd_rn(__fmul_rn(p, f), 2.4022684109e-01f);
-  p = __fadd_rn(__fmul_rn(p, f), 6.9314717694e-01f);
-  p = __fadd_rn(__fmul_rn(p, f), 9.9999998955e-01f);
-  return __fmul_rn(p, __uint_as_float((uint32_t)(k + 127) << 23));
+  p = add_rn(mul_rn(p, f), 1.5669833174e-04f);
+  p = add_rn(mul_rn(p, f), 1.3331825236e-03f);
+  p = add_rn(mul_rn(p, f), 9.6164605538e-03f);
+  p = add_rn(mul_rn(p, f), 5.5504156855e-02f);
+  p = add_rn(mul_rn(p, f), 2.4022684109e-01f);
+  p = add_rn(mul_rn(p, f), 6.9314717694e-01f);
+  p = add_rn(mul_rn(p, f), 9.9999998955e-01f);
+  return mul_rn(p, __uint_as_float((uint32_t)(k + 127) << 23));
 }
 
 }  // namespace mxd

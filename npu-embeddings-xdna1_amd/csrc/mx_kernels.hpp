@@ -15,6 +15,11 @@ hipError_t gelu(const void *x, int x_bf, void *y, int y_bf, int64_t n, int varia
 hipError_t layernorm(const void *x, int x_bf, const void *y, int y_bf, const float *gamma,
                      const float *beta, float eps, int64_t rows, int64_t cols, float *out_f32,
                      uint16_t *out_bf16, hipStream_t s);
+// The accelerator LayerNorm (kernels/layernorm.cc:85-142, conv_even): bf16
+// [rows, cols] in and out (out may alias x), cols % 16 == 0, cols <= 4096,
+// 16-byte aligned x, out, gamma and beta.
+hipError_t layernorm_aie(const uint16_t *x, const float *gamma, const float *beta, float eps,
+                         int64_t rows, int64_t cols, uint16_t *out, hipStream_t s);
 hipError_t softmax_rows(void *x, int bf, int64_t rows, int64_t cols, int64_t stride,
                         const float *mask, int64_t rows_per_mask_row, int variant,
                         hipStream_t s);

@@ -94,6 +94,7 @@ SIGNATURES = {
     "mx_softmax_rows": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _i64, _int]),
     "mx_layernorm": (_int, [_vp, _vp, _int, _vp, _int, _vp, _vp, ctypes.c_float, _i64, _i64,
                             _vp, _vp]),
+    "mx_layernorm_aie": (_int, [_vp, _vp, _vp, _vp, ctypes.c_float, _i64, _i64, _vp]),
     "mx_gelu": (_int, [_vp, _vp, _int, _vp, _int, _i64, _int]),
     "mx_narrow_f32_bf16": (_int, [_vp, _vp, _vp, _i64]),
     "mx_narrow_i32_bf16": (_int, [_vp, _vp, _vp, _i64]),
@@ -285,6 +286,11 @@ def layernorm(ctx, x, y, gamma, beta, eps, rows, cols, out_f32=None, out_bf16=No
     yd = _np_dtype_code(np.empty(0, y.dtype)) if y is not None else MX_F32
     check(lib().mx_layernorm(ctx.stream, x.p, xd, _p(y), yd, gamma.p, beta.p, eps, rows, cols,
                              _p(out_f32), _p(out_bf16)))
+
+
+def layernorm_aie(ctx, x, gamma, beta, eps, rows, cols, out):
+    """mx_layernorm_aie: bf16 x -> bf16 out with the accelerator kernel's arithmetic."""
+    check(lib().mx_layernorm_aie(ctx.stream, x.p, gamma.p, beta.p, eps, rows, cols, out.p))
 
 
 def softmax_rows(ctx, x, rows, cols, stride, mask=None, rows_per_mask_row=1,

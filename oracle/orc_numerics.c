@@ -117,7 +117,9 @@ static inline float aie_exp2(float x) {
 
 static inline float bf(float x) { return orc_from_bf16(orc_to_bf16(x)); }
 
-/* softmax.cc:76-160 with softmax_rne.cc's conv_even. */
+/* softmax.cc:76-160 with softmax_rne.cc's conv_even. The exponentials are
+ * summed as the 16-lane accumulator holds them (:115-145): element j into
+ * partial sum j % 16, in element order, then the 16 partial sums in order. */
 void orc_aie_softmax_bf16(const uint16_t *in, uint16_t *out, int64_t rows,
                           int64_t cols) {
   const float lo = bf(-1.0e30f);
@@ -131,7 +133,7 @@ void orc_aie_softmax_bf16(const uint16_t *in, uint16_t *out, int64_t rows,
       v = v > lo ? v : lo;
       m = v > m ? v : m;
     }
-    float sum = 0.0f;
+    float acc[16] = {0};
     for (int64_t j = 0; j < cols; ++j) {
       float v = orc_from_bf16(x[j]);
       v = v > lo ? v : lo;
@@ -140,8 +142,10 @@ void orc_aie_softmax_bf16(const uint16_t *in, uint16_t *out, int64_t rows,
       float a = d * 1.4426950408889634f;
       a = a > -120.0f ? a : -120.0f;
       e[j] = bf(aie_exp2(a));
-      sum += e[j];
+      acc[j % 16] += e[j];
     }
+    float sum = 0.0f;
+    for (int l = 0; l < 16; ++l) sum += acc[l];
     const float inv = 1.0f / sum;
     for (int64_t j = 0; j < cols; ++j) o[j] = orc_to_bf16(e[j] * inv);
   }

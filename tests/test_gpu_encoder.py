@@ -66,19 +66,29 @@ def test_minilm_full_config(ctx, orc):
     enc.close()
 
 
-def test_bge_base_full_batch_subset_checked(ctx, orc):
+def test_bge_base_full_batch_every_sequence_checked(ctx, orc):
     """bge-base geometry at its full shape (batch 64 x seq 512, 12 layers, CLS
-    pooling) on the GPU; three of its sequences (the longest, the shortest and
-    one more) rerun on the host path."""
+    pooling), the benchmark's own batch, on the GPU; every one of the 64
+    sequences rerun on the host path (in chunks of 16: sequences are
+    independent, which test_oracle_encoder pins on the host), cosine >= 0.9999
+    each."""
+    import os
     m = synth.make_model("bge_base")
     ids, am, lens = synth.make_text_inputs(m)
     enc = mxenc.Encoder(ctx, m)
     got = gpu_embed(ctx, enc, ids, am)
-    pick = [int(np.argmax(lens)), int(np.argmin(lens)), 5]
-    want, _ = oracle_embed(orc, m, np.ascontiguousarray(ids[pick]), np.ascontiguousarray(am[pick]))
-    cos = cosines(got[pick], want)
-    assert np.min(cos) >= COS_MIN, cos
     enc.close()
+    cpus = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else 8
+    orc.orc_set_threads(max(1, min(16, cpus)))
+    want = np.empty_like(got)
+    for lo in range(0, ids.shape[0], 16):
+        sl = slice(lo, lo + 16)
+        want[sl], _ = oracle_embed(orc, m, np.ascontiguousarray(ids[sl]),
+                                   np.ascontiguousarray(am[sl]))
+        print(f"bge-base oracle: sequences {lo}..{lo + 15} done", flush=True)
+    cos = cosines(got, want)
+    print(f"bge-base 64 sequences: min cos {np.min(cos):.8f}, 1 - cos max {1 - np.min(cos):.2e}")
+    assert np.min(cos) >= COS_MIN, cos
 
 
 def test_streams_agree_bitwise(ctx):

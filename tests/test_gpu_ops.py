@@ -228,8 +228,66 @@ def test_softmax_aie_bf16(ctx, orc):
     dx = ctx.put(xb)
     mxenc.softmax_rows(ctx, dx, rows, cols, cols, None, 1, mxenc.MX_SOFTMAX_AIE)
     got = dx.host()
-    # identical exponentials; the fp32 sum order differs: <= 1 bf16 ulp
-    assert np.max(np.abs(got.astype(np.int32) - want.astype(np.int32))) <= 1
+    # the same exponentials summed in the same 16-lane order: bit for bit
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 16), (7, 48), (300, 768), (64, 4096), (17455, 64),
+                                       (33, 200)])
+def test_softmax_aie_bf16_shapes(ctx, orc, rows, cols):
+    """The accelerator softmax at ragged and full row widths, masked tails and
+    a row whose every entry is at the clamp: bit for bit."""
+    rng = np.random.default_rng(rows * 31 + cols)
+    x = (rng.standard_normal((rows, cols)) * 4).astype(np.float32)
+    if rows > 3:
+        x[1, cols // 2:] = -1e30
+        x[2, :] = -3e38
+    xb = to_bf16_bits(x)
+    want = np.empty_like(xb)
+    orc.orc_aie_softmax_bf16(P(xb), P(want), rows, cols)
+    dx = ctx.put(xb)
+    mxenc.softmax_rows(ctx, dx, rows, cols, cols, None, 1, mxenc.MX_SOFTMAX_AIE)
+    assert np.array_equal(dx.host(), want)
+
+
+LN_AIE_SHAPES = [(1, 16), (5, 384), (4096, 768), (17455, 768), (3, 1024), (9, 4096), (6, 48)]
+
+
+@pytest.mark.parametrize("rows,cols", LN_AIE_SHAPES)
+def test_layernorm_aie_bit_exact(ctx, orc, rows, cols):
+    """mx_layernorm_aie (the K2r kernel's arithmetic) against the oracle's
+    restatement, bit for bit: row scales over four decades, a constant row
+    (variance 0: fast_invsqrt of eps), random gamma and beta; in place too."""
+    rng = np.random.default_rng(rows + 7 * cols)
+    sc = np.exp(rng.uniform(np.log(1e-2), np.log(1e2), rows)).astype(np.float32)
+    x = (rng.standard_normal((rows, cols)).astype(np.float32) + 0.3) * sc[:, None]
+    if rows > 2:
+        x[2, :] = 1.5
+    g = (1 + 0.2 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.2 * rng.standard_normal(cols)).astype(np.float32)
+    xb = to_bf16_bits(x)
+    for eps in (1e-12, 1e-5):
+        want = np.empty_like(xb)
+        orc.orc_aie_layernorm_bf16(P(xb), P(want), rows, cols, P(g), P(b), eps)
+        dx, dg, db = ctx.put(xb), ctx.put(g), ctx.put(b)
+        out = ctx.empty(xb.shape, np.uint16)
+        mxenc.layernorm_aie(ctx, dx, dg, db, eps, rows, cols, out)
+        assert np.array_equal(out.host(), want), (rows, cols, eps)
+        mxenc.layernorm_aie(ctx, dx, dg, db, eps, rows, cols, dx)  # in place
+        assert np.array_equal(dx.host(), want)
+
+
+def test_layernorm_aie_refusals(ctx):
+    x = ctx.empty((4, 40), np.uint16)
+    g = ctx.empty((40,), np.float32)
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        mxenc.layernorm_aie(ctx, x, g, g, 1e-5, 4, 40, x)
+    y = ctx.empty((2, 8192), np.uint16)
+    g2 = ctx.empty((8192,), np.float32)
+    with pytest.raises(RuntimeError, match="up to 4096"):
+        mxenc.layernorm_aie(ctx, y, g2, g2, 1e-5, 2, 8192, y)
+    with pytest.raises(RuntimeError, match="bad eps"):
+        mxenc.layernorm_aie(ctx, x, g, g, -1.0, 4, 32, x)
 
 
 # ---- GEMM ------------------------------------------------------------------------
@@ -391,6 +449,15 @@ def _attn_ref(orc, qkv_bits, B, S, H, hd, mask, scale=1.0):
     return out
 
 
+# The attention bar, of the output's scale: the kernel writes a bf16 context
+# (half an ulp: 2^-9 of a value) from bf16 probabilities into the PV product
+# (each p within 2^-9, errors averaging over the keys) with the hardware exp2
+# (~1e-7); the host keeps fp32 throughout. Together about 3e-3 of the largest
+# output at worst; the mean error is the bf16 rounding's, ~1e-3 of the scale.
+ATT_TOL = 5e-3
+ATT_MEAN_TOL = 1e-3
+
+
 @pytest.mark.parametrize("B,S,H,hd", [(4, 128, 3, 32), (3, 512, 2, 64), (2, 64, 12, 64)])
 def test_attention_masked_vs_oracle(ctx, orc, B, S, H, hd):
     rng = np.random.default_rng(S + hd)
@@ -409,8 +476,10 @@ def test_attention_masked_vs_oracle(ctx, orc, B, S, H, hd):
         mxenc.attention(ctx, dq, 3 * d, B, S, H, hd, 1.0, dm, kvl, out, d)
         got = from_bf16_bits(out.host())
         err = np.abs(got - want)
-        assert np.max(err) < 2e-2 * np.max(np.abs(want)), np.max(err)
-        assert np.mean(err) < 2e-3
+        print(f"attention B{B} S{S} H{H} hd{hd}: max err / scale "
+              f"{np.max(err) / np.max(np.abs(want)):.2e}, mean {np.mean(err):.2e}")
+        assert np.max(err) < ATT_TOL * np.max(np.abs(want)), np.max(err)
+        assert np.mean(err) < ATT_MEAN_TOL * np.max(np.abs(want))
 
 
 @pytest.mark.parametrize("B,S,H,scale", [(2, 197, 3, 0.125), (1, 1500, 2, 1.0)])
@@ -424,7 +493,9 @@ def test_attention_unmasked_odd_lengths(ctx, orc, B, S, H, scale):
     out = ctx.empty((B * S, d), np.uint16)
     mxenc.attention(ctx, dq, 3 * d, B, S, H, hd, scale, None, None, out, d)
     got = from_bf16_bits(out.host())
-    assert np.max(np.abs(got - want)) < 2e-2 * np.max(np.abs(want))
+    err = np.abs(got - want)
+    print(f"attention B{B} S{S} H{H}: max err / scale {np.max(err) / np.max(np.abs(want)):.2e}")
+    assert np.max(err) < ATT_TOL * np.max(np.abs(want))
 
 
 @pytest.mark.parametrize("with_mask", [False, True])
@@ -451,8 +522,10 @@ def test_attention_kvlen_holes_and_additive_mask(ctx, orc, with_mask):
                     out, d)
     got = from_bf16_bits(out.host())
     err = np.abs(got - want)
-    assert np.max(err) < 2e-2 * np.max(np.abs(want)), np.max(err)
-    assert np.mean(err) < 2e-3
+    print(f"attention holes mask={with_mask}: max err / scale "
+          f"{np.max(err) / np.max(np.abs(want)):.2e}")
+    assert np.max(err) < ATT_TOL * np.max(np.abs(want)), np.max(err)
+    assert np.mean(err) < ATT_MEAN_TOL * np.max(np.abs(want))
 
 
 def test_attention_row_strides_bit_exact(ctx):
@@ -486,7 +559,7 @@ def test_attention_fully_masked_row_is_uniform(ctx):
     mxenc.attention(ctx, dq, 3 * hd, B, S, H, hd, 1.0, dm, None, out, hd)
     v = from_bf16_bits(qkv)[:, 2 * hd:]
     want = np.repeat(v.mean(0, keepdims=True), S, axis=0)
-    assert np.max(np.abs(from_bf16_bits(out.host()) - want)) < 2e-2
+    assert np.max(np.abs(from_bf16_bits(out.host()) - want)) < ATT_TOL * np.max(np.abs(want))
 
 
 # ---- embedding sum, mask, pooling ------------------------------------------------

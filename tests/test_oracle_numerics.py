@@ -349,3 +349,230 @@ def test_narrow_f32_is_to_bf16(orc):
     orc.orc_narrow_f32_bf16(P(x), P(out), x.size)
     want = ((bits.astype(np.uint64) + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16)
     assert np.array_equal(out, want)
+
+
+# ---- pins of the accelerator-kernel restatements that catch seeded mistakes --
+#
+# Each pin compares a restatement's bf16 output with an fp64 evaluation of the
+# reference kernel's stated arithmetic (exact mean, variance, 1/sqrt, exp2 and
+# erf; the kernel's bf16 narrowing points kept), element by element, to half a
+# bf16 ulp plus the fp32 evaluation error. The inputs are built so that each
+# plausible mistake moves many results past that bound: rounding toward -inf
+# instead of to nearest even (the accelerator's default mode; the _rne kernels
+# set conv_even), one Newton step of fast_invsqrt instead of two, exponentials
+# summed or stored without their bf16 narrowing. test_aie_pins_catch_each_
+# seeded_mistake plants each mistake in a copy of the oracle and checks that
+# its pin fails.
+
+ROOT = __import__("os").path.dirname(__import__("os").path.dirname(
+    __import__("os").path.abspath(__file__)))
+
+
+def _as_f64(u16):
+    return (np.asarray(u16, np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def _to_bf16_rne(v):
+    """fp64 -> nearest-even bf16 bits, through the exact fp32 value when v is
+    one (the models below form fp32-exact or fp64 values)."""
+    f = np.asarray(v, np.float64).astype(np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return r
+
+
+def _bf16_ulp(v):
+    a = np.maximum(np.abs(np.asarray(v, np.float64)), 2.0 ** -126)
+    return 2.0 ** (np.floor(np.log2(a)) - 7)
+
+
+def _aie_sigs(lib):
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.orc_aie_layernorm_bf16.argtypes = [vp, vp, i64, i64, vp, vp, ctypes.c_float]
+    lib.orc_aie_layernorm_bf16.restype = None
+    lib.orc_aie_softmax_bf16.argtypes = [vp, vp, i64, i64]
+    lib.orc_aie_softmax_bf16.restype = None
+    for n in ("orc_aie_gelu_erf_bf16", "orc_aie_gelu_poly_bf16"):
+        getattr(lib, n).argtypes = [vp, vp, i64]
+        getattr(lib, n).restype = None
+    return lib
+
+
+def _ln_pin_inputs():
+    """96 rows of 768: row scales log-uniform over 1e-2 .. 1e2 (so var + eps
+    runs through every mantissa, where fast_invsqrt's one-step error spans 0 ..
+    1.75e-3), an offset of half a scale, random gamma and beta."""
+    rng = np.random.default_rng(31)
+    rows, cols = 96, 768
+    sc = np.exp(rng.uniform(np.log(1e-2), np.log(1e2), rows))
+    x = (rng.standard_normal((rows, cols)) + 0.5 * rng.standard_normal((rows, 1))) * sc[:, None]
+    g = (1 + 0.25 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.25 * rng.standard_normal(cols)).astype(np.float32)
+    return _to_bf16_rne(x), g, b
+
+
+def pin_aie_layernorm(lib):
+    """Fraction of layernorm_rne's outputs off the fp64 model by more than
+    half a bf16 ulp plus the fp32 error (2e-5 of the normalised value: the
+    16-way sums, two-step fast_invsqrt ~5e-6, three roundings)."""
+    xb, g, b = _ln_pin_inputs()
+    rows, cols = xb.shape
+    out = np.empty_like(xb)
+    eps = 1e-12
+    lib.orc_aie_layernorm_bf16(P(xb), P(out), rows, cols, P(g), P(b), eps)
+    x = _as_f64(xb)
+    d = x - x.mean(1, keepdims=True)
+    nrm = d / np.sqrt((d * d).mean(1, keepdims=True) + eps) * g
+    y = nrm + b
+    err = np.abs(_as_f64(out) - y)
+    return float(np.mean(err > 0.5 * _bf16_ulp(y) + 2e-5 * np.abs(nrm) + 1e-7 * np.abs(b)))
+
+
+def _sm_pin_inputs():
+    """32 rows of 16 (a 0 and 15 values in [-1, -1/64) whose exp2(d * log2e)
+    sits 0.30 .. 0.45 ulp above a bf16 grid point, so narrowing each
+    exponential lowers it by that much and the narrowed sum is ~0.25 % under
+    the unnarrowed one), then 16 rows of 64 normal values with a masked tail."""
+    rng = np.random.default_rng(32)
+    cand = -_as_f64(np.arange(0x3C80, 0x3F80, dtype=np.uint16))  # bf16 grid in (-1, -1/64]
+    a = (cand.astype(np.float32) * np.float32(1.4426950408889634)).astype(np.float64)
+    e = 2.0 ** a
+    frac = e / _bf16_ulp(e) % 1.0
+    pool = cand[(frac > 0.30) & (frac < 0.45)]
+    assert pool.size > 40
+    crafted = np.concatenate([np.zeros((32, 1)), rng.choice(pool, (32, 15))], 1)
+    normal = rng.standard_normal((16, 64)) * 3
+    normal[3, 40:] = -1e30
+    return _to_bf16_rne(crafted), _to_bf16_rne(normal)
+
+
+def _sm_model(xb):
+    """softmax.cc:76-160 in fp64 with its bf16 narrowing points: inputs
+    clamped at bf16(-1e30), the row max, d clamped at -100, a = d * log2e in
+    fp32 clamped at -120, e = bf16(2^a), o = bf16(e / sum e)."""
+    x = np.maximum(_as_f64(xb), _as_f64(_to_bf16_rne(-1e30)))
+    m = np.maximum(x.max(1, keepdims=True), -1e30)
+    d = np.maximum(x - m, -100.0).astype(np.float32)
+    a = np.maximum((d * np.float32(1.4426950408889634)).astype(np.float64), -120.0)
+    e = _as_f64(_to_bf16_rne(2.0 ** a))
+    return e / e.sum(1, keepdims=True)
+
+
+def pin_aie_softmax(lib):
+    """Fraction of softmax_rne's outputs off the model by more than half a
+    bf16 ulp plus 4e-6 relative (the fp32 sum and reciprocal)."""
+    worst = 0.0
+    for xb in _sm_pin_inputs():
+        out = np.empty_like(xb)
+        lib.orc_aie_softmax_bf16(P(xb), P(out), xb.shape[0], xb.shape[1])
+        o = _sm_model(xb)
+        err = np.abs(_as_f64(out) - o)
+        live = o > 1e-30
+        bad = err[live] > 0.5 * _bf16_ulp(o[live]) + 4e-6 * o[live]
+        worst = max(worst, float(np.mean(bad)))
+    return worst
+
+
+def pin_aie_gelu(lib):
+    """Fractions of gelu_erf's and gelu_poly's outputs off their fp64 models
+    by more than half a bf16 ulp plus the evaluation error, over every bf16
+    value with 1/16 <= |x| <= 6 (below that GELU is x/2 plus a term under the
+    rounding, which no rounding mode changes): gelu_erf against the exact GELU
+    (A&S 7.1.26 is within
+    1.5e-7 of erf: 1e-6 |x| covers it); gelu_poly against its own degree-8
+    polynomial evaluated in fp64 (the polynomial's fit to GELU is pinned by
+    test_aie_gelu_bf16; this pins the narrowing)."""
+    import scipy.special
+    allb = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    finite = ((allb >> 7) & 0xFF) != 0xFF
+    v = _as_f64(np.where(finite, allb, 0).astype(np.uint16))
+    xb = np.ascontiguousarray(allb[finite & (np.abs(v) <= 6.0) & (np.abs(v) >= 1.0 / 16)])
+    x = _as_f64(xb)
+    fr = []
+    out = np.empty_like(xb)
+    lib.orc_aie_gelu_erf_bf16(P(xb), P(out), xb.size)
+    y = 0.5 * x * (1.0 + scipy.special.erf(x / np.sqrt(2.0)))
+    fr.append(np.mean(np.abs(_as_f64(out) - y) > 0.5 * _bf16_ulp(y) + 1e-6 * np.abs(x)))
+    lib.orc_aie_gelu_poly_bf16(P(xb), P(out), xb.size)
+    u = np.minimum(np.abs(x), 4.0)
+    c = [-7.2340282171e-05, 1.8179518005e-03, -1.7707383379e-02, 8.4577147641e-02,
+         -1.9228671834e-01, 9.8431124458e-02, 3.6137852062e-01, -4.9454128936e-01,
+         -1.3007010117e-04]
+    p = np.zeros_like(u)
+    for k in c:
+        p = p * u + np.float64(np.float32(k))
+    y = np.maximum(x, 0.0) + p
+    fr.append(np.mean(np.abs(_as_f64(out) - y) > 0.5 * _bf16_ulp(y) + 1e-6 * (np.abs(x) + 1)))
+    return float(max(fr))
+
+
+def test_aie_layernorm_pinned(orc):
+    assert pin_aie_layernorm(orc) == 0.0
+
+
+def test_aie_softmax_pinned(orc):
+    assert pin_aie_softmax(orc) == 0.0
+
+
+def test_aie_gelu_pinned(orc):
+    assert pin_aie_gelu(orc) == 0.0
+
+
+_FLOOR = ("{ uint32_t u_; memcpy(&u_, &{v}, 4); uint32_t t_ = u_ >> 16; "
+          "if ((u_ & 0xFFFFu) && (u_ >> 31)) t_ += 1; {dst} = (uint16_t)t_; }")
+
+# (pin, [(text in oracle/orc_numerics.c, replacement, count)])
+SEEDED = {
+    "layernorm rounds toward -inf": (pin_aie_layernorm, [
+        ("      o[j] = orc_to_bf16(y);\n",
+         "      " + _FLOOR.replace("{v}", "y").replace("{dst}", "o[j]") + "\n", 1)]),
+    "fast_invsqrt with one Newton step": (pin_aie_layernorm, [
+        ("  y = y * (1.5f - xhalf * y * y);\n  y = y * (1.5f - xhalf * y * y);\n",
+         "  y = y * (1.5f - xhalf * y * y);\n", 1)]),
+    "softmax rounds toward -inf": (pin_aie_softmax, [
+        ("o[j] = orc_to_bf16(e[j] * inv);",
+         "{ const float q_ = e[j] * inv; " +
+         _FLOOR.replace("{v}", "q_").replace("{dst}", "o[j]") + " }", 1)]),
+    "softmax exponentials not narrowed": (pin_aie_softmax, [
+        ("e[j] = bf(aie_exp2(a));", "e[j] = aie_exp2(a);", 1)]),
+    "softmax sum of unnarrowed exponentials": (pin_aie_softmax, [
+        ("      e[j] = bf(aie_exp2(a));\n      acc[j % 16] += e[j];",
+         "      e[j] = bf(aie_exp2(a));\n      acc[j % 16] += aie_exp2(a);", 1)]),
+    "gelu_erf rounds toward -inf": (pin_aie_gelu, [
+        ("    const float y = x * 0.5f + (fabsf(x) * 0.5f) * eabs;\n    out[i] = orc_to_bf16(y);",
+         "    const float y = x * 0.5f + (fabsf(x) * 0.5f) * eabs;\n    " +
+         _FLOOR.replace("{v}", "y").replace("{dst}", "out[i]"), 1)]),
+    "gelu_poly rounds toward -inf": (pin_aie_gelu, [
+        ("    out[i] = orc_to_bf16((x > 0.0f ? x : 0.0f) + p);",
+         "    const float y_ = (x > 0.0f ? x : 0.0f) + p;\n    " +
+         _FLOOR.replace("{v}", "y_").replace("{dst}", "out[i]"), 1)]),
+}
+
+
+@pytest.mark.parametrize("mistake", sorted(SEEDED))
+def test_aie_pins_catch_each_seeded_mistake(mistake, tmp_path):
+    """A copy of the oracle with one mistake planted (on the CPU) fails the
+    pin of the function it changes."""
+    import os
+    import shutil
+    import subprocess
+    pin, edits = SEEDED[mistake]
+    src = os.path.join(ROOT, "oracle")
+    for f in os.listdir(src):
+        if f.endswith((".c", ".h")):
+            shutil.copy(os.path.join(src, f), tmp_path / f)
+    path = tmp_path / "orc_numerics.c"
+    text = path.read_text()
+    for old, new, count in edits:
+        assert text.count(old) == count, (mistake, old)
+        text = text.replace(old, new)
+    path.write_text(text)
+    so = tmp_path / "liborc_seeded.so"
+    srcs = [str(tmp_path / f) for f in ("orc_pool.c", "orc_numerics.c", "orc_ops.c",
+                                        "orc_encoders.c")]
+    r = subprocess.run(["gcc", "-std=gnu11", "-O2", "-march=x86-64-v3", "-ffp-contract=off",
+                        "-fPIC", "-shared", "-o", str(so)] + srcs + ["-lm", "-lpthread"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    lib = _aie_sigs(ctypes.CDLL(str(so)))
+    assert pin(lib) > 0.01, mistake
