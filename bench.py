@@ -177,6 +177,89 @@ def cpu_baseline(name, sample_batch, threads, int8=False, lanes=4):
                       "wall_s": ldt}}
 
 
+HBM_PEAK_GBS = 8000.0
+
+
+def ops_table(mxenc, np):
+    """The per-op entry points a partial --npu-ops placement runs, each at its
+    bge-base b64 x s512 shape (17,455 packed rows, hidden 768, FFN 3072, 12
+    heads): 2 untimed launches, then 10 timed with HIP events on the op's
+    stream; GB/s over the bytes the op must move (its inputs read once, its
+    outputs written once), against the 8 TB/s HBM peak. Prints one JSON line."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    ctx = mxenc.Context(0)
+    stream = vp(mxenc.lib().mx_stream_handle(ctx.stream))
+    e0, e1 = vp(), vp()
+    assert hip.hipEventCreate(ctypes.byref(e0)) == 0 and hip.hipEventCreate(ctypes.byref(e1)) == 0
+    rng = np.random.default_rng(0)
+    M, d, f, B, S, H = 17455, 768, 3072, 64, 512, 12
+    rows_sm = B * H * S
+
+    def bf16(shape, scale=1.0):
+        x = (rng.standard_normal(shape, dtype=np.float32) * scale)
+        return ctx.put(mxenc.to_bf16_bits(x))
+
+    def f32(shape, scale=1.0):
+        return ctx.put(rng.standard_normal(shape, dtype=np.float32) * scale)
+
+    up_bf, up_f = bf16((M, f)), f32((M, f))
+    sc_bf = bf16((rows_sm, S), 3.0)
+    sc_f = f32((rows_sm, S), 3.0)
+    mask = ctx.put(np.where(rng.random((B, S)) < 0.8, 0.0, -1e30).astype(np.float32))
+    x_f, y_bf = f32((M, d)), bf16((M, d))
+    g, bta = ctx.put(np.ones(d, np.float32)), ctx.put(np.zeros(d, np.float32))
+    out_f, out_bf, out_bf2 = ctx.empty((M, d), np.float32), ctx.empty((M, d), np.uint16), \
+        ctx.empty((M, f), np.uint16)
+    acc_i = ctx.put(rng.integers(-2**20, 2**20, (M, f), dtype=np.int32))
+    n_up, n_sm, n_ln = M * f, rows_sm * S, M * d
+    cases = [
+        ("gelu poly bf16->bf16 (FFN-up, in place)", n_up * 4,
+         lambda: mxenc.gelu(ctx, up_bf, up_bf, mxenc.MX_GELU_POLY)),
+        ("gelu erf A&S bf16->bf16 (FFN-up, in place)", n_up * 4,
+         lambda: mxenc.gelu(ctx, up_bf, up_bf, mxenc.MX_GELU_ERF_AS)),
+        ("gelu poly fp32->bf16 (FFN-up)", n_up * 6,
+         lambda: mxenc.gelu(ctx, up_f, out_bf2, mxenc.MX_GELU_POLY)),
+        ("softmax poly bf16, masked (scores, in place)", n_sm * 4,
+         lambda: mxenc.softmax_rows(ctx, sc_bf, rows_sm, S, S, mask, H * S,
+                                    mxenc.MX_SOFTMAX_POLY)),
+        ("softmax exact fp32, masked (scores, in place)", n_sm * 8,
+         lambda: mxenc.softmax_rows(ctx, sc_f, rows_sm, S, S, mask, H * S,
+                                    mxenc.MX_SOFTMAX_EXACT)),
+        ("softmax accelerator form bf16 (scores, in place)", n_sm * 4,
+         lambda: mxenc.softmax_rows(ctx, sc_bf, rows_sm, S, S, None, 1, mxenc.MX_SOFTMAX_AIE)),
+        ("layernorm fp32 x + bf16 y -> fp32 + bf16", n_ln * 12,
+         lambda: mxenc.layernorm(ctx, x_f, y_bf, g, bta, 1e-12, M, d, out_f, out_bf)),
+        ("layernorm accelerator form bf16 -> bf16", n_ln * 4,
+         lambda: mxenc.layernorm_aie(ctx, y_bf, g, bta, 1e-12, M, d, out_bf)),
+        ("narrow fp32 -> bf16 (FFN-up)", n_up * 6,
+         lambda: mxenc.narrow_f32_bf16(ctx, up_f, out_bf2)),
+        ("narrow int32 -> bf16 (FFN-up)", n_up * 6,
+         lambda: mxenc.narrow_i32_bf16(ctx, acc_i, out_bf2)),
+    ]
+    res = []
+    for name, nbytes, fn in cases:
+        fn()
+        fn()
+        ctx.sync()
+        assert hip.hipEventRecord(e0, stream) == 0
+        for _ in range(10):
+            fn()
+        assert hip.hipEventRecord(e1, stream) == 0
+        assert hip.hipEventSynchronize(e1) == 0
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1) == 0
+        us = ms.value * 1e3 / 10
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res.append({"op": name, "bytes": nbytes, "us": us, "GBps": gbs,
+                    "frac": gbs / HBM_PEAK_GBS})
+        print(f"bench --ops: {name:52s} {us:8.1f} us  {gbs:7.0f} GB/s  "
+              f"{100 * gbs / HBM_PEAK_GBS:5.1f}% of HBM", file=sys.stderr, flush=True)
+    print(json.dumps({"ops": res, "hbm_peak_GBps": HBM_PEAK_GBS}))
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -198,7 +281,13 @@ def main():
                     help="gated-FFN configs: FFN-up then the separate gated pass, instead of "
                          "the activation fused into FFN-up's epilogue")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sustained", action="store_true",
+                    help="skip the sustained-rate run (>= 2 s of back-to-back steps)")
     ap.add_argument("--cpu-sample", type=int, default=16)
+    ap.add_argument("--ops", action="store_true",
+                    help="only time the standalone memory-bound entry points (mx_gelu, "
+                         "mx_softmax_rows, mx_layernorm, mx_layernorm_aie, mx_narrow_*) at "
+                         "the bge-base workload's shapes, with HIP events on their stream")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run narrow_f32_bf16 over 64 Mi fp32 values, 5 times: a "
                          "streaming kernel of known bytes (256 MiB read, 128 MiB written "
@@ -214,6 +303,10 @@ def main():
 
     import mxenc
     from mxenc import synth
+
+    if args.ops:
+        ops_table(mxenc, np)
+        return
 
     if args.calibrate:
         ctx = mxenc.Context(0)
@@ -309,6 +402,20 @@ def main():
     print(f"bench: {args.steps} steps in {dt*1e3:.1f} ms -> {seq_s:.1f} {unit}"
           f"{' (token packing)' if packing else ''}, {lanes} lane(s)", file=sys.stderr,
           flush=True)
+    # Sustained rate: the same lanes back to back for at least 2 s, so that a
+    # power-capped part's settled clock, not its burst, sets the figure.
+    sustained = None
+    if kind == "bert" and not args.no_sustained:
+        per_step = dt / args.steps
+        n_sus = max(args.steps, int(2.2 / per_step) + 1)
+        saved = args.steps
+        args.steps = n_sus
+        sdt = timed(lanes)
+        args.steps = saved
+        sustained = {"value": n_sus * B / sdt, "ms_per_step": sdt / n_sus * 1e3,
+                     "steps": n_sus, "seconds": sdt, "lanes": lanes}
+        print(f"bench: sustained {sustained['value']:.1f} {unit} over {sdt:.2f} s "
+              f"({n_sus} steps)", file=sys.stderr, flush=True)
     one_lane = None
     if lanes > 1:
         odt = timed(1)
@@ -437,6 +544,7 @@ def main():
         "layernorm_ms_per_step": tot["ln_ms"] / args.steps,
         "lanes": lanes,
         "one_lane": one_lane,
+        "sustained": sustained,
         "token_packing": {"on": packing, "rows_per_step": M, "padded_rows_per_step": B * S,
                           "padded": padded} if kind == "bert" else None,
         "cpu_baseline": cpu,

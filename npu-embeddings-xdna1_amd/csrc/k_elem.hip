@@ -115,10 +115,45 @@ __device__ __forceinline__ float gelu_variant(float v, int variant) {
   return gelu_erf_as(v);
 }
 
+// Eight elements per thread per step in 16-byte accesses (a bf16 chunk is one
+// 16-byte load or store, an fp32 chunk two), the variant fixed at compile
+// time; in place is safe (each chunk is read whole before it is written).
+template <bool IN_BF, bool OUT_BF, int VAR>
+__global__ __launch_bounds__(256) void gelu_vec_k(const void *__restrict__ x,
+                                                  void *__restrict__ y, int64_t n8) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float v[8];
+    if (IN_BF) {
+      const uint4 w = ((const uint4 *)x)[i];
+      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = bf2f(u[e] & 0xFFFFu);
+        v[2 * e + 1] = bf2f(u[e] >> 16);
+      }
+    } else {
+      const float4 a = ((const float4 *)x)[2 * i], b = ((const float4 *)x)[2 * i + 1];
+      v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w;
+      v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = gelu_variant(v[e], VAR);
+    if (OUT_BF) {
+      ((uint4 *)y)[i] = make_uint4(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]),
+                                   pack_bf2(v[4], v[5]), pack_bf2(v[6], v[7]));
+    } else {
+      ((float4 *)y)[2 * i] = make_float4(v[0], v[1], v[2], v[3]);
+      ((float4 *)y)[2 * i + 1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+  }
+}
+
+// The elements from lo on, one per thread (tails and unaligned tensors).
 template <bool IN_BF, bool OUT_BF>
-__global__ void gelu_k(const void *__restrict__ x, void *__restrict__ y, int64_t n,
+__global__ void gelu_k(const void *__restrict__ x, void *__restrict__ y, int64_t lo, int64_t n,
                        int variant) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+  for (int64_t i = lo + blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
     const float v = IN_BF ? bf2f(((const uint16_t *)x)[i]) : ((const float *)x)[i];
     const float r = gelu_variant(v, variant);
@@ -461,6 +496,108 @@ __global__ __launch_bounds__(256) void softmax_wave_k(void *x, int bf, int64_t r
   }
 }
 
+// The poly (0) and exact (1) softmax on 16-byte accesses: one wave per NR
+// rows, whose loads are all issued before the first row's reductions (a row
+// of 512 bf16 is 1 KB, too little in flight alone); lane l holds the
+// 8-column chunks l, l + 64, ... of each row (cols <= 512 * NC). cols and the
+// row stride multiples of 8, 16-byte aligned rows and mask.
+template <int NC, int NR, bool BF, int VAR>
+__global__ __launch_bounds__(256) void softmax_vec_k(void *x, int64_t rows, int64_t cols,
+                                                     int64_t stride,
+                                                     const float *__restrict__ mask,
+                                                     int64_t rpm) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = (blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6)) * NR;
+  if (row0 >= rows) return;
+  float v[NR][NC][8];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int64_t row = row0 + r;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int64_t c0 = 8 * (lane + 64 * (int64_t)i);
+      if (row < rows && c0 < cols) {
+        if (BF) {
+          const uint4 w = *(const uint4 *)((const uint16_t *)x + row * stride + c0);
+          const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[r][i][2 * e] = bf2f(u[e] & 0xFFFFu);
+            v[r][i][2 * e + 1] = bf2f(u[e] >> 16);
+          }
+        } else {
+          const float *p = (const float *)x + row * stride + c0;
+          const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+          v[r][i][0] = a.x, v[r][i][1] = a.y, v[r][i][2] = a.z, v[r][i][3] = a.w;
+          v[r][i][4] = b.x, v[r][i][5] = b.y, v[r][i][6] = b.z, v[r][i][7] = b.w;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int64_t row = row0 + r;
+    if (row >= rows) break;
+    const float *mk = mask ? mask + (row / rpm) * cols : nullptr;
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int64_t c0 = 8 * (lane + 64 * (int64_t)i);
+      if (c0 < cols) {
+        if (mk) {
+          const float4 a = *(const float4 *)(mk + c0), b = *(const float4 *)(mk + c0 + 4);
+          const float mm[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[r][i][e] += mm[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, v[r][i][e]);
+      }
+    }
+    m = wave_max(m);
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int64_t c0 = 8 * (lane + 64 * (int64_t)i);
+      if (c0 < cols) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float ex;
+          if (VAR == 0) {
+            float a = (v[r][i][e] - m) * 1.4426950408889634f;
+            a = a > -120.0f ? a : -120.0f;
+            ex = exp2_poly(a);
+          } else {
+            ex = expf(v[r][i][e] - m);
+          }
+          v[r][i][e] = ex;
+          sum += ex;
+        }
+      }
+    }
+    sum = wave_sum(sum);
+    const float inv = VAR == 1 ? (sum > 0.0f ? 1.0f / sum : 0.0f) : 1.0f / sum;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int64_t c0 = 8 * (lane + 64 * (int64_t)i);
+      if (c0 < cols) {
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = v[r][i][e] * inv;
+        if (BF) {  // the hardware conversion: the same bits for every non-NaN value
+          *(uint4 *)((uint16_t *)x + row * stride + c0) =
+              make_uint4(pack_bf2_hw(o[0], o[1]), pack_bf2_hw(o[2], o[3]),
+                         pack_bf2_hw(o[4], o[5]), pack_bf2_hw(o[6], o[7]));
+        } else {
+          float *p = (float *)x + row * stride + c0;
+          *(float4 *)p = make_float4(o[0], o[1], o[2], o[3]);
+          *(float4 *)(p + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        }
+      }
+    }
+  }
+}
+
 // ---- embedding sum + mask ---------------------------------------------------
 
 __global__ __launch_bounds__(256) void embed_sum_k(const int32_t *__restrict__ ids, int64_t rows,
@@ -696,17 +833,43 @@ hipError_t narrow_i32_bf16(const int32_t *in, uint16_t *out, int64_t n, hipStrea
   return hipGetLastError();
 }
 
+template <bool IB, bool OB>
+void gelu_vec_launch(const void *x, void *y, int64_t n8, int variant, hipStream_t s) {
+  const int g = grid_for(n8, kElemThreads);
+  if (variant == 0)
+    gelu_vec_k<IB, OB, 0><<<g, kElemThreads, 0, s>>>(x, y, n8);
+  else if (variant == 1)
+    gelu_vec_k<IB, OB, 1><<<g, kElemThreads, 0, s>>>(x, y, n8);
+  else
+    gelu_vec_k<IB, OB, 2><<<g, kElemThreads, 0, s>>>(x, y, n8);
+}
+
 hipError_t gelu(const void *x, int x_bf, void *y, int y_bf, int64_t n, int variant,
                 hipStream_t s) {
-  const int g = grid_for(n, kElemThreads);
-  if (x_bf && y_bf)
-    gelu_k<true, true><<<g, kElemThreads, 0, s>>>(x, y, n, variant);
-  else if (x_bf)
-    gelu_k<true, false><<<g, kElemThreads, 0, s>>>(x, y, n, variant);
-  else if (y_bf)
-    gelu_k<false, true><<<g, kElemThreads, 0, s>>>(x, y, n, variant);
-  else
-    gelu_k<false, false><<<g, kElemThreads, 0, s>>>(x, y, n, variant);
+  int64_t done = 0;
+  if ((uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 && n >= 8) {
+    const int64_t n8 = n / 8;
+    if (x_bf && y_bf)
+      gelu_vec_launch<true, true>(x, y, n8, variant, s);
+    else if (x_bf)
+      gelu_vec_launch<true, false>(x, y, n8, variant, s);
+    else if (y_bf)
+      gelu_vec_launch<false, true>(x, y, n8, variant, s);
+    else
+      gelu_vec_launch<false, false>(x, y, n8, variant, s);
+    done = n8 * 8;
+  }
+  if (done < n) {
+    const int g = grid_for(n - done, kElemThreads);
+    if (x_bf && y_bf)
+      gelu_k<true, true><<<g, kElemThreads, 0, s>>>(x, y, done, n, variant);
+    else if (x_bf)
+      gelu_k<true, false><<<g, kElemThreads, 0, s>>>(x, y, done, n, variant);
+    else if (y_bf)
+      gelu_k<false, true><<<g, kElemThreads, 0, s>>>(x, y, done, n, variant);
+    else
+      gelu_k<false, false><<<g, kElemThreads, 0, s>>>(x, y, done, n, variant);
+  }
   return hipGetLastError();
 }
 
@@ -781,9 +944,38 @@ hipError_t layernorm_aie(const uint16_t *x, const float *gamma, const float *bet
   return hipGetLastError();
 }
 
+template <int NC, bool BF>
+hipError_t softmax_vec_launch(void *x, int64_t rows, int64_t cols, int64_t stride,
+                              const float *mask, int64_t rpm, int variant, hipStream_t s) {
+  // rows per wave (bf16): 32 values per lane held at most; an fp32 row moves
+  // twice the bytes and runs fastest alone
+  constexpr int NR = !BF || NC >= 4 ? 1 : 4 / NC;
+  const int64_t g = (rows + 4 * NR - 1) / (4 * NR);
+  if (variant == 0)
+    softmax_vec_k<NC, NR, BF, 0><<<(unsigned)g, 256, 0, s>>>(x, rows, cols, stride, mask, rpm);
+  else
+    softmax_vec_k<NC, NR, BF, 1><<<(unsigned)g, 256, 0, s>>>(x, rows, cols, stride, mask, rpm);
+  return hipGetLastError();
+}
+
 hipError_t softmax_rows(void *x, int bf, int64_t rows, int64_t cols, int64_t stride,
                         const float *mask, int64_t rpm, int variant, hipStream_t s) {
   const int g = (int)((rows + 3) / 4);
+  // 16-byte chunks where the rows allow them (the accelerator form keeps the
+  // strided layout, whose 16-lane summation order it reproduces)
+  if (variant != 2 && cols % 8 == 0 && stride % 8 == 0 && (uintptr_t)x % 16 == 0 &&
+      (!mask || (uintptr_t)mask % 16 == 0) && cols <= 4096) {
+    const int64_t nc = (cols + 511) / 512;
+#define MX_SMV_CASE(NC)                                                                   \
+  if (nc <= NC)                                                                           \
+    return bf ? softmax_vec_launch<NC, true>(x, rows, cols, stride, mask, rpm, variant, s) \
+              : softmax_vec_launch<NC, false>(x, rows, cols, stride, mask, rpm, variant, s);
+    MX_SMV_CASE(1)
+    MX_SMV_CASE(2)
+    MX_SMV_CASE(4)
+    MX_SMV_CASE(8)
+#undef MX_SMV_CASE
+  }
   const int64_t nv = (cols + 63) / 64;
 #define MX_SM_CASE(NV)                                                                      \
   if (nv <= NV) {                                                                           \
