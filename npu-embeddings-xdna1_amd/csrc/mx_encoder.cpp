@@ -449,57 +449,69 @@ int site_ln(mx_encoder *enc, mx_stream *s, float *x, const void *y, int y_dt, co
   return ln_l(enc, s, x, MX_F32, y, y_dt, g, b, M, out_f32, enc->i8 ? nullptr : enc->work.xb);
 }
 
-int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
-             int64_t B, int64_t S, const Rows &rows) {
+// The embedding LayerNorm ahead of the first layer (and the RoPE tables).
+int bert_pre(mx_encoder *enc, mx_stream *s, float *x, int64_t S, const Rows &rows) {
+  int rc = enc->desc.rope ? ensure_rope(enc, S) : MX_OK;
+  if (!rc)
+    rc = site_ln(enc, s, x, nullptr, MX_F32, enc->emb_ln[0], enc->emb_ln[1], rows.M, x,
+                 enc->layers[0].ias[SITE_QKV]);
+  return rc;
+}
+
+// Layer l of BertEncoder::run over the rows of one pass, in enc->work.
+int bert_layer(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
+               int64_t B, int64_t S, const Rows &rows, size_t l) {
   const int64_t M = rows.M, d = enc->desc.hidden, f = enc->desc.ffn;
   const int epi = enc->desc.gelu == MX_GELU_ERF ? MX_EPI_GELU_ERF : MX_EPI_GELU_POLY;
   const size_t L = enc->layers.size();
   const bool gated = enc->desc.gated_ffn != MX_GATED_NONE;
   const int64_t fu = gated ? 2 * f : f;
   uint16_t *act = gated ? enc->work.glu : enc->work.up;  // FFN-down's A (bf16 datapath)
-  int rc = enc->desc.rope ? ensure_rope(enc, S) : MX_OK;
+  const LayerW &w = enc->layers[l];
+  const bool fused = gated && enc->fuse_glu && glu_fusable(enc) && w.glu_gen == enc->wgen &&
+                     (enc->i8 ? w.wqg && w.wsg : w.wg != nullptr) && w.bg;
+  int rc = site_gemm(enc, s, w, SITE_QKV, enc->work.xb, M, d, 3 * d, MX_EPI_NONE, nullptr,
+                     enc->work.qkv, MX_BF16);
+  if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S, M, rows.row_pos);
+  if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, &rows);
+  if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.ctxb, MX_BF16, M, d, w.ias[SITE_AO]);
+  // proj: bf16 (the array path's C) or, on the int8 datapath, fp32 as
+  // dequantise_c writes it (host_kernels.hpp:529-600)
+  const int pdt = enc->i8 ? MX_F32 : MX_BF16;
   if (!rc)
-    rc = site_ln(enc, s, x, nullptr, MX_F32, enc->emb_ln[0], enc->emb_ln[1], M, x,
-                 enc->layers[0].ias[SITE_QKV]);
-  for (size_t l = 0; !rc && l < L; ++l) {
-    const LayerW &w = enc->layers[l];
-    const bool fused = gated && enc->fuse_glu && glu_fusable(enc) && w.glu_gen == enc->wgen &&
-                       (enc->i8 ? w.wqg && w.wsg : w.wg != nullptr) && w.bg;
-    rc = site_gemm(enc, s, w, SITE_QKV, enc->work.xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->work.qkv,
-                   MX_BF16);
-    if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S, M, rows.row_pos);
-    if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, &rows);
-    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.ctxb, MX_BF16, M, d, w.ias[SITE_AO]);
-    // proj: bf16 (the array path's C) or, on the int8 datapath, fp32 as
-    // dequantise_c writes it (host_kernels.hpp:529-600)
-    const int pdt = enc->i8 ? MX_F32 : MX_BF16;
+    rc = site_gemm(enc, s, w, SITE_AO, enc->work.ctxb, M, d, d, MX_EPI_NONE, nullptr,
+                   enc->work.proj, pdt);
+  if (!rc) rc = site_ln(enc, s, x, enc->work.proj, pdt, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
+  if (!rc && enc->i8) {
+    // dequant_act_quant (host_kernels.hpp:405-522, bert_encoder.cpp:811-860):
+    // FFN-up dequantised, biased and activated in fp32 (the gated halves
+    // combined in fp32), then quantised per row from those fp32 values.
+    rc = site_gemm(enc, s, w, SITE_UP, nullptr, M, d, fu, gated ? MX_EPI_NONE : epi, nullptr,
+                   enc->work.up, MX_F32);
+    if (!rc && gated) rc = glu_l(enc, s, M, MX_F32);
+    if (!rc) rc = quant_l(enc, s, act, MX_F32, M, f, w.ias[SITE_DOWN]);
+  } else if (!rc && fused) {
+    rc = gemm_glu_l(enc, s, w, M);
+  } else {
     if (!rc)
-      rc = site_gemm(enc, s, w, SITE_AO, enc->work.ctxb, M, d, d, MX_EPI_NONE, nullptr,
-                     enc->work.proj, pdt);
-    if (!rc) rc = site_ln(enc, s, x, enc->work.proj, pdt, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
-    if (!rc && enc->i8) {
-      // dequant_act_quant (host_kernels.hpp:405-522, bert_encoder.cpp:811-860):
-      // FFN-up dequantised, biased and activated in fp32 (the gated halves
-      // combined in fp32), then quantised per row from those fp32 values.
-      rc = site_gemm(enc, s, w, SITE_UP, nullptr, M, d, fu, gated ? MX_EPI_NONE : epi, nullptr,
-                     enc->work.up, MX_F32);
-      if (!rc && gated) rc = glu_l(enc, s, M, MX_F32);
-      if (!rc) rc = quant_l(enc, s, act, MX_F32, M, f, w.ias[SITE_DOWN]);
-    } else if (!rc && fused) {
-      rc = gemm_glu_l(enc, s, w, M);
-    } else {
-      if (!rc)
-        rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, M, d, fu, gated ? MX_EPI_NONE : epi,
-                       nullptr, enc->work.up, MX_BF16);
-      if (!rc && gated) rc = glu_l(enc, s, M, MX_BF16);
-    }
-    if (!rc)
-      rc = site_gemm(enc, s, w, SITE_DOWN, act, M, f, d, MX_EPI_NONE, nullptr, enc->work.proj,
-                     pdt);
-    if (!rc)
-      rc = site_ln(enc, s, x, enc->work.proj, pdt, w.ln[2], w.ln[3], M, x,
-                   l + 1 < L ? enc->layers[l + 1].ias[SITE_QKV] : nullptr);
+      rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, M, d, fu, gated ? MX_EPI_NONE : epi,
+                     nullptr, enc->work.up, MX_BF16);
+    if (!rc && gated) rc = glu_l(enc, s, M, MX_BF16);
   }
+  if (!rc)
+    rc = site_gemm(enc, s, w, SITE_DOWN, act, M, f, d, MX_EPI_NONE, nullptr, enc->work.proj,
+                   pdt);
+  if (!rc)
+    rc = site_ln(enc, s, x, enc->work.proj, pdt, w.ln[2], w.ln[3], M, x,
+                 l + 1 < L ? enc->layers[l + 1].ias[SITE_QKV] : nullptr);
+  return rc;
+}
+
+int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
+             int64_t B, int64_t S, const Rows &rows) {
+  int rc = bert_pre(enc, s, x, S, rows);
+  for (size_t l = 0; !rc && l < enc->layers.size(); ++l)
+    rc = bert_layer(enc, s, x, mask, kvl, B, S, rows, l);
   return rc;
 }
 
@@ -1188,88 +1200,133 @@ int scratch_refusal(const mx_encoder *enc, int64_t B, int64_t S, int64_t rows, s
                   std::to_string(cap) + " (MX_STATIC_SCRATCH_BYTES)");
 }
 
-// EmbedService::chunk minus the tokenizer (embed_service.cpp:29-64): mask and
-// plan, embedding sum, the stack, pooling, then the data refusals. carve null:
-// the encoder's own workspace (ensure_ws sized it). carve set: every buffer
-// is carved from the static scratch -- the batch-shaped ones first, the
-// row-shaped ones once the packed row count is known -- and nothing is
-// allocated.
-int embed_body(mx_encoder *enc, mx_stream *s, const int32_t *ids, const float *attn_mask,
-               int64_t B, int64_t S, float *out, Carver *carve) {
-  if (carve) {
-    const size_t need = plan_bytes(B, S) + (enc->packing ? 0 : rows_bytes(enc, B * S));
-    if (need > carve->cap) return scratch_refusal(enc, B, S, B * S, need, carve->cap, false);
-    carve_plan(*carve, B, S, enc->work);
-    if (!enc->packing) carve_rows(enc, *carve, B * S, enc->work);
-  }
-  int rc = begin_timing(enc, s);
-  if (rc) return rc;
-  Rows rows{B * S};
-  {
-    Bracket br(enc, s->stream, CAT_OTHER);
-    hipError_t e = mxk::mask_build(attn_mask, B, S, enc->work.add_mask, enc->work.kv_len, s->stream);
-    // The plan: seq_start and attention's launch order (both layouts use the
-    // order; kv_len differs per sequence either way).
-    int32_t *order = enc->work.seq_start + B + 1;
-    if (e == hipSuccess) e = mxk::pack_plan(enc->work.kv_len, B, enc->work.seq_start, order, s->stream);
-    if (e == hipSuccess && enc->packing) {
-      // Token packing: the packed row count is needed on the host for the
-      // launches, so it is read back (one small copy per batch; the whole
-      // plan when timing, for the attention work).
-      int32_t total = 0;
-      if (carve) {
-        e = hipMemcpyAsync(&total, enc->work.seq_start + B, sizeof(int32_t),
-                           hipMemcpyDeviceToHost, s->stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
-        if (e != hipSuccess) return hip_fail(e, "reading the packed row count");
-        const size_t need = carve->used + rows_bytes(enc, total);
-        if (need > carve->cap) return scratch_refusal(enc, B, S, total, need, carve->cap, true);
-        carve_rows(enc, *carve, total, enc->work);
+// One embed call: its stream, its workspace, its inputs and output rows,
+// and -- once its plan is read -- the rows it computes.
+struct Pass {
+  mx_stream *s = nullptr;
+  Work w;
+  const int32_t *ids = nullptr;
+  const float *mask = nullptr;
+  float *out = nullptr;
+  int64_t B = 0, S = 0;
+  Rows rows{0};
+};
+
+// The pass's additive mask, kv_len and plan (seq_start, attention's order).
+int pass_plan(mx_encoder *enc, Pass &p) {
+  Bracket br(enc, p.s->stream, CAT_OTHER);
+  hipError_t e = mxk::mask_build(p.mask, p.B, p.S, p.w.add_mask, p.w.kv_len, p.s->stream);
+  if (e == hipSuccess)
+    e = mxk::pack_plan(p.w.kv_len, p.B, p.w.seq_start, p.w.seq_start + p.B + 1, p.s->stream);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "embed launch");
+}
+
+// The pass's rows and its embedding sum. With token packing the packed row
+// count is read back, since the launches are sized on the host (the whole
+// plan when timing, for the attention work); carve, when given, then takes
+// the row-shaped buffers for that many rows from the static scratch.
+int pass_rows(mx_encoder *enc, Pass &p, Carver *carve) {
+  Bracket br(enc, p.s->stream, CAT_OTHER);
+  const int64_t B = p.B, S = p.S;
+  int32_t *order = p.w.seq_start + B + 1;
+  hipError_t e = hipSuccess;
+  p.rows = Rows{B * S};
+  if (enc->packing) {
+    int32_t total = 0;
+    if (!enc->timing) {
+      e = hipMemcpyAsync(&total, p.w.seq_start + B, sizeof(int32_t), hipMemcpyDeviceToHost,
+                         p.s->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(p.s->stream);
+      enc->packed_sq = 0.0;
+    } else {
+      enc->plan_host.resize(static_cast<size_t>(B + 1));
+      e = hipMemcpyAsync(enc->plan_host.data(), p.w.seq_start, (B + 1) * sizeof(int32_t),
+                         hipMemcpyDeviceToHost, p.s->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(p.s->stream);
+      if (e == hipSuccess) {
+        total = enc->plan_host[B];
         enc->packed_sq = 0.0;
-      } else {
-        enc->plan_host.resize(static_cast<size_t>(B + 1));
-        e = hipMemcpyAsync(enc->plan_host.data(), enc->work.seq_start, (B + 1) * sizeof(int32_t),
-                           hipMemcpyDeviceToHost, s->stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
-        if (e == hipSuccess) {
-          total = enc->plan_host[B];
-          enc->packed_sq = 0.0;
-          for (int64_t b = 0; b < B; ++b) {
-            const double L = enc->plan_host[b + 1] - enc->plan_host[b];
-            enc->packed_sq += L * L;
-          }
+        for (int64_t b = 0; b < B; ++b) {
+          const double L = enc->plan_host[b + 1] - enc->plan_host[b];
+          enc->packed_sq += L * L;
         }
       }
-      if (e == hipSuccess)
-        e = mxk::embed_sum_packed(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab,
-                                  enc->pos, enc->type, enc->work.kv_len, enc->work.seq_start,
-                                  enc->work.emb, enc->work.row_pos, s->err_dev, s->stream);
-      rows = Rows{total, enc->work.seq_start, enc->work.row_pos, order};
-    } else if (e == hipSuccess) {
-      e = mxk::embed_sum(ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab, enc->pos,
-                         enc->type, enc->work.emb, s->err_dev, s->stream);
-      rows.order = order;
     }
-    if (e != hipSuccess) return hip_fail(e, "embed launch");
+    if (e != hipSuccess) return hip_fail(e, "reading the packed row count");
+    if (carve) {
+      const size_t need = carve->used + rows_bytes(enc, total);
+      if (need > carve->cap) return scratch_refusal(enc, B, S, total, need, carve->cap, true);
+      carve_rows(enc, *carve, total, p.w);
+    }
+    e = mxk::embed_sum_packed(p.ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab,
+                              enc->pos, enc->type, p.w.kv_len, p.w.seq_start, p.w.emb,
+                              p.w.row_pos, p.s->err_dev, p.s->stream);
+    p.rows = Rows{total, p.w.seq_start, p.w.row_pos, order};
+  } else {
+    e = mxk::embed_sum(p.ids, B, S, enc->desc.hidden, enc->word, enc->desc.vocab, enc->pos,
+                       enc->type, p.w.emb, p.s->err_dev, p.s->stream);
+    p.rows.order = order;
   }
-  rc = run_impl(enc, s, enc->work.emb, enc->work.add_mask, enc->work.kv_len, B, S, &rows);
-  if (rc) return rc;
-  {
-    Bracket br(enc, s->stream, CAT_OTHER);
-    const hipError_t e =
-        mxk::pool_rows(enc->work.emb, attn_mask, B, S, enc->desc.hidden, enc->desc.cls_pool,
-                       enc->desc.l2_normalize, out, s->err_dev, s->stream, rows.seq_start);
-    if (e != hipSuccess) return hip_fail(e, "pool launch");
-  }
-  end_timing(enc, s);
-  int flags = 0;
-  rc = take_data_error(s, &flags);
-  if (rc) return rc;
+  return e == hipSuccess ? MX_OK : hip_fail(e, "embed launch");
+}
+
+int pass_pool(mx_encoder *enc, Pass &p) {
+  Bracket br(enc, p.s->stream, CAT_OTHER);
+  const hipError_t e =
+      mxk::pool_rows(p.w.emb, p.mask, p.B, p.S, enc->desc.hidden, enc->desc.cls_pool,
+                     enc->desc.l2_normalize, p.out, p.s->err_dev, p.s->stream, p.rows.seq_start);
+  return e == hipSuccess ? MX_OK : hip_fail(e, "pool launch");
+}
+
+// The refusals a pass's kernels raise on the data (flag bits of its stream).
+int data_refusal(const mx_encoder *enc, int flags) {
   if (flags & 1)
     return fail(MX_E_DATA, "encoder_embed: a token id is outside [0, " +
                                std::to_string(enc->desc.vocab) + ")");
   if (flags & 2) return fail(MX_E_DATA, "CLS pooling on a sequence whose first token is masked");
   return MX_OK;
+}
+
+// EmbedService::chunk minus the tokenizer (embed_service.cpp:29-64) over the
+// pass: mask and plan, rows and the embedding sum, the stack, pooling, with
+// enc->work the pass's workspace while its kernels are launched. carve: the
+// static scratch.
+int embed_pass(mx_encoder *enc, Pass &p, Carver *carve) {
+  int rc = begin_timing(enc, p.s);
+  if (!rc) rc = pass_plan(enc, p);
+  if (!rc) rc = pass_rows(enc, p, carve);
+  enc->work = p.w;
+  if (!rc) rc = run_bert(enc, p.s, p.w.emb, p.w.add_mask, p.w.kv_len, p.B, p.S, p.rows);
+  if (!rc) rc = pass_pool(enc, p);
+  if (!rc) end_timing(enc, p.s);
+  return rc;
+}
+
+// mx_encoder_embed; carve: the static scratch instead of the encoder's
+// workspace (mx_encoder_embed_static).
+int embed_body(mx_encoder *enc, mx_stream *s, const int32_t *ids, const float *attn_mask,
+               int64_t B, int64_t S, float *out, Carver *carve) {
+  Pass p;
+  p.s = s;
+  p.w = enc->work;
+  p.ids = ids;
+  p.mask = attn_mask;
+  p.out = out;
+  p.B = B;
+  p.S = S;
+  if (carve) {
+    const size_t need = plan_bytes(B, S) + (enc->packing ? 0 : rows_bytes(enc, B * S));
+    if (need > carve->cap) return scratch_refusal(enc, B, S, B * S, need, carve->cap, false);
+    carve_plan(*carve, B, S, p.w);
+    if (!enc->packing) carve_rows(enc, *carve, B * S, p.w);
+  }
+  const Work own = enc->work;
+  int rc = embed_pass(enc, p, carve);
+  enc->work = own;
+  if (rc) return rc;
+  int flags = 0;
+  rc = take_data_error(s, &flags);
+  return rc ? rc : data_refusal(enc, flags);
 }
 
 }  // namespace

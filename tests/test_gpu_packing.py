@@ -99,3 +99,4 @@ def test_packing_then_a_longer_sequence(ctx):
         ids, am, _ = synth.make_text_inputs(m, batch=4, seq=S)
         assert _same(_embed(ctx, enc, ids, am, True), _embed(ctx, enc, ids, am, False))
     enc.close()
+
