@@ -299,8 +299,9 @@ def softmax_rows(ctx, x, rows, cols, stride, mask=None, rows_per_mask_row=1,
                                 cols, stride, _p(mask), rows_per_mask_row, variant))
 
 
-def gemm_wt(ctx, A, M, K, lda, Wt, N, bias, epilogue, residual, C, ldc):
-    cd = _np_dtype_code(np.empty(0, C.dtype))
+def gemm_wt(ctx, A, M, K, lda, Wt, N, bias, epilogue, residual, C, ldc, c_dtype=None):
+    """c_dtype: C's MX_ dtype when C is a raw pointer (a DevBuf carries its own)."""
+    cd = c_dtype if c_dtype is not None else _np_dtype_code(np.empty(0, C.dtype))
     check(lib().mx_gemm_wt(ctx.stream, _p(A), M, K, lda, _p(Wt), N, _p(bias), epilogue,
                            _p(residual), _p(C), cd, ldc))
 
@@ -350,8 +351,9 @@ def widen_panel_i4(ctx, packed, gscale, int4_group, K, N, tile_k, tile_n, mac_s,
                                   tile_n, mac_s, mac_t, _p(out)))
 
 
-def gemm_i8_wt(ctx, A, a_scale, M, K, lda, Wt, wscale, N, bias, epilogue, residual, C, ldc):
-    cd = _np_dtype_code(np.empty(0, C.dtype))
+def gemm_i8_wt(ctx, A, a_scale, M, K, lda, Wt, wscale, N, bias, epilogue, residual, C, ldc,
+               c_dtype=None):
+    cd = c_dtype if c_dtype is not None else _np_dtype_code(np.empty(0, C.dtype))
     check(lib().mx_gemm_i8_wt(ctx.stream, _p(A), _p(a_scale), M, K, lda, _p(Wt), _p(wscale), N,
                               _p(bias), epilogue, _p(residual), _p(C), cd, ldc))
 
