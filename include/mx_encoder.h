@@ -454,7 +454,8 @@ int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids,
  * token packing, else B*S) its position int32, xb / ctx / proj bf16 [hidden],
  * qkv bf16 [3 hidden], up bf16 [ffn] (2 ffn gated, plus the gated product
  * [ffn]), emb fp32 [hidden] and on the int8 datapath xq int8 [max(hidden,
- * ffn)] and its scale fp32; a batch whose workspace exceeds the scratch is
+ * ffn)] and its scale fp32 (there up, the gated product and proj are fp32);
+ * a batch whose workspace exceeds the scratch is
  * refused (MX_E_INVALID, naming both sizes). Also refused: timing on
  * (its events are created on demand) and an encoder whose device tables are
  * stale (MX_E_STATE: call mx_encoder_ready after the last tensor is set;
