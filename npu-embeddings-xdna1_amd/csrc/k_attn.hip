@@ -237,18 +237,29 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
       if (add_mask) masked = masked || __ballot(smk[lane] != 0.0f) != 0;
       float mx = -INFINITY, cc;
       if (masked) {
+        // Lane (li, g) holds keys sub * 32 + 8 rr + 4 g + e of accumulator
+        // element 4 rr + e: four consecutive mask entries, one 16-byte LDS
+        // read. All 64 entries of the staged row are written (the loads clamp
+        // to the sequence's last key), so the reads are unconditional; keys at
+        // or past kv_len take -inf by a select.
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
           if (sub == 1 && !h1) continue;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = sub * 32 + (r >> 2) * 8 + g * 4 + (r & 3);
-            const float mv = t * BKV + key < kvl
-                                 ? (add_mask ? smk[key] * 1.4426950408889634f : 0.0f)
-                                 : -INFINITY;
-            const float v = __builtin_fmaf(sc[sub][r], scale_log2e, mv);
-            sc[sub][r] = v;
-            mx = fmaxf(mx, v);
+          for (int rr = 0; rr < 4; ++rr) {
+            const int key0 = sub * 32 + rr * 8 + g * 4;
+            float4 m4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (add_mask) m4 = *(const float4 *)(smk + key0);
+            const float mk[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = rr * 4 + e;
+              const float mv =
+                  t * BKV + key0 + e < kvl ? mk[e] * 1.4426950408889634f : -INFINITY;
+              const float v = __builtin_fmaf(sc[sub][r], scale_log2e, mv);
+              sc[sub][r] = v;
+              mx = fmaxf(mx, v);
+            }
           }
         }
         cc = 1.0f;
