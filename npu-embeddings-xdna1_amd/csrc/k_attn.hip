@@ -217,17 +217,20 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
       // probabilities and PV products are skipped -- each would be exp2(-inf)
       // = 0.
       const bool h1 = t * BKV + 32 < kvl;
+      // Each half's chain starts from an immediate zero accumulator; a
+      // skipped second half is left unset (nothing reads it), so no register
+      // copies merge it with the computed one.
       f32x16 sc[2];
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[sub][r] = 0.0f;
         if (sub == 1 && !h1) continue;
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
           const bf16x8 kf = *(const bf16x8 *)(sl + (sub * 32 + li) * ROWB +
                                               (((2 * kk + g) ^ swk) * 16));
-          sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sc[sub], 0, 0, 0);
+          sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk],
+                                                            kk == 0 ? f32x16{} : sc[sub], 0,
+                                                            0, 0);
         }
       }
       // The tile needs logits (mask added, keys past kv_len at -inf) if it
