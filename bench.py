@@ -260,6 +260,85 @@ def ops_table(mxenc, np):
     ctx.close()
 
 
+def gemm_vs_library(mxenc, np):
+    """The four bge-base GEMM sites at the packed row count (M 17,455): this
+    library's kernel (bf16 C, bias, no activation; FFN-up also with its fused
+    gelu8) beside torch.addmm on the same bf16 operands, which ROCm's PyTorch
+    routes to hipBLASLt. Medians of 7 runs of 30 launches with HIP events on
+    each side's stream. A reference point for the kernel, not a product path."""
+    import ctypes
+    import torch
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    ctx = mxenc.Context(0)
+    stream = vp(mxenc.lib().mx_stream_handle(ctx.stream))
+    e0, e1 = vp(), vp()
+    assert hip.hipEventCreate(ctypes.byref(e0)) == 0 and hip.hipEventCreate(ctypes.byref(e1)) == 0
+    rng = np.random.default_rng(0)
+    M = 17455
+
+    def ours(fn):
+        fn()
+        fn()
+        ctx.sync()
+        ts = []
+        for _ in range(7):
+            assert hip.hipEventRecord(e0, stream) == 0
+            for _ in range(30):
+                fn()
+            assert hip.hipEventRecord(e1, stream) == 0
+            assert hip.hipEventSynchronize(e1) == 0
+            ms = ctypes.c_float()
+            assert hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1) == 0
+            ts.append(ms.value * 1e3 / 30)
+        return float(np.median(ts))
+
+    def lib(fn):
+        fn()
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(7):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(30):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3 / 30)
+        return float(np.median(ts))
+
+    res = []
+    for site, K, N in [("qkv", 768, 2304), ("attn_out", 768, 768), ("ffn_up", 768, 3072),
+                       ("ffn_down", 3072, 768)]:
+        a32 = rng.standard_normal((M, K), dtype=np.float32)
+        w32 = rng.standard_normal((N, K), dtype=np.float32) * 0.05
+        b32 = rng.standard_normal(N, dtype=np.float32) * 0.1
+        A, W, bias = ctx.put(mxenc.to_bf16_bits(a32)), ctx.put(mxenc.to_bf16_bits(w32)), ctx.put(b32)
+        C = ctx.empty((M, N), np.uint16)
+        flop = 2.0 * M * N * K
+        row = {"site": site, "M": M, "N": N, "K": K,
+               "plan": mxenc.lib().mx_gemm_plan_for(M, N, K, mxenc.MX_BF16, 0, 0).decode()}
+        row["ours_us"] = ours(lambda: mxenc.gemm_wt(ctx, A, M, K, K, W, N, bias,
+                                                    mxenc.MX_EPI_NONE, None, C, N))
+        if site == "ffn_up":
+            row["ours_gelu8_us"] = ours(lambda: mxenc.gemm_wt(ctx, A, M, K, K, W, N, bias,
+                                                              mxenc.MX_EPI_GELU_POLY, None, C, N))
+        ta = torch.from_numpy(a32).to("cuda:0", torch.bfloat16)
+        tw = torch.from_numpy(w32).to("cuda:0", torch.bfloat16)
+        tb = torch.from_numpy(b32).to("cuda:0", torch.bfloat16)
+        row["hipblaslt_us"] = lib(lambda: torch.addmm(tb, ta, tw.t()))
+        row["ours_tflops"] = flop / (row["ours_us"] * 1e-6) / 1e12
+        row["hipblaslt_tflops"] = flop / (row["hipblaslt_us"] * 1e-6) / 1e12
+        res.append(row)
+        print(f"bench --gemm-vs-library: {site:8s} ours {row['ours_us']:6.1f} us "
+              f"({row['ours_tflops']:5.0f} TF/s)  hipBLASLt {row['hipblaslt_us']:6.1f} us "
+              f"({row['hipblaslt_tflops']:5.0f} TF/s)", file=sys.stderr, flush=True)
+        del ta, tw, tb
+    print(json.dumps({"gemm_vs_library": res}))
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -288,6 +367,9 @@ def main():
                     help="only time the standalone memory-bound entry points (mx_gelu, "
                          "mx_softmax_rows, mx_layernorm, mx_layernorm_aie, mx_narrow_*) at "
                          "the bge-base workload's shapes, with HIP events on their stream")
+    ap.add_argument("--gemm-vs-library", action="store_true",
+                    help="only time the four bge-base GEMM sites on this library's kernel "
+                         "and on torch.addmm (hipBLASLt) over the same bf16 operands")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run narrow_f32_bf16 over 64 Mi fp32 values, 5 times: a "
                          "streaming kernel of known bytes (256 MiB read, 128 MiB written "
@@ -306,6 +388,10 @@ def main():
 
     if args.ops:
         ops_table(mxenc, np)
+        return
+
+    if args.gemm_vs_library:
+        gemm_vs_library(mxenc, np)
         return
 
     if args.calibrate:
