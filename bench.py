@@ -560,12 +560,16 @@ def main():
     # (M, N, K, epilogue, residual, bf16 C) of each site: the BERT stack
     # narrows its projections to bf16 for the residual-fused LayerNorm; the
     # pre-LN stacks add them into the fp32 residual stream in the epilogue.
+    # The int8 datapath keeps FFN-up's activation and the BERT projections in
+    # fp32, as dequantise_c writes them.
+    bfc = not args.int8
     if kind == "bert":
-        sites = [("qkv", (M, 3 * d, d, 0, False, True)), ("attn_out", (M, d, d, 0, False, True)),
-                 ("ffn_up", (M, f, d, 1, False, True)), ("ffn_down", (M, d, f, 0, False, True))]
+        sites = [("qkv", (M, 3 * d, d, 0, False, True)), ("attn_out", (M, d, d, 0, False, bfc)),
+                 ("ffn_up", (M, f, d, 1, False, bfc)), ("ffn_down", (M, d, f, 0, False, bfc))]
     else:
-        sites = [("qkv", (M, 3 * d, d, 0, False, True)), ("attn_out", (M, d, d, 0, True, False)),
-                 ("ffn_up", (M, f, d, 2, False, True)), ("ffn_down", (M, d, f, 0, True, False))]
+        sites = [("qkv", (M, 3 * d, d, 0, False, True)),
+                 ("attn_out", (M, d, d, 0, True, False)),
+                 ("ffn_up", (M, f, d, 2, False, bfc)), ("ffn_down", (M, d, f, 0, True, False))]
     groups = {}
     for i, (sname, (mm, nn, kk, epi, res, cbf)) in enumerate(sites):
         plan = mxenc.lib().mx_gemm_plan_for(mm, nn, kk, mxenc.MX_BF16 if cbf else mxenc.MX_F32,
