@@ -10,7 +10,11 @@ bge-base geometry at batch 64 x seq 512 by default. The embed path packs each
 sequence's rows before its kv_len (the padding past it is never attended and
 never pooled; the pooled output is the padded computation's bit for bit);
 the same steps are also timed padded, as EmbedService::chunk computes them,
-and reported beside (--padded makes the padded run the headline). The
+and reported beside (--padded makes the padded run the headline). With CLS
+pooling the last layer's attention-out, LayerNorms and FFN run over each
+sequence's first row only (the rows pooling reads; the output is unchanged bit
+for bit); the packed rate with the last layer over every row is reported
+beside. The
 steps are split over --lanes concurrent lanes (default 2: the reference's
 --pipeline lanes, EmbedService::embed's workers), each an encoder clone on its
 own stream; the one-lane rate is reported beside. Weights are random-init
@@ -350,7 +354,8 @@ def main():
                          "an encoder clone on its own stream and host thread with its own "
                          "copy of the batch in HBM; the timed steps are split over them")
     ap.add_argument("--no-padded-rate", action="store_true",
-                    help="do not time the padded comparison (profiling runs)")
+                    help="do not time the padded and the last-layer-over-every-row "
+                         "comparisons (profiling runs)")
     ap.add_argument("--padded", action="store_true",
                     help="the headline computes every padded row (token packing off)")
     ap.add_argument("--int8", action="store_true",
@@ -415,6 +420,10 @@ def main():
     ctx = mxenc.Context(0)
     enc = mxenc.Encoder(ctx, m, int8=synth.quantise_model(m) if args.int8 else None)
     packing = kind == "bert" and not args.padded
+    # CLS pruning (the last layer's row-wise half over each sequence's first
+    # row; the pooled output is unchanged bit for bit) goes with packing: the
+    # padded run is EmbedService::chunk's computation, every row in every layer.
+    pruning = packing and m["cls_pool"]
     lanes = max(1, args.lanes) if kind == "bert" else 1
     lane_ctx, lane_enc, lane_step = [ctx], [enc], []
     if kind == "bert":
@@ -426,6 +435,7 @@ def main():
             lane_enc.append(enc.clone(c))
         for c, e in zip(lane_ctx, lane_enc):
             e.set_packing(packing)
+            e.set_cls_pruning(pruning)
             e.set_fusion(not args.no_fusion)
             d_ids, d_am = c.put(ids), c.put(am)
             out = c.empty((B, m["hidden"]), np.float32)
@@ -508,16 +518,33 @@ def main():
         one_lane = {"value": args.steps * B / odt, "ms_per_step": odt / args.steps * 1e3}
         print(f"bench: one lane {one_lane['value']:.1f} {unit} "
               f"({one_lane['ms_per_step']:.2f} ms/step)", file=sys.stderr, flush=True)
+    all_rows = None
+    if pruning and not args.no_padded_rate:
+        # The same packed steps with the last layer over every row.
+        for e in lane_enc:
+            e.set_cls_pruning(False)
+        step()
+        ctx.sync()
+        adt = timed(lanes)
+        for e in lane_enc:
+            e.set_cls_pruning(True)
+        all_rows = {"value": args.steps * B / adt, "ms_per_step": adt / args.steps * 1e3,
+                    "lanes": lanes}
+        print(f"bench: last layer over every row {all_rows['value']:.1f} {unit} "
+              f"({all_rows['ms_per_step']:.2f} ms/step)", file=sys.stderr, flush=True)
     padded = None
     if packing and not args.no_padded_rate:
-        # The same steps with every padded row computed (EmbedService::chunk).
+        # The same steps with every padded row computed in every layer
+        # (EmbedService::chunk).
         for e in lane_enc:
             e.set_packing(False)
+            e.set_cls_pruning(False)
         step()
         ctx.sync()
         pdt = timed(lanes)
         for e in lane_enc:
             e.set_packing(True)
+            e.set_cls_pruning(pruning)
         padded = {"value": args.steps * B / pdt, "ms_per_step": pdt / args.steps * 1e3,
                   "rows_per_step": B * S, "lanes": lanes}
         print(f"bench: padded {padded['value']:.1f} {unit} ({padded['ms_per_step']:.2f} ms/step)",
@@ -525,6 +552,10 @@ def main():
 
     # The same steps again with a HIP event pair around every launch, on the
     # stream the kernels run on: per-kernel-family durations for the roofline.
+    # This pass runs the last layer over every row, so that every launch of a
+    # site is the same kernel at the workload's full row count.
+    if pruning:
+        enc.set_cls_pruning(False)
     enc.set_timing(True)
     tot = {"gemm_ms": 0.0, "attn_ms": 0.0, "ln_ms": 0.0, "other_ms": 0.0, "gemm_flop": 0.0,
            "attn_flop": 0.0, "gemm_n": 0, "attn_n": 0}
@@ -545,6 +576,7 @@ def main():
             site_flop[i] += t.gemm_site_flop[i]
             site_n[i] += t.gemm_site_launches[i]
     enc.set_timing(False)
+    enc.set_cls_pruning(pruning)
     gemm_tflops = tot["gemm_flop"] / (tot["gemm_ms"] * 1e-3) / 1e12
     attn_tflops = tot["attn_flop"] / (tot["attn_ms"] * 1e-3) / 1e12
     print(f"bench: GEMM {tot['gemm_ms']/args.steps:.2f} ms/step ({gemm_tflops:.0f} TFLOP/s, "
@@ -637,6 +669,8 @@ def main():
         "sustained": sustained,
         "token_packing": {"on": packing, "rows_per_step": M, "padded_rows_per_step": B * S,
                           "padded": padded} if kind == "bert" else None,
+        "cls_pruning": {"on": pruning, "last_layer_rows": B if pruning else M,
+                        "last_layer_all_rows": all_rows} if kind == "bert" else None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -476,6 +476,17 @@ int mx_encoder_embed_static(mx_encoder *enc, mx_stream *s, const int32_t *ids,
  * per batch. mx_encoder_run always computes every row (it returns them all). */
 int mx_encoder_set_packing(mx_encoder *enc, int on);
 
+/* CLS pruning in mx_encoder_embed (on by default; no counterpart in the
+ * reference, which runs every row through every layer): with CLS pooling
+ * only each sequence's first row of the last layer reaches the pooled output,
+ * and in that layer only attention reads the other rows (as keys and values).
+ * So the last layer's attention runs over all rows, and its attention-out
+ * GEMM, LayerNorms and FFN over the B first rows alone. Every one of those
+ * operations is row by row, so the pooled output is the unpruned
+ * computation's, bit for bit. Mean pooling and mx_encoder_run are not
+ * affected; off restores the last layer over every row. */
+int mx_encoder_set_cls_pruning(mx_encoder *enc, int on);
+
 /* The gated FFN (swiglu_cpu, bert_encoder.cpp:582-627) fused into FFN-up's
  * GEMM epilogue (on by default): FFN-up's operand is kept a second time with
  * its lo and hi rows interleaved, and the GEMM writes lo * act(hi) directly,

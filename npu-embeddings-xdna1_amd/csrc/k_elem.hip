@@ -723,15 +723,17 @@ constexpr int POOL_U = 16, POOL_CH = 1024;
 __global__ __launch_bounds__(1024) void pool_k(const float *__restrict__ h,
                                                const float *__restrict__ am, int64_t S,
                                                int64_t d, int cls, int l2, float *out,
-                                               int *err, const int32_t *__restrict__ seq_start) {
+                                               int *err, const int32_t *__restrict__ seq_start,
+                                               int compact) {
   extern __shared__ double acc[];
   __shared__ double nrm_s;
   __shared__ __align__(16) float msk[POOL_CH];
   const int64_t b = blockIdx.x;
   const float *amb = am + b * S;
   // Packed rows: the loop below reads row s only where the mask is nonzero,
-  // i.e. only rows s < kv_len[b], the ones packing kept.
-  const float *hb = h + (seq_start ? (int64_t)seq_start[b] : b * S) * d;
+  // i.e. only rows s < kv_len[b], the ones packing kept. compact (CLS
+  // pooling): h holds only the sequences' first rows, row b for sequence b.
+  const float *hb = h + (compact ? b : seq_start ? (int64_t)seq_start[b] : b * S) * d;
   if (cls) {
     if (amb[0] == 0.0f) {
       if (threadIdx.x == 0) atomicOr(err, 2);
@@ -1008,10 +1010,35 @@ hipError_t mask_build(const float *am, int64_t B, int64_t S, float *add_mask, in
 }
 
 hipError_t pool_rows(const float *h, const float *am, int64_t B, int64_t S, int64_t d, int cls,
-                     int l2, float *out, int *err, hipStream_t s, const int32_t *seq_start) {
+                     int l2, float *out, int *err, hipStream_t s, const int32_t *seq_start,
+                     bool compact) {
+  if (compact && !cls) return hipErrorInvalidValue;
   const int nt = d >= 1024 ? 1024 : (int)((d + 63) / 64 * 64);
   pool_k<<<(unsigned)B, nt, (size_t)d * sizeof(double), s>>>(h, am, S, d, cls, l2, out, err,
-                                                             seq_start);
+                                                             seq_start, compact ? 1 : 0);
+  return hipGetLastError();
+}
+
+// Sequence b's first row (seq_start[b], or b * S) of the fp32 residual
+// stream x and of the bf16 attention context ctx, both [*, d], into row b of
+// xc and ctxc. One block per sequence; d % 4 == 0, 16-byte aligned rows.
+__global__ __launch_bounds__(256) void gather_cls_k(const float *__restrict__ x,
+                                                    const uint16_t *__restrict__ ctx,
+                                                    const int32_t *__restrict__ seq_start,
+                                                    int64_t S, int64_t d, float *__restrict__ xc,
+                                                    uint16_t *__restrict__ ctxc) {
+  const int64_t b = blockIdx.x;
+  const int64_t r = seq_start ? (int64_t)seq_start[b] : b * S;
+  for (int64_t c = (int64_t)threadIdx.x * 4; c < d; c += (int64_t)blockDim.x * 4) {
+    *(float4 *)(xc + b * d + c) = *(const float4 *)(x + r * d + c);
+    *(uint2 *)(ctxc + b * d + c) = *(const uint2 *)(ctx + r * d + c);
+  }
+}
+
+hipError_t gather_cls(const float *x, const uint16_t *ctx, const int32_t *seq_start, int64_t B,
+                      int64_t S, int64_t d, float *xc, uint16_t *ctxc, hipStream_t s) {
+  if (d % 4) return hipErrorInvalidValue;
+  gather_cls_k<<<(unsigned)B, 256, 0, s>>>(x, ctx, seq_start, S, d, xc, ctxc);
   return hipGetLastError();
 }
 

@@ -110,6 +110,9 @@ struct mx_encoder {
   // Token packing (embed): seq_start [B + 1] and each packed row's position
   // (work.seq_start, work.row_pos).
   bool packing = true;
+  // CLS pooling: the last layer's attention-out, FFN and LayerNorms over the
+  // sequences' first rows only (mx_encoder_set_cls_pruning)
+  bool prune_cls = true;
   // The last packed plan read back (seq_start[0..B]) and its sum of squared
   // lengths: the attention work of a packed pass.
   std::vector<int32_t> plan_host;
@@ -459,9 +462,26 @@ int bert_pre(mx_encoder *enc, mx_stream *s, float *x, int64_t S, const Rows &row
 }
 
 // Layer l of BertEncoder::run over the rows of one pass, in enc->work.
-int bert_layer(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
-               int64_t B, int64_t S, const Rows &rows, size_t l) {
-  const int64_t M = rows.M, d = enc->desc.hidden, f = enc->desc.ffn;
+// The attention half of layer l over the pass's rows: QKV, RoPE, attention
+// into enc->work.ctxb.
+int layer_attn(mx_encoder *enc, mx_stream *s, const float *mask, const int32_t *kvl, int64_t B,
+               int64_t S, const Rows &rows, size_t l) {
+  const int64_t M = rows.M, d = enc->desc.hidden;
+  const LayerW &w = enc->layers[l];
+  int rc = site_gemm(enc, s, w, SITE_QKV, enc->work.xb, M, d, 3 * d, MX_EPI_NONE, nullptr,
+                     enc->work.qkv, MX_BF16);
+  if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S, M, rows.row_pos);
+  if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, &rows);
+  return rc;
+}
+
+// The row-wise half of layer l over M rows -- x the residual stream and ctx
+// the attention context (bf16), both [M, d]: attention-out, the residual
+// LayerNorm, the FFN, the second LayerNorm. Each row's result depends on that
+// row alone.
+int layer_rows(mx_encoder *enc, mx_stream *s, float *x, const uint16_t *ctx, int64_t M,
+               size_t l) {
+  const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
   const int epi = enc->desc.gelu == MX_GELU_ERF ? MX_EPI_GELU_ERF : MX_EPI_GELU_POLY;
   const size_t L = enc->layers.size();
   const bool gated = enc->desc.gated_ffn != MX_GATED_NONE;
@@ -470,17 +490,12 @@ int bert_layer(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const
   const LayerW &w = enc->layers[l];
   const bool fused = gated && enc->fuse_glu && glu_fusable(enc) && w.glu_gen == enc->wgen &&
                      (enc->i8 ? w.wqg && w.wsg : w.wg != nullptr) && w.bg;
-  int rc = site_gemm(enc, s, w, SITE_QKV, enc->work.xb, M, d, 3 * d, MX_EPI_NONE, nullptr,
-                     enc->work.qkv, MX_BF16);
-  if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S, M, rows.row_pos);
-  if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, &rows);
-  if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.ctxb, MX_BF16, M, d, w.ias[SITE_AO]);
+  int rc = enc->i8 ? quant_l(enc, s, ctx, MX_BF16, M, d, w.ias[SITE_AO]) : MX_OK;
   // proj: bf16 (the array path's C) or, on the int8 datapath, fp32 as
   // dequantise_c writes it (host_kernels.hpp:529-600)
   const int pdt = enc->i8 ? MX_F32 : MX_BF16;
   if (!rc)
-    rc = site_gemm(enc, s, w, SITE_AO, enc->work.ctxb, M, d, d, MX_EPI_NONE, nullptr,
-                   enc->work.proj, pdt);
+    rc = site_gemm(enc, s, w, SITE_AO, ctx, M, d, d, MX_EPI_NONE, nullptr, enc->work.proj, pdt);
   if (!rc) rc = site_ln(enc, s, x, enc->work.proj, pdt, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
   if (!rc && enc->i8) {
     // dequant_act_quant (host_kernels.hpp:405-522, bert_encoder.cpp:811-860):
@@ -507,11 +522,41 @@ int bert_layer(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const
   return rc;
 }
 
+// Layer l of BertEncoder::run over the rows of one pass, in enc->work.
+int bert_layer(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
+               int64_t B, int64_t S, const Rows &rows, size_t l) {
+  int rc = layer_attn(enc, s, mask, kvl, B, S, rows, l);
+  return rc ? rc : layer_rows(enc, s, x, enc->work.ctxb, rows.M, l);
+}
+
+// pooled (nullable): with CLS pooling and CLS pruning on, the last layer's
+// row-wise half runs over each sequence's first row only -- its other rows
+// reach neither the pooled output nor a later layer -- gathered into the QKV
+// buffer (free once attention has run) with the context rows in xb, and
+// *pooled points at those B rows (row b for sequence b). Otherwise *pooled
+// stays null and x holds every row.
 int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
-             int64_t B, int64_t S, const Rows &rows) {
+             int64_t B, int64_t S, const Rows &rows, float **pooled = nullptr) {
   int rc = bert_pre(enc, s, x, S, rows);
-  for (size_t l = 0; !rc && l < enc->layers.size(); ++l)
-    rc = bert_layer(enc, s, x, mask, kvl, B, S, rows, l);
+  const size_t L = enc->layers.size();
+  const bool prune = pooled && enc->prune_cls && enc->desc.cls_pool;
+  for (size_t l = 0; !rc && l < L; ++l) {
+    if (!prune || l + 1 < L) {
+      rc = bert_layer(enc, s, x, mask, kvl, B, S, rows, l);
+      continue;
+    }
+    rc = layer_attn(enc, s, mask, kvl, B, S, rows, l);
+    float *xc = reinterpret_cast<float *>(enc->work.qkv);
+    uint16_t *cc = enc->work.xb;
+    if (!rc) {
+      Bracket br(enc, s->stream, CAT_OTHER);
+      const hipError_t e = mxk::gather_cls(x, enc->work.ctxb, rows.seq_start, B, S,
+                                           enc->desc.hidden, xc, cc, s->stream);
+      if (e != hipSuccess) rc = hip_fail(e, "CLS row gather");
+    }
+    if (!rc) rc = layer_rows(enc, s, xc, cc, B, l);
+    if (!rc) *pooled = xc;
+  }
   return rc;
 }
 
@@ -833,6 +878,7 @@ int mx_encoder_clone(mx_encoder *enc, mx_encoder **out) {
   c->i8 = enc->i8;
   c->rope_inv = enc->rope_inv;
   c->packing = enc->packing;
+  c->prune_cls = enc->prune_cls;
   for (int i = 0; i < 2; ++i) {
     c->emb_ln[i] = enc->emb_ln[i];
     c->fin_ln[i] = enc->fin_ln[i];
@@ -1270,11 +1316,17 @@ int pass_rows(mx_encoder *enc, Pass &p, Carver *carve) {
   return e == hipSuccess ? MX_OK : hip_fail(e, "embed launch");
 }
 
-int pass_pool(mx_encoder *enc, Pass &p) {
+// pooled: the sequences' first rows alone (run_bert's CLS pruning), or null
+// for the pass's rows in p.w.emb.
+int pass_pool(mx_encoder *enc, Pass &p, const float *pooled) {
   Bracket br(enc, p.s->stream, CAT_OTHER);
   const hipError_t e =
-      mxk::pool_rows(p.w.emb, p.mask, p.B, p.S, enc->desc.hidden, enc->desc.cls_pool,
-                     enc->desc.l2_normalize, p.out, p.s->err_dev, p.s->stream, p.rows.seq_start);
+      pooled ? mxk::pool_rows(pooled, p.mask, p.B, p.S, enc->desc.hidden, 1,
+                              enc->desc.l2_normalize, p.out, p.s->err_dev, p.s->stream, nullptr,
+                              true)
+             : mxk::pool_rows(p.w.emb, p.mask, p.B, p.S, enc->desc.hidden, enc->desc.cls_pool,
+                              enc->desc.l2_normalize, p.out, p.s->err_dev, p.s->stream,
+                              p.rows.seq_start);
   return e == hipSuccess ? MX_OK : hip_fail(e, "pool launch");
 }
 
@@ -1296,8 +1348,9 @@ int embed_pass(mx_encoder *enc, Pass &p, Carver *carve) {
   if (!rc) rc = pass_plan(enc, p);
   if (!rc) rc = pass_rows(enc, p, carve);
   enc->work = p.w;
-  if (!rc) rc = run_bert(enc, p.s, p.w.emb, p.w.add_mask, p.w.kv_len, p.B, p.S, p.rows);
-  if (!rc) rc = pass_pool(enc, p);
+  float *pooled = nullptr;
+  if (!rc) rc = run_bert(enc, p.s, p.w.emb, p.w.add_mask, p.w.kv_len, p.B, p.S, p.rows, &pooled);
+  if (!rc) rc = pass_pool(enc, p, pooled);
   if (!rc) end_timing(enc, p.s);
   return rc;
 }
@@ -1492,6 +1545,13 @@ int mx_encoder_set_packing(mx_encoder *enc, int on) {
   clear_error();
   if (!enc) return fail(MX_E_INVALID, "encoder_set_packing: null encoder");
   enc->packing = on != 0;
+  return MX_OK;
+}
+
+int mx_encoder_set_cls_pruning(mx_encoder *enc, int on) {
+  clear_error();
+  if (!enc) return fail(MX_E_INVALID, "encoder_set_cls_pruning: null encoder");
+  enc->prune_cls = on != 0;
   return MX_OK;
 }
 

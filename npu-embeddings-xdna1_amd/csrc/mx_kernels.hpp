@@ -28,10 +28,15 @@ hipError_t embed_sum(const int32_t *ids, int64_t B, int64_t S, int64_t d, const 
                      hipStream_t s);
 hipError_t mask_build(const float *attn_mask, int64_t B, int64_t S, float *add_mask,
                       int32_t *kv_len, hipStream_t s);
-// seq_start (nullable): the packed layout of the rows (pack_plan).
+// seq_start (nullable): the packed layout of the rows (pack_plan). compact
+// (CLS pooling only): h holds just each sequence's first row, row b.
 hipError_t pool_rows(const float *h, const float *attn_mask, int64_t B, int64_t S, int64_t d,
                      int cls, int l2, float *out, int *err, hipStream_t s,
-                     const int32_t *seq_start = nullptr);
+                     const int32_t *seq_start = nullptr, bool compact = false);
+// Each sequence's first row (seq_start[b], or b * S) of x fp32 and ctx bf16
+// ([*, d], d % 4 == 0) into row b of xc and ctxc.
+hipError_t gather_cls(const float *x, const uint16_t *ctx, const int32_t *seq_start, int64_t B,
+                      int64_t S, int64_t d, float *xc, uint16_t *ctxc, hipStream_t s);
 // Token packing: seq_start[0..B] = exclusive scan of kv_len (seq_start[B] =
 // packed rows) and, when order is non-null, order[0..B) = the sequence
 // indices by decreasing kv_len (attention's launch order); the embedding sum

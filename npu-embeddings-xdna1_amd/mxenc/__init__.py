@@ -116,6 +116,7 @@ SIGNATURES = {
     "mx_encoder_whisper": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "mx_encoder_set_timing": (_int, [_vp, _int]),
     "mx_encoder_set_packing": (_int, [_vp, _int]),
+    "mx_encoder_set_cls_pruning": (_int, [_vp, _int]),
     "mx_encoder_set_fusion": (_int, [_vp, _int]),
     "mx_encoder_timings": (_int, [_vp, ctypes.POINTER(Timings)]),
     "mx_npue_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
@@ -577,6 +578,9 @@ class Encoder:
 
     def set_packing(self, on):
         check(lib().mx_encoder_set_packing(self.handle, int(on)))
+
+    def set_cls_pruning(self, on):
+        check(lib().mx_encoder_set_cls_pruning(self.handle, int(on)))
 
     def set_fusion(self, on):
         check(lib().mx_encoder_set_fusion(self.handle, int(on)))

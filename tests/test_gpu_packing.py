@@ -100,3 +100,58 @@ def test_packing_then_a_longer_sequence(ctx):
         assert _same(_embed(ctx, enc, ids, am, True), _embed(ctx, enc, ids, am, False))
     enc.close()
 
+
+
+def _embed_pruned(ctx, enc, ids, am, packing, prune):
+    enc.set_cls_pruning(prune)
+    try:
+        return _embed(ctx, enc, ids, am, packing)
+    finally:
+        enc.set_cls_pruning(True)
+
+
+def test_cls_pruning_is_bitwise_the_full_last_layer(ctx):
+    """CLS pooling: the last layer's attention-out, LayerNorms and FFN over each
+    sequence's first row only give the pooled output of the last layer over
+    every row, bit for bit -- on the benchmark's own batch, packed and padded."""
+    m = synth.make_model("bge_base")
+    ids, am, _ = synth.make_text_inputs(m)
+    enc = mxenc.Encoder(ctx, m)
+    for packing in (True, False):
+        pruned = _embed_pruned(ctx, enc, ids, am, packing, True)
+        full = _embed_pruned(ctx, enc, ids, am, packing, False)
+        assert _same(pruned, full), f"packing={packing}"
+    enc.close()
+
+
+def test_cls_pruning_int8_and_mean_pooling(ctx):
+    """The int8 datapath (the context quantised from the gathered rows), and
+    mean pooling, where pruning does not apply and changes nothing."""
+    m = synth.make_model("bge_base", layers=3)
+    ids, am, _ = synth.make_text_inputs(m, batch=16, seq=512)
+    enc = mxenc.Encoder(ctx, m, int8=synth.quantise_model(m))
+    assert _same(_embed_pruned(ctx, enc, ids, am, True, True),
+                 _embed_pruned(ctx, enc, ids, am, True, False))
+    enc.close()
+    m = synth.make_model("minilm", layers=2)
+    assert not m["cls_pool"]
+    ids, am, _ = synth.make_text_inputs(m, batch=8, seq=128)
+    enc = mxenc.Encoder(ctx, m)
+    assert _same(_embed_pruned(ctx, enc, ids, am, True, True),
+                 _embed_pruned(ctx, enc, ids, am, True, False))
+    enc.close()
+
+
+def test_cls_pruning_masked_cls_is_still_refused(ctx):
+    """A sequence whose first token is masked cannot be CLS-pooled: refused
+    by name with pruning on, as without it."""
+    m = synth.make_model("bge_base", layers=1)
+    ids, am, _ = synth.make_text_inputs(m, batch=4, seq=64)
+    am[2, 0] = 0.0
+    enc = mxenc.Encoder(ctx, m)
+    out = ctx.empty((4, m["hidden"]), np.float32)
+    for prune in (True, False):
+        enc.set_cls_pruning(prune)
+        with pytest.raises(mxenc.MxError, match="first token is masked"):
+            enc.embed(ctx.put(ids), ctx.put(am), 4, 64, out)
+    enc.close()
