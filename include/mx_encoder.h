@@ -480,10 +480,11 @@ int mx_encoder_set_packing(mx_encoder *enc, int on);
  * reference, which runs every row through every layer): with CLS pooling
  * only each sequence's first row of the last layer reaches the pooled output,
  * and in that layer only attention reads the other rows (as keys and values).
- * So the last layer's attention runs over all rows, and its attention-out
- * GEMM, LayerNorms and FFN over the B first rows alone. Every one of those
- * operations is row by row, so the pooled output is the unpruned
- * computation's, bit for bit. Mean pooling and mx_encoder_run are not
+ * So the last layer's QKV GEMM runs over all rows, its attention computes the
+ * first query of each sequence (over all its keys), and its attention-out
+ * GEMM, LayerNorms and FFN run over the B first rows alone. Every query and
+ * every row-wise operation is computed on its own, so the pooled output is
+ * the unpruned computation's, bit for bit. Mean pooling and mx_encoder_run are not
  * affected; off restores the last layer over every row. */
 int mx_encoder_set_cls_pruning(mx_encoder *enc, int on);
 

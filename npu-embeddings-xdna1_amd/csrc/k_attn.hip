@@ -91,7 +91,8 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
                                                    uint16_t *__restrict__ ctx, int64_t ldo,
                                                    int n_qblk, int force_logits,
                                                    const int32_t *__restrict__ seq_start,
-                                                   const int32_t *__restrict__ order) {
+                                                   const int32_t *__restrict__ order,
+                                                   int q_lim) {
   constexpr int NKK = HD / 16, NHT = HD / 32;
   constexpr int ROWB = HD * 2, TILE = BKV * ROWB;  // bytes per row and per operand tile
   constexpr int SLOT = 2 * TILE + BKV * 4;         // K, V, mask row
@@ -126,7 +127,10 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
   const int lim = seq_start ? kvl : S;
   if (qb * BQ >= lim) return;
   const uint16_t *base = qkv + row0 * ldq;
-  const bool live = qb * BQ + wave * 32 < lim;
+  // Queries at or past q_lim (the first q_lim of each sequence are asked for)
+  // are neither computed nor stored; their waves still stage K and V.
+  const int qend = lim < q_lim ? lim : q_lim;
+  const bool live = qb * BQ + wave * 32 < qend;
 
   // Q fragments (B operand of S^T = K Q^T), waited for before the loop.
   const int q = qb * BQ + wave * 32 + li;
@@ -330,7 +334,7 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
 
   const float l = l_run + __shfl_xor(l_run, 32);
   const float inv = 1.0f / l;
-  if (q < lim) {
+  if (q < qend) {
     uint16_t *dst = ctx + (row0 + q) * ldo + h * HD;
 #pragma unroll
     for (int ht = 0; ht < NHT; ++ht)
@@ -351,18 +355,19 @@ namespace mxk {
 
 hipError_t attention(const AttnArgs &a, hipStream_t s) {
   constexpr int nw = 4, bq = 32 * nw;
-  const int n_qblk = (int)((a.S + bq - 1) / bq);
+  const int64_t qs = a.q_rows > 0 && a.q_rows < a.S ? a.q_rows : a.S;
+  const int n_qblk = (int)((qs + bq - 1) / bq);
   const int64_t blocks = a.B * a.H * n_qblk;
   const float sl2e = a.scale * 1.4426950408889634f;
   const int force_logits = a.scale > 0.0f ? 0 : 1;  // raw-score max needs scale > 0
   if (a.hd == 64)
     attn_dma_k<64, nw><<<(unsigned)blocks, 64 * nw, 0, s>>>(
         a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e, a.add_mask, a.kv_len, a.ctx, a.ld_ctx,
-        n_qblk, force_logits, a.seq_start, a.order);
+        n_qblk, force_logits, a.seq_start, a.order, (int)qs);
   else if (a.hd == 32)
     attn_dma_k<32, nw><<<(unsigned)blocks, 64 * nw, 0, s>>>(
         a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e, a.add_mask, a.kv_len, a.ctx, a.ld_ctx,
-        n_qblk, force_logits, a.seq_start, a.order);
+        n_qblk, force_logits, a.seq_start, a.order, (int)qs);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -145,7 +145,7 @@ int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t 
 int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
                       int64_t H, int64_t hd, float scale, const float *add_mask,
                       const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx,
-                      const int32_t *seq_start, const int32_t *order) {
+                      const int32_t *seq_start, const int32_t *order, int64_t q_rows) {
   if (!s) return fail(MX_E_INVALID, "attention: null stream");
   if (!qkv || !ctx) return fail(MX_E_INVALID, "attention: null qkv or ctx");
   if (B <= 0 || S <= 0 || H <= 0) return fail(MX_E_INVALID, "attention: zero dimension");
@@ -169,8 +169,9 @@ int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t
   if (seq_start && !kv_len)
     return fail(MX_E_INVALID, "attention: packed rows need kv_len");
   if (order && !kv_len) return fail(MX_E_INVALID, "attention: a launch order needs kv_len");
-  mxk::AttnArgs a{qkv, ld_qkv, B, S, H, hd, scale, add_mask, kv_len, ctx, ld_ctx, seq_start,
-                  order};
+  if (q_rows < 0) return fail(MX_E_INVALID, "attention: negative query count");
+  mxk::AttnArgs a{qkv, ld_qkv, B,      S,        H,     hd,   scale, add_mask,
+                  kv_len, ctx,  ld_ctx, seq_start, order, q_rows};
   const hipError_t e = mxk::attention(a, s->stream);
   return e == hipSuccess ? MX_OK : hip_fail(e, "attention launch");
 }

@@ -420,8 +420,9 @@ struct Rows {
   const int32_t *seq_start = nullptr, *row_pos = nullptr, *order = nullptr;
 };
 
+// q_rows: 0 for every query, else only each sequence's first q_rows.
 int attn_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, const float *mask,
-           const int32_t *kv_len, const Rows *rows = nullptr) {
+           const int32_t *kv_len, const Rows *rows = nullptr, int64_t q_rows = 0) {
   Bracket br(enc, s->stream, CAT_ATTN);
   const int64_t d = enc->desc.hidden;
   // Packed rows: each sequence attends over its own kv_len rows only.
@@ -429,7 +430,8 @@ int attn_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, const float *mas
   enc->attn_flop += 4.0 * enc->desc.heads * sq * enc->desc.head_dim;
   return attention_checked(s, enc->work.qkv, 3 * d, B, S, enc->desc.heads, enc->desc.head_dim,
                            enc->desc.attn_scale, mask, kv_len, enc->work.ctxb, d,
-                           rows ? rows->seq_start : nullptr, rows ? rows->order : nullptr);
+                           rows ? rows->seq_start : nullptr, rows ? rows->order : nullptr,
+                           q_rows);
 }
 
 // One GEMM site of a layer on the encoder's datapath: bf16 A (A_bf) times
@@ -463,15 +465,16 @@ int bert_pre(mx_encoder *enc, mx_stream *s, float *x, int64_t S, const Rows &row
 
 // Layer l of BertEncoder::run over the rows of one pass, in enc->work.
 // The attention half of layer l over the pass's rows: QKV, RoPE, attention
-// into enc->work.ctxb.
+// into enc->work.ctxb (q_rows: 0 for every query, else each sequence's first
+// q_rows only).
 int layer_attn(mx_encoder *enc, mx_stream *s, const float *mask, const int32_t *kvl, int64_t B,
-               int64_t S, const Rows &rows, size_t l) {
+               int64_t S, const Rows &rows, size_t l, int64_t q_rows = 0) {
   const int64_t M = rows.M, d = enc->desc.hidden;
   const LayerW &w = enc->layers[l];
   int rc = site_gemm(enc, s, w, SITE_QKV, enc->work.xb, M, d, 3 * d, MX_EPI_NONE, nullptr,
                      enc->work.qkv, MX_BF16);
   if (!rc && enc->desc.rope) rc = rope_l(enc, s, B, S, M, rows.row_pos);
-  if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, &rows);
+  if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, &rows, q_rows);
   return rc;
 }
 
@@ -530,8 +533,9 @@ int bert_layer(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const
 }
 
 // pooled (nullable): with CLS pooling and CLS pruning on, the last layer's
-// row-wise half runs over each sequence's first row only -- its other rows
-// reach neither the pooled output nor a later layer -- gathered into the QKV
+// attention computes each sequence's first query only (over all its keys)
+// and its row-wise half runs over that first row only -- the other rows reach
+// neither the pooled output nor a later layer -- gathered into the QKV
 // buffer (free once attention has run) with the context rows in xb, and
 // *pooled points at those B rows (row b for sequence b). Otherwise *pooled
 // stays null and x holds every row.
@@ -545,7 +549,7 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
       rc = bert_layer(enc, s, x, mask, kvl, B, S, rows, l);
       continue;
     }
-    rc = layer_attn(enc, s, mask, kvl, B, S, rows, l);
+    rc = layer_attn(enc, s, mask, kvl, B, S, rows, l, 1);  // the first query's context
     float *xc = reinterpret_cast<float *>(enc->work.qkv);
     uint16_t *cc = enc->work.xb;
     if (!rc) {

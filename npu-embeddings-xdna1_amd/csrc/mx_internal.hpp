@@ -52,7 +52,8 @@ int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t 
 int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
                       int64_t H, int64_t hd, float scale, const float *add_mask,
                       const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx,
-                      const int32_t *seq_start = nullptr, const int32_t *order = nullptr);
+                      const int32_t *seq_start = nullptr, const int32_t *order = nullptr,
+                      int64_t q_rows = 0);
 // An int8 operand on the device: the [K, N] weight as an [N, K] int8 panel
 // (from row-major int8, or untiled from a container's block panel when tile_k
 // > 0), wscale [N] copied, ias = 1 / asmooth [K] computed once in fp32.

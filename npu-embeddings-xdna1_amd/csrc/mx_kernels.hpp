@@ -190,6 +190,9 @@ struct AttnArgs {
   // Launch order (nullable): the B sequence indices, longest kv_len first;
   // the blocks of order[0] are dispatched first.
   const int32_t *order = nullptr;
+  // 0: every query; else only the first q_rows queries of each sequence are
+  // computed and stored (their keys and values are all of the sequence's).
+  int64_t q_rows = 0;
 };
 hipError_t attention(const AttnArgs &a, hipStream_t s);
 
