@@ -30,7 +30,7 @@ CONFIGS = {
     "bge_large": dict(kind="bert", layers=24, hidden=1024, heads=16, head_dim=64, ffn=4096,
                       vocab=30522, max_pos=512, batch=128, seq=512, len_lo=512, len_hi=512,
                       cls_pool=True, sep=False),
-    # The RoPE / gated-FFN BERT archs at bge-base geometry (no BASELINE
+    # The RoPE / gated-FFN BERT archs at bge-base geometry (no benchmark
     # workload names them; they exercise the nomic and gte encoder paths):
     # nomic-embed-text (SwiGLU, RoPE base 1000, mean pooling) and
     # gte-multilingual-base (exact-erf GeGLU, RoPE from an explicit frequency

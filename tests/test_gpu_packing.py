@@ -124,6 +124,19 @@ def test_cls_pruning_is_bitwise_the_full_last_layer(ctx):
     enc.close()
 
 
+def test_cls_pruning_gte_rope_geglu(ctx):
+    """gte (RoPE, GeGLU fused into FFN-up, CLS pooling): the pruned layer's
+    gated FFN over the gathered rows."""
+    m = synth.make_model("gte", layers=2, ln_random=True)
+    assert m["cls_pool"]
+    ids, am, _ = synth.make_text_inputs(m, batch=7, seq=192)
+    enc = mxenc.Encoder(ctx, m)
+    for packing in (True, False):
+        assert _same(_embed_pruned(ctx, enc, ids, am, packing, True),
+                     _embed_pruned(ctx, enc, ids, am, packing, False)), f"packing={packing}"
+    enc.close()
+
+
 def test_cls_pruning_int8_and_mean_pooling(ctx):
     """The int8 datapath (the context quantised from the gathered rows), and
     mean pooling, where pruning does not apply and changes nothing."""
