@@ -554,8 +554,7 @@ def main():
     # stream the kernels run on: per-kernel-family durations for the roofline.
     # This pass runs the last layer over every row, so that every launch of a
     # site is the same kernel at the workload's full row count.
-    if pruning:
-        enc.set_cls_pruning(False)
+    enc.set_cls_pruning(False)
     enc.set_timing(True)
     tot = {"gemm_ms": 0.0, "attn_ms": 0.0, "ln_ms": 0.0, "other_ms": 0.0, "gemm_flop": 0.0,
            "attn_flop": 0.0, "gemm_n": 0, "attn_n": 0}
@@ -576,7 +575,8 @@ def main():
             site_flop[i] += t.gemm_site_flop[i]
             site_n[i] += t.gemm_site_launches[i]
     enc.set_timing(False)
-    enc.set_cls_pruning(pruning)
+    # (ViT prunes its last layer whenever no hidden state is returned.)
+    enc.set_cls_pruning(pruning if kind == "bert" else True)
     gemm_tflops = tot["gemm_flop"] / (tot["gemm_ms"] * 1e-3) / 1e12
     attn_tflops = tot["attn_flop"] / (tot["attn_ms"] * 1e-3) / 1e12
     print(f"bench: GEMM {tot['gemm_ms']/args.steps:.2f} ms/step ({gemm_tflops:.0f} TFLOP/s, "
@@ -669,8 +669,9 @@ def main():
         "sustained": sustained,
         "token_packing": {"on": packing, "rows_per_step": M, "padded_rows_per_step": B * S,
                           "padded": padded} if kind == "bert" else None,
-        "cls_pruning": {"on": pruning, "last_layer_rows": B if pruning else M,
-                        "last_layer_all_rows": all_rows} if kind == "bert" else None,
+        "cls_pruning": ({"on": pruning, "last_layer_rows": B if pruning else M,
+                         "last_layer_all_rows": all_rows} if kind == "bert" else
+                        {"on": True, "last_layer_rows": B} if kind == "vit" else None),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

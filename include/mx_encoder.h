@@ -484,8 +484,11 @@ int mx_encoder_set_packing(mx_encoder *enc, int on);
  * first query of each sequence (over all its keys), and its attention-out
  * GEMM, LayerNorms and FFN run over the B first rows alone. Every query and
  * every row-wise operation is computed on its own, so the pooled output is
- * the unpruned computation's, bit for bit. Mean pooling and mx_encoder_run are not
- * affected; off restores the last layer over every row. */
+ * the unpruned computation's, bit for bit. mx_encoder_vit without a hidden
+ * state to return prunes its last layer the same way (only the CLS rows reach
+ * the head, after the final LayerNorm, which then runs over those rows alone).
+ * Mean pooling, mx_encoder_run and mx_encoder_whisper are not affected; off
+ * restores the last layer over every row. */
 int mx_encoder_set_cls_pruning(mx_encoder *enc, int on);
 
 /* The gated FFN (swiglu_cpu, bert_encoder.cpp:582-627) fused into FFN-up's
@@ -502,7 +505,8 @@ int mx_encoder_set_fusion(mx_encoder *enc, int on);
  * GEMM + bias -> [CLS; patches] + positions -> the pre-LN layers and final
  * LayerNorm -> CLS rows -> head GEMM + bias -> logits fp32 [B, labels]
  * (device). hidden (nullable, device, fp32 [B*(np+1), hidden]) receives the
- * final hidden state. Tensors: "patch_embed.weight" [3*patch^2, hidden],
+ * final hidden state; without it the last layer is CLS-pruned
+ * (mx_encoder_set_cls_pruning). Tensors: "patch_embed.weight" [3*patch^2, hidden],
  * "patch_embed.bias", "cls_token" [hidden], "position" [np+1, hidden],
  * "head.weight" [hidden, labels] (label fastest, as head.cpp reads it),
  * "head.bias" [labels]. image % patch == 0, patch % 8 == 0, image % 4 == 0.

@@ -564,30 +564,58 @@ int run_bert(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const i
   return rc;
 }
 
+// cls_rows (nullable): when only each sequence's first row of the final
+// hidden state is wanted (the ViT head) and CLS pruning is on, the last layer
+// computes attention for the first query only and its attention-out, FFN and
+// the final LayerNorm over those B rows, gathered into the QKV buffer (free
+// once attention has run); *cls_rows points at them (row b for sequence b).
+// Otherwise *cls_rows stays null and x holds every row.
 int run_preln(mx_encoder *enc, mx_stream *s, float *x, const float *mask, const int32_t *kvl,
-              int64_t B, int64_t S) {
+              int64_t B, int64_t S, float **cls_rows = nullptr) {
   const int64_t M = B * S, d = enc->desc.hidden, f = enc->desc.ffn;
   const int epi = enc->desc.gelu == MX_GELU_POLY ? MX_EPI_GELU_POLY : MX_EPI_GELU_ERF;
+  const size_t L = enc->layers.size();
+  const bool prune = cls_rows && enc->prune_cls;
+  float *xc = reinterpret_cast<float *>(enc->work.qkv);
   int rc = MX_OK;
-  for (size_t l = 0; !rc && l < enc->layers.size(); ++l) {
+  for (size_t l = 0; !rc && l < L; ++l) {
     const LayerW &w = enc->layers[l];
+    const bool last = prune && l + 1 == L;
     rc = site_ln(enc, s, x, nullptr, MX_F32, w.ln[0], w.ln[1], M, nullptr, w.ias[SITE_QKV]);
     if (!rc)
       rc = site_gemm(enc, s, w, SITE_QKV, enc->work.xb, M, d, 3 * d, MX_EPI_NONE, nullptr, enc->work.qkv,
                      MX_BF16);
-    if (!rc) rc = attn_l(enc, s, B, S, mask, kvl);
-    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.ctxb, MX_BF16, M, d, w.ias[SITE_AO]);
-    if (!rc) rc = site_gemm(enc, s, w, SITE_AO, enc->work.ctxb, M, d, d, MX_EPI_NONE, x, x, MX_F32);
-    if (!rc) rc = site_ln(enc, s, x, nullptr, MX_F32, w.ln[2], w.ln[3], M, nullptr, w.ias[SITE_UP]);
+    if (!rc) rc = attn_l(enc, s, B, S, mask, kvl, nullptr, last ? 1 : 0);
+    // the rows the rest of the layer runs over
+    int64_t Mr = M;
+    float *xr = x;
+    const uint16_t *ctx = enc->work.ctxb;
+    if (!rc && last) {
+      Bracket br(enc, s->stream, CAT_OTHER);
+      const hipError_t e =
+          mxk::gather_cls(x, enc->work.ctxb, nullptr, B, S, d, xc, enc->work.xb, s->stream);
+      if (e != hipSuccess) rc = hip_fail(e, "CLS row gather");
+      Mr = B;
+      xr = xc;
+      ctx = enc->work.xb;
+    }
+    if (!rc && enc->i8) rc = quant_l(enc, s, ctx, MX_BF16, Mr, d, w.ias[SITE_AO]);
+    if (!rc) rc = site_gemm(enc, s, w, SITE_AO, ctx, Mr, d, d, MX_EPI_NONE, xr, xr, MX_F32);
+    if (!rc) rc = site_ln(enc, s, xr, nullptr, MX_F32, w.ln[2], w.ln[3], Mr, nullptr, w.ias[SITE_UP]);
     // int8: FFN-up's activation in fp32 up to its quantiser, as the dequantise
     // -> GELU -> quantise_a_int8 sequence keeps it (npu_ops.cpp:334-361)
     if (!rc)
-      rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, M, d, f, epi, nullptr, enc->work.up,
+      rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, Mr, d, f, epi, nullptr, enc->work.up,
                      enc->i8 ? MX_F32 : MX_BF16);
-    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.up, MX_F32, M, f, w.ias[SITE_DOWN]);
-    if (!rc) rc = site_gemm(enc, s, w, SITE_DOWN, enc->work.up, M, f, d, MX_EPI_NONE, x, x, MX_F32);
+    if (!rc && enc->i8) rc = quant_l(enc, s, enc->work.up, MX_F32, Mr, f, w.ias[SITE_DOWN]);
+    if (!rc) rc = site_gemm(enc, s, w, SITE_DOWN, enc->work.up, Mr, f, d, MX_EPI_NONE, xr, xr, MX_F32);
   }
-  if (!rc) rc = ln_l(enc, s, x, MX_F32, nullptr, MX_F32, enc->fin_ln[0], enc->fin_ln[1], M, x, nullptr);
+  const bool pruned = prune && L > 0;
+  float *xf = pruned ? xc : x;
+  if (!rc)
+    rc = ln_l(enc, s, xf, MX_F32, nullptr, MX_F32, enc->fin_ln[0], enc->fin_ln[1],
+              pruned ? B : M, xf, nullptr);
+  if (!rc && pruned) *cls_rows = xc;
   return rc;
 }
 
@@ -1490,11 +1518,15 @@ int mx_encoder_vit(mx_encoder *enc, mx_stream *s, const float *pixels, int64_t B
                                            (int)np, (int)d, x, s->stream);
     if (e != hipSuccess) return hip_fail(e, "vit assemble launch");
   }
-  rc = run_preln(enc, s, x, nullptr, nullptr, B, S);
+  // Without a hidden state to return, only the CLS rows reach the head.
+  float *cls_rows = nullptr;
+  rc = run_preln(enc, s, x, nullptr, nullptr, B, S, hidden ? nullptr : &cls_rows);
   if (rc) return rc;
   {
     Bracket br(enc, s->stream, CAT_OTHER);
-    const hipError_t e = mxk::gather_rows_bf16(x, S * d, B, (int)d, enc->f_cls, s->stream);
+    const hipError_t e =
+        cls_rows ? mxk::gather_rows_bf16(cls_rows, d, B, (int)d, enc->f_cls, s->stream)
+                 : mxk::gather_rows_bf16(x, S * d, B, (int)d, enc->f_cls, s->stream);
     if (e != hipSuccess) return hip_fail(e, "cls gather launch");
   }
   rc = front_gemm(enc, s, enc->f_cls, d, B, d, enc->head_w, dd.labels, enc->head_b, MX_EPI_NONE,

@@ -198,6 +198,31 @@ def oracle_vit(orc, m, px):
     return logits, x
 
 
+def test_vit_cls_pruning_is_bitwise(ctx):
+    """Without a hidden state to return, mx_encoder_vit runs the last layer's
+    attention for the CLS query only and its attention-out, FFN and the final
+    LayerNorm over the CLS rows (the rows the head reads): the logits equal
+    those of the unpruned stack, and of a call that asks for the hidden state,
+    bit for bit."""
+    m = synth.make_model("vit_base", layers=2, ln_random=True)
+    B = 8
+    px = synth.make_pixels(m, batch=B)
+    enc = mxenc.Encoder(ctx, m)
+    d_px = ctx.put(px)
+    out = []
+    for prune, with_hidden in ((True, False), (False, False), (True, True)):
+        enc.set_cls_pruning(prune)
+        logits = ctx.empty((B, m["labels"]), np.float32)
+        hid = ctx.empty((B * m["seq"], m["hidden"]), np.float32) if with_hidden else None
+        enc.vit(d_px, B, logits, hid)
+        out.append(logits.host())
+    enc.set_cls_pruning(True)
+    enc.close()
+    assert np.all(np.isfinite(out[0]))
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
+    assert np.array_equal(out[0].view(np.uint32), out[2].view(np.uint32))
+
+
 def test_vit_full_config(ctx, orc):
     """ViT-B/16 at 224x224, the configuration's batch of 256 images: patch
     embedding, CLS + positions, 12 pre-LN layers over 197 tokens, final LN and
