@@ -155,14 +155,15 @@ def test_partial_placement_refused(ctx):
 def test_bge_large_full_batch_subset_checked(ctx, orc):
     """bge-large geometry at its full shape (batch 128 x seq 512, 24 layers,
     d 1024, 16 heads, every sequence full length): the whole batch on the GPU,
-    two sequences rerun on the host path."""
+    nine sequences spread over it (every 16th and the last) rerun on the host
+    path."""
     m = synth.make_model("bge_large")
     ids, am, _ = synth.make_text_inputs(m)
     enc = mxenc.Encoder(ctx, m)
     got = gpu_embed(ctx, enc, ids, am)
     enc.close()
     assert np.all(np.isfinite(got))
-    pick = [0, 77]
+    pick = list(range(0, ids.shape[0], 16)) + [ids.shape[0] - 1]
     want, _ = oracle_embed(orc, m, np.ascontiguousarray(ids[pick]), np.ascontiguousarray(am[pick]))
     cos = cosines(got[pick], want)
     assert np.min(cos) >= COS_MIN, cos
@@ -226,8 +227,8 @@ def test_vit_cls_pruning_is_bitwise(ctx):
 def test_vit_full_config(ctx, orc):
     """ViT-B/16 at 224x224, the configuration's batch of 256 images: patch
     embedding, CLS + positions, 12 pre-LN layers over 197 tokens, final LN and
-    the 1000-way head, all on the GPU; two images rerun on the host path
-    (hidden state per token and the logits)."""
+    the 1000-way head, all on the GPU; every eighth image and the last (33)
+    rerun on the host path (hidden state per token and the logits)."""
     m = synth.make_model("vit_base", ln_random=True)
     B, d, S = m["batch"], m["hidden"], m["seq"]
     px = synth.make_pixels(m)
@@ -239,7 +240,7 @@ def test_vit_full_config(ctx, orc):
     lg, h = logits.host(), hid.host()
     enc.close()
     assert np.all(np.isfinite(lg)) and np.all(np.isfinite(h))
-    pick = [0, B - 1]
+    pick = list(range(0, B, 8)) + [B - 1]
     want_lg, want_x = oracle_vit(orc, m, np.ascontiguousarray(px[pick]))
     for i, b in enumerate(pick):
         cos = cosines(h[b * S:(b + 1) * S], want_x[i * S:(i + 1) * S])
@@ -265,8 +266,9 @@ def oracle_whisper(orc, m, mel):
 def test_whisper_full_config(ctx, orc):
     """Whisper-large-v3 encoder geometry, the configuration's 8 x 128 mels x
     3000 frames: conv1 + GELU, conv2 (stride 2) + GELU, positions, 32 pre-LN
-    layers over 1500 positions (unmasked) and the final LN on the GPU; one
-    sample rerun on the host path, every one of its 1500 rows checked."""
+    layers over 1500 positions (unmasked) and the final LN on the GPU; the
+    first and last samples rerun on the host path, every one of their 1500
+    rows checked."""
     m = synth.make_model("whisper_enc", ln_random=True)
     B, d, S = m["batch"], m["hidden"], m["seq"]
     mel = synth.make_mel(m)
@@ -277,6 +279,8 @@ def test_whisper_full_config(ctx, orc):
     h = hid.host()
     enc.close()
     assert np.all(np.isfinite(h))
-    want = oracle_whisper(orc, m, np.ascontiguousarray(mel[:1]))
-    cos = cosines(h[:S], want)
-    assert np.min(cos) >= COS_MIN, np.min(cos)
+    pick = [0, B - 1]
+    want = oracle_whisper(orc, m, np.ascontiguousarray(mel[pick]))
+    for i, b in enumerate(pick):
+        cos = cosines(h[b * S:(b + 1) * S], want[i * S:(i + 1) * S])
+        assert np.min(cos) >= COS_MIN, (b, np.min(cos))
