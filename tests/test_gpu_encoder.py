@@ -107,6 +107,25 @@ def test_streams_agree_bitwise(ctx):
     enc.close()
 
 
+@pytest.mark.parametrize("S,valid", [(512, 512), (72, 41), (8, 1)])
+def test_bge_base_single_sequence(ctx, orc, S, valid):
+    """One sequence (batch 1) at the full length, with padding at a length
+    that fills no tile, and of a single token: a one-row-tile GEMM, a partly
+    filled key tile, attention over one key. (The host path's sequence length
+    is a multiple of 8, as the reference's is.)"""
+    m = synth.make_model("bge_base", layers=2, ln_random=True)
+    ids, am, _ = synth.make_text_inputs(m, batch=1, seq=S)
+    am[:] = 0.0
+    am[0, :valid] = 1.0
+    ids[0, valid:] = 0
+    enc = mxenc.Encoder(ctx, m)
+    got = gpu_embed(ctx, enc, ids, am)
+    enc.close()
+    want, _ = oracle_embed(orc, m, ids, am)
+    cos = cosines(got, want)
+    assert np.min(cos) >= COS_MIN, cos
+
+
 def _preln_case(ctx, orc, name, B, layers, eps):
     m = synth.make_model(name, layers=layers, ln_random=True)
     S, d = m["seq"], m["hidden"]

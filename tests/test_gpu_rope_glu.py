@@ -137,6 +137,24 @@ def test_rope_gated_stack_vs_oracle(ctx, orc, name):
 
 
 @pytest.mark.parametrize("name", ["nomic", "gte"])
+def test_rope_gated_bench_geometry(ctx, orc, name):
+    """The arch at its benchmark shape (12 layers at bge-base width, batch 64 x
+    seq 512, valid lengths U[64, 512]): the whole batch on the GPU, every
+    eighth sequence and the last rerun on the host path."""
+    m = synth.make_model(name, ln_random=True)
+    ids, am, _ = synth.make_text_inputs(m)
+    enc = mxenc.Encoder(ctx, m)
+    got = _gpu_embed(ctx, enc, ids, am)
+    enc.close()
+    assert np.all(np.isfinite(got))
+    pick = list(range(0, ids.shape[0], 8)) + [ids.shape[0] - 1]
+    want = _oracle_embed(orc, m, np.ascontiguousarray(ids[pick]),
+                         np.ascontiguousarray(am[pick]))
+    cos = _cos(got[pick], want)
+    assert cos.min() >= 0.9999, cos
+
+
+@pytest.mark.parametrize("name", ["nomic", "gte"])
 def test_rope_gated_container_is_bitwise_the_set_encoder(tmp_path, ctx, name):
     m = synth.make_model(name, layers=2, ln_random=True)
     path = str(tmp_path / f"{name}.npue")
