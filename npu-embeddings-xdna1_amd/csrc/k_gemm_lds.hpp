@@ -378,6 +378,8 @@ __device__ __forceinline__ void gemm_lds_body(
     }
   };
 
+  constexpr bool SAME_LOADS_P = Cfg::LOADS_HI == Cfg::LOADS_LO;
+  static_assert(Cfg::LOADS_HI * (NS - 1) < 64, "vmcnt holds at most 63");
   acc_t acc[TN][TM];
 #pragma unroll
   for (int j = 0; j < TN; ++j)
@@ -795,11 +797,22 @@ __device__ __forceinline__ void gemm_lds_body(
     }
   };
 
-  // Prologue: slabs 0 .. NS-1 in flight; k-step 0 of slab 0 into set 0.
+  // Prologue: slabs 0 .. NS-1 in flight; k-step 0 of slab 0 into set 0. Only
+  // slab 0 is waited for here (with the tile's epilogue vectors, issued with
+  // it): this wave's loads of slabs 1 .. NS-1 -- all in the first tile, which
+  // has at least NS slabs, so no epilogue vectors among them -- stay in
+  // flight, and the main loop waits for slab 1 before its first barrier.
 #pragma unroll
   for (int s = 0; s < NS; ++s)
     if (s < nslab) issue();
-  wait_vmcnt<0>();
+  if (nslab >= NS) {
+    if (SAME_LOADS_P || wave < Cfg::NHI)
+      wait_vmcnt<Cfg::LOADS_HI *(NS - 1)>();
+    else
+      wait_vmcnt<Cfg::LOADS_LO *(NS - 1)>();
+  } else {
+    wait_vmcnt<0>();
+  }
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   read_set(0, pos[0], fa0, fb0);
