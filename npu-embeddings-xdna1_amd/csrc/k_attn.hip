@@ -132,17 +132,7 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
   const int qend = lim < q_lim ? lim : q_lim;
   const bool live = qb * BQ + wave * 32 < qend;
 
-  // Q fragments (B operand of S^T = K Q^T), waited for before the loop.
   const int q = qb * BQ + wave * 32 + li;
-  bf16x8 qf[NKK];
-#pragma unroll
-  for (int kk = 0; kk < NKK; ++kk) {
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (q < lim) v = *(const uint4 *)(base + (int64_t)q * ldq + h * HD + kk * 16 + g * 8);
-    qf[kk] = __builtin_bit_cast(bf16x8, v);
-  }
-#pragma unroll
-  for (int kk = 0; kk < NKK; ++kk) asm volatile("" ::"v"(qf[kk]));
 
   // Key tile t -> slot t % NSL: wave w moves the K and V rows of 1 KB pieces
   // p = w, w + NW, ... (PR rows each: lane l fills row PR p + l / CPR,
@@ -210,6 +200,18 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
   const int ntile = (kvl + BKV - 1) / BKV;
   issue(0);
   if (ntile > 1) issue(1);
+  // Q fragments (B operand of S^T = K Q^T), loaded after the first key tiles'
+  // loads are issued so the two latencies overlap, and waited for before the
+  // loop (the wait drains every load of this wave, tile 1's included).
+  bf16x8 qf[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) {
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (q < lim) v = *(const uint4 *)(base + (int64_t)q * ldq + h * HD + kk * 16 + g * 8);
+    qf[kk] = __builtin_bit_cast(bf16x8, v);
+  }
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) asm volatile("" ::"v"(qf[kk]));
   wait_next(ntile > 1);
   __syncthreads();
   for (int t = 0; t < ntile; ++t) {
