@@ -247,6 +247,14 @@ __global__ __launch_bounds__(256) void layernorm_wave4_k(
   const int lane = threadIdx.x & 63;
   const int64_t row = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
   if (row >= rows) return;
+  // gamma and beta are read with the row, so their latency runs under its
+  // loads instead of after the two reductions.
+  float4 gm[NQ], bt[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    gm[i] = *(const float4 *)(gamma + i * 256 + lane * 4);
+    bt[i] = *(const float4 *)(beta + i * 256 + lane * 4);
+  }
   float4 v[NQ];
 #pragma unroll
   for (int i = 0; i < NQ; ++i) {
@@ -278,13 +286,11 @@ __global__ __launch_bounds__(256) void layernorm_wave4_k(
 #pragma unroll
   for (int i = 0; i < NQ; ++i) {
     const int c = i * 256 + lane * 4;
-    const float4 gm = *(const float4 *)(gamma + c);
-    const float4 bt = *(const float4 *)(beta + c);
     float4 r;
-    r.x = __builtin_fmaf((v[i].x - mean) * is, gm.x, bt.x);
-    r.y = __builtin_fmaf((v[i].y - mean) * is, gm.y, bt.y);
-    r.z = __builtin_fmaf((v[i].z - mean) * is, gm.z, bt.z);
-    r.w = __builtin_fmaf((v[i].w - mean) * is, gm.w, bt.w);
+    r.x = __builtin_fmaf((v[i].x - mean) * is, gm[i].x, bt[i].x);
+    r.y = __builtin_fmaf((v[i].y - mean) * is, gm[i].y, bt[i].y);
+    r.z = __builtin_fmaf((v[i].z - mean) * is, gm[i].z, bt[i].z);
+    r.w = __builtin_fmaf((v[i].w - mean) * is, gm[i].w, bt[i].w);
     const int64_t off = row * cols + c;
     if (out_f32) *(float4 *)(out_f32 + off) = r;
     if (out_bf16) *(uint2 *)(out_bf16 + off) = make_uint2(pack_bf2(r.x, r.y), pack_bf2(r.z, r.w));
