@@ -101,6 +101,18 @@ __global__ __launch_bounds__(256) void layernorm_quant_k(
   const int lane = threadIdx.x & 63;
   const int64_t row = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
   if (row >= rows) return;
+  // gamma, beta and the next GEMM's ias are read with the row, so their
+  // latency runs under its loads instead of after the two reductions.
+  float4 gm[NQ], bt[NQ], ia[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int c = i * 256 + lane * 4;
+    if (c < cols) {
+      gm[i] = *(const float4 *)(gamma + c);
+      bt[i] = *(const float4 *)(beta + c);
+      ia[i] = *(const float4 *)(ias + c);
+    }
+  }
   float4 v[NQ];
   float s = 0.0f;
 #pragma unroll
@@ -139,15 +151,13 @@ __global__ __launch_bounds__(256) void layernorm_quant_k(
   for (int i = 0; i < NQ; ++i) {
     const int c = i * 256 + lane * 4;
     if (c < cols) {
-      const float4 gm = *(const float4 *)(gamma + c);
-      const float4 bt = *(const float4 *)(beta + c);
       float4 r;
-      r.x = __builtin_fmaf((v[i].x - mean) * is, gm.x, bt.x);
-      r.y = __builtin_fmaf((v[i].y - mean) * is, gm.y, bt.y);
-      r.z = __builtin_fmaf((v[i].z - mean) * is, gm.z, bt.z);
-      r.w = __builtin_fmaf((v[i].w - mean) * is, gm.w, bt.w);
+      r.x = __builtin_fmaf((v[i].x - mean) * is, gm[i].x, bt[i].x);
+      r.y = __builtin_fmaf((v[i].y - mean) * is, gm[i].y, bt[i].y);
+      r.z = __builtin_fmaf((v[i].z - mean) * is, gm[i].z, bt[i].z);
+      r.w = __builtin_fmaf((v[i].w - mean) * is, gm[i].w, bt[i].w);
       if (out_f32) *(float4 *)(out_f32 + row * cols + c) = r;
-      v[i] = mul4(r, *(const float4 *)(ias + c));
+      v[i] = mul4(r, ia[i]);
       mx = absmax4(mx, v[i]);
     }
   }
