@@ -516,12 +516,21 @@ __global__ __launch_bounds__(256) void softmax_vec_k(void *x, int64_t rows, int6
   const int64_t row0 = (blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6)) * NR;
   if (row0 >= rows) return;
   float v[NR][NC][8];
+  // The mask entries are read with the rows (added to them right away), so
+  // their latency runs under the row loads instead of after them.
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     const int64_t row = row0 + r;
+    const float *mk = mask && row < rows ? mask + (row / rpm) * cols : nullptr;
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const int64_t c0 = 8 * (lane + 64 * (int64_t)i);
+      float4 ma = make_float4(0.0f, 0.0f, 0.0f, 0.0f), mb = ma;
+      if (mk && c0 < cols) {
+        ma = *(const float4 *)(mk + c0);
+        mb = *(const float4 *)(mk + c0 + 4);
+      }
+      const float mm[8] = {ma.x, ma.y, ma.z, ma.w, mb.x, mb.y, mb.z, mb.w};
       if (row < rows && c0 < cols) {
         if (BF) {
           const uint4 w = *(const uint4 *)((const uint16_t *)x + row * stride + c0);
@@ -537,6 +546,10 @@ __global__ __launch_bounds__(256) void softmax_vec_k(void *x, int64_t rows, int6
           v[r][i][0] = a.x, v[r][i][1] = a.y, v[r][i][2] = a.z, v[r][i][3] = a.w;
           v[r][i][4] = b.x, v[r][i][5] = b.y, v[r][i][6] = b.z, v[r][i][7] = b.w;
         }
+        if (mk) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[r][i][e] += mm[e];
+        }
       }
     }
   }
@@ -544,18 +557,11 @@ __global__ __launch_bounds__(256) void softmax_vec_k(void *x, int64_t rows, int6
   for (int r = 0; r < NR; ++r) {
     const int64_t row = row0 + r;
     if (row >= rows) break;
-    const float *mk = mask ? mask + (row / rpm) * cols : nullptr;
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const int64_t c0 = 8 * (lane + 64 * (int64_t)i);
       if (c0 < cols) {
-        if (mk) {
-          const float4 a = *(const float4 *)(mk + c0), b = *(const float4 *)(mk + c0 + 4);
-          const float mm[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) v[r][i][e] += mm[e];
-        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) m = fmaxf(m, v[r][i][e]);
       }
