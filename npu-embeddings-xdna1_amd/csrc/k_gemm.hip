@@ -208,7 +208,13 @@ GemmPath pick(const GemmArgs &a) {
   int t = gemm_lds_tile(a.M, a.N, deep);
   if (t == 1 && a.epilogue >= EPI_GLU_SILU) t = 0;  // 96-column waves cannot pair blocks
   if (t == 0 && deep) return PATH_LDS_256x256_DEEP;
-  if (t == 3 && deep && a.c_bf16 && !a.residual) return PATH_LDS_128x128_DEEP;
+  // The 128 x 128 tile on 128-byte slabs keeps one slab in flight ahead, the
+  // 64-byte form three: a launch of a few tiles per XCD (the CLS-pruned last
+  // layer's 64-row GEMMs) waits on every slab's load and runs faster with
+  // three ahead. Both run the same MFMA chain over K for every element.
+  if (t == 3 && deep && a.c_bf16 && !a.residual &&
+      ((a.M + 127) / 128) * ((a.N + 127) / 128) * 8 > cu_count())
+    return PATH_LDS_128x128_DEEP;
   return paths[t];
 }
 
