@@ -695,6 +695,7 @@ __global__ __launch_bounds__(256) void pack_plan_k(const int32_t *__restrict__ k
   }
 }
 
+template <bool V4>
 __global__ __launch_bounds__(256) void embed_sum_packed_k(
     const int32_t *__restrict__ ids, int64_t rows, int64_t S, int64_t d,
     const float *__restrict__ word, int64_t vocab, const float *__restrict__ pos,
@@ -716,7 +717,16 @@ __global__ __launch_bounds__(256) void embed_sum_packed_k(
   }
   const float *wv = word + (int64_t)id * d;
   const float *pv = pos + s * d;
-  for (int64_t c = lane; c < d; c += 64) emb[p * d + c] = (wv[c] + pv[c]) + type0[c];
+  if (V4) {  // d % 4 == 0 and 16-byte aligned rows: four columns per lane
+    for (int64_t c = 4 * lane; c < d; c += 256) {
+      const float4 w = *(const float4 *)(wv + c), q = *(const float4 *)(pv + c);
+      const float4 t = *(const float4 *)(type0 + c);
+      *(float4 *)(emb + p * d + c) =
+          make_float4((w.x + q.x) + t.x, (w.y + q.y) + t.y, (w.z + q.z) + t.z, (w.w + q.w) + t.w);
+    }
+  } else {
+    for (int64_t c = lane; c < d; c += 64) emb[p * d + c] = (wv[c] + pv[c]) + type0[c];
+  }
 }
 
 // ---- pooling (app_state.hpp:335-374), bit-exact with the host form ----------
@@ -1065,8 +1075,14 @@ hipError_t embed_sum_packed(const int32_t *ids, int64_t B, int64_t S, int64_t d,
                             const float *type0, const int32_t *kv_len, const int32_t *seq_start,
                             float *emb, int32_t *row_pos, int *err, hipStream_t s) {
   const int64_t rows = B * S;
-  embed_sum_packed_k<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(
-      ids, rows, S, d, word, vocab, pos, type0, kv_len, seq_start, emb, row_pos, err);
+  const bool v4 = d % 4 == 0 && (uintptr_t)word % 16 == 0 && (uintptr_t)pos % 16 == 0 &&
+                  (uintptr_t)type0 % 16 == 0 && (uintptr_t)emb % 16 == 0;
+  if (v4)
+    embed_sum_packed_k<true><<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(
+        ids, rows, S, d, word, vocab, pos, type0, kv_len, seq_start, emb, row_pos, err);
+  else
+    embed_sum_packed_k<false><<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(
+        ids, rows, S, d, word, vocab, pos, type0, kv_len, seq_start, emb, row_pos, err);
   return hipGetLastError();
 }
 
