@@ -3,8 +3,7 @@
     python npu-embeddings-xdna1_amd/build.py [--jobs N]
 
 Every library source under csrc/ is compiled with hipcc for gfx950 only and
-linked into _build/libmx_encoder.so beside this file; csrc/probe_mfma_clock.hip
-becomes the measurement program _build/probe_mfma_clock. Packed-fp32 instructions are
+linked into _build/libmx_encoder.so beside this file. Packed-fp32 instructions are
 disabled for all device code (-packed-fp32-ops); hipcc's host pass warns that
 it does not know that feature, which is harmless.
 """
@@ -60,7 +59,6 @@ def build(jobs=None, verbose=False):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
-    build_probe()
     build_abi_check()
     return LIB
 
@@ -81,22 +79,6 @@ def build_abi_check():
         raise RuntimeError("g++ failed on abi_check.cpp:\n" + r.stdout + r.stderr)
     os.replace(ABI_CHECK + ".tmp", ABI_CHECK)
     return ABI_CHECK
-
-
-PROBE = os.path.join(OUT, "probe_mfma_clock")
-
-
-def build_probe():
-    """The clock / MFMA / LDS measurement program (csrc/probe_mfma_clock.hip),
-    an executable beside the library that also calls it through the C ABI."""
-    cmd = [HIPCC] + [f for f in FLAGS if f != "-fPIC"] + [
-        os.path.join(CSRC, "probe_mfma_clock.hip"), "-o", PROBE + ".tmp", "-L", OUT,
-        "-lmx_encoder", "-Wl,-rpath,$ORIGIN"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError("hipcc failed on probe_mfma_clock.hip:\n" + r.stdout + r.stderr)
-    os.replace(PROBE + ".tmp", PROBE)
-    return PROBE
 
 
 if __name__ == "__main__":
