@@ -444,26 +444,47 @@ int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids,
  * the library runs on holds from mx_create until the process ends. */
 #define MX_STATIC_SCRATCH_BYTES ((size_t)128 << 20)
 /* mx_encoder_embed without allocating: no counterpart in the reference. For
- * callers that cannot allocate device memory (code under HIP graph capture,
- * tight serving loops, harnesses that forbid hipMalloc). The same inputs,
- * output and refusals as mx_encoder_embed, bit for bit the same pooled rows;
- * its workspace is carved from the library's static scratch
- * (MX_STATIC_SCRATCH_BYTES per GPU) instead of the encoder's own. The
- * workspace is, in 256-byte pieces, the mask [B, S] fp32, kv_len [B] and the
- * plan [2B + 1] int32, then per computed row (the packed row count with
- * token packing, else B*S) its position int32, xb / ctx / proj bf16 [hidden],
- * qkv bf16 [3 hidden], up bf16 [ffn] (2 ffn gated, plus the gated product
- * [ffn]), emb fp32 [hidden] and on the int8 datapath xq int8 [max(hidden,
- * ffn)] and its scale fp32 (there up, the gated product and proj are fp32);
- * a batch whose workspace exceeds the scratch is
- * refused (MX_E_INVALID, naming both sizes). Also refused: timing on
- * (its events are created on demand) and an encoder whose device tables are
- * stale (MX_E_STATE: call mx_encoder_ready after the last tensor is set;
+ * callers that cannot allocate device memory (tight serving loops, harnesses
+ * that forbid hipMalloc). The call is allocation-free and host-synchronous: it
+ * reads the packed row count and the refusal flag back, so it cannot run
+ * under HIP graph capture (a capturing stream is refused, MX_E_STATE, before
+ * any launch or copy). The same inputs, output and refusals as
+ * mx_encoder_embed, bit for bit the same pooled rows; its workspace is carved
+ * from the library's static scratch (MX_STATIC_SCRATCH_BYTES per GPU) instead
+ * of the encoder's own. The workspace is, in 256-byte pieces, the mask [B, S]
+ * fp32, kv_len [B] and the plan [2B + 1] int32, then per computed row (the
+ * packed row count with token packing, else B*S) its position int32, xb / ctx
+ * / proj bf16 [hidden], qkv bf16 [3 hidden], up bf16 [ffn] (2 ffn gated, plus
+ * the gated product [ffn]), emb fp32 [hidden] and on the int8 datapath xq
+ * int8 [max(hidden, ffn)] and its scale fp32 (there up, the gated product and
+ * proj are fp32); a batch whose workspace exceeds the scratch is refused
+ * (MX_E_INVALID, naming both sizes). Also refused: timing on (its events are
+ * created on demand) and an encoder whose device tables are stale
+ * (MX_E_STATE: call mx_encoder_ready after the last tensor is set;
  * mx_encoder_from_npue and mx_encoder_clone return ready encoders). Every
- * call on one GPU shares that GPU's scratch: calls that overlap on one GPU,
- * from any encoder or stream, race. Synchronises s. */
+ * call on one GPU shares that GPU's scratch, so a call holds the GPU's guard
+ * (mx_static_guard_hold) from its first use of the scratch until it has
+ * synchronised s: a call that overlaps it on the same GPU, from any encoder,
+ * stream or thread, is refused (MX_E_STATE, naming the overlap) instead of
+ * racing. Synchronises s. */
 int mx_encoder_embed_static(mx_encoder *enc, mx_stream *s, const int32_t *ids,
                             const float *attn_mask, int64_t B, int64_t S, float *out);
+
+/* The per-GPU guard of the static scratch (no counterpart in the reference;
+ * for callers that cannot allocate and serialise their own use of the
+ * scratch, and for tests of the overlap refusal). mx_static_guard_hold takes
+ * device's guard as an mx_encoder_embed_static call does for its duration:
+ * MX_E_STATE, naming the overlap, if a call or a hold already has it. While it
+ * is held, mx_encoder_embed_static on that device is refused the same way.
+ * mx_static_guard_release gives it back (MX_E_STATE if it is not held).
+ * Host-only: neither touches the GPU. */
+int mx_static_guard_hold(int device);
+int mx_static_guard_release(int device);
+
+/* How many device allocations (hipMalloc calls) the library has made in this
+ * process: contexts' streams, staged weights, encoder workspaces, mx_alloc.
+ * mx_encoder_embed_static adds none. Host-only. */
+int64_t mx_device_allocations(void);
 
 /* Token packing in mx_encoder_embed (on by default): the only rows of a
  * sequence that reach its pooled row are those before kv_len (every later

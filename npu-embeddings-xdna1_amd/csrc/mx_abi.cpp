@@ -52,7 +52,7 @@ int stage_panel(mx_ctx *ctx, const void *kn_host, int dtype, int64_t K, int64_t 
   int rc = use_device(ctx);
   if (rc) return rc;
   void *p = nullptr;
-  hipError_t e = hipMalloc(&p, panel.size() * 2);
+  hipError_t e = dev_malloc((void **)&p, panel.size() * 2);
   if (e != hipSuccess) return hip_fail(e, "stage_weight: hipMalloc");
   e = hipMemcpy(p, panel.data(), panel.size() * 2, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
@@ -94,9 +94,9 @@ int stage_tiled_panel(mx_ctx *ctx, const uint16_t *panel_host, int64_t K, int64_
   if (rc) return rc;
   const size_t bytes = static_cast<size_t>(K) * N * 2;
   void *tiled = nullptr, *wt = nullptr;
-  hipError_t e = hipMalloc(&tiled, bytes);
+  hipError_t e = dev_malloc((void **)&tiled, bytes);
   if (e != hipSuccess) return hip_fail(e, "stage_weight_panel: hipMalloc");
-  e = hipMalloc(&wt, bytes);
+  e = dev_malloc((void **)&wt, bytes);
   if (e != hipSuccess) {
     (void)hipFree(tiled);
     return hip_fail(e, "stage_weight_panel: hipMalloc");
@@ -319,7 +319,7 @@ int mx_stream_create(mx_ctx *ctx, mx_stream **out) {
     delete s;
     return hip_fail(e, "hipStreamCreate");
   }
-  e = hipMalloc(&s->err_dev, sizeof(int));
+  e = dev_malloc((void **)&s->err_dev, sizeof(int));
   if (e == hipSuccess) e = hipMemset(s->err_dev, 0, sizeof(int));
   if (e != hipSuccess) {
     (void)hipStreamDestroy(s->stream);
@@ -352,7 +352,7 @@ int mx_alloc(mx_ctx *ctx, size_t bytes, void **dev) {
   if (!dev) return fail(MX_E_INVALID, "mx_alloc: null out");
   int rc = use_device(ctx);
   if (rc) return rc;
-  const hipError_t e = hipMalloc(dev, bytes ? bytes : 1);
+  const hipError_t e = dev_malloc(dev, bytes ? bytes : 1);
   return e == hipSuccess ? MX_OK : hip_fail(e, "hipMalloc");
 }
 

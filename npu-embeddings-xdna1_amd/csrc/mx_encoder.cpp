@@ -145,7 +145,7 @@ void free_dev(T *&p) {
 }
 
 int dev_alloc(void **p, size_t bytes, const char *what) {
-  const hipError_t e = hipMalloc(p, bytes);
+  const hipError_t e = dev_malloc(p, bytes);
   return e == hipSuccess ? MX_OK : hip_fail(e, what);
 }
 
@@ -706,7 +706,7 @@ int stage_i8_panel(mx_ctx *ctx, const int8_t *kn, int64_t K, int64_t N, int8_t *
     for (int64_t n = 0; n < N; ++n)
       panel[static_cast<size_t>(n) * K + k] = kn[static_cast<size_t>(k) * N + n];
   void *p = nullptr;
-  hipError_t e = hipMalloc(&p, panel.size());
+  hipError_t e = dev_malloc((void **)&p, panel.size());
   if (e == hipSuccess) e = hipMemcpy(p, panel.data(), panel.size(), hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     if (p) (void)hipFree(p);
@@ -1470,17 +1470,40 @@ int mx_encoder_embed_static(mx_encoder *enc, mx_stream *s, const int32_t *ids,
   if (enc->timing)
     return fail(MX_E_STATE, "encoder_embed_static: timing is on (its events are created on "
                             "demand); mx_encoder_set_timing(enc, 0) first");
+  // The call reads the packed row count and the refusal flag back with stream
+  // synchronisations, which a capturing stream does not allow: refused before
+  // any launch or copy.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s->stream, &cap);
+  if (e != hipSuccess) return hip_fail(e, "encoder_embed_static: hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(MX_E_STATE, "encoder_embed_static: the stream is capturing a graph; this call "
+                            "synchronises its stream and cannot be captured");
   void *scratch = nullptr;
   rc = use_device(enc->ctx);
   if (!rc) rc = static_scratch(enc->ctx->device, &scratch);
   if (!rc) rc = check_placement();
   if (!rc) rc = check_prepared(enc, S);
   if (rc) return rc;
+  // One call at a time per GPU: the guard is held until the call has
+  // synchronised its stream (embed_body ends with that), so the scratch is
+  // idle again when it is released.
+  const int device = enc->ctx->device;
+  rc = static_guard_enter(device, "encoder_embed_static");
+  if (rc) return rc;
   Carver carve{static_cast<uint8_t *>(scratch), static_scratch_bytes()};
   const Work own = enc->work;  // the encoder's workspace, back in place on return
   enc->work = Work{};
   rc = embed_body(enc, s, ids, attn_mask, B, S, out, &carve);
   enc->work = own;
+  if (rc) {
+    // A failed call may leave work queued that uses the scratch: drain the
+    // stream before the guard is given back.
+    const std::string msg = mx_last_error();
+    (void)hipStreamSynchronize(s->stream);
+    set_error(msg);
+  }
+  static_guard_leave(device);
   return rc;
 }
 

@@ -1,10 +1,12 @@
 // mx_host.cpp -- the host-only part of the C ABI: the thread-local error
-// message every refusal sets, and the --npu-ops placement registry
-// (runtime/include/common/npu_ops_flag.hpp:75-268). No HIP here: the
+// message every refusal sets, the --npu-ops placement registry
+// (runtime/include/common/npu_ops_flag.hpp:75-268), the per-device guard of
+// the static scratch and the device-allocation count. No HIP here: the
 // container reader (mx_npue.cpp) and this file build with any C++17 compiler,
 // which is how the sanitizer build of the untrusted-input paths compiles them.
 #include "mx_host.hpp"
 
+#include <atomic>
 #include <cctype>
 #include <cstring>
 #include <mutex>
@@ -59,6 +61,35 @@ std::set<std::string> placed_ops() {
   std::lock_guard<std::mutex> lk(g_ops_mu);
   return g_ops;
 }
+
+// ---- the static scratch's per-device guard --------------------------------
+// mx_encoder_embed_static holds its device's entry for the whole call (every
+// such call is host-synchronous); a call that finds the entry held is refused
+// instead of racing on the shared scratch.
+
+static std::mutex g_static_mu;
+static std::set<int> g_static_held;
+
+int static_guard_enter(int device, const char *who) {
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  if (!g_static_held.insert(device).second)
+    return fail(MX_E_STATE, std::string(who) + ": the static scratch of device " +
+                                std::to_string(device) +
+                                " is in use by another call; calls that overlap on one GPU "
+                                "share it and are refused");
+  return MX_OK;
+}
+
+int static_guard_leave(int device) {
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  return g_static_held.erase(device) ? MX_OK : MX_E_STATE;
+}
+
+// ---- device allocations ----------------------------------------------------
+
+static std::atomic<int64_t> g_allocs{0};
+
+void count_device_allocation() { g_allocs.fetch_add(1, std::memory_order_relaxed); }
 
 }  // namespace mx
 
@@ -115,6 +146,23 @@ const char *mx_op_codes(void) {
   static const std::string s = codes_joined();
   return s.c_str();
 }
+
+int mx_static_guard_hold(int device) {
+  clear_error();
+  if (device < 0) return fail(MX_E_INVALID, "static_guard_hold: negative device");
+  return static_guard_enter(device, "static_guard_hold");
+}
+
+int mx_static_guard_release(int device) {
+  clear_error();
+  if (device < 0) return fail(MX_E_INVALID, "static_guard_release: negative device");
+  if (static_guard_leave(device))
+    return fail(MX_E_STATE, "static_guard_release: the static scratch of device " +
+                                std::to_string(device) + " is not held");
+  return MX_OK;
+}
+
+int64_t mx_device_allocations(void) { return g_allocs.load(std::memory_order_relaxed); }
 
 int mx_ops_check_flag(const char *flag) {
   clear_error();

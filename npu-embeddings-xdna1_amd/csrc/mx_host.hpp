@@ -17,6 +17,14 @@ void set_error(const std::string &msg);
 void clear_error();
 int fail(int code, const std::string &msg);
 
+// The static scratch's per-device guard (mx_encoder_embed_static): enter
+// refuses with MX_E_STATE, naming `who`, when a call on that device holds it.
+int static_guard_enter(int device, const char *who);
+int static_guard_leave(int device);
+
+// Every device allocation the library makes is counted (mx_device_allocations).
+void count_device_allocation();
+
 // The codes --npu-ops placed on the GPU (mx_ops_parse).
 std::set<std::string> placed_ops();
 

@@ -24,7 +24,7 @@ constexpr int64_t kMaxI8K = 2147483647LL / (127 * 127);
 template <typename T>
 int upload(const T *host, size_t count, T **dev, const char *what) {
   void *p = nullptr;
-  hipError_t e = hipMalloc(&p, count * sizeof(T));
+  hipError_t e = dev_malloc((void **)&p, count * sizeof(T));
   if (e != hipSuccess) return hip_fail(e, what);
   e = hipMemcpy(p, host, count * sizeof(T), hipMemcpyHostToDevice);
   if (e != hipSuccess) {
@@ -79,7 +79,7 @@ int stage_i8(mx_ctx *ctx, const int8_t *kn_host, const float *wscale_host,
     rc = upload(kn_host, n, &tiled, "stage_weight_i8: panel");
     if (!rc) {
       void *wq = nullptr;
-      hipError_t e = hipMalloc(&wq, n);
+      hipError_t e = dev_malloc((void **)&wq, n);
       if (e == hipSuccess) {
         op.wq = static_cast<int8_t *>(wq);
         e = mxk::untile_panel_i8(tiled, K, N, (int)tile_k, (int)tile_n, (int)mac_s, (int)mac_t,
@@ -140,7 +140,7 @@ int stage_i4(mx_ctx *ctx, const uint8_t *packed_host, const float *gscale_host, 
                        "stage_weight_panel_i4: gscale");
   if (!rc) {
     void *p = nullptr;
-    const hipError_t e = hipMalloc(&p, static_cast<size_t>(K) * N);
+    const hipError_t e = dev_malloc((void **)&p, static_cast<size_t>(K) * N);
     if (e != hipSuccess) rc = hip_fail(e, "stage_weight_panel_i4: hipMalloc");
     tiled = static_cast<int8_t *>(p);
   }
@@ -165,7 +165,7 @@ int stage_i4(mx_ctx *ctx, const uint8_t *packed_host, const float *gscale_host, 
   }
   if (!rc) {
     void *wq = nullptr;
-    hipError_t e = hipMalloc(&wq, static_cast<size_t>(K) * N);
+    hipError_t e = dev_malloc((void **)&wq, static_cast<size_t>(K) * N);
     if (e == hipSuccess) {
       op.wq = static_cast<int8_t *>(wq);
       e = mxk::untile_panel_i8(tiled, K, N, (int)tile_k, (int)tile_n, (int)mac_s, (int)mac_t,

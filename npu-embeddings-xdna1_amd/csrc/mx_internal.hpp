@@ -14,6 +14,13 @@ namespace mx {
 
 int hip_fail(hipError_t e, const char *what);
 
+// Every device allocation of the library goes through here, so that it is
+// counted (mx_device_allocations).
+inline hipError_t dev_malloc(void **p, size_t bytes) {
+  count_device_allocation();
+  return hipMalloc(p, bytes);
+}
+
 struct WeightSlot {
   uint16_t *wt = nullptr;  // [N, K] bf16 (a bf16 operand)
   int64_t K = 0, N = 0;

@@ -14,6 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(HERE), "_build", "libmx_encoder.so")
 
 MX_OK = 0
+MX_E_INVALID, MX_E_DEVICE, MX_E_UNSUPPORTED, MX_E_STATE, MX_E_DATA = -1, -2, -3, -4, -5
 MX_F32, MX_BF16, MX_I32, MX_I8 = 0, 1, 2, 3
 MX_EPI_NONE, MX_EPI_GELU_POLY, MX_EPI_GELU_ERF = 0, 1, 2
 MX_GELU_POLY, MX_GELU_ERF, MX_GELU_ERF_AS = 0, 1, 2
@@ -112,6 +113,9 @@ SIGNATURES = {
     "mx_encoder_run": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64]),
     "mx_encoder_embed": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "mx_encoder_embed_static": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "mx_static_guard_hold": (_int, [_int]),
+    "mx_static_guard_release": (_int, [_int]),
+    "mx_device_allocations": (_i64, []),
     "mx_encoder_vit": (_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
     "mx_encoder_whisper": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "mx_encoder_set_timing": (_int, [_vp, _int]),

@@ -71,6 +71,30 @@ def test_removed_flags_refused(L, flag, hint):
     assert L.mx_ops_check_flag(b"--npu-ops") == 0
 
 
+def test_static_scratch_guard_refuses_an_overlap(L):
+    """The per-GPU guard mx_encoder_embed_static holds for its whole call, taken
+    here as a call would take it: a second holder on the same device is refused
+    by name (that is the overlap refusal), other devices are independent, and
+    releasing makes it available again. Host-only: no GPU, no timing."""
+    assert L.mx_static_guard_hold(3) == mxenc.MX_OK
+    assert L.mx_static_guard_hold(3) == mxenc.MX_E_STATE
+    msg = L.mx_last_error().decode()
+    assert "device 3" in msg and "in use by another call" in msg
+    assert L.mx_static_guard_hold(4) == mxenc.MX_OK  # another GPU's scratch
+    assert L.mx_static_guard_release(3) == mxenc.MX_OK
+    assert L.mx_static_guard_release(3) == mxenc.MX_E_STATE  # not held any more
+    assert "not held" in L.mx_last_error().decode()
+    assert L.mx_static_guard_hold(3) == mxenc.MX_OK
+    for dev in (3, 4):
+        assert L.mx_static_guard_release(dev) == mxenc.MX_OK
+    assert L.mx_static_guard_hold(-1) == -1
+
+
+def test_device_allocation_count_starts_at_zero_without_a_device(L):
+    """Nothing has allocated device memory in a process without a GPU."""
+    assert L.mx_device_allocations() == 0
+
+
 def test_null_arguments_refused_without_a_device(L):
     assert L.mx_create(0, None) == -1
     assert "null" in L.mx_last_error().decode()

@@ -80,6 +80,62 @@ def test_static_embed_shared_scratch_two_encoders(ctx):
     e2.close()
 
 
+def test_static_embed_allocates_nothing_as_first_call(ctx):
+    """On a freshly readied encoder that has never run mx_encoder_embed (so it
+    has no workspace), mx_encoder_embed_static runs twice -- the second call
+    smaller -- without a single device allocation by the library; the rows are
+    then mx_encoder_embed's, bit for bit."""
+    m, _ = CASES["minilm"]()
+    enc = mxenc.Encoder(ctx, m)
+    enc.ready()
+    L = mxenc.lib()
+    batches = []
+    for B, S in ((24, 128), (6, 40)):
+        ids, am, _ = synth.make_text_inputs(m, batch=B, seq=S, seed=B * 7 + S)
+        batches.append((ids, am, ctx.put(ids), ctx.put(am),
+                        ctx.empty((B, m["hidden"]), np.float32)))
+    before = L.mx_device_allocations()
+    for ids, am, d_ids, d_am, out in batches:
+        B, S = ids.shape
+        enc.embed_static(d_ids, d_am, B, S, out)
+    ctx.sync()
+    assert L.mx_device_allocations() == before
+    for ids, am, d_ids, d_am, out in batches:
+        B, S = ids.shape
+        got = out.host()
+        want = ctx.empty((B, m["hidden"]), np.float32)
+        enc.embed(d_ids, d_am, B, S, want)
+        assert np.array_equal(want.host().view(np.uint32), got.view(np.uint32)), (B, S)
+    # mx_encoder_embed does allocate (its workspace): the counter sees it
+    assert L.mx_device_allocations() > before
+    enc.close()
+
+
+def test_static_embed_refuses_an_overlapping_call(ctx):
+    """While another call holds this GPU's static scratch (here: the guard held
+    as a call holds it), mx_encoder_embed_static is refused by name before it
+    touches the scratch; once the guard is back, the same call runs and gives
+    mx_encoder_embed's rows. Nothing depends on timing."""
+    m, _ = CASES["minilm"]()
+    enc = mxenc.Encoder(ctx, m)
+    ids, am, _ = synth.make_text_inputs(m, batch=4, seq=64)
+    d_ids, d_am = ctx.put(ids), ctx.put(am)
+    out = ctx.empty((4, m["hidden"]), np.float32)
+    L = mxenc.lib()
+    assert L.mx_static_guard_hold(0) == mxenc.MX_OK
+    try:
+        with pytest.raises(RuntimeError, match="in use by another call"):
+            enc.embed_static(d_ids, d_am, 4, 64, out)
+    finally:
+        assert L.mx_static_guard_release(0) == mxenc.MX_OK
+    want, got = embed_both(ctx, enc, ids, am)
+    assert np.array_equal(want.view(np.uint32), got.view(np.uint32))
+    # the guard is free again after a call (and after a refused one)
+    assert L.mx_static_guard_hold(0) == mxenc.MX_OK
+    assert L.mx_static_guard_release(0) == mxenc.MX_OK
+    enc.close()
+
+
 def test_static_embed_refusals(ctx):
     m = synth.make_model("bge_base", layers=1)
     enc = mxenc.Encoder(ctx, m)
