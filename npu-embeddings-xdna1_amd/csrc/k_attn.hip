@@ -42,11 +42,14 @@
 //
 // VALU economy (the softmax, not the MFMAs, bounds this kernel): a key tile
 // that reaches no further than kv_len and whose mask entries are all zero (a
-// wave ballot over the staged mask row) skips the per-score mask add and takes
-// its max on the raw scores (scale > 0), and each probability is one FMA into
-// exp2. The running max m moves (and O and l are rescaled) only when a tile's
-// max exceeds it by more than 8 in log2 units, so probabilities stay below
-// 2^8 and most tiles skip the rescale; the result O / l is the same quotient.
+// wave ballot over the staged mask row) skips the per-score mask add (scale >
+// 0), and each probability is one FMA into exp2. Only the first key tile
+// takes a maximum: it fixes the reference point m of the exponentials, and a
+// later tile pays for a maximum, a rescale of O and l and a second pass of
+// exponentials only when its probabilities sum past 2^24 -- so most tiles
+// carry no max, no cross-lane exchange and no rescale; the result O / l is
+// the same quotient. The row sum adds the bf16 probabilities two at a time
+// (v_dot2c_f32_bf16 against 1.0).
 #include "mx_common.hpp"
 #include "mx_kernels.hpp"
 
@@ -244,7 +247,7 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
       const float *smk = (const float *)(sl + 2 * TILE);
       bool masked = (t + 1) * BKV > kvl || force_logits;
       if (add_mask) masked = masked || __ballot(smk[lane] != 0.0f) != 0;
-      float mx = -INFINITY, cc;
+      float cc;
       if (masked) {
         // Lane (li, g) holds keys sub * 32 + 8 rr + 4 g + e of accumulator
         // element 4 rr + e: four consecutive mask entries, one 16-byte LDS
@@ -265,43 +268,69 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
               const int r = rr * 4 + e;
               const float mv =
                   t * BKV + key0 + e < kvl ? mk[e] * 1.4426950408889634f : -INFINITY;
-              const float v = __builtin_fmaf(sc[sub][r], scale_log2e, mv);
-              sc[sub][r] = v;
-              mx = fmaxf(mx, v);
+              sc[sub][r] = __builtin_fmaf(sc[sub][r], scale_log2e, mv);
             }
           }
         }
         cc = 1.0f;
       } else {
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[sub][r]);
-        mx *= scale_log2e;
         cc = scale_log2e;
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      if (mx > m_run + 8.0f) {
-        const float alpha = __builtin_amdgcn_exp2f(m_run - mx);
-        m_run = mx;
+      // The query's largest logit in this tile (both lanes of the query).
+      auto tile_max = [&]() {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+          if (sub == 1 && !h1) continue;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[sub][r]);
+        }
+        mx *= cc;
+        return fmaxf(mx, __shfl_xor(mx, 32));
+      };
+      // Probabilities p = 2^(logit - m_run), rounded to bf16 in pairs for the
+      // PV MFMA; the row sum adds the bf16 pairs (v_dot2c_f32_bf16 with 1.0),
+      // so the normaliser is the sum of the very weights PV applies.
+      bf16x8 pk[4];
+      float ps;
+      auto exps = [&]() {
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+        const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+        ps = 0.0f;
+#pragma unroll
+        for (int ch = 0; ch < 4; ++ch) {
+          const int sub = ch >> 1, c = ch & 1;
+          if (sub == 1 && !h1) continue;
+#pragma unroll
+          for (int jj = 0; jj < 8; jj += 2) {
+            bf16x2_t pr;
+            pr[0] = (__bf16)__builtin_amdgcn_exp2f(
+                __builtin_fmaf(sc[sub][c * 8 + jj], cc, -m_run));
+            pr[1] = (__bf16)__builtin_amdgcn_exp2f(
+                __builtin_fmaf(sc[sub][c * 8 + jj + 1], cc, -m_run));
+            pk[ch][jj] = pr[0];
+            pk[ch][jj + 1] = pr[1];
+            ps = __builtin_amdgcn_fdot2_f32_bf16(pr, one, ps, false);
+          }
+        }
+      };
+      // The reference point m_run is the first tile's maximum and moves only
+      // when a later tile's probabilities sum past 2^24 (or overflow): then
+      // that tile's maximum is taken, O and l are rescaled and the tile's
+      // probabilities recomputed. Below that bound every p is at most 2^24,
+      // far inside fp32 and bf16 range, and O / l is the same quotient.
+      if (t == 0) m_run = tile_max();
+      exps();
+      if (__ballot(!(ps <= 16777216.0f)) != 0) {
+        const float mn = fmaxf(m_run, tile_max());
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+        m_run = mn;
         l_run *= alpha;
 #pragma unroll
         for (int ht = 0; ht < NHT; ++ht)
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[ht][r] *= alpha;
-      }
-      bf16x8 pk[4];
-      float ps = 0.0f;
-#pragma unroll
-      for (int ch = 0; ch < 4; ++ch) {
-        const int sub = ch >> 1, c = ch & 1;
-        if (sub == 1 && !h1) continue;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[sub][c * 8 + jj], cc, -m_run));
-          ps += p;
-          pk[ch][jj] = (__bf16)p;
-        }
+        exps();
       }
       l_run += ps;
       // O^T += V^T P^T: lane (hd row li, half g) needs keys 16ch + 4g + 0..3
