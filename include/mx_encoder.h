@@ -51,6 +51,19 @@ typedef enum {
   MX_EPI_GELU_POLY = 1, /* gelu8 / gelu_cpu (bert_encoder.cpp:532-580)        */
   MX_EPI_GELU_ERF = 2   /* 0.5x(1+erf(x/sqrt2)) (app_state.hpp:116-120)       */
 } mx_epilogue;
+/* A flag OR'ed into a GEMM epilogue: the narrowed C of the array designs
+ * (c_elem_bytes == 2, runtime/src/design.cpp:255; the export default,
+ * tools/data/npu_targets.json:10). The finished accumulator is rounded to bf16
+ * first -- fp32 to nearest even, int32 in one rounding of the integer -- and
+ * the bias is added (bf16 datapath: from_bf16(c) + bias, bert_encoder.cpp:
+ * 874-900) or the dequantisation applied (int8: fma(from_bf16(c) * a_scale,
+ * wscale, bias), host_kernels.hpp:529-560) to that value, then the activation
+ * (dequant_act_bf16, bert_encoder.cpp:633-712). No residual; for an fp32 C on
+ * the bf16 datapath, no activation (the reference activates on the way into
+ * the next bf16 A); on the int8 datapath not with the raw int32 C. Shapes the
+ * direct-to-LDS kernel does not take (K % 32, misalignment, no bias) are
+ * refused. */
+#define MX_EPI_NARROW_C 32
 
 typedef enum {
   MX_GELU_POLY = 0,   /* gelu_cpu / gelu_poly_rne.cc: degree-8 fit            */
@@ -124,7 +137,8 @@ int mx_release_weight(mx_ctx *ctx, int slot);
  * ([K, N] as staged), bf16 A with row stride lda (elements), fp32 accumulate,
  * fp32 bias (nullable), optional fp32 residual [M, N] with stride ldc (may
  * alias C when c_dtype is MX_F32; the pre-LN encoders' x += proj), C fp32 or
- * bf16 (RNE) with row stride ldc. K % 8 == 0, lda % 8 == 0, 16-byte aligned A. */
+ * bf16 (RNE) with row stride ldc. K % 8 == 0, lda % 8 == 0, 16-byte aligned A.
+ * epilogue | MX_EPI_NARROW_C: the array design's narrowed C (see above). */
 int mx_gemm(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t lda,
             int wslot, const float *bias, int epilogue, const float *residual,
             void *C, int c_dtype, int64_t ldc);
@@ -288,7 +302,10 @@ int mx_quantise_a_int8(mx_stream *s, const void *a, int a_dtype, int64_t rows, i
  * the optional fp32 residual, and C as fp32 or bf16. c_dtype MX_I32 stores
  * the raw int32 accumulators (the design's C before dequantise_c; no bias,
  * residual or epilogue). K % 64 == 0, 256 <= K <= 133144 (K * 127^2 < 2^31),
- * N % 4 == 0, lda % 16 == 0, 16-byte aligned A, C, bias and wscale. */
+ * N % 4 == 0, lda % 16 == 0, 16-byte aligned A, C, bias and wscale.
+ * epilogue | MX_EPI_NARROW_C: the design's narrowed C -- the int32 product
+ * rounded to bf16 once (narrow_i32_bf16) before dequantise_c's 2-byte branch
+ * (host_kernels.hpp:529-560) -- no residual, not with MX_I32 C. */
 int mx_gemm_i8(mx_stream *s, const int8_t *A, const float *a_scale, int64_t M, int64_t K,
                int64_t lda, int wslot, const float *bias, int epilogue, const float *residual,
                void *C, int c_dtype, int64_t ldc);
@@ -519,6 +536,22 @@ int mx_encoder_set_cls_pruning(mx_encoder *enc, int on);
  * GEMM-then-glu pair's, bit for bit; off runs that pair. No counterpart in
  * the reference, whose host path runs the two steps. */
 int mx_encoder_set_fusion(mx_encoder *enc, int on);
+
+/* The narrowed C of the array designs (off by default): c_elem_bytes == 2
+ * (runtime/src/design.cpp:255), the export default ("c_bf16": true,
+ * tools/data/npu_targets.json:10). Every GEMM of the BERT stack rounds its
+ * finished accumulator to bf16 before the bias or the dequantisation
+ * (MX_EPI_NARROW_C), as BertEncoder::gemm's array branch then computes on the
+ * host (bert_encoder.cpp:741-924): the QKV result from_bf16(c) + bias; the
+ * attention-out and FFN-down results from_bf16(c) + bias kept in fp32 for the
+ * residual LayerNorm (:874-900); FFN-up through dequant_act_bf16 (:633-712:
+ * from_bf16(c) + bias, GELU or the gated halves combined in fp32, one
+ * rounding to bf16); on an int8 container fma(from_bf16(c) * a_scale, wscale,
+ * bias) (dequantise_c's and dequant_act_quant's 2-byte branches,
+ * host_kernels.hpp:405-560). The gated FFN then runs unfused. Off: the
+ * accumulator enters the epilogue in fp32 (int32) as it is. BERT encoders
+ * only (MX_E_UNSUPPORTED otherwise). */
+int mx_encoder_set_narrowed_c(mx_encoder *enc, int on);
 
 /* VitEncoder::run + head_matvec (runtime/src/vit/encoder.cpp:222-431,
  * runtime/src/vit/head.cpp:16-49), every step on the GPU: pixels fp32

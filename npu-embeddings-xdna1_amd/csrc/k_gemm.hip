@@ -173,6 +173,7 @@ template <int BM, int BN, int WGM, int WGN, int NS>
 hipError_t gemm_lds_launch(const GemmArgs &a, int grid, hipStream_t s);
 hipError_t gemm_lds_deep_launch(const GemmArgs &a, int grid, hipStream_t s);
 hipError_t gemm_lds_128_deep_launch(const GemmArgs &a, int grid, hipStream_t s);
+hipError_t gemm_lds_nc_launch(const GemmArgs &a, int grid, hipStream_t s);
 
 namespace {
 
@@ -313,6 +314,10 @@ const char *gemm_config_name(int64_t M, int64_t N, int64_t K) {
 }
 
 hipError_t gemm(const GemmArgs &a, hipStream_t s) {
+  if (a.epilogue & EPI_NARROW_C) {
+    if (!lds_path_ok(a) || a.residual) return hipErrorInvalidValue;
+    return gemm_lds_nc_launch(a, cu_count(), s);
+  }
   const GemmPath p = pick(a);
   // The fused gated FFN exists only on the LDS-pipelined kernel.
   if (a.epilogue >= EPI_GLU_SILU && (p == PATH_STAGED || a.N % 64)) return hipErrorInvalidValue;

@@ -87,6 +87,33 @@ hipError_t launch_deep(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
+// A narrowed C (EPI_NARROW_C: the int32 product rounded to bf16 once before
+// the dequantisation; no residual, not the raw product): the 256 x 256 tile,
+// or the 128 x 128 tile where the product is too small for it.
+hipError_t launch_nc(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
+  if (a.residual || a.c_dtype == 2) return hipErrorInvalidValue;
+  const int e = a.epilogue & ~EPI_NARROW_C;
+  constexpr int NC = EPI_NARROW_C;
+#define MX_I8_NC(BM, BN, WGM, WGN, NS)                                                        \
+  switch (e) {                                                                                \
+    case 0:                                                                                   \
+      return a.c_dtype == 1 ? launch_t<BM, BN, WGM, WGN, NS, NC, false, 1>(a, grid, s)        \
+                            : launch_t<BM, BN, WGM, WGN, NS, NC, false, 0>(a, grid, s);       \
+    case 1:                                                                                   \
+      return a.c_dtype == 1 ? launch_t<BM, BN, WGM, WGN, NS, NC | 1, false, 1>(a, grid, s)    \
+                            : launch_t<BM, BN, WGM, WGN, NS, NC | 1, false, 0>(a, grid, s);   \
+    case 2:                                                                                   \
+      return a.c_dtype == 1 ? launch_t<BM, BN, WGM, WGN, NS, NC | 2, false, 1>(a, grid, s)    \
+                            : launch_t<BM, BN, WGM, WGN, NS, NC | 2, false, 0>(a, grid, s);   \
+    default: return hipErrorInvalidValue;                                                     \
+  }
+  if (mxk::gemm_lds_tile(a.M, a.N, false) == 0) {
+    MX_I8_NC(256, 256, 2, 4, 3)
+  }
+  MX_I8_NC(128, 128, 2, 2, 4)
+#undef MX_I8_NC
+}
+
 }  // namespace
 
 namespace mxk {
@@ -99,6 +126,7 @@ bool gemm_i8_deep(const GemmI8Args &a) {
 
 hipError_t gemm_i8(const GemmI8Args &a, hipStream_t s) {
   const int grid = cu_count();
+  if (a.epilogue & EPI_NARROW_C) return launch_nc(a, grid, s);
   const bool deep = gemm_i8_deep(a);
   int t = gemm_lds_tile(a.M, a.N, deep);
   if (t == 1 && a.epilogue >= EPI_GLU_SILU) t = 0;  // 96-column waves cannot pair blocks

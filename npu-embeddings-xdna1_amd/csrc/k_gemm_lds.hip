@@ -118,6 +118,34 @@ hipError_t gemm_lds_128_deep_launch(const GemmArgs &a, int grid, hipStream_t s) 
   }
 }
 
+// A narrowed C (EPI_NARROW_C; no residual): the 256 x 256 tile on 64-byte
+// slabs, or the 128 x 128 tile where the product is too small for it; a bf16
+// C with any activation, or an fp32 C without one (the BERT projections and
+// the gated FFN's halves, which the host adds the bias to in fp32).
+hipError_t gemm_lds_nc_launch(const GemmArgs &a, int grid, hipStream_t s) {
+  if (a.residual) return hipErrorInvalidValue;
+  const int e = a.epilogue & ~EPI_NARROW_C;
+  constexpr int NC = EPI_NARROW_C;
+#define MX_LDS_NC(BM, BN, WGM, WGN, NS)                                                   \
+  if (a.c_bf16) {                                                                         \
+    switch (e) {                                                                          \
+      case 0: return gemm_lds_launch_t<BM, BN, WGM, WGN, NS, NC, false, true>(a, grid, s); \
+      case 1:                                                                             \
+        return gemm_lds_launch_t<BM, BN, WGM, WGN, NS, NC | 1, false, true>(a, grid, s);   \
+      case 2:                                                                             \
+        return gemm_lds_launch_t<BM, BN, WGM, WGN, NS, NC | 2, false, true>(a, grid, s);   \
+      default: return hipErrorInvalidValue;                                               \
+    }                                                                                     \
+  }                                                                                       \
+  if (e == 0) return gemm_lds_launch_t<BM, BN, WGM, WGN, NS, NC, false, false>(a, grid, s); \
+  return hipErrorInvalidValue;
+  if (gemm_lds_tile(a.M, a.N, false) == 0) {
+    MX_LDS_NC(256, 256, 2, 4, 3)
+  }
+  MX_LDS_NC(128, 128, 2, 2, 4)
+#undef MX_LDS_NC
+}
+
 template hipError_t gemm_lds_launch<256, 256, 2, 4, 3>(const GemmArgs &, int, hipStream_t);
 template hipError_t gemm_lds_launch<128, 256, 2, 4, 4>(const GemmArgs &, int, hipStream_t);
 template hipError_t gemm_lds_launch<128, 128, 2, 2, 4>(const GemmArgs &, int, hipStream_t);

@@ -18,6 +18,14 @@
 // then the activation and the store. RAW stores the int32 accumulators
 // themselves (the design's C before dequantisation).
 //
+// Narrowed C (EPI | EPI_NARROW_C): the array designs that narrow C on the core
+// (c_elem_bytes == 2, the export default) round the finished accumulator to
+// bf16 -- fp32 to nearest even (narrow_f32_bf16), int32 in one rounding of the
+// integer (narrow_i32_bf16) -- and the host adds the bias or dequantises from
+// that bf16 value (host_kernels.hpp:529-560, bert_encoder.cpp:633-712,
+// :874-900). With the bit set, the epilogue reads the accumulator through the
+// same rounding before anything else.
+//
 // Grid. One block per CU walks a list of BM x BN output tiles; its slabs
 // (RB = 64 or 128 bytes of K per row: 32 or 64 bf16, 64 or 128 int8; 128-byte
 // rows make every load request a whole 128-byte line and halve the barriers
@@ -89,6 +97,10 @@
 namespace mxlds {
 
 using namespace mxd;
+
+// The epilogue bit of a narrowed C (see above); the rest of EPI is the
+// activation (mx_epilogue) or a fused gated FFN (8, 9).
+constexpr int EPI_NARROW_C = mxk::EPI_NARROW_C;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
@@ -243,12 +255,15 @@ __device__ __forceinline__ void gemm_lds_body(
   static_assert(I8 || !RAW, "RAW is the int8 datapath's");
   static_assert(!RAW || (EPI == 0 && !RES && !CBF), "RAW stores the accumulators as they are");
   constexpr int TM = Cfg::TM, TN = Cfg::TN, ESZ = Cfg::ESZ;
-  // EPI 8 / 9: the gated FFN fused (GLU), C = lo * act(hi) in bf16 (act 1
+  constexpr bool NC = (EPI & EPI_NARROW_C) != 0;
+  constexpr int EPB = EPI & ~EPI_NARROW_C;
+  // EPB 8 / 9: the gated FFN fused (GLU), C = lo * act(hi) in bf16 (act 1
   // SiLU, 2 exact-erf GELU), Wt's rows interleaved in groups of 16 (8 lo, 8
   // hi): each 32-column accumulator block gives 16 columns of C.
-  constexpr bool GLU = EPI >= 8;
-  constexpr int GACT = EPI - 7, EPA = GLU ? 0 : EPI;
-  static_assert(!GLU || (EPI <= 9 && CBF && !RES && !RAW), "GLU: bf16 C, no residual");
+  constexpr bool GLU = EPB >= 8;
+  constexpr int GACT = EPB - 7, EPA = GLU ? 0 : EPB;
+  static_assert(!GLU || (EPB <= 9 && CBF && !RES && !RAW && !NC), "GLU: bf16 C, no residual");
+  static_assert(!NC || (!RES && !RAW), "a narrowed C: no residual, not the raw product");
   static_assert(!GLU || TN % 2 == 0, "GLU pairs a wave's column blocks");
   // The bf16 kernel always has a bias (the launcher routes others away); the
   // int8 kernel takes it as optional.
@@ -387,6 +402,17 @@ __device__ __forceinline__ void gemm_lds_body(
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][i][r] = 0;
+  // Accumulator element r of block (j, i) as the epilogue reads it: as it is,
+  // or (NC) rounded to bf16 first.
+  auto accf = [&](int j, int i, int r) -> float {
+    if constexpr (I8) {
+      if constexpr (NC) return bf2f(i32_to_bf16((int)acc[j][i][r]));
+      return (float)acc[j][i][r];
+    } else {
+      if constexpr (NC) return bf2f(f2bf(acc[j][i][r]));
+      return acc[j][i][r];
+    }
+  };
 
   // Fragment addressing: at k-step kk lane (row li, k-half g) reads logical
   // chunk 2*kk + g of its row, at its swizzled position (rows 32*x + li all
@@ -478,9 +504,8 @@ __device__ __forceinline__ void gemm_lds_body(
     // The epilogue's value of accumulator (j, i) element q * 4 + e: the bias
     // (dequantisation) added, before the activation.
     auto pre = [&](int j, int i, int q, int e, float bb, float ww, float sa) {
-      if (I8)
-        return __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + e], sa), ww, bb);
-      return (float)acc[j][i][q * 4 + e] + bb;
+      if (I8) return __builtin_fmaf(__fmul_rn(accf(j, i, q * 4 + e), sa), ww, bb);
+      return accf(j, i, q * 4 + e) + bb;
     };
     float4 b[4], w[4];
     uint4 wv[2];
@@ -610,18 +635,18 @@ __device__ __forceinline__ void gemm_lds_body(
         if (I8) {
           const float4 w = *(const float4 *)(wsl + cl + q * 8 + g * 4);
           v.x = gemm_epilogue(
-              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 0], sa), w.x, b.x), EPI);
+              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 0], sa), w.x, b.x), EPB);
           v.y = gemm_epilogue(
-              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 1], sa), w.y, b.y), EPI);
+              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 1], sa), w.y, b.y), EPB);
           v.z = gemm_epilogue(
-              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 2], sa), w.z, b.z), EPI);
+              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 2], sa), w.z, b.z), EPB);
           v.w = gemm_epilogue(
-              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 3], sa), w.w, b.w), EPI);
+              __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 3], sa), w.w, b.w), EPB);
         } else {
-          v.x = gemm_epilogue(acc[j][i][q * 4 + 0] + b.x, EPI);
-          v.y = gemm_epilogue(acc[j][i][q * 4 + 1] + b.y, EPI);
-          v.z = gemm_epilogue(acc[j][i][q * 4 + 2] + b.z, EPI);
-          v.w = gemm_epilogue(acc[j][i][q * 4 + 3] + b.w, EPI);
+          v.x = gemm_epilogue(acc[j][i][q * 4 + 0] + b.x, EPB);
+          v.y = gemm_epilogue(acc[j][i][q * 4 + 1] + b.y, EPB);
+          v.z = gemm_epilogue(acc[j][i][q * 4 + 2] + b.z, EPB);
+          v.w = gemm_epilogue(acc[j][i][q * 4 + 3] + b.w, EPB);
         }
         vq[q] = v;
       }
@@ -697,20 +722,20 @@ __device__ __forceinline__ void gemm_lds_body(
             const float4 b = has_bias ? *(const float4 *)(bl + cl + q * 8 + g * 4)
                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             const float4 w = *(const float4 *)(wsl + cl + q * 8 + g * 4);
-            v.x = gemm_epilogue(
-                __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 0], sa), w.x, b.x), EPI);
-            v.y = gemm_epilogue(
-                __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 1], sa), w.y, b.y), EPI);
-            v.z = gemm_epilogue(
-                __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 2], sa), w.z, b.z), EPI);
-            v.w = gemm_epilogue(
-                __builtin_fmaf(__fmul_rn((float)acc[j][i][q * 4 + 3], sa), w.w, b.w), EPI);
+            v.x = gemm_epilogue(__builtin_fmaf(__fmul_rn(accf(j, i, q * 4 + 0), sa), w.x, b.x),
+                                EPB);
+            v.y = gemm_epilogue(__builtin_fmaf(__fmul_rn(accf(j, i, q * 4 + 1), sa), w.y, b.y),
+                                EPB);
+            v.z = gemm_epilogue(__builtin_fmaf(__fmul_rn(accf(j, i, q * 4 + 2), sa), w.z, b.z),
+                                EPB);
+            v.w = gemm_epilogue(__builtin_fmaf(__fmul_rn(accf(j, i, q * 4 + 3), sa), w.w, b.w),
+                                EPB);
           } else {
             const float4 b = *(const float4 *)(bl + cl + q * 8 + g * 4);
-            v.x = gemm_epilogue(acc[j][i][q * 4 + 0] + b.x, EPI);
-            v.y = gemm_epilogue(acc[j][i][q * 4 + 1] + b.y, EPI);
-            v.z = gemm_epilogue(acc[j][i][q * 4 + 2] + b.z, EPI);
-            v.w = gemm_epilogue(acc[j][i][q * 4 + 3] + b.w, EPI);
+            v.x = gemm_epilogue(accf(j, i, q * 4 + 0) + b.x, EPB);
+            v.y = gemm_epilogue(accf(j, i, q * 4 + 1) + b.y, EPB);
+            v.z = gemm_epilogue(accf(j, i, q * 4 + 2) + b.z, EPB);
+            v.w = gemm_epilogue(accf(j, i, q * 4 + 3) + b.w, EPB);
           }
           if (STG_BF) {
             const uint2 w = make_uint2(pack_bf2_hw(v.x, v.y), pack_bf2_hw(v.z, v.w));

@@ -132,13 +132,22 @@ int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t 
   if (ldc < N) return fail(MX_E_INVALID, "gemm: ldc < N");
   if (!aligned(A, 16) || !aligned(Wt, 16))
     return fail(MX_E_INVALID, "gemm: A and the weight panel must be 16-byte aligned");
-  if (epilogue < MX_EPI_NONE || epilogue > MX_EPI_GELU_ERF)
+  const bool narrow = (epilogue & MX_EPI_NARROW_C) != 0;
+  const int act = epilogue & ~MX_EPI_NARROW_C;
+  if (act < MX_EPI_NONE || act > MX_EPI_GELU_ERF)
     return fail(MX_E_INVALID, "gemm: unknown epilogue " + std::to_string(epilogue));
   if (c_dtype != MX_F32 && c_dtype != MX_BF16)
     return fail(MX_E_INVALID, "gemm: C dtype must be MX_F32 or MX_BF16");
+  if (narrow && (residual || (c_dtype == MX_F32 && act != MX_EPI_NONE)))
+    return fail(MX_E_UNSUPPORTED, "gemm: a narrowed C takes no residual, and an fp32 one no "
+                                  "activation");
   mxk::GemmArgs a{A, lda, Wt, M, N, K, bias, epilogue, residual, C, c_dtype == MX_BF16 ? 1 : 0,
                   ldc};
   const hipError_t e = mxk::gemm(a, s->stream);
+  if (narrow && e == hipErrorInvalidValue)
+    return fail(MX_E_UNSUPPORTED, "gemm: a narrowed C runs on the direct-to-LDS kernel only "
+                                  "(K % 32 == 0, K >= 128, N % 4 == 0, a bias, 16-byte aligned "
+                                  "operands)");
   return e == hipSuccess ? MX_OK : hip_fail(e, "gemm launch");
 }
 

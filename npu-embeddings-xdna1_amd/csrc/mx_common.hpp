@@ -20,6 +20,31 @@ __device__ __forceinline__ uint16_t f2bf(float x) {
 
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 
+// int32 -> bf16 in one nearest-even rounding of the integer itself (the
+// array's narrow_i32_bf16 kernel): keep the top 8 significant bits of |v|,
+// round on the dropped bits.
+__device__ __forceinline__ uint16_t i32_to_bf16(int32_t v) {
+  if (v == 0) return 0;
+  const uint32_t sign = v < 0 ? 0x8000u : 0u;
+  const uint32_t a = v < 0 ? (uint32_t)(-(int64_t)v) : (uint32_t)v;
+  int e = 31 - __clz(a);
+  uint32_t mant;
+  if (e <= 7) {
+    mant = a << (7 - e);
+  } else {
+    const int sh = e - 7;
+    mant = a >> sh;
+    const uint32_t rem = a & ((1u << sh) - 1u);
+    const uint32_t half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (mant & 1u))) ++mant;
+    if (mant == 256u) {
+      mant = 128u;
+      ++e;
+    }
+  }
+  return (uint16_t)(sign | ((uint32_t)(e + 127) << 7) | (mant & 0x7Fu));
+}
+
 // Two fp32 -> packed bf16 by the hardware conversion (v_cvt_pk_bf16_f32, round
 // to nearest even): identical to f2bf for every non-NaN input; a NaN becomes a
 // quiet NaN instead of f2bf's carry pattern. For results held to a tolerance

@@ -107,6 +107,10 @@ struct mx_encoder {
   float *rope_cos = nullptr, *rope_sin = nullptr;
   int64_t rope_rows = 0;
   bool i8 = false;       // set by mx_encoder_ready: every GEMM operand is int8
+  // The array designs' narrowed C (mx_encoder_set_narrowed_c): every GEMM's
+  // accumulator rounded to bf16 before its bias / dequantisation.
+  bool narrow_c = false;
+  bool ws_wide = false;  // the workspace holds proj / up / glu in fp32
   // Token packing (embed): seq_start [B + 1] and each packed row's position
   // (work.seq_start, work.row_pos).
   bool packing = true;
@@ -152,9 +156,13 @@ int dev_alloc(void **p, size_t bytes, const char *what) {
 int ensure_ws_rows(mx_encoder *enc, int64_t rows, int64_t B);
 int ensure_mask_ws(mx_encoder *enc, int64_t B, int64_t rows);
 
+// proj, up and the gated product in fp32: the int8 datapath (dequantise_c's
+// C, dequant_act_quant's activation) and a narrowed C (from_bf16(c) + bias).
+bool wide_acts(const mx_encoder *enc) { return enc->i8 || enc->narrow_c; }
+
 int ensure_ws(mx_encoder *enc, int64_t B, int64_t S) {
   const int64_t rows = B * S;
-  if (rows > enc->ws_rows || (enc->i8 && !enc->work.xq)) {
+  if (rows > enc->ws_rows || (enc->i8 && !enc->work.xq) || (wide_acts(enc) && !enc->ws_wide)) {
     const int64_t want = rows > enc->ws_rows ? rows : enc->ws_rows;
     return ensure_ws_rows(enc, want, B);
   }
@@ -178,8 +186,9 @@ int ensure_ws_rows(mx_encoder *enc, int64_t rows, int64_t B) {
     int rc = dev_alloc((void **)&enc->work.xb, rows * d * 2, "workspace xb");
     if (!rc) rc = dev_alloc((void **)&enc->work.qkv, rows * 3 * d * 2, "workspace qkv");
     if (!rc) rc = dev_alloc((void **)&enc->work.ctxb, rows * d * 2, "workspace ctx");
-    // int8: FFN-up's activation stays fp32 up to its quantiser
-    const int64_t ab = enc->i8 ? 4 : 2;
+    // int8: FFN-up's activation stays fp32 up to its quantiser; a narrowed C
+    // keeps from_bf16(c) + bias in fp32
+    const int64_t ab = wide_acts(enc) ? 4 : 2;
     if (!rc) rc = dev_alloc((void **)&enc->work.up, rows * fu * ab, "workspace up");
     if (!rc && enc->desc.gated_ffn)
       rc = dev_alloc((void **)&enc->work.glu, rows * f * ab, "workspace gated");
@@ -191,6 +200,7 @@ int ensure_ws_rows(mx_encoder *enc, int64_t rows, int64_t B) {
     if (!rc && enc->i8) rc = dev_alloc((void **)&enc->work.sa, rows * 4, "workspace sa");
     if (rc) return rc;
     enc->ws_rows = rows;
+    enc->ws_wide = ab == 4;
   }
   return ensure_mask_ws(enc, B, rows);
 }
@@ -330,9 +340,9 @@ int rope_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, int64_t M,
                       enc->desc.head_dim, enc->rope_cos, enc->rope_sin, M, row_pos);
 }
 
-int glu_l(mx_encoder *enc, mx_stream *s, int64_t M, int dtype) {
+int glu_l(mx_encoder *enc, mx_stream *s, int64_t M, int in_dtype, int out_dtype) {
   Bracket br(enc, s->stream, CAT_OTHER);
-  return glu_checked(s, enc->work.up, dtype, enc->work.glu, dtype, M, enc->desc.ffn,
+  return glu_checked(s, enc->work.up, in_dtype, enc->work.glu, out_dtype, M, enc->desc.ffn,
                      enc->desc.gated_ffn);
 }
 
@@ -439,6 +449,7 @@ int attn_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, const float *mas
 int site_gemm(mx_encoder *enc, mx_stream *s, const LayerW &w, int site, const uint16_t *A_bf,
               int64_t M, int64_t K, int64_t N, int epi, const float *resid, void *C,
               int c_dtype) {
+  if (enc->narrow_c) epi |= MX_EPI_NARROW_C;
   if (enc->i8)
     return gemm_i8_l(enc, s, site, M, K, w.wq[site], w.ws[site], N, w.b[site], epi, resid, C,
                      c_dtype);
@@ -491,12 +502,14 @@ int layer_rows(mx_encoder *enc, mx_stream *s, float *x, const uint16_t *ctx, int
   const int64_t fu = gated ? 2 * f : f;
   uint16_t *act = gated ? enc->work.glu : enc->work.up;  // FFN-down's A (bf16 datapath)
   const LayerW &w = enc->layers[l];
-  const bool fused = gated && enc->fuse_glu && glu_fusable(enc) && w.glu_gen == enc->wgen &&
-                     (enc->i8 ? w.wqg && w.wsg : w.wg != nullptr) && w.bg;
+  const bool fused = gated && enc->fuse_glu && !enc->narrow_c && glu_fusable(enc) &&
+                     w.glu_gen == enc->wgen && (enc->i8 ? w.wqg && w.wsg : w.wg != nullptr) &&
+                     w.bg;
   int rc = enc->i8 ? quant_l(enc, s, ctx, MX_BF16, M, d, w.ias[SITE_AO]) : MX_OK;
-  // proj: bf16 (the array path's C) or, on the int8 datapath, fp32 as
-  // dequantise_c writes it (host_kernels.hpp:529-600)
-  const int pdt = enc->i8 ? MX_F32 : MX_BF16;
+  // proj: bf16 (the array path's C) or fp32 -- on the int8 datapath as
+  // dequantise_c writes it (host_kernels.hpp:529-600), with a narrowed C as
+  // from_bf16(c) + bias (bert_encoder.cpp:874-900)
+  const int pdt = wide_acts(enc) ? MX_F32 : MX_BF16;
   if (!rc)
     rc = site_gemm(enc, s, w, SITE_AO, ctx, M, d, d, MX_EPI_NONE, nullptr, enc->work.proj, pdt);
   if (!rc) rc = site_ln(enc, s, x, enc->work.proj, pdt, w.ln[0], w.ln[1], M, x, w.ias[SITE_UP]);
@@ -506,15 +519,21 @@ int layer_rows(mx_encoder *enc, mx_stream *s, float *x, const uint16_t *ctx, int
     // combined in fp32), then quantised per row from those fp32 values.
     rc = site_gemm(enc, s, w, SITE_UP, nullptr, M, d, fu, gated ? MX_EPI_NONE : epi, nullptr,
                    enc->work.up, MX_F32);
-    if (!rc && gated) rc = glu_l(enc, s, M, MX_F32);
+    if (!rc && gated) rc = glu_l(enc, s, M, MX_F32, MX_F32);
     if (!rc) rc = quant_l(enc, s, act, MX_F32, M, f, w.ias[SITE_DOWN]);
   } else if (!rc && fused) {
     rc = gemm_glu_l(enc, s, w, M);
+  } else if (!rc && gated && enc->narrow_c) {
+    // dequant_act_bf16's gated branch (bert_encoder.cpp:633-712): both halves
+    // from_bf16(c) + bias in fp32, combined in fp32, rounded once to bf16.
+    rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, M, d, fu, MX_EPI_NONE, nullptr,
+                   enc->work.up, MX_F32);
+    if (!rc) rc = glu_l(enc, s, M, MX_F32, MX_BF16);
   } else {
     if (!rc)
       rc = site_gemm(enc, s, w, SITE_UP, enc->work.xb, M, d, fu, gated ? MX_EPI_NONE : epi,
                      nullptr, enc->work.up, MX_BF16);
-    if (!rc && gated) rc = glu_l(enc, s, M, MX_BF16);
+    if (!rc && gated) rc = glu_l(enc, s, M, MX_BF16, MX_BF16);
   }
   if (!rc)
     rc = site_gemm(enc, s, w, SITE_DOWN, act, M, f, d, MX_EPI_NONE, nullptr, enc->work.proj,
@@ -911,6 +930,7 @@ int mx_encoder_clone(mx_encoder *enc, mx_encoder **out) {
   c->rope_inv = enc->rope_inv;
   c->packing = enc->packing;
   c->prune_cls = enc->prune_cls;
+  c->narrow_c = enc->narrow_c;
   for (int i = 0; i < 2; ++i) {
     c->emb_ln[i] = enc->emb_ln[i];
     c->fin_ln[i] = enc->fin_ln[i];
@@ -1236,7 +1256,7 @@ size_t rows_bytes(const mx_encoder *enc, int64_t rows) {
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
   const bool gated = enc->desc.gated_ffn != MX_GATED_NONE;
   size_t n = Carver::piece(rows * 4);                                  // row_pos
-  const int64_t ab = enc->i8 ? 4 : 2;  // int8: FFN-up's activation and proj in fp32
+  const int64_t ab = wide_acts(enc) ? 4 : 2;  // int8 / narrowed C: up and proj in fp32
   n += 2 * Carver::piece(rows * d * 2) + Carver::piece(rows * d * ab);  // xb ctx proj
   n += Carver::piece(rows * 3 * d * 2);                                 // qkv
   n += Carver::piece(rows * (gated ? 2 * f : f) * ab);                 // up
@@ -1256,7 +1276,7 @@ void carve_rows(const mx_encoder *enc, Carver &c, int64_t rows, Work &w) {
   w.row_pos = c.take<int32_t>(rows);
   w.xb = c.take<uint16_t>(rows * d);
   w.ctxb = c.take<uint16_t>(rows * d);
-  const int64_t ab = enc->i8 ? 2 : 1;  // int8: FFN-up's activation and proj in fp32
+  const int64_t ab = wide_acts(enc) ? 2 : 1;  // int8 / narrowed C: up and proj in fp32
   w.proj = c.take<uint16_t>(rows * d * ab);
   w.qkv = c.take<uint16_t>(rows * 3 * d);
   w.up = c.take<uint16_t>(rows * (gated ? 2 * f : f) * ab);
@@ -1618,6 +1638,17 @@ int mx_encoder_set_fusion(mx_encoder *enc, int on) {
   clear_error();
   if (!enc) return fail(MX_E_INVALID, "encoder_set_fusion: null encoder");
   enc->fuse_glu = on != 0;
+  return MX_OK;
+}
+
+int mx_encoder_set_narrowed_c(mx_encoder *enc, int on) {
+  clear_error();
+  if (!enc) return fail(MX_E_INVALID, "encoder_set_narrowed_c: null encoder");
+  if (on && (enc->desc.arch != MX_ARCH_BERT || enc->desc.front != MX_FRONT_NONE))
+    return fail(MX_E_UNSUPPORTED, "encoder_set_narrowed_c: the narrowed C is the BERT stack's "
+                                  "datapath (bert_encoder.cpp:741-924); the pre-LN encoders add "
+                                  "their projections into the residual in the GEMM epilogue");
+  enc->narrow_c = on != 0;
   return MX_OK;
 }
 

@@ -210,10 +210,15 @@ int gemm_i8_checked(mx_stream *s, const int8_t *A, const float *a_scale, int64_t
                                   " is below K or not a multiple of 16");
   if (N % 4) return fail(MX_E_UNSUPPORTED, "gemm_i8: N % 4 != 0");
   if (ldc < N) return fail(MX_E_INVALID, "gemm_i8: ldc < N");
-  if (epilogue < MX_EPI_NONE || epilogue > MX_EPI_GELU_ERF)
+  const bool narrow = (epilogue & MX_EPI_NARROW_C) != 0;
+  const int act = epilogue & ~MX_EPI_NARROW_C;
+  if (act < MX_EPI_NONE || act > MX_EPI_GELU_ERF)
     return fail(MX_E_INVALID, "gemm_i8: unknown epilogue " + std::to_string(epilogue));
   if (c_dtype != MX_F32 && c_dtype != MX_BF16 && c_dtype != MX_I32)
     return fail(MX_E_INVALID, "gemm_i8: C dtype must be MX_F32, MX_BF16 or MX_I32");
+  if (narrow && (residual || c_dtype == MX_I32))
+    return fail(MX_E_UNSUPPORTED, "gemm_i8: a narrowed C takes no residual and is not the raw "
+                                  "MX_I32 product");
   if (c_dtype == MX_I32) {
     if (bias || residual || epilogue != MX_EPI_NONE)
       return fail(MX_E_INVALID, "gemm_i8: MX_I32 C is the raw accumulator -- no bias, "

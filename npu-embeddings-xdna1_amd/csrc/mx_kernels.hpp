@@ -80,6 +80,10 @@ hipError_t gemm(const GemmArgs &a, hipStream_t s);
 // C is [M, f] = lo * act(hi), each product of the two bf16-rounded GEMM
 // outputs, as the GEMM followed by glu() computes it. f % 32 == 0.
 constexpr int EPI_GLU_SILU = 8, EPI_GLU_GELU = 9;
+// An epilogue flag on both datapaths (MX_EPI_NARROW_C): the accumulator is
+// rounded to bf16 before the bias or the dequantisation, as the array designs
+// that narrow C on the core compute (no residual; the LDS-pipelined kernel).
+constexpr int EPI_NARROW_C = 32;
 // Wt [2f, row_bytes] (or a [2f] vector, row_bytes 4) -> the interleaved row
 // order above. row_bytes % 4 == 0.
 hipError_t glu_interleave(const void *src, void *dst, int64_t f, int64_t row_bytes,

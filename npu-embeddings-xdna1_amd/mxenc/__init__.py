@@ -17,6 +17,7 @@ MX_OK = 0
 MX_E_INVALID, MX_E_DEVICE, MX_E_UNSUPPORTED, MX_E_STATE, MX_E_DATA = -1, -2, -3, -4, -5
 MX_F32, MX_BF16, MX_I32, MX_I8 = 0, 1, 2, 3
 MX_EPI_NONE, MX_EPI_GELU_POLY, MX_EPI_GELU_ERF = 0, 1, 2
+MX_EPI_NARROW_C = 32
 MX_GELU_POLY, MX_GELU_ERF, MX_GELU_ERF_AS = 0, 1, 2
 MX_SOFTMAX_POLY, MX_SOFTMAX_EXACT, MX_SOFTMAX_AIE = 0, 1, 2
 MX_ARCH_BERT, MX_ARCH_PRELN = 0, 1
@@ -122,6 +123,7 @@ SIGNATURES = {
     "mx_encoder_set_packing": (_int, [_vp, _int]),
     "mx_encoder_set_cls_pruning": (_int, [_vp, _int]),
     "mx_encoder_set_fusion": (_int, [_vp, _int]),
+    "mx_encoder_set_narrowed_c": (_int, [_vp, _int]),
     "mx_encoder_timings": (_int, [_vp, ctypes.POINTER(Timings)]),
     "mx_npue_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "mx_npue_close": (None, [_vp]),
@@ -588,6 +590,10 @@ class Encoder:
 
     def set_fusion(self, on):
         check(lib().mx_encoder_set_fusion(self.handle, int(on)))
+
+    def set_narrowed_c(self, on):
+        """mx_encoder_set_narrowed_c: the array designs' bf16-narrowed C."""
+        check(lib().mx_encoder_set_narrowed_c(self.handle, int(on)))
 
     def set_timing(self, on):
         check(lib().mx_encoder_set_timing(self.handle, int(on)))

@@ -149,7 +149,10 @@ int orc_pool_rows(const float *h, const float *attn_mask, int64_t B, int64_t S,
 
 /* ---- AIE kernel restatements (bf16 in/out; the accelerator ops the GPU
  * kernels replace). bf16 narrowing here is RNE (the *_rne.cc variants and
- * narrow_*.cc all set conv_even). ---------------------------------------- */
+ * narrow_*.cc all set conv_even). The softmax and LayerNorm sums end in
+ * aie::reduce_add over 16 lanes, whose order the reference does not define
+ * (the AIE API is outside it): lane 0 to 15 in turn is ASSUMED -- parity
+ * unpinned for that one step (orc_numerics.c, aie_reduce_add16). -------- */
 /* softmax.cc:76-160 (softmax_rne.cc:42-52): per row of `cols`: x = max(x,
  * -1e30) (in bf16); m = max; d = max(x - m, -100); arg = max(d*log2e, -120);
  * e = bf16(exp2_poly(arg)); sum over e in fp32; inv = 1/sum; out =
@@ -282,6 +285,46 @@ void orc_dequantise_c(const int32_t *C, int64_t rows, int64_t N, const float *a_
 void orc_gemm_i8_dequant(const float *A, int64_t M, int64_t K, const float *ias,
                          const int8_t *Wq, const float *wscale, const float *bias,
                          int64_t N, float *out);
+
+/* ---- the narrowed C of the array designs (c_elem_bytes == 2) -------------
+ * The export default narrows C to bf16 on the core ("c_bf16": true,
+ * tools/data/npu_targets.json:10; design.cpp:255) and the host finishes from
+ * the bf16 value:
+ * orc_dequantise_c_bf16: dequantise_c's 2-byte branch (host_kernels.hpp:
+ * 529-560), out = fma(from_bf16(C) * sa[r], wscale[n], bias[n]) (the AVX2
+ * form; the scalar tail is contracted to the same FMA at the reference's
+ * -O2 -march=x86-64-v3). Pinned bit-exact against oracle/_ref's dequantise_c
+ * with c_bytes = 2.
+ * orc_bias_c_bf16: the bf16-C branch of BertEncoder::gemm (bert_encoder.cpp:
+ * 874-900), out = from_bf16(C) + bias[n] in fp32. Pinned by the closed form
+ * (an exact widening and one IEEE add).
+ * orc_dequant_act_bf16: BertEncoder::dequant_act_bf16 (bert_encoder.cpp:
+ * 633-712) for a 2-byte C: v = from_bf16(C) + bias in fp32, then gelu8
+ * (gated 0) or the gated halves (1 SiLU / 2 exact-erf GeLU, as orc_glu,
+ * out_n = N/2), then bf16_fill into dst [rows, out_n]. bert_encoder.cpp does
+ * not build here; pinned by composing oracle/_ref's gelu8 and to_bf16 on
+ * the closed-form v (tests), and the gated halves by orc_glu's own pins. */
+void orc_dequantise_c_bf16(const uint16_t *C, int64_t rows, int64_t N, const float *a_scale,
+                           const float *wscale, const float *bias, float *out);
+void orc_bias_c_bf16(const uint16_t *C, int64_t rows, int64_t N, const float *bias,
+                     float *out);
+void orc_dequant_act_bf16(const uint16_t *C, int64_t rows, int64_t N, int gated,
+                          const float *bias, uint16_t *dst);
+
+/* The arithmetic of the array datapath in the whole-stack restatements
+ * (orc_bert_run, orc_bert_run_i8), a bit set; 0 (the default) is the host
+ * fallback. ORC_ARR_A_BF16: every bf16-datapath GEMM rounds its A to bf16
+ * first (BertEncoder::gemm's bf16_fill, bert_encoder.cpp:776-782).
+ * ORC_ARR_C_BF16: the narrowed C -- bf16 GEMMs give from_bf16(bf16(acc)) +
+ * bias (orc_bias_c_bf16), int8 GEMMs dequantise narrow_i32_bf16(acc)
+ * (orc_dequantise_c_bf16). ORC_ARR_ATTN_BF16: Q, K, V after the QKV GEMM (and
+ * RoPE) and the attention context are rounded to bf16 (the array attention's
+ * bf16 operands, attention_npu, bert_encoder.cpp:1151-1181). Returns the
+ * previous setting. Not thread-safe: set it between runs. */
+#define ORC_ARR_A_BF16 1
+#define ORC_ARR_C_BF16 2
+#define ORC_ARR_ATTN_BF16 4
+int orc_set_array_arith(int flags);
 
 /* The int8 operands of a BERT stack: per layer and GEMM (qkv, attn_out,
  * ffn_up, ffn_down) the [K, N] int8 weight, its [N] column scale and the [K]

@@ -9,6 +9,72 @@
 
 static float *falloc(size_t n) { return (float *)malloc(n * sizeof(float)); }
 
+/* ---- the array datapath's arithmetic (orc_set_array_arith) ---------------- */
+
+static int g_arr = 0;
+
+int orc_set_array_arith(int flags) {
+  const int prev = g_arr;
+  g_arr = flags;
+  return prev;
+}
+
+/* One bf16-datapath GEMM of the stack: gemm_nt on the host's fp32 A, or the
+ * array's form -- A rounded to bf16 (ORC_ARR_A_BF16), the accumulator rounded
+ * to bf16 before the bias (ORC_ARR_C_BF16). gemm_nt adds the bias after the
+ * whole k chain, so acc then + bias is the same sum. */
+static void gemm_site(const float *A, int64_t rows, const float *W, int64_t K, int64_t N,
+                      const float *bias, float *out) {
+  if (!g_arr) {
+    orc_gemm_nt(A, rows, W, K, N, bias, out);
+    return;
+  }
+  float *a = NULL;
+  if (g_arr & ORC_ARR_A_BF16) {
+    a = falloc((size_t)(rows * K));
+    memcpy(a, A, (size_t)(rows * K) * sizeof(float));
+    orc_round_bf16_inplace(a, (size_t)(rows * K));
+  }
+  if (!(g_arr & ORC_ARR_C_BF16)) {
+    orc_gemm_nt(a ? a : A, rows, W, K, N, bias, out);
+  } else {
+    orc_gemm_nt(a ? a : A, rows, W, K, N, NULL, out);
+    uint16_t *c = (uint16_t *)malloc((size_t)(rows * N) * sizeof(uint16_t));
+    orc_bf16_fill(c, out, (size_t)(rows * N));
+    orc_bias_c_bf16(c, rows, N, bias, out);
+    free(c);
+  }
+  free(a);
+}
+
+/* One int8-datapath GEMM: quantise -> exact int32 product -> dequantise_c,
+ * from the int32 C or (ORC_ARR_C_BF16) from narrow_i32_bf16 of it. */
+static void gemm_i8_site(const float *A, int64_t M, int64_t K, const float *ias,
+                         const int8_t *Wq, const float *wscale, const float *bias, int64_t N,
+                         float *out) {
+  if (!(g_arr & ORC_ARR_C_BF16)) {
+    orc_gemm_i8_dequant(A, M, K, ias, Wq, wscale, bias, N, out);
+    return;
+  }
+  int8_t *q = (int8_t *)malloc((size_t)(M * K));
+  float *sa = falloc((size_t)M);
+  int32_t *c = (int32_t *)malloc((size_t)(M * N) * sizeof(int32_t));
+  uint16_t *cb = (uint16_t *)malloc((size_t)(M * N) * sizeof(uint16_t));
+  orc_quantise_a_int8(A, M, K, ias, q, sa);
+  orc_gemm_i8(q, M, K, Wq, N, c);
+  orc_narrow_i32_bf16(c, cb, M * N);
+  orc_dequantise_c_bf16(cb, M, N, sa, wscale, bias, out);
+  free(q);
+  free(sa);
+  free(c);
+  free(cb);
+}
+
+/* Q, K, V or a context rounded to bf16 (ORC_ARR_ATTN_BF16). */
+static void attn_bf16(float *x, size_t n) {
+  if (g_arr & ORC_ARR_ATTN_BF16) orc_round_bf16_inplace(x, n);
+}
+
 /* BertEncoder::run, every op on the host (bert_encoder.cpp:1419-1598 with
  * gemm_on_array() false, host_ln/host_sm/host_gelu true, attn_ null). */
 void orc_bert_run(const orc_encoder *m, float *x, const float *add_mask,
@@ -30,23 +96,25 @@ void orc_bert_run(const orc_encoder *m, float *x, const float *add_mask,
   orc_layer_norm_rows(x, rows, d, m->emb_ln_g, m->emb_ln_b, eps);
   for (int64_t l = 0; l < L; ++l) {
     memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
-    orc_gemm_nt(x, rows, m->w_qkv + l * d * 3 * d, d, 3 * d, m->b_qkv + l * 3 * d, qkv);
+    gemm_site(x, rows, m->w_qkv + l * d * 3 * d, d, 3 * d, m->b_qkv + l * 3 * d, qkv);
     if (m->rope_cos) orc_rope_qkv(qkv, rows, S, H, hd, m->rope_cos, m->rope_sin);
+    attn_bf16(qkv, (size_t)(rows * 3 * d));
     orc_qk(qkv, B, S, H, hd, scores);
     orc_softmax_rows_poly(scores, B * H * S, S, add_mask, H * S);
     orc_av(scores, qkv, B, S, H, hd, ctx);
-    orc_gemm_nt(ctx, rows, m->w_ao + l * d * d, d, d, m->b_ao + l * d, proj);
+    attn_bf16(ctx, (size_t)(rows * d));
+    gemm_site(ctx, rows, m->w_ao + l * d * d, d, d, m->b_ao + l * d, proj);
     orc_add_into(x, proj, residual, (size_t)(rows * d));
     orc_layer_norm_rows(x, rows, d, m->ln1_g + l * d, m->ln1_b + l * d, eps);
     memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
-    orc_gemm_nt(x, rows, m->w_up + l * d * fu, d, fu, m->b_up + l * fu, up);
+    gemm_site(x, rows, m->w_up + l * d * fu, d, fu, m->b_up + l * fu, up);
     if (m->gated) {
       orc_glu(up, rows, f, (int)m->gated, gated);
     } else {
       orc_gelu_poly_inplace(up, (size_t)(rows * f));
     }
-    orc_gemm_nt(m->gated ? gated : up, rows, m->w_down + l * f * d, f, d, m->b_down + l * d,
-                proj);
+    gemm_site(m->gated ? gated : up, rows, m->w_down + l * f * d, f, d, m->b_down + l * d,
+              proj);
     orc_add_into(x, proj, residual, (size_t)(rows * d));
     orc_layer_norm_rows(x, rows, d, m->ln2_g + l * d, m->ln2_b + l * d, eps);
   }
@@ -157,17 +225,19 @@ void orc_bert_run_i8(const orc_encoder *m, const orc_i8_operands *q, float *x,
   float *up = falloc((size_t)(rows * fu));
   float *gated = m->gated ? falloc((size_t)(rows * f)) : NULL;
   float *residual = falloc((size_t)(rows * d));
-#define GEMM_I8(i, A, bias, out)                                                        \
-  orc_gemm_i8_dequant((A), rows, Ks[i], q->ias[i] + l * Ks[i], q->wq[i] + l * Ks[i] * Ns[i], \
-                      q->wscale[i] + l * Ns[i], (bias), Ns[i], (out))
+#define GEMM_I8(i, A, bias, out)                                                          \
+  gemm_i8_site((A), rows, Ks[i], q->ias[i] + l * Ks[i], q->wq[i] + l * Ks[i] * Ns[i], \
+               q->wscale[i] + l * Ns[i], (bias), Ns[i], (out))
   orc_layer_norm_rows(x, rows, d, m->emb_ln_g, m->emb_ln_b, eps);
   for (int64_t l = 0; l < L; ++l) {
     memcpy(residual, x, (size_t)(rows * d) * sizeof(float));
     GEMM_I8(0, x, m->b_qkv + l * 3 * d, qkv);
     if (m->rope_cos) orc_rope_qkv(qkv, rows, S, H, hd, m->rope_cos, m->rope_sin);
+    attn_bf16(qkv, (size_t)(rows * 3 * d));
     orc_qk(qkv, B, S, H, hd, scores);
     orc_softmax_rows_poly(scores, B * H * S, S, add_mask, H * S);
     orc_av(scores, qkv, B, S, H, hd, ctx);
+    attn_bf16(ctx, (size_t)(rows * d));
     GEMM_I8(1, ctx, m->b_ao + l * d, proj);
     orc_add_into(x, proj, residual, (size_t)(rows * d));
     orc_layer_norm_rows(x, rows, d, m->ln1_g + l * d, m->ln1_b + l * d, eps);

@@ -512,14 +512,36 @@ typedef struct {
 
 static void gemm_i8_worker(void *p, int w, int nw) {
   const gemm_i8_task *t = (const gemm_i8_task *)p;
+  const int64_t N = t->N, N32 = N / 32 * 32;
   for (int64_t m = w; m < t->M; m += nw) {
-    int32_t *c = t->C + m * t->N;
-    for (int64_t n = 0; n < t->N; ++n) c[n] = 0;
+    int32_t *c = t->C + m * N;
     const int8_t *a = t->A + m * t->K;
+    /* 32 columns at a time in four int32 accumulators (integer sums are exact
+     * in any order), the rest one column at a time */
+    for (int64_t n = 0; n < N32; n += 32) {
+      __m256i c0 = _mm256_setzero_si256(), c1 = c0, c2 = c0, c3 = c0;
+      for (int64_t k = 0; k < t->K; ++k) {
+        const __m256i av = _mm256_set1_epi32(a[k]);
+        const int8_t *wr = t->W + k * N + n;
+        c0 = _mm256_add_epi32(c0, _mm256_mullo_epi32(av, _mm256_cvtepi8_epi32(
+                                                             _mm_loadl_epi64((const __m128i *)wr))));
+        c1 = _mm256_add_epi32(c1, _mm256_mullo_epi32(av, _mm256_cvtepi8_epi32(_mm_loadl_epi64(
+                                                             (const __m128i *)(wr + 8)))));
+        c2 = _mm256_add_epi32(c2, _mm256_mullo_epi32(av, _mm256_cvtepi8_epi32(_mm_loadl_epi64(
+                                                             (const __m128i *)(wr + 16)))));
+        c3 = _mm256_add_epi32(c3, _mm256_mullo_epi32(av, _mm256_cvtepi8_epi32(_mm_loadl_epi64(
+                                                             (const __m128i *)(wr + 24)))));
+      }
+      _mm256_storeu_si256((__m256i *)(c + n), c0);
+      _mm256_storeu_si256((__m256i *)(c + n + 8), c1);
+      _mm256_storeu_si256((__m256i *)(c + n + 16), c2);
+      _mm256_storeu_si256((__m256i *)(c + n + 24), c3);
+    }
+    for (int64_t n = N32; n < N; ++n) c[n] = 0;
     for (int64_t k = 0; k < t->K; ++k) {
       const int32_t av = a[k];
-      const int8_t *wr = t->W + k * t->N;
-      for (int64_t n = 0; n < t->N; ++n) c[n] += av * (int32_t)wr[n];
+      const int8_t *wr = t->W + k * N;
+      for (int64_t n = N32; n < N; ++n) c[n] += av * (int32_t)wr[n];
     }
   }
 }
@@ -564,4 +586,61 @@ void orc_gemm_i8_dequant(const float *A, int64_t M, int64_t K, const float *ias,
   free(q);
   free(sa);
   free(c);
+}
+
+/* ---- the narrowed C (c_elem_bytes == 2) ----------------------------------- */
+
+typedef struct {
+  const uint16_t *C;
+  const float *sa, *ws, *bias;
+  float *out;
+  uint16_t *dst;
+  int64_t rows, N;
+  int gated;
+} cbf_task;
+
+static void deq_bf16_worker(void *p, int w, int nw) {
+  const cbf_task *t = (const cbf_task *)p;
+  for (int64_t r = w; r < t->rows; r += nw) {
+    const float sa = t->sa[r];
+    for (int64_t n = 0; n < t->N; ++n)
+      t->out[r * t->N + n] =
+          fmaf(orc_from_bf16(t->C[r * t->N + n]) * sa, t->ws[n], t->bias[n]);
+  }
+}
+
+void orc_dequantise_c_bf16(const uint16_t *C, int64_t rows, int64_t N, const float *a_scale,
+                           const float *wscale, const float *bias, float *out) {
+  cbf_task t = {C, a_scale, wscale, bias, out, NULL, rows, N, 0};
+  orc_run(deq_bf16_worker, &t);
+}
+
+static void bias_bf16_worker(void *p, int w, int nw) {
+  const cbf_task *t = (const cbf_task *)p;
+  for (int64_t r = w; r < t->rows; r += nw)
+    for (int64_t n = 0; n < t->N; ++n)
+      t->out[r * t->N + n] = orc_from_bf16(t->C[r * t->N + n]) + t->bias[n];
+}
+
+void orc_bias_c_bf16(const uint16_t *C, int64_t rows, int64_t N, const float *bias,
+                     float *out) {
+  cbf_task t = {C, NULL, NULL, bias, out, NULL, rows, N, 0};
+  orc_run(bias_bf16_worker, &t);
+}
+
+void orc_dequant_act_bf16(const uint16_t *C, int64_t rows, int64_t N, int gated,
+                          const float *bias, uint16_t *dst) {
+  float *v = (float *)malloc((size_t)(rows * N) * sizeof(float));
+  orc_bias_c_bf16(C, rows, N, bias, v);
+  if (!gated) {
+    orc_gelu_poly_inplace(v, (size_t)(rows * N));
+    orc_bf16_fill(dst, v, (size_t)(rows * N));
+  } else {
+    const int64_t f = N / 2;
+    float *g = (float *)malloc((size_t)(rows * f) * sizeof(float));
+    orc_glu(v, rows, f, gated, g);
+    orc_bf16_fill(dst, g, (size_t)(rows * f));
+    free(g);
+  }
+  free(v);
 }

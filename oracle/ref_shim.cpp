@@ -89,6 +89,18 @@ int ref_dequantise_c(const int32_t *c, int64_t rows, int64_t N, const float *a_s
   }
 }
 
+// The same for the 2-byte C of a design that narrows C on the core (c_bytes =
+// 2, bf16 bits): 0, or -1 when refused.
+int ref_dequantise_c_bf16(const uint16_t *c, int64_t rows, int64_t N, const float *a_scale,
+                          const float *wscale, const float *bias, float *out) {
+  try {
+    app::dequantise_c(c, 2, rows, N, a_scale, wscale, bias, out, serial_rows);
+    return 0;
+  } catch (const std::exception &) {
+    return -1;
+  }
+}
+
 // ---- the .npue reader and B-panel untile (model.cpp, host_b.hpp) ----------
 // Each returns a negative value when the reference throws; *err (when given)
 // receives the exception text.

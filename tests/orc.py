@@ -100,6 +100,10 @@ def load():
         "orc_rope_tables": (None, [_c_i64, _c_i64, ctypes.c_double, _vp, _vp, _vp]),
         "orc_rope_qkv": (None, [_vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp]),
         "orc_glu": (None, [_vp, _c_i64, _c_i64, ctypes.c_int, _vp]),
+        "orc_dequantise_c_bf16": (None, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
+        "orc_bias_c_bf16": (None, [_vp, _c_i64, _c_i64, _vp, _vp]),
+        "orc_dequant_act_bf16": (None, [_vp, _c_i64, _c_i64, ctypes.c_int, _vp, _vp]),
+        "orc_set_array_arith": (ctypes.c_int, [ctypes.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -124,6 +128,7 @@ def load_ref():
         "ref_gemm_nt": (None, [_vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, ctypes.c_int]),
         "ref_quantise_a_int8": (None, [_vp, _c_i64, _c_i64, _vp, _vp, _vp]),
         "ref_dequantise_c": (ctypes.c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
+        "ref_dequantise_c_bf16": (ctypes.c_int, [_vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp]),
         "ref_npue_host_b_kn": (ctypes.c_longlong, [ctypes.c_char_p, ctypes.c_char_p, _vp,
                                                    ctypes.c_longlong, ctypes.c_char_p,
                                                    ctypes.c_size_t]),
@@ -143,6 +148,24 @@ def load_ref():
         f.restype = res
         f.argtypes = args
     return lib
+
+
+ORC_ARR_A_BF16, ORC_ARR_C_BF16, ORC_ARR_ATTN_BF16 = 1, 2, 4
+
+
+class array_arith:
+    """Context manager: the oracle's whole-stack restatements run with the
+    array datapath's arithmetic bits (orc_set_array_arith) set."""
+
+    def __init__(self, flags):
+        self.flags = flags
+
+    def __enter__(self):
+        self.prev = load().orc_set_array_arith(self.flags)
+        return self
+
+    def __exit__(self, *exc):
+        load().orc_set_array_arith(self.prev)
 
 
 def bf16_round(x):
