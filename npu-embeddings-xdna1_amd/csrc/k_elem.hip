@@ -45,29 +45,7 @@ __global__ void narrow_f32_scalar_k(const float *__restrict__ in, uint16_t *__re
     out[i] = f2bf(in[i]);
 }
 
-// int32 -> bf16 in one nearest-even rounding of the integer itself: keep the
-// top 8 significant bits of |v|, round on the dropped bits.
-__device__ __forceinline__ uint16_t i32_to_bf16(int32_t v) {
-  if (v == 0) return 0;
-  const uint32_t sign = v < 0 ? 0x8000u : 0u;
-  const uint32_t a = v < 0 ? (uint32_t)(-(int64_t)v) : (uint32_t)v;
-  int e = 31 - __clz(a);
-  uint32_t mant;
-  if (e <= 7) {
-    mant = a << (7 - e);
-  } else {
-    const int sh = e - 7;
-    mant = a >> sh;
-    const uint32_t rem = a & ((1u << sh) - 1u);
-    const uint32_t half = 1u << (sh - 1);
-    if (rem > half || (rem == half && (mant & 1u))) ++mant;
-    if (mant == 256u) {
-      mant = 128u;
-      ++e;
-    }
-  }
-  return (uint16_t)(sign | ((uint32_t)(e + 127) << 7) | (mant & 0x7Fu));
-}
+// i32_to_bf16 (mx_common.hpp): int32 -> bf16 in one rounding of the integer.
 
 __global__ void narrow_i32_vec_k(const int4 *__restrict__ in, uint4 *__restrict__ out,
                                  int64_t n8) {
@@ -338,7 +316,9 @@ __global__ __launch_bounds__(256) void layernorm_any_k(
 // ---- LayerNorm with the accelerator kernel's arithmetic ---------------------
 // kernels/layernorm.cc:85-142 under layernorm_rne.cc's conv_even: bf16 in and
 // out; 16 fp32 partial sums per pass (column j into sum j % 16, in column
-// order), the 16 added in order; the biased variance about that mean;
+// order), the 16 added in order (aie::reduce_add's order is not defined by
+// the reference; lane 0 to 15 in turn is an assumption shared with the
+// oracle); the biased variance about that mean;
 // fast_invsqrt of var + eps (the 0x5f3759df estimate and two Newton steps,
 // layernorm.cc:65-75); y = (d * inv_std) * gamma + beta narrowed to bf16 to
 // nearest even. Every product and sum rounds on its own (no FMA).
@@ -471,8 +451,9 @@ __global__ __launch_bounds__(256) void softmax_wave_k(void *x, int bf, int64_t r
   if (variant == 2) {
     // softmax.cc:115-145's 16-lane accumulator: column j into partial sum
     // j % 16 in column order (columns l, l + 16, l + 32, l + 48 of each
-    // 64-column group sit in lanes l .. l + 48), then the 16 in order. Lanes
-    // 0 .. 15 hold the partial sums; every lane adds them itself.
+    // 64-column group sit in lanes l .. l + 48), then the 16 in order (the
+    // assumed order of aie::reduce_add, as in the oracle). Lanes 0 .. 15 hold
+    // the partial sums; every lane adds them itself.
     float part = 0.0f;
     const int l = lane & 15;
 #pragma unroll

@@ -117,9 +117,24 @@ static inline float aie_exp2(float x) {
 
 static inline float bf(float x) { return orc_from_bf16(orc_to_bf16(x)); }
 
+/* aie::reduce_add of a 16-lane fp32 accumulator, the last step of the AIE
+ * kernels' sums (softmax.cc:115-145, layernorm.cc:85-142). The AIE API that
+ * defines reduce_add is not part of the reference (it ships in the mlir-aie
+ * wheel, mlir_aie_no_rtti 1.4.3.dev55+g10767b5), so its order is not known:
+ * this adds lane 0 to lane 15 one after another. PARITY UNPINNED for this
+ * order (a hardware reduction may well be a pairwise tree); everything ahead
+ * of it -- which element lands in which lane, each lane's own in-order sum --
+ * follows the kernel source. The GPU kernels use the same order, so they are
+ * bit-exact against this restatement, not against the array. */
+static float aie_reduce_add16(const float acc[16]) {
+  float s = 0.0f;
+  for (int l = 0; l < 16; ++l) s += acc[l];
+  return s;
+}
+
 /* softmax.cc:76-160 with softmax_rne.cc's conv_even. The exponentials are
  * summed as the 16-lane accumulator holds them (:115-145): element j into
- * partial sum j % 16, in element order, then the 16 partial sums in order. */
+ * partial sum j % 16, in element order, then aie_reduce_add16. */
 void orc_aie_softmax_bf16(const uint16_t *in, uint16_t *out, int64_t rows,
                           int64_t cols) {
   const float lo = bf(-1.0e30f);
@@ -144,8 +159,7 @@ void orc_aie_softmax_bf16(const uint16_t *in, uint16_t *out, int64_t rows,
       e[j] = bf(aie_exp2(a));
       acc[j % 16] += e[j];
     }
-    float sum = 0.0f;
-    for (int l = 0; l < 16; ++l) sum += acc[l];
+    const float sum = aie_reduce_add16(acc);
     const float inv = 1.0f / sum;
     for (int64_t j = 0; j < cols; ++j) o[j] = orc_to_bf16(e[j] * inv);
   }
@@ -176,17 +190,13 @@ void orc_aie_layernorm_bf16(const uint16_t *in, uint16_t *out, int64_t rows,
     /* 16-lane accumulators, then one reduction, as the AIE vector code. */
     float acc[16] = {0};
     for (int64_t j = 0; j < cols; ++j) acc[j % 16] += orc_from_bf16(x[j]);
-    float s = 0.0f;
-    for (int l = 0; l < 16; ++l) s += acc[l];
-    const float mean = s * inv_cols;
+    const float mean = aie_reduce_add16(acc) * inv_cols;
     float acc2[16] = {0};
     for (int64_t j = 0; j < cols; ++j) {
       const float d = orc_from_bf16(x[j]) - mean;
       acc2[j % 16] += d * d;
     }
-    float v = 0.0f;
-    for (int l = 0; l < 16; ++l) v += acc2[l];
-    const float var = v * inv_cols;
+    const float var = aie_reduce_add16(acc2) * inv_cols;
     const float is = fast_invsqrt(var + eps);
     for (int64_t j = 0; j < cols; ++j) {
       const float d = orc_from_bf16(x[j]) - mean;
