@@ -391,6 +391,57 @@ def test_i8_stack_bge_base_full_batch_subset_checked(ctx, orc):
                      _oracle_embed(orc, _dequantised(m, q8), ii, aa), "bge-base int8")
 
 
+def test_i8_stack_bge_base_every_sequence_gap_is_the_grid(ctx, orc):
+    """bge-base at its full shape on the int8 datapath, every one of the 64
+    sequences rerun on the oracle (chunks of 16; sequences are independent).
+
+    What the GPU~host int8 gap is. Rounding Q, K, V and the attention context
+    to bf16 in the oracle (ORC_ARR_ATTN_BF16, what the GPU's attention does)
+    moves the oracle only ~5 % closer to the GPU, so that rounding is not the
+    cause. The cause is the int8 grid itself: any ulp-level difference ahead
+    of a quantiser (LayerNorm sum order, attention arithmetic) moves some
+    values across a rounding boundary by a whole step, and from there the two
+    runs carry independent draws of the grid noise. The same gap appears
+    between two HOST runs that differ only by that bf16 rounding (e_self).
+    So the bar: (1) the GPU differs from the host int8 stack by no more than
+    the host differs from itself under that perturbation (means over the 64
+    sequences, within 25 %); (2) the GPU int8 result is as accurate as the
+    host's against the fp32 stack on the dequantised operands (mean within
+    10 %, every sequence within 25 % of the host's worst); (3) no sequence
+    differs from the host by more than 2.5 times the scheme's own error."""
+    from orc import array_arith, ORC_ARR_ATTN_BF16
+    m = synth.make_model("bge_base")
+    q8 = synth.quantise_model(m)
+    ids, am, lens = synth.make_text_inputs(m)
+    enc = mxenc.Encoder(ctx, m, int8=q8)
+    got = _gpu_embed(ctx, enc, ids, am)
+    enc.close()
+    host8, host8a, hostf = [], [], []
+    md = _dequantised(m, q8)
+    for lo in range(0, 64, 16):
+        ii, aa = np.ascontiguousarray(ids[lo:lo + 16]), np.ascontiguousarray(am[lo:lo + 16])
+        print(f"int8 bge-base oracle: sequences {lo}..{lo + 15}", flush=True)
+        host8.append(_oracle_embed(orc, m, ii, aa, q8))
+        with array_arith(ORC_ARR_ATTN_BF16):
+            host8a.append(_oracle_embed(orc, m, ii, aa, q8))
+        hostf.append(_oracle_embed(orc, md, ii, aa))
+    host8, host8a, hostf = (np.concatenate(x) for x in (host8, host8a, hostf))
+    e_pair = 1.0 - _cos(got, host8)
+    e_pair_a = 1.0 - _cos(got, host8a)
+    e_self = 1.0 - _cos(host8, host8a)
+    e_scheme = 1.0 - _cos(host8, hostf)
+    e_gpu = 1.0 - _cos(got, hostf)
+    print(f"bge-base int8, 64 sequences, 1-cos mean / max: gpu~host8 {e_pair.mean():.3e} / "
+          f"{e_pair.max():.3e}; gpu~host8(bf16 attention) {e_pair_a.mean():.3e} / "
+          f"{e_pair_a.max():.3e}; host8~host8(bf16 attention) {e_self.mean():.3e} / "
+          f"{e_self.max():.3e}; host8~fp32 {e_scheme.mean():.3e} / {e_scheme.max():.3e}; "
+          f"gpu8~fp32 {e_gpu.mean():.3e} / {e_gpu.max():.3e}")
+    assert e_pair.mean() <= 1.25 * e_self.mean(), (e_pair.mean(), e_self.mean())
+    assert e_gpu.mean() <= 1.1 * e_scheme.mean(), (e_gpu.mean(), e_scheme.mean())
+    assert e_gpu.max() <= 1.25 * e_scheme.max(), (e_gpu.max(), e_scheme.max())
+    assert np.all(e_pair <= 2.5 * e_scheme), np.max(e_pair / e_scheme)
+
+
 def test_i8_container_is_bitwise_the_set_encoder(tmp_path, ctx):
     """An --int8 container (I8 block panels with .wscale/.asmooth) loaded by
     mx_encoder_from_npue runs bit-identically to the same operands set by
