@@ -196,6 +196,45 @@ def test_softmax_poly_masked(ctx, orc):
     assert np.all(got[H * S:2 * H * S, 70:] < 1e-30)
 
 
+@pytest.mark.parametrize("bf", [False, True], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("variant", ["poly", "exact"])
+@pytest.mark.parametrize("rows,cols", [(33, 8), (250, 136), (4099, 512), (18, 384), (7, 264),
+                                       (1030, 1024)])
+def test_softmax_16_byte_paths_against_the_host(ctx, orc, rows, cols, variant, bf):
+    """The 16-byte softmax paths (sixteen lanes per row up to 512 columns, a
+    wave per row group beyond) over ragged widths and row counts, masked
+    tails, a fully masked row (-1e30 everywhere: uniform, as the host) and a
+    row with a logit spread past the host's -120 clamp, against the host
+    softmax on the same (bf16-rounded) inputs, plus one bf16 rounding for a
+    bf16 output."""
+    rng = np.random.default_rng(rows * 7 + cols)
+    H, S = 1, cols
+    B = rows
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    x[0, : cols // 2] += 150.0  # probabilities of the other half below 2^-120
+    mask = np.zeros((B, S), np.float32)
+    mask[min(1, B - 1), cols // 3:] = -1e30
+    mask[min(2, B - 1), :] = -1e30
+    if bf:
+        x = from_bf16_bits(to_bf16_bits(x))
+    want = x.copy()
+    fn = orc.orc_softmax_rows_poly if variant == "poly" else orc.orc_softmax_rows_exact
+    fn(P(want), rows, cols, P(mask), 1)
+    code = mxenc.MX_SOFTMAX_POLY if variant == "poly" else mxenc.MX_SOFTMAX_EXACT
+    dx, dm = ctx.put(to_bf16_bits(x) if bf else x), ctx.put(mask)
+    mxenc.softmax_rows(ctx, dx, rows, cols, cols, dm, 1, code)
+    got = from_bf16_bits(dx.host()) if bf else dx.host()
+    # the poly variant within 1e-6 of the host; the exact one (fp32 expf
+    # against the host's std::exp, another sum order) within 1e-5 relative
+    # (1e-12 absolute for the tiny probabilities), as the wide-row test states
+    base = 1e-6 if variant == "poly" else np.abs(want) * 1e-5 + 1e-12
+    tol = base + (np.abs(want) * 2.0 ** -8 if bf else 0.0)
+    assert np.all(np.abs(got - want) <= tol), np.max(np.abs(got - want) - tol)
+    if rows > 2:
+        assert np.allclose(got[2], 1.0 / cols, rtol=1e-2)  # fully masked: uniform
+    assert np.all(got[0, cols // 2:] < 1e-30)
+
+
 @pytest.mark.parametrize("cols", [197, 1500])
 def test_softmax_exact_wide_rows(ctx, orc, cols):
     rng = np.random.default_rng(cols)
