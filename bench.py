@@ -439,7 +439,7 @@ def main():
     # padded run is EmbedService::chunk's computation, every row in every layer.
     pruning = packing and m["cls_pool"]
     lanes = max(1, args.lanes) if kind == "bert" else 1
-    lane_ctx, lane_enc, lane_step = [ctx], [enc], []
+    lane_ctx, lane_enc, lane_step, lane_queue = [ctx], [enc], [], []
     if kind == "bert":
         ids, am, lens = synth.make_text_inputs(m)
         B, S = ids.shape
@@ -455,6 +455,8 @@ def main():
             out = c.empty((B, m["hidden"]), np.float32)
             lane_step.append(lambda e=e, d_ids=d_ids, d_am=d_am, out=out:
                              e.embed(d_ids, d_am, B, S, out))
+            lane_queue.append(lambda e=e, d_ids=d_ids, d_am=d_am, out=out:
+                              e.embed_async(d_ids, d_am, B, S, out))
         step = lane_step[0]
         unit = "sequences/s"
     elif kind == "vit":
@@ -532,6 +534,19 @@ def main():
         one_lane = {"value": args.steps * B / odt, "ms_per_step": odt / args.steps * 1e3}
         print(f"bench: one lane {one_lane['value']:.1f} {unit} "
               f"({one_lane['ms_per_step']:.2f} ms/step)", file=sys.stderr, flush=True)
+    one_lane_queued = None
+    if lane_queue:
+        # One lane with mx_encoder_embed_async: every step queued behind the
+        # last, the refusal flag read once, at the closing sync.
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            lane_queue[0]()
+        ctx.sync()
+        qdt = time.perf_counter() - t0
+        one_lane_queued = {"value": args.steps * B / qdt, "ms_per_step": qdt / args.steps * 1e3}
+        print(f"bench: one lane, queued {one_lane_queued['value']:.1f} {unit} "
+              f"({one_lane_queued['ms_per_step']:.2f} ms/step)", file=sys.stderr, flush=True)
     all_rows = None
     if pruning and not args.no_padded_rate:
         # The same packed steps with the last layer over every row.
@@ -680,6 +695,7 @@ def main():
         "layernorm_ms_per_step": tot["ln_ms"] / args.steps,
         "lanes": lanes,
         "one_lane": one_lane,
+        "one_lane_queued": one_lane_queued,
         "sustained": sustained,
         "token_packing": {"on": packing, "rows_per_step": M, "padded_rows_per_step": B * S,
                           "padded": padded} if kind == "bert" else None,

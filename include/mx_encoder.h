@@ -109,7 +109,8 @@ int mx_stream_create(mx_ctx *ctx, mx_stream **out);
 void mx_stream_destroy(mx_stream *s);
 /* Wait for every op issued on s. The reference's dispatch is synchronous
  * (Design::dispatch_only, runtime/src/design.cpp:502-532); a caller wanting
- * those semantics calls mx_sync after each op. */
+ * those semantics calls mx_sync after each op. Reports (MX_E_DATA) and clears
+ * the data refusals that mx_encoder_embed_async calls left on s. */
 int mx_sync(mx_stream *s);
 /* The stream's hipStream_t, for callers that interleave their own work. */
 void *mx_stream_handle(mx_stream *s);
@@ -456,6 +457,20 @@ int mx_encoder_run(mx_encoder *enc, mx_stream *s, float *x_io,
  * out [B, hidden] (device). BERT only. Synchronises s. */
 int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids,
                      const float *attn_mask, int64_t B, int64_t S, float *out);
+/* mx_encoder_embed without its closing wait: no counterpart in the reference
+ * (chunk() returns the pooled rows). For callers that queue the next batch
+ * while this one runs, on one stream. The call enqueues the same work and
+ * returns once it is queued; out is complete when s is synchronised. The
+ * refusals the kernels raise on the data (a token id outside the vocabulary,
+ * CLS pooling on a masked first token) stay in s's flag until it is next
+ * read: by mx_sync(s), which reports them (MX_E_DATA) and clears it, or by a
+ * synchronous call on s, which reports them as its own. Refusals of the
+ * arguments come back from this call, as from mx_encoder_embed. ids,
+ * attn_mask and out must stay valid until s is synchronised, and one
+ * encoder's calls must share one stream (they share its workspace; a batch
+ * larger than any before waits for the device before the workspace grows). */
+int mx_encoder_embed_async(mx_encoder *enc, mx_stream *s, const int32_t *ids,
+                           const float *attn_mask, int64_t B, int64_t S, float *out);
 
 /* The static scratch of mx_encoder_embed_static: device memory that every GPU
  * the library runs on holds from mx_create until the process ends. */
@@ -510,8 +525,12 @@ int64_t mx_device_allocations(void);
  * LayerNorms over the packed row count, attention per sequence over its own
  * rows. The pooled output is the padded computation's, bit for bit;
  * EmbedService::chunk (embed_service.cpp:29-64) computes the padded batch,
- * which off restores. The packed row count is read back to the host once
- * per batch. mx_encoder_run always computes every row (it returns them all). */
+ * which off restores. The packed row count stays on the device: the
+ * launches are sized for B*S rows and every row-wise kernel stops at the
+ * count, so the host does not wait in the middle of the call (with timing
+ * on, and in mx_encoder_embed_static, it is read back instead). The call
+ * still synchronises its stream once, at its end, to read the refusal flag.
+ * mx_encoder_run always computes every row (it returns them all). */
 int mx_encoder_set_packing(mx_encoder *enc, int on);
 
 /* CLS pruning in mx_encoder_embed (on by default; no counterpart in the

@@ -148,11 +148,11 @@ template <int NP>
 __global__ __launch_bounds__(256) void layernorm_wave_k(
     const void *__restrict__ x, int x_bf, const void *__restrict__ y, int y_bf,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps,
-    int64_t rows, float *out_f32, uint16_t *out_bf16) {
+    int64_t rows, float *out_f32, uint16_t *out_bf16, const int32_t *rows_dev) {
   constexpr int cols = NP * 128;
   const int lane = threadIdx.x & 63;
   const int64_t row = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  if (row >= live_rows(rows, rows_dev)) return;
   float v[2 * NP];
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
@@ -220,11 +220,11 @@ template <int NQ>
 __global__ __launch_bounds__(256) void layernorm_wave4_k(
     const void *__restrict__ x, int x_bf, const void *__restrict__ y, int y_bf,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps,
-    int64_t rows, float *out_f32, uint16_t *out_bf16) {
+    int64_t rows, float *out_f32, uint16_t *out_bf16, const int32_t *rows_dev) {
   constexpr int cols = NQ * 256;
   const int lane = threadIdx.x & 63;
   const int64_t row = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  if (row >= live_rows(rows, rows_dev)) return;
   // gamma and beta are read with the row, so their latency runs under its
   // loads instead of after the two reductions.
   float4 gm[NQ], bt[NQ];
@@ -279,10 +279,10 @@ __global__ __launch_bounds__(256) void layernorm_wave4_k(
 __global__ __launch_bounds__(256) void layernorm_any_k(
     const void *__restrict__ x, int x_bf, const void *__restrict__ y, int y_bf,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps,
-    int64_t rows, int64_t cols, float *out_f32, uint16_t *out_bf16) {
+    int64_t rows, int64_t cols, float *out_f32, uint16_t *out_bf16, const int32_t *rows_dev) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
-  if (row >= rows) return;
+  if (row >= live_rows(rows, rows_dev)) return;
   auto load = [&](int64_t c) {
     const int64_t off = row * cols + c;
     float a = x_bf ? bf2f(((const uint16_t *)x)[off]) : ((const float *)x)[off];
@@ -652,7 +652,8 @@ __global__ __launch_bounds__(256) void mask_k(const float *__restrict__ am, int6
 constexpr int64_t ORDER_MAX_B = 8192;
 __global__ __launch_bounds__(256) void pack_plan_k(const int32_t *__restrict__ kv_len, int64_t B,
                                                    int32_t *__restrict__ seq_start,
-                                                   int32_t *__restrict__ order) {
+                                                   int32_t *__restrict__ order,
+                                                   int32_t *__restrict__ total_out) {
   if (threadIdx.x == 0) {
     int32_t acc = 0;
     for (int64_t b = 0; b < B; ++b) {
@@ -660,6 +661,7 @@ __global__ __launch_bounds__(256) void pack_plan_k(const int32_t *__restrict__ k
       acc += kv_len[b];
     }
     seq_start[B] = acc;
+    if (total_out) *total_out = acc;
   }
   if (!order) return;
   for (int64_t b = threadIdx.x; b < B; b += blockDim.x) {
@@ -880,7 +882,7 @@ hipError_t gelu(const void *x, int x_bf, void *y, int y_bf, int64_t n, int varia
 
 hipError_t layernorm(const void *x, int x_bf, const void *y, int y_bf, const float *gamma,
                      const float *beta, float eps, int64_t rows, int64_t cols, float *out_f32,
-                     uint16_t *out_bf16, hipStream_t s) {
+                     uint16_t *out_bf16, hipStream_t s, const int32_t *rows_dev) {
   const int rpb = 4;  // rows (waves) per block
   const int g = (int)((rows + rpb - 1) / rpb);
   bool aligned = ((uintptr_t)x % 8 == 0) && (!y || (uintptr_t)y % 8 == 0) &&
@@ -896,7 +898,7 @@ hipError_t layernorm(const void *x, int x_bf, const void *y, int y_bf, const flo
 #define MX_LN4_CASE(nq)                                                                   \
   case nq:                                                                                \
     layernorm_wave4_k<nq><<<g, 256, 0, s>>>(x, x_bf, y, y_bf, gamma, beta, eps, rows,     \
-                                            out_f32, out_bf16);                           \
+                                            out_f32, out_bf16, rows_dev);                 \
     return hipGetLastError();
     switch (cols / 256) {
       MX_LN4_CASE(1)
@@ -915,7 +917,7 @@ hipError_t layernorm(const void *x, int x_bf, const void *y, int y_bf, const flo
 #define MX_LN_CASE(np)                                                                     \
   case np:                                                                                 \
     layernorm_wave_k<np><<<g, 256, 0, s>>>(x, x_bf, y, y_bf, gamma, beta, eps, rows,      \
-                                           out_f32, out_bf16);                            \
+                                           out_f32, out_bf16, rows_dev);                  \
     return hipGetLastError();
     switch (cols / 128) {
       MX_LN_CASE(1)
@@ -935,7 +937,7 @@ hipError_t layernorm(const void *x, int x_bf, const void *y, int y_bf, const flo
 #undef MX_LN_CASE
   }
   layernorm_any_k<<<(unsigned)rows, 256, 0, s>>>(x, x_bf, y, y_bf, gamma, beta, eps, rows, cols,
-                                                 out_f32, out_bf16);
+                                                 out_f32, out_bf16, rows_dev);
   return hipGetLastError();
 }
 
@@ -1046,8 +1048,8 @@ hipError_t gather_cls(const float *x, const uint16_t *ctx, const int32_t *seq_st
 }
 
 hipError_t pack_plan(const int32_t *kv_len, int64_t B, int32_t *seq_start, int32_t *order,
-                     hipStream_t s) {
-  pack_plan_k<<<1, 256, 0, s>>>(kv_len, B, seq_start, order);
+                     hipStream_t s, int32_t *total_out) {
+  pack_plan_k<<<1, 256, 0, s>>>(kv_len, B, seq_start, order, total_out);
   return hipGetLastError();
 }
 

@@ -42,7 +42,7 @@ template <int BM, int BN, int BK, int WM, int WN>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_bf16_k(
     const uint16_t *__restrict__ A, int64_t lda, const uint16_t *__restrict__ Wt, int M, int N,
     int K, const float *__restrict__ bias, int epi, const float *residual, void *C, int c_bf16,
-    int64_t ldc, int tiles_m, int tiles_n) {
+    int64_t ldc, int tiles_m, int tiles_n, const int32_t *rows_dev) {
   using Cfg = GemmCfg<BM, BN, BK, WM, WN>;
   constexpr int LDK = Cfg::LDK, NT = Cfg::NT, CPR = Cfg::CPR;
   constexpr int TM = Cfg::TM, TN = Cfg::TN;
@@ -55,6 +55,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_bf16_k(
   if ((total & 7) == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
   const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
+  M = (int)live_rows(M, rows_dev);
+  if (m0 >= M) return;  // the whole block: a tile past the live rows
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / Cfg::NWN, wn = wave - wm * Cfg::NWN;
@@ -157,7 +159,7 @@ hipError_t launch(const mxk::GemmArgs &a, hipStream_t s) {
   const int blocks = tiles_m * tiles_n;
   gemm_bf16_k<BM, BN, BK, WM, WN><<<blocks, Cfg::NT, 0, s>>>(
       a.A, a.lda, a.Wt, (int)a.M, (int)a.N, (int)a.K, a.bias, a.epilogue, a.residual, a.C,
-      a.c_bf16, a.ldc, tiles_m, tiles_n);
+      a.c_bf16, a.ldc, tiles_m, tiles_n, a.rows_dev);
   return hipGetLastError();
 }
 
@@ -206,7 +208,8 @@ GemmPath pick(const GemmArgs &a) {
   static const GemmPath paths[] = {PATH_LDS_256x256, PATH_LDS_256x192, PATH_LDS_128x256,
                                    PATH_LDS_128x128};
   const bool deep = deep_ok(a);
-  int t = gemm_lds_tile(a.M, a.N, deep);
+  const int64_t m = gemm_pick_rows(a.M, a.m_hint);
+  int t = gemm_lds_tile(m, a.N, deep);
   if (t == 1 && a.epilogue >= EPI_GLU_SILU) t = 0;  // 96-column waves cannot pair blocks
   if (t == 0 && deep) return PATH_LDS_256x256_DEEP;
   // The 128 x 128 tile on 128-byte slabs keeps one slab in flight ahead, the
@@ -214,7 +217,7 @@ GemmPath pick(const GemmArgs &a) {
   // layer's 64-row GEMMs) waits on every slab's load and runs faster with
   // three ahead. Both run the same MFMA chain over K for every element.
   if (t == 3 && deep && a.c_bf16 && !a.residual &&
-      ((a.M + 127) / 128) * ((a.N + 127) / 128) * 8 > cu_count())
+      ((m + 127) / 128) * ((a.N + 127) / 128) * 8 > cu_count())
     return PATH_LDS_128x128_DEEP;
   return paths[t];
 }

@@ -14,10 +14,11 @@ __global__ __launch_bounds__(WGM *WGN * 64) void gemm_i8_k(
     const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ Wt, int M, int N,
     int K, const float *__restrict__ a_scale, const float *__restrict__ wscale,
     const float *__restrict__ bias, const float *residual, void *C, int64_t ldc, int tiles_m,
-    int tiles_n) {
+    int tiles_n, const int32_t *rows_dev) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   gemm_lds_body<BM, BN, WGM, WGN, NS, EPI, RES, OUT == 1, true, OUT == 2, RB>(
-      A, lda, Wt, M, N, K, bias, residual, C, ldc, tiles_m, tiles_n, a_scale, wscale, smem);
+      A, lda, Wt, M, N, K, bias, residual, C, ldc, tiles_m, tiles_n, a_scale, wscale, smem,
+      rows_dev);
 }
 
 template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, int OUT, int RB = 64>
@@ -35,7 +36,8 @@ hipError_t launch_t(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
   const int ntiles = tiles_m * tiles_n;
   const int g = mxk::persistent_grid(ntiles, grid);
   kern<<<g, Cfg::NT, Cfg::LDS, s>>>(a.A, a.lda, a.Wt, (int)a.M, (int)a.N, (int)a.K, a.a_scale,
-                                    a.wscale, a.bias, a.residual, a.C, a.ldc, tiles_m, tiles_n);
+                                    a.wscale, a.bias, a.residual, a.C, a.ldc, tiles_m, tiles_n,
+                                    a.rows_dev);
   return hipGetLastError();
 }
 
@@ -107,7 +109,7 @@ hipError_t launch_nc(const mxk::GemmI8Args &a, int grid, hipStream_t s) {
                             : launch_t<BM, BN, WGM, WGN, NS, NC | 2, false, 0>(a, grid, s);   \
     default: return hipErrorInvalidValue;                                                     \
   }
-  if (mxk::gemm_lds_tile(a.M, a.N, false) == 0) {
+  if (mxk::gemm_lds_tile(mxk::gemm_pick_rows(a.M, a.m_hint), a.N, false) == 0) {
     MX_I8_NC(256, 256, 2, 4, 3)
   }
   MX_I8_NC(128, 128, 2, 2, 4)
@@ -128,7 +130,7 @@ hipError_t gemm_i8(const GemmI8Args &a, hipStream_t s) {
   const int grid = cu_count();
   if (a.epilogue & EPI_NARROW_C) return launch_nc(a, grid, s);
   const bool deep = gemm_i8_deep(a);
-  int t = gemm_lds_tile(a.M, a.N, deep);
+  int t = gemm_lds_tile(gemm_pick_rows(a.M, a.m_hint), a.N, deep);
   if (t == 1 && a.epilogue >= EPI_GLU_SILU) t = 0;  // 96-column waves cannot pair blocks
   switch (t) {
     case 0: return deep ? launch_deep(a, grid, s) : launch<256, 256, 2, 4, 3>(a, grid, s);

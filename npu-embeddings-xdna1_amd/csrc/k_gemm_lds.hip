@@ -13,10 +13,11 @@ template <int BM, int BN, int WGM, int WGN, int NS, int EPI, bool RES, bool CBF,
 __global__ __launch_bounds__(WGM *WGN * 64) void gemm_lds_k(
     const uint16_t *__restrict__ A, int64_t lda, const uint16_t *__restrict__ Wt, int M, int N,
     int K, const float *__restrict__ bias, const float *residual, void *C, int64_t ldc,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, const int32_t *rows_dev) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   gemm_lds_body<BM, BN, WGM, WGN, NS, EPI, RES, CBF, false, false, RB>(
-      A, lda, Wt, M, N, K, bias, residual, C, ldc, tiles_m, tiles_n, nullptr, nullptr, smem);
+      A, lda, Wt, M, N, K, bias, residual, C, ldc, tiles_m, tiles_n, nullptr, nullptr, smem,
+      rows_dev);
 }
 
 }  // namespace
@@ -39,7 +40,7 @@ hipError_t gemm_lds_launch_t(const GemmArgs &a, int grid, hipStream_t s) {
   const int g = mxk::persistent_grid(ntiles, grid);
   kern<<<g, Cfg::NT, Cfg::LDS, s>>>((const uint16_t *)a.A, a.lda, (const uint16_t *)a.Wt,
                                     (int)a.M, (int)a.N, (int)a.K, a.bias, a.residual, a.C, a.ldc,
-                                    tiles_m, tiles_n);
+                                    tiles_m, tiles_n, a.rows_dev);
   return hipGetLastError();
 }
 
@@ -139,7 +140,7 @@ hipError_t gemm_lds_nc_launch(const GemmArgs &a, int grid, hipStream_t s) {
   }                                                                                       \
   if (e == 0) return gemm_lds_launch_t<BM, BN, WGM, WGN, NS, NC, false, false>(a, grid, s); \
   return hipErrorInvalidValue;
-  if (gemm_lds_tile(a.M, a.N, false) == 0) {
+  if (gemm_lds_tile(gemm_pick_rows(a.M, a.m_hint), a.N, false) == 0) {
     MX_LDS_NC(256, 256, 2, 4, 3)
   }
   MX_LDS_NC(128, 128, 2, 2, 4)

@@ -246,7 +246,7 @@ __device__ __forceinline__ void gemm_lds_body(
     const void *__restrict__ A, int64_t lda, const void *__restrict__ Wt, int M, int N, int K,
     const float *__restrict__ bias, const float *residual, void *C, int64_t ldc, int tiles_m,
     int tiles_n, const float *__restrict__ a_scale, const float *__restrict__ wscale,
-    uint8_t *smem) {
+    uint8_t *smem, const int32_t *rows_dev) {
   constexpr bool STG_BF = CBF && !RES;
   using Cfg = LdsCfg<BM, BN, WGM, WGN, NS, I8, stg_kind(CBF, RES), RB>;
   using PT = Path<I8>;
@@ -269,6 +269,12 @@ __device__ __forceinline__ void gemm_lds_body(
   // int8 kernel takes it as optional.
   const bool has_bias = !RAW && (!I8 || bias != nullptr);
 
+  // The live rows (M is then the bound A and C hold): the tile rows past them
+  // are not walked.
+  if (rows_dev) {
+    M = (int)live_rows(M, rows_dev);
+    tiles_m = (M + BM - 1) / BM;
+  }
   // This block's tiles: t(i) = first + i * stride, i < my_tiles. With a grid
   // that is a multiple of 8, XCD x owns tiles [x*chunk, (x+1)*chunk) and its
   // G/8 blocks interleave over them.

@@ -39,11 +39,12 @@ __global__ __launch_bounds__(256) void rope_qkv_k(uint16_t *__restrict__ qkv, in
                                                   int64_t rows, int S, int H, int hd,
                                                   const float *__restrict__ cos_t,
                                                   const float *__restrict__ sin_t,
-                                                  const int32_t *__restrict__ row_pos) {
+                                                  const int32_t *__restrict__ row_pos,
+                                                  const int32_t *rows_dev) {
   const int half = hd / 2, d = H * hd;
   const int per_head = half / PAIRS;  // thread units per head
   const int units = 2 * H * per_head;
-  const int64_t total = rows * units;
+  const int64_t total = live_rows(rows, rows_dev) * units;
   for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
        t += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = t / units;
@@ -103,8 +104,8 @@ __device__ __forceinline__ float4 load4(const void *p, bool bf, int64_t off) {
 
 template <bool IN_BF, bool OUT_BF, int ACT>
 __global__ __launch_bounds__(256) void glu_k(const void *__restrict__ in, void *__restrict__ out,
-                                             int64_t rows, int64_t f) {
-  const int64_t q4 = f / 4, total = rows * q4;
+                                             int64_t rows, int64_t f, const int32_t *rows_dev) {
+  const int64_t q4 = f / 4, total = live_rows(rows, rows_dev) * q4;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = i / q4, j = (i - r * q4) * 4;
@@ -148,7 +149,7 @@ hipError_t glu_interleave(const void *src, void *dst, int64_t f, int64_t row_byt
 
 hipError_t rope_qkv(uint16_t *qkv, int64_t ld, int64_t rows, int S, int H, int hd,
                     const float *cos_t, const float *sin_t, hipStream_t s,
-                    const int32_t *row_pos) {
+                    const int32_t *row_pos, const int32_t *rows_dev) {
   // Four pairs where their 8- and 16-byte accesses are aligned.
   const bool wide = hd % 8 == 0 && ld % 4 == 0 && (uintptr_t)qkv % 8 == 0 &&
                     (uintptr_t)cos_t % 16 == 0 && (uintptr_t)sin_t % 16 == 0;
@@ -157,22 +158,28 @@ hipError_t rope_qkv(uint16_t *qkv, int64_t ld, int64_t rows, int S, int H, int h
   int64_t g = (total + 255) / 256;
   if (g > 65536) g = 65536;
   if (pairs == 4)
-    rope_qkv_k<4><<<(unsigned)g, 256, 0, s>>>(qkv, ld, rows, S, H, hd, cos_t, sin_t, row_pos);
+    rope_qkv_k<4><<<(unsigned)g, 256, 0, s>>>(qkv, ld, rows, S, H, hd, cos_t, sin_t, row_pos,
+                                              rows_dev);
   else
-    rope_qkv_k<2><<<(unsigned)g, 256, 0, s>>>(qkv, ld, rows, S, H, hd, cos_t, sin_t, row_pos);
+    rope_qkv_k<2><<<(unsigned)g, 256, 0, s>>>(qkv, ld, rows, S, H, hd, cos_t, sin_t, row_pos,
+                                              rows_dev);
   return hipGetLastError();
 }
 
 hipError_t glu(const void *in, int in_bf, void *out, int out_bf, int64_t rows, int64_t f, int act,
-               hipStream_t s) {
+               hipStream_t s, const int32_t *rows_dev) {
   const int64_t total = rows * (f / 4);
   int64_t g = (total + 255) / 256;
   if (g > 65536) g = 65536;
 #define MX_GLU(A)                                                                          \
-  if (in_bf && out_bf) glu_k<true, true, A><<<(unsigned)g, 256, 0, s>>>(in, out, rows, f); \
-  else if (in_bf) glu_k<true, false, A><<<(unsigned)g, 256, 0, s>>>(in, out, rows, f);     \
-  else if (out_bf) glu_k<false, true, A><<<(unsigned)g, 256, 0, s>>>(in, out, rows, f);    \
-  else glu_k<false, false, A><<<(unsigned)g, 256, 0, s>>>(in, out, rows, f);
+  if (in_bf && out_bf)                                                                     \
+    glu_k<true, true, A><<<(unsigned)g, 256, 0, s>>>(in, out, rows, f, rows_dev);          \
+  else if (in_bf)                                                                          \
+    glu_k<true, false, A><<<(unsigned)g, 256, 0, s>>>(in, out, rows, f, rows_dev);         \
+  else if (out_bf)                                                                         \
+    glu_k<false, true, A><<<(unsigned)g, 256, 0, s>>>(in, out, rows, f, rows_dev);         \
+  else                                                                                     \
+    glu_k<false, false, A><<<(unsigned)g, 256, 0, s>>>(in, out, rows, f, rows_dev);
   if (act == 1) {
     MX_GLU(1)
   } else {

@@ -70,10 +70,11 @@ __global__ __launch_bounds__(256) void quantise_rows_k(const void *__restrict__ 
                                                        int64_t rows, int K,
                                                        const float *__restrict__ ias,
                                                        int8_t *__restrict__ q, int64_t ldq,
-                                                       float *__restrict__ a_scale) {
+                                                       float *__restrict__ a_scale,
+                                                       const int32_t *rows_dev) {
   const int lane = threadIdx.x & 63;
   const int64_t row = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  if (row >= live_rows(rows, rows_dev)) return;
   float4 t[NQ];
   float mx = 0.0f;
 #pragma unroll
@@ -97,10 +98,10 @@ __global__ __launch_bounds__(256) void layernorm_quant_k(
     const float *__restrict__ x, const void *__restrict__ y, int y_bf,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps, int64_t rows,
     int cols, float *out_f32, const float *__restrict__ ias, int8_t *__restrict__ q,
-    float *__restrict__ a_scale) {
+    float *__restrict__ a_scale, const int32_t *rows_dev) {
   const int lane = threadIdx.x & 63;
   const int64_t row = blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  if (row >= live_rows(rows, rows_dev)) return;
   // gamma, beta and the next GEMM's ias are read with the row, so their
   // latency runs under its loads instead of after the two reductions.
   float4 gm[NQ], bt[NQ], ia[NQ];
@@ -178,15 +179,16 @@ int quant_groups(int64_t K) {
 
 hipError_t quantise_rows(const void *a, int a_bf, int64_t lda, int64_t rows, int64_t K,
                          const float *ias, int8_t *q, int64_t ldq, float *a_scale,
-                         hipStream_t s) {
+                         hipStream_t s, const int32_t *rows_dev) {
   const int g = (int)((rows + 3) / 4);
 #define MX_Q_CASE(nq)                                                                         \
   case nq:                                                                                    \
     if (a_bf)                                                                                 \
-      quantise_rows_k<nq, true><<<g, 256, 0, s>>>(a, lda, rows, (int)K, ias, q, ldq, a_scale); \
+      quantise_rows_k<nq, true><<<g, 256, 0, s>>>(a, lda, rows, (int)K, ias, q, ldq, a_scale, \
+                                                  rows_dev);                                  \
     else                                                                                      \
       quantise_rows_k<nq, false><<<g, 256, 0, s>>>(a, lda, rows, (int)K, ias, q, ldq,         \
-                                                   a_scale);                                  \
+                                                   a_scale, rows_dev);                        \
     return hipGetLastError();
   switch (quant_groups(K)) {
     MX_Q_CASE(1)
@@ -210,12 +212,12 @@ hipError_t quantise_rows(const void *a, int a_bf, int64_t lda, int64_t rows, int
 hipError_t layernorm_quant(const float *x, const void *y, int y_bf, const float *gamma,
                            const float *beta, float eps, int64_t rows, int64_t cols,
                            float *out_f32, const float *ias, int8_t *q, float *a_scale,
-                           hipStream_t s) {
+                           hipStream_t s, const int32_t *rows_dev) {
   const int g = (int)((rows + 3) / 4);
 #define MX_LQ_CASE(nq)                                                                    \
   case nq:                                                                                \
     layernorm_quant_k<nq><<<g, 256, 0, s>>>(x, y, y_bf, gamma, beta, eps, rows, (int)cols, \
-                                            out_f32, ias, q, a_scale);                    \
+                                            out_f32, ias, q, a_scale, rows_dev);          \
     return hipGetLastError();
   switch (quant_groups(cols)) {
     MX_LQ_CASE(1)

@@ -119,7 +119,7 @@ static bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_
 
 int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t lda,
                  const uint16_t *Wt, int64_t N, const float *bias, int epilogue,
-                 const float *residual, void *C, int c_dtype, int64_t ldc) {
+                 const float *residual, void *C, int c_dtype, int64_t ldc, const Live &live) {
   if (!s) return fail(MX_E_INVALID, "gemm: null stream");
   if (!A || !Wt || !C) return fail(MX_E_INVALID, "gemm: null A, weight or C");
   if (M <= 0 || N <= 0 || K <= 0) return fail(MX_E_INVALID, "gemm: zero dimension");
@@ -142,7 +142,7 @@ int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t 
     return fail(MX_E_UNSUPPORTED, "gemm: a narrowed C takes no residual, and an fp32 one no "
                                   "activation");
   mxk::GemmArgs a{A, lda, Wt, M, N, K, bias, epilogue, residual, C, c_dtype == MX_BF16 ? 1 : 0,
-                  ldc};
+                  ldc, live.dev, live.hint};
   const hipError_t e = mxk::gemm(a, s->stream);
   if (narrow && e == hipErrorInvalidValue)
     return fail(MX_E_UNSUPPORTED, "gemm: a narrowed C runs on the direct-to-LDS kernel only "
@@ -204,7 +204,7 @@ void rope_tables_host(int64_t S, int64_t hd, double theta, const float *inv_freq
 
 int rope_checked(mx_stream *s, uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S, int64_t H,
                  int64_t hd, const float *cos_t, const float *sin_t, int64_t rows,
-                 const int32_t *row_pos) {
+                 const int32_t *row_pos, const Live &live) {
   if (!s) return fail(MX_E_INVALID, "rope_qkv: null stream");
   if (!qkv || !cos_t || !sin_t) return fail(MX_E_INVALID, "rope_qkv: null qkv or table");
   if (B <= 0 || S <= 0 || H <= 0 || hd <= 0) return fail(MX_E_INVALID, "rope_qkv: zero dimension");
@@ -217,12 +217,12 @@ int rope_checked(mx_stream *s, uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t
     return fail(MX_E_INVALID, "rope_qkv: misaligned qkv or table");
   if (B * S > INT32_MAX) return fail(MX_E_INVALID, "rope_qkv: too many rows");
   const hipError_t e = mxk::rope_qkv(qkv, ld_qkv, rows < 0 ? B * S : rows, (int)S, (int)H,
-                                     (int)hd, cos_t, sin_t, s->stream, row_pos);
+                                     (int)hd, cos_t, sin_t, s->stream, row_pos, live.dev);
   return e == hipSuccess ? MX_OK : hip_fail(e, "rope_qkv launch");
 }
 
 int glu_checked(mx_stream *s, const void *up, int up_dtype, void *out, int out_dtype,
-                int64_t rows, int64_t f, int act) {
+                int64_t rows, int64_t f, int act, const Live &live) {
   if (!s) return fail(MX_E_INVALID, "glu: null stream");
   if (!up || !out) return fail(MX_E_INVALID, "glu: null up or out");
   if (rows <= 0 || f <= 0) return fail(MX_E_INVALID, "glu: zero dimension");
@@ -234,17 +234,18 @@ int glu_checked(mx_stream *s, const void *up, int up_dtype, void *out, int out_d
   if (!aligned(up, up_dtype == MX_F32 ? 16 : 8) || !aligned(out, out_dtype == MX_F32 ? 16 : 8))
     return fail(MX_E_INVALID, "glu: misaligned up or out");
   const hipError_t e = mxk::glu(up, up_dtype == MX_BF16, out, out_dtype == MX_BF16, rows, f, act,
-                                s->stream);
+                                s->stream, live.dev);
   return e == hipSuccess ? MX_OK : hip_fail(e, "glu launch");
 }
 
 int take_data_error(mx_stream *s, int *flags) {
-  int h = 0;
-  hipError_t e = hipMemcpyAsync(&h, s->err_dev, sizeof(int), hipMemcpyDeviceToHost, s->stream);
+  int h[2] = {0, 0};
+  hipError_t e = hipMemcpyAsync(h, s->err_dev, sizeof(h), hipMemcpyDeviceToHost, s->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
   if (e != hipSuccess) return hip_fail(e, "reading the refusal flag");
-  *flags = h;
-  if (h) {
+  *flags = h[0];
+  if (h[1] > 0) s->last_rows = h[1];
+  if (h[0]) {
     e = hipMemsetAsync(s->err_dev, 0, sizeof(int), s->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) return hip_fail(e, "clearing the refusal flag");
@@ -328,8 +329,8 @@ int mx_stream_create(mx_ctx *ctx, mx_stream **out) {
     delete s;
     return hip_fail(e, "hipStreamCreate");
   }
-  e = dev_malloc((void **)&s->err_dev, sizeof(int));
-  if (e == hipSuccess) e = hipMemset(s->err_dev, 0, sizeof(int));
+  e = dev_malloc((void **)&s->err_dev, 2 * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(s->err_dev, 0, 2 * sizeof(int));
   if (e != hipSuccess) {
     (void)hipStreamDestroy(s->stream);
     delete s;
@@ -350,9 +351,20 @@ void mx_stream_destroy(mx_stream *s) {
 }
 
 int mx_sync(mx_stream *s) {
+  clear_error();
   if (!s) return fail(MX_E_INVALID, "mx_sync: null stream");
-  const hipError_t e = hipStreamSynchronize(s->stream);
-  return e == hipSuccess ? MX_OK : hip_fail(e, "hipStreamSynchronize");
+  // The refusals of asynchronous calls (mx_encoder_embed_async) wait in the
+  // stream's flag until here.
+  int flags = 0;
+  const int rc = take_data_error(s, &flags);
+  if (rc) return rc;
+  if (flags & 1)
+    return fail(MX_E_DATA, "mx_sync: an asynchronous embed on this stream met a token id "
+                           "outside the vocabulary (its row was embedded as zeros)");
+  if (flags & 2)
+    return fail(MX_E_DATA, "mx_sync: an asynchronous embed on this stream CLS-pooled a "
+                           "sequence whose first token is masked");
+  return MX_OK;
 }
 
 void *mx_stream_handle(mx_stream *s) { return s ? static_cast<void *>(s->stream) : nullptr; }

@@ -61,6 +61,16 @@ __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
   return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
 }
 
+// The rows a launch runs over: `rows` (the launch's bound, what its buffers
+// hold), or fewer when rows_dev is given -- a count an earlier kernel on the
+// stream wrote on the device (token packing's packed row total), read here so
+// that the host never waits for it. Clamped to [0, rows].
+__device__ __forceinline__ int64_t live_rows(int64_t rows, const int32_t *rows_dev) {
+  if (!rows_dev) return rows;
+  const int64_t r = *rows_dev;
+  return r < 0 ? 0 : (r < rows ? r : rows);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);

@@ -121,6 +121,12 @@ struct mx_encoder {
   // lengths: the attention work of a packed pass.
   std::vector<int32_t> plan_host;
   double packed_sq = 0.0;
+  // A packed pass whose row total stays on the device (no host wait in the
+  // middle of the call): the launches over live_bound rows (the B * S the
+  // workspace holds) take live -- the total's device address, and as the GEMM
+  // tile hint the stream's last total read with its refusal flag.
+  mx::Live live;
+  int64_t live_bound = 0;
   // timing
   bool timing = false;
   std::vector<hipEvent_t> events;
@@ -169,9 +175,19 @@ int ensure_ws(mx_encoder *enc, int64_t B, int64_t S) {
   return ensure_mask_ws(enc, B, rows);
 }
 
+// Work already queued (mx_encoder_embed_async) may still use the workspace a
+// regrowth frees: wait for the device first.
+int drain_workspace(const mx_encoder *enc) {
+  if (!enc->work.xb && !enc->work.add_mask) return MX_OK;
+  const hipError_t e = hipDeviceSynchronize();
+  return e == hipSuccess ? MX_OK : hip_fail(e, "workspace regrowth: draining queued work");
+}
+
 int ensure_ws_rows(mx_encoder *enc, int64_t rows, int64_t B) {
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
   {
+    const int drc = drain_workspace(enc);
+    if (drc) return drc;
     free_dev(enc->work.xb);
     free_dev(enc->work.qkv);
     free_dev(enc->work.ctxb);
@@ -211,6 +227,8 @@ int ensure_mask_ws(mx_encoder *enc, int64_t B, int64_t rows) {
   if (B > enc->ws_batch || rows > enc->ws_mask_rows) {
     const int64_t nb = B > enc->ws_batch ? B : enc->ws_batch;
     const int64_t nr = rows > enc->ws_mask_rows ? rows : enc->ws_mask_rows;
+    const int drc = drain_workspace(enc);
+    if (drc) return drc;
     free_dev(enc->work.add_mask);
     free_dev(enc->work.kv_len);
     free_dev(enc->work.seq_start);
@@ -269,20 +287,27 @@ int check_placement() {
                   "/ mx_softmax_rows / mx_layernorm / mx_gelu.");
 }
 
+// The live rows of a launch over M rows: the pass's device-side count when M
+// is the pass's row bound, else M itself.
+mx::Live live_of(const mx_encoder *enc, int64_t M) {
+  return M == enc->live_bound ? enc->live : mx::Live{};
+}
+
 int gemm_l(mx_encoder *enc, mx_stream *s, int site, const uint16_t *A, int64_t M, int64_t K,
            const uint16_t *Wt, int64_t N, const float *bias, int epi, const float *resid,
            void *C, int c_dtype) {
   Bracket br(enc, s->stream, CAT_GEMM + 16 * site);
   enc->gemm_flop += 2.0 * M * N * K;
   enc->site_flop[site] += 2.0 * M * N * K;
-  return gemm_checked(s, A, M, K, K, Wt, N, bias, epi, resid, C, c_dtype, N);
+  return gemm_checked(s, A, M, K, K, Wt, N, bias, epi, resid, C, c_dtype, N, live_of(enc, M));
 }
 
 int ln_l(mx_encoder *enc, mx_stream *s, const void *x, int x_dt, const void *y, int y_dt,
          const float *g, const float *b, int64_t rows, float *of, uint16_t *ob) {
   Bracket br(enc, s->stream, CAT_LN);
-  const hipError_t e = mxk::layernorm(x, x_dt == MX_BF16, y, y_dt == MX_BF16, g, b,
-                                      enc->desc.ln_eps, rows, enc->desc.hidden, of, ob, s->stream);
+  const hipError_t e =
+      mxk::layernorm(x, x_dt == MX_BF16, y, y_dt == MX_BF16, g, b, enc->desc.ln_eps, rows,
+                     enc->desc.hidden, of, ob, s->stream, live_of(enc, rows).dev);
   return e == hipSuccess ? MX_OK : hip_fail(e, "layernorm launch");
 }
 
@@ -295,21 +320,22 @@ int gemm_i8_l(mx_encoder *enc, mx_stream *s, int site, int64_t M, int64_t K, con
   Bracket br(enc, s->stream, CAT_GEMM + 16 * site);
   enc->gemm_flop += 2.0 * M * N * K;
   enc->site_flop[site] += 2.0 * M * N * K;
-  return gemm_i8_checked(s, enc->work.xq, enc->work.sa, M, K, K, Wq, ws, N, bias, epi, resid, C, c_dtype,
-                         N);
+  return gemm_i8_checked(s, enc->work.xq, enc->work.sa, M, K, K, Wq, ws, N, bias, epi, resid, C,
+                         c_dtype, N, live_of(enc, M));
 }
 
 int lnq_l(mx_encoder *enc, mx_stream *s, const float *x, const void *y, int y_dt, const float *g,
           const float *b, int64_t rows, float *of, const float *ias) {
   Bracket br(enc, s->stream, CAT_LN);
   return layernorm_i8_checked(s, x, y, y_dt, g, b, enc->desc.ln_eps, rows, enc->desc.hidden, of,
-                              ias, enc->work.xq, enc->work.sa);
+                              ias, enc->work.xq, enc->work.sa, live_of(enc, rows));
 }
 
 int quant_l(mx_encoder *enc, mx_stream *s, const void *a, int a_dtype, int64_t rows, int64_t K,
             const float *ias) {
   Bracket br(enc, s->stream, CAT_OTHER);
-  return quantise_checked(s, a, a_dtype, K, rows, K, ias, enc->work.xq, K, enc->work.sa);
+  return quantise_checked(s, a, a_dtype, K, rows, K, ias, enc->work.xq, K, enc->work.sa,
+                          live_of(enc, rows));
 }
 
 // RoPE tables for positions [0, S), built on the host once (double angles,
@@ -337,13 +363,14 @@ int rope_l(mx_encoder *enc, mx_stream *s, int64_t B, int64_t S, int64_t M,
            const int32_t *row_pos) {
   Bracket br(enc, s->stream, CAT_OTHER);
   return rope_checked(s, enc->work.qkv, 3 * enc->desc.hidden, B, S, enc->desc.heads,
-                      enc->desc.head_dim, enc->rope_cos, enc->rope_sin, M, row_pos);
+                      enc->desc.head_dim, enc->rope_cos, enc->rope_sin, M, row_pos,
+                      live_of(enc, M));
 }
 
 int glu_l(mx_encoder *enc, mx_stream *s, int64_t M, int in_dtype, int out_dtype) {
   Bracket br(enc, s->stream, CAT_OTHER);
   return glu_checked(s, enc->work.up, in_dtype, enc->work.glu, out_dtype, M, enc->desc.ffn,
-                     enc->desc.gated_ffn);
+                     enc->desc.gated_ffn, live_of(enc, M));
 }
 
 // Whether FFN-up can carry the gated FFN in its epilogue: whole 64-row
@@ -410,13 +437,16 @@ int gemm_glu_l(mx_encoder *enc, mx_stream *s, const LayerW &w, int64_t M) {
   enc->site_flop[SITE_UP] += 2.0 * M * 2 * f * d;
   const int epi =
       enc->desc.gated_ffn == MX_GATED_SILU ? mxk::EPI_GLU_SILU : mxk::EPI_GLU_GELU;
+  const mx::Live lv = live_of(enc, M);
   hipError_t e;
   if (enc->i8) {
-    const mxk::GemmI8Args a{enc->work.xq, d,       w.wqg,   M, 2 * f, d,   enc->work.sa,
-                            w.wsg,   w.bg,    epi,     nullptr,  enc->work.glu, 1, f};
+    const mxk::GemmI8Args a{enc->work.xq, d,   w.wqg, M,       2 * f,         d,
+                            enc->work.sa, w.wsg, w.bg, epi, nullptr, enc->work.glu,
+                            1,            f,     lv.dev, lv.hint};
     e = mxk::gemm_i8(a, s->stream);
   } else {
-    const mxk::GemmArgs a{enc->work.xb, d, w.wg, M, 2 * f, d, w.bg, epi, nullptr, enc->work.glu, 1, f};
+    const mxk::GemmArgs a{enc->work.xb, d, w.wg, M, 2 * f, d, w.bg, epi, nullptr, enc->work.glu,
+                          1,            f, lv.dev, lv.hint};
     e = mxk::gemm(a, s->stream);
   }
   return e == hipSuccess ? MX_OK : hip_fail(e, "gemm launch (FFN-up with the gated FFN)");
@@ -1314,15 +1344,20 @@ struct Pass {
 int pass_plan(mx_encoder *enc, Pass &p) {
   Bracket br(enc, p.s->stream, CAT_OTHER);
   hipError_t e = mxk::mask_build(p.mask, p.B, p.S, p.w.add_mask, p.w.kv_len, p.s->stream);
+  // The packed total also goes to the stream's flag block (word 1), read with
+  // the refusal flag at the end of the call: the next pass's tile hint.
   if (e == hipSuccess)
-    e = mxk::pack_plan(p.w.kv_len, p.B, p.w.seq_start, p.w.seq_start + p.B + 1, p.s->stream);
+    e = mxk::pack_plan(p.w.kv_len, p.B, p.w.seq_start, p.w.seq_start + p.B + 1, p.s->stream,
+                       p.s->err_dev + 1);
   return e == hipSuccess ? MX_OK : hip_fail(e, "embed launch");
 }
 
-// The pass's rows and its embedding sum. With token packing the packed row
-// count is read back, since the launches are sized on the host (the whole
-// plan when timing, for the attention work); carve, when given, then takes
-// the row-shaped buffers for that many rows from the static scratch.
+// The pass's rows and its embedding sum. With token packing the launches are
+// sized on the host for B * S rows and the packed total stays on the device,
+// where every row-wise kernel of the pass reads it (enc->live): the host never
+// waits in the middle of the call. Two cases read it back instead: timing
+// (the whole plan, for the attention work) and the static scratch (carve,
+// which takes the row-shaped buffers for exactly that many rows).
 int pass_rows(mx_encoder *enc, Pass &p, Carver *carve) {
   Bracket br(enc, p.s->stream, CAT_OTHER);
   const int64_t B = p.B, S = p.S;
@@ -1330,25 +1365,29 @@ int pass_rows(mx_encoder *enc, Pass &p, Carver *carve) {
   hipError_t e = hipSuccess;
   p.rows = Rows{B * S};
   if (enc->packing) {
-    int32_t total = 0;
-    if (!enc->timing) {
-      e = hipMemcpyAsync(&total, p.w.seq_start + B, sizeof(int32_t), hipMemcpyDeviceToHost,
-                         p.s->stream);
-      if (e == hipSuccess) e = hipStreamSynchronize(p.s->stream);
-      enc->packed_sq = 0.0;
-    } else {
+    int64_t total = B * S;
+    enc->packed_sq = 0.0;
+    if (enc->timing) {
       enc->plan_host.resize(static_cast<size_t>(B + 1));
       e = hipMemcpyAsync(enc->plan_host.data(), p.w.seq_start, (B + 1) * sizeof(int32_t),
                          hipMemcpyDeviceToHost, p.s->stream);
       if (e == hipSuccess) e = hipStreamSynchronize(p.s->stream);
       if (e == hipSuccess) {
         total = enc->plan_host[B];
-        enc->packed_sq = 0.0;
         for (int64_t b = 0; b < B; ++b) {
           const double L = enc->plan_host[b + 1] - enc->plan_host[b];
           enc->packed_sq += L * L;
         }
       }
+    } else if (carve) {
+      int32_t t = 0;
+      e = hipMemcpyAsync(&t, p.w.seq_start + B, sizeof(int32_t), hipMemcpyDeviceToHost,
+                         p.s->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(p.s->stream);
+      total = t;
+    } else {
+      enc->live = mx::Live{p.w.seq_start + B, p.s->last_rows};
+      enc->live_bound = B * S;
     }
     if (e != hipSuccess) return hip_fail(e, "reading the packed row count");
     if (carve) {
@@ -1408,9 +1447,11 @@ int embed_pass(mx_encoder *enc, Pass &p, Carver *carve) {
 }
 
 // mx_encoder_embed; carve: the static scratch instead of the encoder's
-// workspace (mx_encoder_embed_static).
+// workspace (mx_encoder_embed_static); wait: read the refusal flag at the end
+// (synchronising the stream), else leave it for mx_sync
+// (mx_encoder_embed_async).
 int embed_body(mx_encoder *enc, mx_stream *s, const int32_t *ids, const float *attn_mask,
-               int64_t B, int64_t S, float *out, Carver *carve) {
+               int64_t B, int64_t S, float *out, Carver *carve, bool wait = true) {
   Pass p;
   p.s = s;
   p.w = enc->work;
@@ -1428,7 +1469,9 @@ int embed_body(mx_encoder *enc, mx_stream *s, const int32_t *ids, const float *a
   const Work own = enc->work;
   int rc = embed_pass(enc, p, carve);
   enc->work = own;
-  if (rc) return rc;
+  enc->live = mx::Live{};
+  enc->live_bound = 0;
+  if (rc || !wait) return rc;
   int flags = 0;
   rc = take_data_error(s, &flags);
   return rc ? rc : data_refusal(enc, flags);
@@ -1480,6 +1523,18 @@ int mx_encoder_embed(mx_encoder *enc, mx_stream *s, const int32_t *ids, const fl
   if (!rc) rc = ensure_ws(enc, B, S);
   if (rc) return rc;
   return embed_body(enc, s, ids, attn_mask, B, S, out, nullptr);
+}
+
+int mx_encoder_embed_async(mx_encoder *enc, mx_stream *s, const int32_t *ids,
+                           const float *attn_mask, int64_t B, int64_t S, float *out) {
+  clear_error();
+  int rc = embed_args(enc, s, ids, attn_mask, B, S, out, "encoder_embed_async");
+  if (!rc) rc = use_device(enc->ctx);
+  if (!rc) rc = check_placement();
+  if (!rc) rc = mx_encoder_ready(enc);
+  if (!rc) rc = ensure_ws(enc, B, S);
+  if (rc) return rc;
+  return embed_body(enc, s, ids, attn_mask, B, S, out, nullptr, false);
 }
 
 int mx_encoder_embed_static(mx_encoder *enc, mx_stream *s, const int32_t *ids,

@@ -186,7 +186,7 @@ int stage_i4(mx_ctx *ctx, const uint8_t *packed_host, const float *gscale_host, 
 int gemm_i8_checked(mx_stream *s, const int8_t *A, const float *a_scale, int64_t M, int64_t K,
                     int64_t lda, const int8_t *Wt, const float *wscale, int64_t N,
                     const float *bias, int epilogue, const float *residual, void *C,
-                    int c_dtype, int64_t ldc) {
+                    int c_dtype, int64_t ldc, const Live &live) {
   // The 32-bit row offsets come first: a shape the kernel cannot address is
   // refused whatever else is wrong with the call.
   if (!mxk::lds_offsets_fit(lda, K, 1))
@@ -246,13 +246,16 @@ int gemm_i8_checked(mx_stream *s, const int8_t *A, const float *a_scale, int64_t
                     residual,
                     C,
                     c_dtype == MX_BF16 ? 1 : c_dtype == MX_I32 ? 2 : 0,
-                    ldc};
+                    ldc,
+                    live.dev,
+                    live.hint};
   const hipError_t e = mxk::gemm_i8(a, s->stream);
   return e == hipSuccess ? MX_OK : hip_fail(e, "gemm_i8 launch");
 }
 
 int quantise_checked(mx_stream *s, const void *a, int a_dtype, int64_t lda, int64_t rows,
-                     int64_t K, const float *ias, int8_t *q, int64_t ldq, float *a_scale) {
+                     int64_t K, const float *ias, int8_t *q, int64_t ldq, float *a_scale,
+                     const Live &live) {
   if (!s) return fail(MX_E_INVALID, "quantise_a_int8: null stream");
   if (!a || !ias || !q || !a_scale)
     return fail(MX_E_INVALID, "quantise_a_int8: null a, ias, q or a_scale");
@@ -269,14 +272,14 @@ int quantise_checked(mx_stream *s, const void *a, int a_dtype, int64_t lda, int6
   if (rows > (int64_t)INT32_MAX * 4)
     return fail(MX_E_INVALID, "quantise_a_int8: too many rows");
   const hipError_t e = mxk::quantise_rows(a, a_dtype == MX_BF16, lda, rows, K, ias, q, ldq,
-                                          a_scale, s->stream);
+                                          a_scale, s->stream, live.dev);
   return e == hipSuccess ? MX_OK : hip_fail(e, "quantise_a_int8 launch");
 }
 
 int layernorm_i8_checked(mx_stream *s, const float *x, const void *y, int y_dtype,
                          const float *gamma, const float *beta, float eps, int64_t rows,
                          int64_t cols, float *out_f32, const float *ias, int8_t *q,
-                         float *a_scale) {
+                         float *a_scale, const Live &live) {
   if (!s) return fail(MX_E_INVALID, "layernorm_i8: null stream");
   if (!x || !gamma || !beta || !ias || !q || !a_scale)
     return fail(MX_E_INVALID, "layernorm_i8: null x, gamma, beta, ias, q or a_scale");
@@ -293,7 +296,7 @@ int layernorm_i8_checked(mx_stream *s, const float *x, const void *y, int y_dtyp
     return fail(MX_E_INVALID, "layernorm_i8: misaligned tensor");
   if (rows > (int64_t)INT32_MAX * 4) return fail(MX_E_INVALID, "layernorm_i8: too many rows");
   const hipError_t e = mxk::layernorm_quant(x, y, y_dtype == MX_BF16, gamma, beta, eps, rows, cols,
-                                            out_f32, ias, q, a_scale, s->stream);
+                                            out_f32, ias, q, a_scale, s->stream, live.dev);
   return e == hipSuccess ? MX_OK : hip_fail(e, "layernorm_i8 launch");
 }
 

@@ -41,7 +41,12 @@ struct mx_ctx {
 struct mx_stream {
   mx_ctx *ctx = nullptr;
   hipStream_t stream = nullptr;
-  int *err_dev = nullptr;  // device flag for kernels that refuse data
+  // Two device words: [0] the flags of kernels that refuse data, [1] the last
+  // packed row total a pass planned on this stream.
+  int *err_dev = nullptr;
+  // Word 1 as last read with the flags (host): the GEMM tile hint of the next
+  // packed pass on this stream.
+  int last_rows = 0;
 };
 
 namespace mx {
@@ -52,10 +57,20 @@ int use_device(const mx_ctx *ctx);
 // device panel.
 int stage_panel(mx_ctx *ctx, const void *kn_host, int dtype, int64_t K, int64_t N,
                 uint16_t **out);
+// The live rows of a launch whose row count is known on the device only
+// (token packing's packed total, left on the device so the host never waits
+// for it): dev points at the count (the launch's M is then the bound its
+// buffers hold), hint is the row count its GEMM tile is chosen for (every
+// tile gives the same bits; the choice moves the time only). Default: M rows.
+struct Live {
+  const int32_t *dev = nullptr;
+  int64_t hint = 0;
+};
 // Validated launches shared by the per-op entry points and the encoder.
 int gemm_checked(mx_stream *s, const uint16_t *A, int64_t M, int64_t K, int64_t lda,
                  const uint16_t *Wt, int64_t N, const float *bias, int epilogue,
-                 const float *residual, void *C, int c_dtype, int64_t ldc);
+                 const float *residual, void *C, int c_dtype, int64_t ldc,
+                 const Live &live = Live{});
 int attention_checked(mx_stream *s, const uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S,
                       int64_t H, int64_t hd, float scale, const float *add_mask,
                       const int32_t *kv_len, uint16_t *ctx, int64_t ld_ctx,
@@ -84,23 +99,25 @@ int stage_i4(mx_ctx *ctx, const uint8_t *packed_host, const float *gscale_host, 
 int gemm_i8_checked(mx_stream *s, const int8_t *A, const float *a_scale, int64_t M, int64_t K,
                     int64_t lda, const int8_t *Wt, const float *wscale, int64_t N,
                     const float *bias, int epilogue, const float *residual, void *C,
-                    int c_dtype, int64_t ldc);
+                    int c_dtype, int64_t ldc, const Live &live = Live{});
 int quantise_checked(mx_stream *s, const void *a, int a_dtype, int64_t lda, int64_t rows,
-                     int64_t K, const float *ias, int8_t *q, int64_t ldq, float *a_scale);
+                     int64_t K, const float *ias, int8_t *q, int64_t ldq, float *a_scale,
+                     const Live &live = Live{});
 int layernorm_i8_checked(mx_stream *s, const float *x, const void *y, int y_dtype,
                          const float *gamma, const float *beta, float eps, int64_t rows,
                          int64_t cols, float *out_f32, const float *ias, int8_t *q,
-                         float *a_scale);
+                         float *a_scale, const Live &live = Live{});
 // The RoPE / gated-FFN archs: host tables, and validated launches.
 void rope_tables_host(int64_t S, int64_t hd, double theta, const float *inv_freq, float *cos_t,
                       float *sin_t);
 // rows / row_pos: packed rows (rows < 0: the dense B*S).
 int rope_checked(mx_stream *s, uint16_t *qkv, int64_t ld_qkv, int64_t B, int64_t S, int64_t H,
                  int64_t hd, const float *cos_t, const float *sin_t, int64_t rows = -1,
-                 const int32_t *row_pos = nullptr);
+                 const int32_t *row_pos = nullptr, const Live &live = Live{});
 int glu_checked(mx_stream *s, const void *up, int up_dtype, void *out, int out_dtype,
-                int64_t rows, int64_t f, int act);
-// Read and clear the stream's data-refusal flag (synchronises the stream).
+                int64_t rows, int64_t f, int act, const Live &live = Live{});
+// Read and clear the stream's data-refusal flag (synchronises the stream);
+// word 1, the last packed row total, goes to s->last_rows.
 int take_data_error(mx_stream *s, int *flags);
 // The static device scratch of mx_encoder_embed_static (mx_static.hip): its
 // address on each device is looked up once, by mx_create with that device

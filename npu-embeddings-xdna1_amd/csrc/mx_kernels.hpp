@@ -1,6 +1,11 @@
 // mx_kernels.hpp -- host-side launchers of the gfx950 kernels. Shapes and
 // pointers are validated by the C ABI layer before any of these is called;
 // each launcher only picks a kernel variant and a grid.
+//
+// rows_dev (nullable) on the row-wise launchers: the live row count, an int on
+// the device that an earlier kernel of the stream wrote (token packing's
+// packed total); the grid covers `rows`, the bound the buffers hold, and the
+// kernels skip the rows at or past the live count.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -14,7 +19,7 @@ hipError_t gelu(const void *x, int x_bf, void *y, int y_bf, int64_t n, int varia
                 hipStream_t s);
 hipError_t layernorm(const void *x, int x_bf, const void *y, int y_bf, const float *gamma,
                      const float *beta, float eps, int64_t rows, int64_t cols, float *out_f32,
-                     uint16_t *out_bf16, hipStream_t s);
+                     uint16_t *out_bf16, hipStream_t s, const int32_t *rows_dev = nullptr);
 // The accelerator LayerNorm (kernels/layernorm.cc:85-142, conv_even): bf16
 // [rows, cols] in and out (out may alias x), cols % 16 == 0, cols <= 4096,
 // 16-byte aligned x, out, gamma and beta.
@@ -41,9 +46,9 @@ hipError_t gather_cls(const float *x, const uint16_t *ctx, const int32_t *seq_st
 // packed rows) and, when order is non-null, order[0..B) = the sequence
 // indices by decreasing kv_len (attention's launch order); the embedding sum
 // of the rows s < kv_len[b] into packed row seq_start[b] + s, with
-// row_pos[packed row] = s.
+// row_pos[packed row] = s. total_out (nullable): a second copy of seq_start[B].
 hipError_t pack_plan(const int32_t *kv_len, int64_t B, int32_t *seq_start, int32_t *order,
-                     hipStream_t s);
+                     hipStream_t s, int32_t *total_out = nullptr);
 hipError_t embed_sum_packed(const int32_t *ids, int64_t B, int64_t S, int64_t d,
                             const float *word, int64_t vocab, const float *pos,
                             const float *type0, const int32_t *kv_len, const int32_t *seq_start,
@@ -70,6 +75,12 @@ struct GemmArgs {
   void *C;
   int c_bf16;
   int64_t ldc;
+  // rows_dev (nullable): the live row count on the device (<= M, which is then
+  // the bound the buffers hold); m_hint (> 0): the row count the tile is
+  // chosen for instead of M -- every tile runs the same MFMA chain over K for
+  // each element, so the choice moves the time only, never a bit of C.
+  const int32_t *rows_dev = nullptr;
+  int64_t m_hint = 0;
 };
 hipError_t gemm(const GemmArgs &a, hipStream_t s);
 
@@ -93,6 +104,9 @@ hipError_t glu_interleave(const void *src, void *dst, int64_t f, int64_t row_byt
 // 2: 128x256, 3: 128x128; deep: the 256 x 256 tile would run on 128-byte
 // slabs) and the resident blocks of a persistent launch.
 int gemm_lds_tile(int64_t M, int64_t N, bool deep);
+// The row count a launch's tile is chosen for: the hint when one is given
+// (and below M), else M.
+inline int64_t gemm_pick_rows(int64_t M, int64_t hint) { return hint > 0 && hint < M ? hint : M; }
 int cu_count();
 // Blocks of a persistent launch over ntiles tiles with `grid` resident: at
 // most one per tile, rounded up to a whole number per XCD (a multiple of 8)
@@ -130,6 +144,8 @@ struct GemmI8Args {
   void *C;
   int c_dtype;  // 0 fp32, 1 bf16, 2 int32 (raw accumulators)
   int64_t ldc;
+  const int32_t *rows_dev = nullptr;  // as GemmArgs
+  int64_t m_hint = 0;
 };
 hipError_t gemm_i8(const GemmI8Args &a, hipStream_t s);
 // Whether the 256 x 256 tile runs on 128-byte slabs for this call.
@@ -140,13 +156,13 @@ bool gemm_i8_deep(const GemmI8Args &a);
 // K <= 8192.
 hipError_t quantise_rows(const void *a, int a_bf, int64_t lda, int64_t rows, int64_t K,
                          const float *ias, int8_t *q, int64_t ldq, float *a_scale,
-                         hipStream_t s);
+                         hipStream_t s, const int32_t *rows_dev = nullptr);
 // add_norm_quant: LayerNorm(x + y) -> out_f32 (nullable) and its quantisation
 // with ias -> q, a_scale. cols % 4 == 0, cols <= 4096.
 hipError_t layernorm_quant(const float *x, const void *y, int y_bf, const float *gamma,
                            const float *beta, float eps, int64_t rows, int64_t cols,
                            float *out_f32, const float *ias, int8_t *q, float *a_scale,
-                           hipStream_t s);
+                           hipStream_t s, const int32_t *rows_dev = nullptr);
 int quant_groups(int64_t K);
 
 // The RoPE / gated-FFN archs (k_glu.hip): in-place RoPE of Q and K in bf16
@@ -154,9 +170,9 @@ int quant_groups(int64_t K);
 // row_pos (nullable): each row's position (packed rows), else row % S.
 hipError_t rope_qkv(uint16_t *qkv, int64_t ld, int64_t rows, int S, int H, int hd,
                     const float *cos_t, const float *sin_t, hipStream_t s,
-                    const int32_t *row_pos = nullptr);
+                    const int32_t *row_pos = nullptr, const int32_t *rows_dev = nullptr);
 hipError_t glu(const void *in, int in_bf, void *out, int out_bf, int64_t rows, int64_t f, int act,
-               hipStream_t s);
+               hipStream_t s, const int32_t *rows_dev = nullptr);
 
 // Container operand tiled (tile_k, tile_n) with (mac_s, mac_t) sub-tiles ->
 // [N, K] panel (k_panel.hip). Shapes checked by the caller.

@@ -113,6 +113,7 @@ SIGNATURES = {
     "mx_encoder_ready": (_int, [_vp]),
     "mx_encoder_run": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64]),
     "mx_encoder_embed": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "mx_encoder_embed_async": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "mx_encoder_embed_static": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "mx_static_guard_hold": (_int, [_int]),
     "mx_static_guard_release": (_int, [_int]),
@@ -565,6 +566,12 @@ class Encoder:
     def embed(self, ids, attn_mask, B, S, out):
         check(lib().mx_encoder_embed(self.handle, self.ctx.stream, _p(ids), _p(attn_mask), B,
                                      S, _p(out)))
+
+    def embed_async(self, ids, attn_mask, B, S, out):
+        """mx_encoder_embed_async: the embed queued without its closing wait;
+        out is complete (and the data refusals reported) at ctx.sync()."""
+        check(lib().mx_encoder_embed_async(self.handle, self.ctx.stream, _p(ids),
+                                           _p(attn_mask), B, S, _p(out)))
 
     def embed_static(self, ids, attn_mask, B, S, out):
         """mx_encoder_embed_static: the same embed with its workspace carved from

@@ -90,6 +90,26 @@ def test_int8_packed_equals_padded(ctx):
     assert _same(packed, padded)
 
 
+def test_packed_count_on_the_device_whatever_the_tile_hint(ctx):
+    """The packed row count stays on the device; the GEMM tile is picked from
+    the previous call's count. Batches of very different packed counts in
+    turn -- each call's hint is the other batch's count, or none on the
+    first call -- give the padded computation's rows bit for bit."""
+    m = synth.make_model("bge_base", layers=2)
+    enc = mxenc.Encoder(ctx, m)
+    ids, am, _ = synth.make_text_inputs(m, batch=32, seq=512)
+    short = am.copy()
+    short[:, 80:] = 0.0                       # ~2,560 packed rows
+    full = np.ones_like(am)                   # 16,384 rows: the bound itself
+    want = {}
+    for name, mask in (("short", short), ("full", full), ("mixed", am)):
+        want[name] = _embed(ctx, enc, ids, mask, False)
+    for name in ("short", "full", "mixed", "short", "mixed", "full", "short"):
+        mask = {"short": short, "full": full, "mixed": am}[name]
+        assert _same(_embed(ctx, enc, ids, mask, True), want[name]), name
+    enc.close()
+
+
 def test_packing_then_a_longer_sequence(ctx):
     """Workspaces regrow when the sequence grows at a fixed batch (mask,
     positions and packed rows)."""
