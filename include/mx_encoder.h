@@ -527,8 +527,9 @@ int64_t mx_device_allocations(void);
  * EmbedService::chunk (embed_service.cpp:29-64) computes the padded batch,
  * which off restores. The packed row count stays on the device: the
  * launches are sized for B*S rows and every row-wise kernel stops at the
- * count, so the host does not wait in the middle of the call (with timing
- * on, and in mx_encoder_embed_static, it is read back instead). The call
+ * count, so the host does not wait in the middle of the call (it is read
+ * back instead with timing on, in mx_encoder_embed_static and on a stream's
+ * first packed call, whose GEMM tiles have no earlier count to go by). The call
  * still synchronises its stream once, at its end, to read the refusal flag.
  * mx_encoder_run always computes every row (it returns them all). */
 int mx_encoder_set_packing(mx_encoder *enc, int on);

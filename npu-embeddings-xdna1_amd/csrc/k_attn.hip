@@ -226,27 +226,49 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
       // probabilities and PV products are skipped -- each would be exp2(-inf)
       // = 0.
       const bool h1 = t * BKV + 32 < kvl;
+      // The staged mask entry this lane tests, read first: its latency runs
+      // under the score MFMAs instead of after them.
+      const float *smk = (const float *)(sl + 2 * TILE);
+      float mword = smk[lane];  // unused (and never written) without a mask
       // Each half's chain starts from an immediate zero accumulator; a
       // skipped second half is left unset (nothing reads it), so no register
-      // copies merge it with the computed one.
+      // copies merge it with the computed one. With both halves live their
+      // two chains alternate, each k-step's fragments read one step ahead, so
+      // neither the LDS reads nor a chain's dependent MFMAs stall the wave.
       f32x16 sc[2];
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        if (sub == 1 && !h1) continue;
+      auto kfrag = [&](int sub, int kk) {
+        return *(const bf16x8 *)(sl + (sub * 32 + li) * ROWB + (((2 * kk + g) ^ swk) * 16));
+      };
+      if (h1) {
+        bf16x8 ka = kfrag(0, 0), kb = kfrag(1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // k-step 0's two reads
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
-          const bf16x8 kf = *(const bf16x8 *)(sl + (sub * 32 + li) * ROWB +
-                                              (((2 * kk + g) ^ swk) * 16));
-          sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk],
-                                                            kk == 0 ? f32x16{} : sc[sub], 0,
-                                                            0, 0);
+          bf16x8 na = ka, nb = kb;
+          if (kk + 1 < NKK) {
+            na = kfrag(0, kk + 1);
+            nb = kfrag(1, kk + 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the next k-step's reads
+          }
+          sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[kk], kk == 0 ? f32x16{} : sc[0],
+                                                          0, 0, 0);
+          sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb, qf[kk], kk == 0 ? f32x16{} : sc[1],
+                                                          0, 0, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // then this k-step's MFMAs
+          ka = na;
+          kb = nb;
         }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+          sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfrag(0, kk), qf[kk],
+                                                          kk == 0 ? f32x16{} : sc[0], 0, 0, 0);
       }
       // The tile needs logits (mask added, keys past kv_len at -inf) if it
       // reaches past kv_len or has a nonzero mask entry.
-      const float *smk = (const float *)(sl + 2 * TILE);
       bool masked = (t + 1) * BKV > kvl || force_logits;
-      if (add_mask) masked = masked || __ballot(smk[lane] != 0.0f) != 0;
+      asm volatile("" : "+v"(mword));  // first read of the mask entry: after the MFMAs
+      if (add_mask) masked = masked || __ballot(mword != 0.0f) != 0;
       float cc;
       if (masked) {
         // Lane (li, g) holds keys sub * 32 + 8 rr + 4 g + e of accumulator

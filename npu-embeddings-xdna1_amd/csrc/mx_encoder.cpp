@@ -1355,9 +1355,10 @@ int pass_plan(mx_encoder *enc, Pass &p) {
 // The pass's rows and its embedding sum. With token packing the launches are
 // sized on the host for B * S rows and the packed total stays on the device,
 // where every row-wise kernel of the pass reads it (enc->live): the host never
-// waits in the middle of the call. Two cases read it back instead: timing
-// (the whole plan, for the attention work) and the static scratch (carve,
-// which takes the row-shaped buffers for exactly that many rows).
+// waits in the middle of the call. Three cases read it back instead: timing
+// (the whole plan, for the attention work), the static scratch (carve, which
+// takes the row-shaped buffers for exactly that many rows) and the first
+// packed pass on a stream (no earlier total to choose the GEMM tiles by).
 int pass_rows(mx_encoder *enc, Pass &p, Carver *carve) {
   Bracket br(enc, p.s->stream, CAT_OTHER);
   const int64_t B = p.B, S = p.S;
@@ -1379,12 +1380,15 @@ int pass_rows(mx_encoder *enc, Pass &p, Carver *carve) {
           enc->packed_sq += L * L;
         }
       }
-    } else if (carve) {
+    } else if (carve || p.s->last_rows <= 0) {
+      // (also the first packed pass on a stream: no earlier total to pick the
+      // GEMM tiles by)
       int32_t t = 0;
       e = hipMemcpyAsync(&t, p.w.seq_start + B, sizeof(int32_t), hipMemcpyDeviceToHost,
                          p.s->stream);
       if (e == hipSuccess) e = hipStreamSynchronize(p.s->stream);
       total = t;
+      if (e == hipSuccess && t > 0) p.s->last_rows = t;
     } else {
       enc->live = mx::Live{p.w.seq_start + B, p.s->last_rows};
       enc->live_bound = B * S;
