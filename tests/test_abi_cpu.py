@@ -102,6 +102,11 @@ def test_null_arguments_refused_without_a_device(L):
     assert L.mx_attention(None, None, 0, 1, 1, 1, 64, 1.0, None, None, None, 64) == -1
     assert L.mx_softmax_rows(None, None, 0, 1, 1, 1, None, 1, 0) == -1
     assert L.mx_encoder_create(None, None, None) == -1
+    for fn in ("mx_encoder_embed", "mx_encoder_embed_async", "mx_encoder_embed_static"):
+        assert getattr(L, fn)(None, None, None, None, 1, 1, None) == -1, fn
+        err = L.mx_last_error().decode()
+        assert "null" in err and fn[3:] in err, (fn, err)
+    assert L.mx_sync(None) == -1 and "null stream" in L.mx_last_error().decode()
 
 
 def test_no_silent_cpu_fallback(L):
