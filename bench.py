@@ -42,6 +42,12 @@ INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
 HBM_PEAK_GBS = 8000.0
 
 
+# The lane count each BERT config runs fastest at on one MI355X (bench.py --lanes 2, 3, 4):
+# bge-base 15.8k / 15.3k / 14.9k seq/s; MiniLM's small batches, whose GEMMs fill a fraction
+# of the chip, 129k / 172k / 135k sustained.
+LANES_DEFAULT = {"minilm": 3}
+
+
 def kernel_name(plan, epi, res, cbf, i8=False):
     """The rocprof name of the GEMM instantiation a plan from mx_gemm_plan_for
     runs, e.g. lds_256x256x64_w64x128_ns2_persistent (bf16) ->
@@ -363,10 +369,12 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="bge_base")
-    ap.add_argument("--lanes", type=int, default=2,
+    ap.add_argument("--lanes", type=int, default=None,
                     help="BERT configs: concurrent lanes (the reference's --pipeline), each "
                          "an encoder clone on its own stream and host thread with its own "
-                         "copy of the batch in HBM; the timed steps are split over them")
+                         "copy of the batch in HBM; the timed steps are split over them. "
+                         "Default: the fastest count measured for the config (MiniLM's "
+                         "b32 x s128 batches 3, the others 2)")
     ap.add_argument("--no-padded-rate", action="store_true",
                     help="do not time the padded and the last-layer-over-every-row "
                          "comparisons (profiling runs)")
@@ -438,6 +446,8 @@ def main():
     # row; the pooled output is unchanged bit for bit) goes with packing: the
     # padded run is EmbedService::chunk's computation, every row in every layer.
     pruning = packing and m["cls_pool"]
+    if args.lanes is None:
+        args.lanes = LANES_DEFAULT.get(args.config, 2)
     lanes = max(1, args.lanes) if kind == "bert" else 1
     lane_ctx, lane_enc, lane_step, lane_queue = [ctx], [enc], [], []
     if kind == "bert":
