@@ -497,12 +497,24 @@ __global__ __launch_bounds__(256) void softmax_vec_k(void *x, int64_t rows, int6
   const int64_t row0 = (blockIdx.x * (int64_t)(blockDim.x / 64) + (threadIdx.x >> 6)) * NR;
   if (row0 >= rows) return;
   float v[NR][NC][8];
+  // The mask row of row0 + r: one division per wave (row0 / rpm, the rest
+  // carried), not one per row -- a 64-bit division is dozens of vector
+  // instructions.
+  int64_t mrow = 0, mrem = 0;
+  if (mask) {
+    mrow = row0 / rpm;
+    mrem = row0 - mrow * rpm;
+  }
   // The mask entries are read with the rows (added to them right away), so
   // their latency runs under the row loads instead of after them.
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     const int64_t row = row0 + r;
-    const float *mk = mask && row < rows ? mask + (row / rpm) * cols : nullptr;
+    if (r > 0 && ++mrem == rpm) {
+      mrem = 0;
+      ++mrow;
+    }
+    const float *mk = mask && row < rows ? mask + mrow * cols : nullptr;
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const int64_t c0 = 8 * (lane + 64 * (int64_t)i);
