@@ -119,6 +119,13 @@ class Encoder {
              float *out) {
     check(mx_encoder_embed(e_, lane.get(), ids, mask, B, S, out));
   }
+  // The same embed queued without its closing wait (no counterpart in the
+  // reference): the rows are ready, and a data refusal is thrown, at the
+  // lane's next sync().
+  void embed_async(Lane &lane, const int32_t *ids, const float *mask, int64_t B, int64_t S,
+                   float *out) {
+    check(mx_encoder_embed_async(e_, lane.get(), ids, mask, B, S, out));
+  }
 
  private:
   mx_encoder *e_ = nullptr;

@@ -124,6 +124,19 @@ int run_gpu(int argc, char **argv) {
   std::vector<float> out(static_cast<size_t>(B * hidden));
   lane.to_host(out.data(), d_out.get(), out.size() * 4);
   lane.sync();
+  // The queued embed gives the same rows once the lane is synchronised.
+  mxgpu::Buffer d_out2(be, static_cast<size_t>(B * hidden) * 4);
+  enc.embed_async(lane, static_cast<const int32_t *>(d_ids.get()),
+                  static_cast<const float *>(d_mask.get()), B, S,
+                  static_cast<float *>(d_out2.get()));
+  lane.sync();
+  std::vector<float> out2(out.size());
+  lane.to_host(out2.data(), d_out2.get(), out2.size() * 4);
+  lane.sync();
+  if (std::memcmp(out.data(), out2.data(), out.size() * 4) != 0) {
+    std::printf("FAIL: embed_async rows differ from embed's\n");
+    ++failures;
+  }
   // A refusal on the live device also arrives as an exception.
   expect_refusal(mx_encoder_embed(enc.get(), lane.get(), static_cast<const int32_t *>(d_ids.get()),
                                   static_cast<const float *>(d_mask.get()), 0, S,
