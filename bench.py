@@ -363,6 +363,30 @@ def gemm_vs_library(mxenc, np):
     ctx.close()
 
 
+def service_rate(mxenc, np, enc, lanes, ids, am, n_req, unit):
+    """The PCIe-inclusive rate: mx_embed_service_embed over host token ids and
+    masks (a request of n_req chunks of B sequences over `lanes` lanes, each
+    chunk copied in, embedded and its pooled rows copied back), as the
+    reference's EmbedService::embed serves a request
+    (runtime/src/server/embed_service.cpp:66-108). Not `value`, whose inputs
+    are resident. A request of two chunks per lane warms every lane first."""
+    B, S = ids.shape
+    svc = mxenc.EmbedService(enc, lanes, B, S)
+    req_ids, req_am = np.tile(ids, (n_req, 1)), np.tile(am, (n_req, 1))
+    svc.embed(req_ids[: 2 * lanes * B], req_am[: 2 * lanes * B])
+    time.sleep(0.05)  # a quiet gap that sets the timed request apart in a trace
+    t0 = time.perf_counter()
+    svc.embed(req_ids, req_am)
+    vdt = time.perf_counter() - t0
+    svc.close()
+    out = {"value": n_req * B / vdt, "sequences": n_req * B, "lanes": lanes, "chunk": B,
+           "seconds": vdt}
+    print(f"bench: service (host ids in, pooled rows out) {out['value']:.1f} {unit} "
+          f"({n_req * B} sequences in chunks of {B} over {lanes} lane(s))",
+          file=sys.stderr, flush=True)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -387,6 +411,9 @@ def main():
                     help="gated-FFN configs: FFN-up then the separate gated pass, instead of "
                          "the activation fused into FFN-up's epilogue")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--service", action="store_true",
+                    help="only the PCIe-inclusive rate: one request of --steps chunks "
+                         "through mx_embed_service_embed from host memory")
     ap.add_argument("--no-sustained", action="store_true",
                     help="skip the sustained-rate run (>= 2 s of back-to-back steps)")
     ap.add_argument("--cpu-sample", type=int, default=16)
@@ -450,9 +477,25 @@ def main():
         args.lanes = LANES_DEFAULT.get(args.config, 2)
     lanes = max(1, args.lanes) if kind == "bert" else 1
     lane_ctx, lane_enc, lane_step, lane_queue = [ctx], [enc], [], []
+    if args.service and kind != "bert":
+        print(json.dumps({"error": "--service runs the BERT configs"}))
+        sys.exit(2)
     if kind == "bert":
         ids, am, lens = synth.make_text_inputs(m)
         B, S = ids.shape
+        if args.service:
+            # No other lanes: the service's streams take hardware queues of
+            # their own.
+            enc.set_packing(packing)
+            enc.set_cls_pruning(pruning)
+            enc.set_fusion(not args.no_fusion)
+            enc.set_timing(False)
+            print(json.dumps({"service": service_rate(mxenc, np, enc, lanes, ids, am,
+                                                      args.steps, "sequences/s"),
+                              "config": args.config}))
+            enc.close()
+            ctx.close()
+            return
         for _ in range(lanes - 1):
             c = mxenc.Context(0)
             lane_ctx.append(c)
@@ -665,6 +708,20 @@ def main():
         if tj.get("kernel") == dom_name and tj.get("workload") == args.config:
             traffic = tj.get("hbm_bytes_per_launch")
 
+    service = None
+    if kind == "bert" and not args.no_sustained:
+        # The service's lanes run side by side only on hardware queues of their
+        # own (HIP maps streams onto GPU_MAX_HW_QUEUES queues, 4 by default):
+        # the other lanes' streams are released first. About half a second of
+        # chunks at the resident rate, at least --steps of them.
+        for e in lane_enc[1:]:
+            e.close()
+        for c in lane_ctx[1:]:
+            c.close()
+        lane_enc, lane_ctx = lane_enc[:1], lane_ctx[:1]
+        service = service_rate(mxenc, np, enc, lanes, ids, am,
+                               max(args.steps, int(0.5 / (dt / args.steps))), unit)
+
     cpu = None
     if not args.no_cpu_baseline and kind == "bert":
         cpu = cpu_baseline(args.config, args.cpu_sample, host_threads(), args.int8)
@@ -706,6 +763,7 @@ def main():
         "lanes": lanes,
         "one_lane": one_lane,
         "one_lane_queued": one_lane_queued,
+        "service": service,
         "sustained": sustained,
         "token_packing": {"on": packing, "rows_per_step": M, "padded_rows_per_step": B * S,
                           "padded": padded} if kind == "bert" else None,

@@ -625,7 +625,14 @@ int mx_encoder_timings(mx_encoder *enc, mx_timings *out);
  * embedding sum, the encoder, pooling, into its rows of out_host. The first
  * failing chunk stops the rest and its refusal is returned (:80-92). Results
  * do not depend on the lane count or the chunk size. One call at a time per
- * service; `enc` must outlive it. */
+ * service; `enc` must outlive it.
+ * A lane keeps two chunks in flight: inputs staged in pinned host slots and
+ * copied by DMA, the embed queued without a wait, the pooled rows copied back
+ * while the lane's next chunk runs. Lanes overlap on the GPU only on hardware
+ * queues of their own: HIP maps streams onto GPU_MAX_HW_QUEUES queues (4 by
+ * default), and two lanes whose streams share one run one after the other --
+ * create the service before other long-lived streams, or keep lanes plus the
+ * process's other live streams within that count. */
 typedef struct mx_embed_service mx_embed_service;
 int mx_embed_service_create(mx_encoder *enc, int lanes, int64_t batch, int64_t seq,
                             mx_embed_service **out);

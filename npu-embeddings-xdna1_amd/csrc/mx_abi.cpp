@@ -54,10 +54,10 @@ int stage_panel(mx_ctx *ctx, const void *kn_host, int dtype, int64_t K, int64_t 
   void *p = nullptr;
   hipError_t e = dev_malloc((void **)&p, panel.size() * 2);
   if (e != hipSuccess) return hip_fail(e, "stage_weight: hipMalloc");
-  e = hipMemcpy(p, panel.data(), panel.size() * 2, hipMemcpyHostToDevice);
+  e = upload(p, panel.data(), panel.size() * 2);
   if (e != hipSuccess) {
     (void)hipFree(p);
-    return hip_fail(e, "stage_weight: hipMemcpy");
+    return hip_fail(e, "stage_weight: upload");
   }
   *out = static_cast<uint16_t *>(p);
   return MX_OK;
@@ -101,11 +101,15 @@ int stage_tiled_panel(mx_ctx *ctx, const uint16_t *panel_host, int64_t K, int64_
     (void)hipFree(tiled);
     return hip_fail(e, "stage_weight_panel: hipMalloc");
   }
-  e = hipMemcpy(tiled, panel_host, bytes, hipMemcpyHostToDevice);
-  if (e == hipSuccess)
-    e = mxk::untile_panel(static_cast<const uint16_t *>(tiled), K, N, (int)tile_k, (int)tile_n,
-                          (int)mac_s, (int)mac_t, static_cast<uint16_t *>(wt), nullptr);
-  if (e == hipSuccess) e = hipDeviceSynchronize();
+  {
+    SetupStream st;
+    e = st.h2d(tiled, panel_host, bytes);
+    if (e == hipSuccess)
+      e = mxk::untile_panel(static_cast<const uint16_t *>(tiled), K, N, (int)tile_k,
+                            (int)tile_n, (int)mac_s, (int)mac_t, static_cast<uint16_t *>(wt),
+                            st.s);
+    if (e == hipSuccess) e = st.finish();
+  }
   (void)hipFree(tiled);
   if (e != hipSuccess) {
     (void)hipFree(wt);
@@ -330,7 +334,8 @@ int mx_stream_create(mx_ctx *ctx, mx_stream **out) {
     return hip_fail(e, "hipStreamCreate");
   }
   e = dev_malloc((void **)&s->err_dev, 2 * sizeof(int));
-  if (e == hipSuccess) e = hipMemset(s->err_dev, 0, 2 * sizeof(int));
+  if (e == hipSuccess) e = hipMemsetAsync(s->err_dev, 0, 2 * sizeof(int), s->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
   if (e != hipSuccess) {
     (void)hipStreamDestroy(s->stream);
     delete s;

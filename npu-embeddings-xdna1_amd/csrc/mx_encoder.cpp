@@ -352,8 +352,8 @@ int ensure_rope(mx_encoder *enc, int64_t S) {
   int rc = dev_alloc((void **)&enc->rope_cos, c.size() * 4, "rope table");
   if (!rc) rc = dev_alloc((void **)&enc->rope_sin, sn.size() * 4, "rope table");
   if (rc) return rc;
-  hipError_t e = hipMemcpy(enc->rope_cos, c.data(), c.size() * 4, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(enc->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice);
+  hipError_t e = upload(enc->rope_cos, c.data(), c.size() * 4);
+  if (e == hipSuccess) e = upload(enc->rope_sin, sn.data(), sn.size() * 4);
   if (e != hipSuccess) return hip_fail(e, "rope table upload");
   enc->rope_rows = S;
   return MX_OK;
@@ -390,6 +390,7 @@ int ensure_glu_operands(mx_encoder *enc) {
   if (!enc->owns_weights || !enc->fuse_glu || !glu_fusable(enc)) return MX_OK;
   const int64_t d = enc->desc.hidden, f = enc->desc.ffn;
   bool synced = false;
+  SetupStream st;
   for (LayerW &w : enc->layers) {
     if (w.glu_gen == enc->wgen) continue;
     if (!synced) {  // the source tensors may still be in flight
@@ -405,23 +406,23 @@ int ensure_glu_operands(mx_encoder *enc) {
     free_dev(w.wsg);
     w.glu_gen = 0;
     int rc = dev_alloc((void **)&w.bg, 2 * f * 4, "gated FFN-up bias");
-    hipError_t e = rc ? hipSuccess : mxk::glu_interleave(w.b[SITE_UP], w.bg, f, 4, nullptr);
+    hipError_t e = rc ? hipSuccess : mxk::glu_interleave(w.b[SITE_UP], w.bg, f, 4, st.s);
     if (!rc && e == hipSuccess) {
       if (enc->i8) {
         rc = dev_alloc((void **)&w.wqg, 2 * f * d, "gated FFN-up operand");
         if (!rc) rc = dev_alloc((void **)&w.wsg, 2 * f * 4, "gated FFN-up wscale");
-        if (!rc) e = mxk::glu_interleave(w.wq[SITE_UP], w.wqg, f, d, nullptr);
-        if (!rc && e == hipSuccess) e = mxk::glu_interleave(w.ws[SITE_UP], w.wsg, f, 4, nullptr);
+        if (!rc) e = mxk::glu_interleave(w.wq[SITE_UP], w.wqg, f, d, st.s);
+        if (!rc && e == hipSuccess) e = mxk::glu_interleave(w.ws[SITE_UP], w.wsg, f, 4, st.s);
       } else {
         rc = dev_alloc((void **)&w.wg, 2 * f * d * 2, "gated FFN-up operand");
-        if (!rc) e = mxk::glu_interleave(w.w[SITE_UP], w.wg, f, d * 2, nullptr);
+        if (!rc) e = mxk::glu_interleave(w.w[SITE_UP], w.wg, f, d * 2, st.s);
       }
     }
     if (rc) return rc;
     if (e != hipSuccess) return hip_fail(e, "gated FFN interleave");
   }
   if (synced) {
-    const hipError_t e = hipDeviceSynchronize();
+    const hipError_t e = st.finish();
     if (e != hipSuccess) return hip_fail(e, "gated FFN interleave");
     for (LayerW &w : enc->layers) w.glu_gen = enc->wgen;
   }
@@ -756,7 +757,7 @@ int stage_i8_panel(mx_ctx *ctx, const int8_t *kn, int64_t K, int64_t N, int8_t *
       panel[static_cast<size_t>(n) * K + k] = kn[static_cast<size_t>(k) * N + n];
   void *p = nullptr;
   hipError_t e = dev_malloc((void **)&p, panel.size());
-  if (e == hipSuccess) e = hipMemcpy(p, panel.data(), panel.size(), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = upload(p, panel.data(), panel.size());
   if (e != hipSuccess) {
     if (p) (void)hipFree(p);
     return hip_fail(e, "int8 operand upload");
@@ -1003,7 +1004,7 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
     free_dev(dst);
     int r = dev_alloc((void **)&dst, want * 4, name.c_str());
     if (r) return r;
-    const hipError_t e = hipMemcpy(dst, src, want * 4, hipMemcpyHostToDevice);
+    const hipError_t e = upload(dst, src, want * 4);
     return e == hipSuccess ? MX_OK : hip_fail(e, name.c_str());
   };
   auto put_f32 = [&](float *&dst, int64_t want) -> int {
@@ -1162,7 +1163,7 @@ int mx_encoder_set(mx_encoder *enc, const char *name_c, const void *host, int dt
     free_dev(enc->type);
     int r = dev_alloc((void **)&enc->type, count * 4, name.c_str());
     if (r) return r;
-    const hipError_t e = hipMemcpy(enc->type, host, count * 4, hipMemcpyHostToDevice);
+    const hipError_t e = upload(enc->type, host, count * 4);
     return e == hipSuccess ? MX_OK : hip_fail(e, name.c_str());
   }
   return fail(MX_E_INVALID, "encoder_set: unknown tensor '" + name + "'");

@@ -26,7 +26,7 @@ int upload(const T *host, size_t count, T **dev, const char *what) {
   void *p = nullptr;
   hipError_t e = dev_malloc((void **)&p, count * sizeof(T));
   if (e != hipSuccess) return hip_fail(e, what);
-  e = hipMemcpy(p, host, count * sizeof(T), hipMemcpyHostToDevice);
+  e = mx::upload(p, host, count * sizeof(T));
   if (e != hipSuccess) {
     (void)hipFree(p);
     return hip_fail(e, what);
@@ -79,13 +79,14 @@ int stage_i8(mx_ctx *ctx, const int8_t *kn_host, const float *wscale_host,
     rc = upload(kn_host, n, &tiled, "stage_weight_i8: panel");
     if (!rc) {
       void *wq = nullptr;
+      SetupStream st;
       hipError_t e = dev_malloc((void **)&wq, n);
       if (e == hipSuccess) {
         op.wq = static_cast<int8_t *>(wq);
         e = mxk::untile_panel_i8(tiled, K, N, (int)tile_k, (int)tile_n, (int)mac_s, (int)mac_t,
-                                 op.wq, nullptr);
+                                 op.wq, st.s);
       }
-      if (e == hipSuccess) e = hipDeviceSynchronize();
+      if (e == hipSuccess) e = st.finish();
       (void)hipFree(tiled);
       if (e != hipSuccess) rc = hip_fail(e, "stage_weight_i8: untile");
     }
@@ -145,9 +146,10 @@ int stage_i4(mx_ctx *ctx, const uint8_t *packed_host, const float *gscale_host, 
     tiled = static_cast<int8_t *>(p);
   }
   if (!rc) {
+    SetupStream st;
     hipError_t e = mxk::widen_i4_panel(packed, K, N, (int)tile_k, (int)tile_n, (int)mac_s,
-                                       (int)mac_t, gs, g, tiled, nullptr);
-    if (e == hipSuccess) e = hipDeviceSynchronize();
+                                       (int)mac_t, gs, g, tiled, st.s);
+    if (e == hipSuccess) e = st.finish();
     if (e != hipSuccess) rc = hip_fail(e, "stage_weight_panel_i4: widen");
   }
   if (packed) (void)hipFree(packed);
@@ -165,13 +167,14 @@ int stage_i4(mx_ctx *ctx, const uint8_t *packed_host, const float *gscale_host, 
   }
   if (!rc) {
     void *wq = nullptr;
+    SetupStream st;
     hipError_t e = dev_malloc((void **)&wq, static_cast<size_t>(K) * N);
     if (e == hipSuccess) {
       op.wq = static_cast<int8_t *>(wq);
       e = mxk::untile_panel_i8(tiled, K, N, (int)tile_k, (int)tile_n, (int)mac_s, (int)mac_t,
-                               op.wq, nullptr);
+                               op.wq, st.s);
     }
-    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = st.finish();
     if (e != hipSuccess) rc = hip_fail(e, "stage_weight_panel_i4: untile");
   }
   if (tiled) (void)hipFree(tiled);

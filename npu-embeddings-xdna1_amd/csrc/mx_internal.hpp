@@ -21,6 +21,37 @@ inline hipError_t dev_malloc(void **p, size_t bytes) {
   return hipMalloc(p, bytes);
 }
 
+// One-off set-up work (weight uploads and reshapes, table uploads) runs on a
+// stream made for it and destroyed when the work is done. The library never
+// uses HIP's null stream: once created it holds one of the process's
+// GPU_MAX_HW_QUEUES hardware queues (4 by default) for good, and streams that
+// share a hardware queue run one after the other.
+struct SetupStream {
+  hipStream_t s = nullptr;
+  hipError_t e = hipSuccess;
+  SetupStream() { e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking); }
+  ~SetupStream() {
+    if (s) {
+      (void)hipStreamSynchronize(s);
+      (void)hipStreamDestroy(s);
+    }
+  }
+  SetupStream(const SetupStream &) = delete;
+  SetupStream &operator=(const SetupStream &) = delete;
+  hipError_t h2d(void *dst, const void *src, size_t bytes) {
+    return e != hipSuccess ? e : hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s);
+  }
+  // Wait for everything queued on it.
+  hipError_t finish() { return e != hipSuccess ? e : hipStreamSynchronize(s); }
+};
+
+// A host -> device copy that is complete when it returns (on a set-up stream).
+inline hipError_t upload(void *dst, const void *src, size_t bytes) {
+  SetupStream st;
+  const hipError_t e = st.h2d(dst, src, bytes);
+  return e != hipSuccess ? e : st.finish();
+}
+
 struct WeightSlot {
   uint16_t *wt = nullptr;  // [N, K] bf16 (a bf16 operand)
   int64_t K = 0, N = 0;

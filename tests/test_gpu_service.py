@@ -68,6 +68,25 @@ def test_service_first_error_is_the_calls(ctx):
     e.close()
 
 
+def test_service_one_lane_refusal_mid_request(ctx):
+    # One lane holds two chunks in flight: the refusal of chunk 2 (of 6) is
+    # read while chunk 3 is queued. The call fails with it; the next request
+    # gives the clean rows bit for bit (no flag or slot left over).
+    m = synth.make_model("minilm", layers=1, cls_pool=True)
+    e = mxenc.Encoder(ctx, m)
+    ids, am, _ = synth.make_text_inputs(m, batch=24)
+    svc = mxenc.EmbedService(e, 1, 4, ids.shape[1])
+    want = gpu_embed(ctx, e, ids, am)
+    bad = am.copy()
+    bad[9, 0] = 0.0
+    with pytest.raises(mxenc.MxError, match="first token is masked"):
+        svc.embed(ids, bad)
+    got = svc.embed(ids, am)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    svc.close()
+    e.close()
+
+
 def test_service_and_clone_refusals(ctx, enc):
     with pytest.raises(mxenc.MxError, match="lanes must be 1..64"):
         mxenc.EmbedService(enc, 0, 8, 128)
