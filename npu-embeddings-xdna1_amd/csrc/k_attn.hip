@@ -1,10 +1,15 @@
 // k_attn.hip -- fused masked attention on gfx950 MFMA: QK^T, additive-mask
 // softmax and PV in one pass per (sequence, head, 128-query block); the score
-// matrix never reaches HBM. A block is 4 waves and three blocks share a CU.
-// (8-wave blocks of 256 queries, which halve the K/V tiles staged per query,
-// measured slower on the bge-base batch: 0.85 against 0.68 ms per batch --
-// fewer, larger blocks leave more query waves idle on short sequences, and at
-// two blocks per CU the kernel spills.)
+// matrix never reaches HBM. A block is 4 waves. With head_dim 64 the key tiles
+// are 32 keys and four blocks share a CU (four waves per SIMD: 104 VGPRs, a
+// 33 KB ring); waves in flight are what hide this kernel's latency, and the
+// 64-key tiles' 156 VGPRs and 49 KB ring allowed only three (0.60 against
+// 0.55 ms per bge-base batch). With head_dim 32 a 32-key tile is less than a
+// 1 KB load per wave, and the tiles stay 64 keys, three blocks per CU. (8-wave
+// blocks of 256 queries, which halve the K/V tiles staged per query, measured
+// slower on the bge-base batch: 0.85 against 0.68 ms per batch -- fewer,
+// larger blocks leave more query waves idle on short sequences, and at two
+// blocks per CU the kernel spills.)
 //
 // Each wave owns 32 queries and computes the TRANSPOSED score tile
 // S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (keys on rows, queries on
@@ -18,8 +23,8 @@
 //
 // Staging. K, V and the tile's mask row go global -> LDS by direct loads
 // (global_load_lds_dwordx4 / _dword, issued from inline assembly so the
-// compiler adds no waits) into a ring of NSL slots, NSL - 1 64-key tiles
-// ahead; no registers hold K or V in flight. V stays row-major in LDS: the PV
+// compiler adds no waits) into a ring of NSL slots, NSL - 1 key tiles ahead;
+// no registers hold K or V in flight. V stays row-major in LDS: the PV
 // operand V^T is read with ds_read_b64_tr_b16, which hands each lane of a
 // 16-lane group one column of the 4 x 16 bf16 block the group addresses (lane
 // j of the group receives element j % 4 of group lane 4e + j / 4's 8 bytes,
@@ -57,10 +62,6 @@ using namespace mxd;
 
 namespace {
 
-constexpr int BKV = 64;
-
-constexpr int NSL = 3;
-
 __device__ __forceinline__ void dma16o(uint64_t base, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff),
                "s"(base)
@@ -84,10 +85,10 @@ __device__ __forceinline__ void vm_wait() {
 typedef short v4s __attribute__((ext_vector_type(4)));
 
 // NW waves of 32 queries per block (BQ = 32 NW queries share each staged K/V
-// tile); the second bound is waves per SIMD: three 4-wave blocks per CU (the
-// LDS ring of a block is ~49 KB).
-template <int HD, int NW>
-__global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restrict__ qkv,
+// tile), key tiles of BKV (32 or 64) keys in a ring of NSL slots, and WPS
+// waves per SIMD as the second launch bound.
+template <int HD, int NW, int BKV, int NSL, int WPS>
+__global__ __launch_bounds__(NW * 64, WPS) void attn_dma_k(const uint16_t *__restrict__ qkv,
                                                    int64_t ldq, int S, int H, float scale_log2e,
                                                    const float *__restrict__ add_mask,
                                                    const int32_t *__restrict__ kv_len,
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
 
   // Key tile t -> slot t % NSL: wave w moves the K and V rows of 1 KB pieces
   // p = w, w + NW, ... (PR rows each: lane l fills row PR p + l / CPR,
-  // 16-byte position l % CPR); wave 0 also the tile's 64 mask entries.
+  // 16-byte position l % CPR); wave 0 also the tile's BKV mask entries.
   const uint64_t kb64 = uni64((uint64_t)(uintptr_t)(base + d + h * HD));
   const uint64_t vb64 = uni64((uint64_t)(uintptr_t)(base + 2 * d + h * HD));
   const uint64_t mb64 = add_mask ? uni64((uint64_t)(uintptr_t)(add_mask + (int64_t)b * S)) : 0;
@@ -165,7 +166,7 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
       dma16o(kb64 + toff, roff + (uint32_t)((ppos ^ swz_k(row)) * 16), slot + p * 1024);
       dma16o(vb64 + toff, roff + (uint32_t)((ppos ^ swz_v(row)) * 16), slot + TILE + p * 1024);
     }
-    if (wave == 0 && add_mask) {
+    if (wave == 0 && add_mask && lane < BKV) {
       int key = t * BKV + lane;
       key = key < S ? key : S - 1;
       dma4o(mb64 + (uint64_t)(t * BKV) * 4, (uint32_t)(key - t * BKV) * 4, slot + 2 * TILE);
@@ -221,15 +222,16 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
     if (t + 2 < ntile) issue(t + 2);
     const uint8_t *sl = sm + (t % NSL) * SLOT;
     if (live) {
-      // The tile's second 32 keys all at or past kv_len (the last tile of a
-      // sequence whose length is <= 32 past a multiple of 64): their scores,
+      // A 64-key tile's second 32 keys all at or past kv_len (the last tile of
+      // a sequence whose length is <= 32 past a multiple of 64): their scores,
       // probabilities and PV products are skipped -- each would be exp2(-inf)
-      // = 0.
-      const bool h1 = t * BKV + 32 < kvl;
+      // = 0. A 32-key tile is its first half alone.
+      const bool h1 = BKV == 64 && t * BKV + 32 < kvl;
       // The staged mask entry this lane tests, read first: its latency runs
       // under the score MFMAs instead of after them.
       const float *smk = (const float *)(sl + 2 * TILE);
-      float mword = smk[lane];  // unused (and never written) without a mask
+      // (unused, and never written, without a mask; a 32-key row has 32)
+      float mword = lane < BKV ? smk[lane] : 0.0f;
       // Each half's chain starts from an immediate zero accumulator; a
       // skipped second half is left unset (nothing reads it), so no register
       // copies merge it with the computed one. With both halves live their
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(NW * 64, 3) void attn_dma_k(const uint16_t *__restr
       if (masked) {
         // Lane (li, g) holds keys sub * 32 + 8 rr + 4 g + e of accumulator
         // element 4 rr + e: four consecutive mask entries, one 16-byte LDS
-        // read. All 64 entries of the staged row are written (the loads clamp
+        // read. All BKV entries of the staged row are written (the loads clamp
         // to the sequence's last key), so the reads are unconditional; keys at
         // or past kv_len take -inf by a select.
 #pragma unroll
@@ -413,12 +415,14 @@ hipError_t attention(const AttnArgs &a, hipStream_t s) {
   const int64_t blocks = a.B * a.H * n_qblk;
   const float sl2e = a.scale * 1.4426950408889634f;
   const int force_logits = a.scale > 0.0f ? 0 : 1;  // raw-score max needs scale > 0
+  // head_dim 64: 32-key tiles, a 4-slot ring, four blocks per CU; head_dim 32:
+  // 64-key tiles, 3 slots, three blocks per CU.
   if (a.hd == 64)
-    attn_dma_k<64, nw><<<(unsigned)blocks, 64 * nw, 0, s>>>(
+    attn_dma_k<64, nw, 32, 4, 4><<<(unsigned)blocks, 64 * nw, 0, s>>>(
         a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e, a.add_mask, a.kv_len, a.ctx, a.ld_ctx,
         n_qblk, force_logits, a.seq_start, a.order, (int)qs);
   else if (a.hd == 32)
-    attn_dma_k<32, nw><<<(unsigned)blocks, 64 * nw, 0, s>>>(
+    attn_dma_k<32, nw, 64, 3, 3><<<(unsigned)blocks, 64 * nw, 0, s>>>(
         a.qkv, a.ld_qkv, (int)a.S, (int)a.H, sl2e, a.add_mask, a.kv_len, a.ctx, a.ld_ctx,
         n_qblk, force_logits, a.seq_start, a.order, (int)qs);
   else
