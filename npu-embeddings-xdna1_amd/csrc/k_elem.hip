@@ -434,7 +434,7 @@ __global__ __launch_bounds__(256) void softmax_wave_k(void *x, int bf, int64_t r
       if (variant == 0) {
         float a = (v[i] - m) * 1.4426950408889634f;
         a = a > -120.0f ? a : -120.0f;
-        e = exp2_poly(a);
+        e = exp2_poly_neg(a);
       } else if (variant == 1) {
         e = expf(v[i] - m);
       } else {
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(256) void softmax_wave_k(void *x, int bf, int64_t r
         d = d > -100.0f ? d : -100.0f;
         float a = mul_rn(d, 1.4426950408889634f);
         a = a > -120.0f ? a : -120.0f;
-        e = bf2f(f2bf(exp2_poly_aie(a)));
+        e = bf2f(f2bf(exp2_poly_aie_neg(a)));
       }
       if (variant != 2) s += e;
     }
@@ -571,7 +571,7 @@ __global__ __launch_bounds__(256) void softmax_vec_k(void *x, int64_t rows, int6
           if (VAR == 0) {
             float a = (v[r][i][e] - m) * 1.4426950408889634f;
             a = a > -120.0f ? a : -120.0f;
-            ex = exp2_poly(a);
+            ex = exp2_poly_neg(a);
           } else {
             ex = expf(v[r][i][e] - m);
           }

@@ -149,6 +149,24 @@ __device__ __forceinline__ float exp2_poly(float x) {
   return p * __uint_as_float((uint32_t)(k + 127) << 23);
 }
 
+// exp2_poly for x in [-120, 0], where the softmaxes clamp their argument: the
+// same polynomial, scaled by v_ldexp_f32 (one instruction) instead of a
+// multiply by 2^k built in the exponent field (three). p * 2^k is exact and
+// normal there (p in (0.5, 1], k >= -120), so both give the same bits; every
+// float in [-120, 0] was checked (tests/test_exp2_scaling_cpu.py).
+__device__ __forceinline__ float exp2_poly_neg(float x) {
+  const int k = (int)x;
+  const float f = x - (float)k;
+  float p = __builtin_fmaf(1.5483275463e-05f, f, 1.5669833174e-04f);
+  p = __builtin_fmaf(p, f, 1.3331825236e-03f);
+  p = __builtin_fmaf(p, f, 9.6164605538e-03f);
+  p = __builtin_fmaf(p, f, 5.5504156855e-02f);
+  p = __builtin_fmaf(p, f, 2.4022684109e-01f);
+  p = __builtin_fmaf(p, f, 6.9314717694e-01f);
+  p = __builtin_fmaf(p, f, 9.9999998955e-01f);
+  return __builtin_amdgcn_ldexpf(p, k);
+}
+
 // swiglu_cpu's SiLU (bert_encoder.cpp:582-627): x / (1 + 2^max(-x log2e,
 // -120)) with the exp2 polynomial above, each operation rounded on its own as
 // the host's AVX2 form is (no multiply-add contraction of the polynomial's
@@ -202,6 +220,23 @@ __device__ __forceinline__ float exp2_poly_aie(float x) {
   p = add_rn(mul_rn(p, f), 6.9314717694e-01f);
   p = add_rn(mul_rn(p, f), 9.9999998955e-01f);
   return mul_rn(p, __uint_as_float((uint32_t)(k + 127) << 23));
+}
+
+// exp2_poly_aie for x in [-120, 0] (the accelerator softmax's clamp), scaled
+// by v_ldexp_f32: the same bits there, for the reason exp2_poly_neg gives;
+// every float in [-120, 0] was checked (tests/test_exp2_scaling_cpu.py).
+__device__ __forceinline__ float exp2_poly_aie_neg(float x) {
+  const int k = (int)x;
+  const float f = sub_rn(x, (float)k);
+  float p = 1.5483275463e-05f;
+  p = add_rn(mul_rn(p, f), 1.5669833174e-04f);
+  p = add_rn(mul_rn(p, f), 1.3331825236e-03f);
+  p = add_rn(mul_rn(p, f), 9.6164605538e-03f);
+  p = add_rn(mul_rn(p, f), 5.5504156855e-02f);
+  p = add_rn(mul_rn(p, f), 2.4022684109e-01f);
+  p = add_rn(mul_rn(p, f), 6.9314717694e-01f);
+  p = add_rn(mul_rn(p, f), 9.9999998955e-01f);
+  return __builtin_amdgcn_ldexpf(p, k);
 }
 
 }  // namespace mxd
