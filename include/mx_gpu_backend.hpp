@@ -12,6 +12,8 @@
  *   Encoder    BertEncoder (bert_encoder.cpp:1419-1598) built from a
  *              container, with EmbedService::chunk's embed
  *              (embed_service.cpp:29-64) from token ids on
+ *   EmbedService  EmbedService::embed (embed_service.cpp:66-108) minus the
+ *              tokenizer: host ids and masks in, host rows out, over lanes
  */
 #ifndef MX_GPU_BACKEND_HPP
 #define MX_GPU_BACKEND_HPP
@@ -129,6 +131,29 @@ class Encoder {
 
  private:
   mx_encoder *e_ = nullptr;
+};
+
+class EmbedService {
+ public:
+  // make_service's lanes (embed_service.cpp:110-119): `lanes` workers, each
+  // an encoder clone on a stream of its own, chunks of `batch` sequences of
+  // length `seq`. `enc` must outlive the service.
+  EmbedService(Encoder &enc, int lanes, int64_t batch, int64_t seq) {
+    check(mx_embed_service_create(enc.get(), lanes, batch, seq, &svc_));
+  }
+  ~EmbedService() { mx_embed_service_destroy(svc_); }
+  EmbedService(const EmbedService &) = delete;
+  EmbedService &operator=(const EmbedService &) = delete;
+  mx_embed_service *get() const { return svc_; }
+  // n sequences: ids int32 [n, seq] and the 1/0 masks fp32 [n, seq] (host)
+  // -> pooled, L2-normalised fp32 [n, hidden] (host). The first failing
+  // chunk's refusal is thrown; the others are not run.
+  void embed(const int32_t *ids, const float *mask, int64_t n, float *out) {
+    check(mx_embed_service_embed(svc_, ids, mask, n, out));
+  }
+
+ private:
+  mx_embed_service *svc_ = nullptr;
 };
 
 }  // namespace mxgpu

@@ -137,6 +137,17 @@ int run_gpu(int argc, char **argv) {
     std::printf("FAIL: embed_async rows differ from embed's\n");
     ++failures;
   }
+  // The embed service from host memory, two lanes in chunks of 3 sequences:
+  // the same rows, whatever the chunking.
+  {
+    mxgpu::EmbedService svc(enc, 2, 3, S);
+    std::vector<float> out3(out.size());
+    svc.embed(ids.data(), mask.data(), B, out3.data());
+    if (std::memcmp(out.data(), out3.data(), out.size() * 4) != 0) {
+      std::printf("FAIL: the embed service's rows differ from embed's\n");
+      ++failures;
+    }
+  }
   // A refusal on the live device also arrives as an exception.
   expect_refusal(mx_encoder_embed(enc.get(), lane.get(), static_cast<const int32_t *>(d_ids.get()),
                                   static_cast<const float *>(d_mask.get()), 0, S,

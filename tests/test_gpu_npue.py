@@ -283,7 +283,9 @@ def test_cxx_caller_embeds_what_the_binding_embeds(tmp_path, ctx):
     """The C++17 caller (tests/abi_cxx/abi_check.cpp over include/
     mx_gpu_backend.hpp, built by the host compiler and linked to the library)
     loads a container and embeds a batch in a process of its own; its pooled
-    rows are bit for bit the ctypes binding's."""
+    rows are bit for bit the ctypes binding's. In the same process it checks
+    the queued embed and the embed service (two lanes, chunks of 3) give the
+    same rows."""
     import os
     import subprocess
     m = synth.make_model("minilm", layers=2, ln_random=True)
