@@ -567,6 +567,34 @@ def test_attention_kvlen_holes_and_additive_mask(ctx, orc, with_mask):
     assert np.mean(err) < ATT_MEAN_TOL * np.max(np.abs(want))
 
 
+@pytest.mark.parametrize("hd", [64, 32])
+def test_attention_key_tile_edge_lengths(ctx, orc, hd):
+    """Sequence lengths on either side of the key-tile edges (32-key tiles at
+    head_dim 64, 64-key tiles at 32) and -1e30 / finite mask entries inside
+    middle tiles, with kv_len, against the oracle."""
+    lens = np.array([1, 2, 31, 32, 33, 63, 64, 65, 95, 96, 97, 128], np.int32)
+    B, S, H = len(lens), 128, 2
+    d = H * hd
+    rng = np.random.default_rng(101 + hd)
+    qkv = to_bf16_bits(rng.standard_normal((B * S, 3 * d)).astype(np.float32))
+    mask = np.zeros((B, S), np.float32)
+    for b, n in enumerate(lens):
+        mask[b, n:] = -1e30
+    mask[8, 40] = -1e30   # a hole in the second 32-key tile
+    mask[10, 70] = -2.0   # a finite entry in the third
+    mask[11, 33:37] = 0.5
+    want = _attn_ref(orc, qkv, B, S, H, hd, mask)
+    dq, dm, dk = ctx.put(qkv), ctx.put(mask), ctx.put(lens)
+    out = ctx.empty((B * S, d), np.uint16)
+    mxenc.attention(ctx, dq, 3 * d, B, S, H, hd, 1.0, dm, dk, out, d)
+    got = from_bf16_bits(out.host())
+    scale = np.max(np.abs(want))
+    for b, n in enumerate(lens):  # only the rows before kv_len are the attention's
+        rows = slice(b * S, b * S + n)
+        err = np.abs(got[rows] - want[rows])
+        assert np.max(err) < ATT_TOL * scale, (b, n, np.max(err) / scale)
+
+
 def test_attention_row_strides_bit_exact(ctx):
     """QKV rows wider than 3*d (a row stride of 3*d + 8) and a ctx stride of
     d + 4 give the same bits as the dense layout (head_dim 64 and 32)."""
