@@ -475,7 +475,7 @@ def main():
     pruning = packing and m["cls_pool"]
     if args.lanes is None:
         args.lanes = LANES_DEFAULT.get(args.config, 2)
-    lanes = max(1, args.lanes) if kind == "bert" else 1
+    lanes = max(1, args.lanes)
     lane_ctx, lane_enc, lane_step, lane_queue = [ctx], [enc], [], []
     if args.service and kind != "bert":
         print(json.dumps({"error": "--service runs the BERT configs"}))
@@ -512,18 +512,25 @@ def main():
                               e.embed_async(d_ids, d_am, B, S, out))
         step = lane_step[0]
         unit = "sequences/s"
-    elif kind == "vit":
-        B, S = m["batch"], m["seq"]
-        d_px = ctx.put(synth.make_pixels(m))
-        logits = ctx.empty((B, m["labels"]), np.float32)
-        step = lambda: enc.vit(d_px, B, logits)  # noqa: E731
-        unit = "images/s"
     else:
+        # ViT / Whisper: the lanes are encoder clones on streams of their own,
+        # each with its own input and output buffers.
         B, S = m["batch"], m["seq"]
-        d_mel = ctx.put(synth.make_mel(m))
-        hid = ctx.empty((B * S, m["hidden"]), np.float32)
-        step = lambda: enc.whisper(d_mel, B, hid)  # noqa: E731
-        unit = "samples/s"
+        x = synth.make_pixels(m) if kind == "vit" else synth.make_mel(m)
+        for _ in range(lanes - 1):
+            c = mxenc.Context(0)
+            lane_ctx.append(c)
+            lane_enc.append(enc.clone(c))
+        for c, e in zip(lane_ctx, lane_enc):
+            d_x = c.put(x)
+            if kind == "vit":
+                o = c.empty((B, m["labels"]), np.float32)
+                lane_step.append(lambda e=e, d_x=d_x, o=o: e.vit(d_x, B, o))
+            else:
+                o = c.empty((B * S, m["hidden"]), np.float32)
+                lane_step.append(lambda e=e, d_x=d_x, o=o: e.whisper(d_x, B, o))
+        step = lane_step[0]
+        unit = "images/s" if kind == "vit" else "samples/s"
     print(f"bench: {args.config} B={B} S={S} L={m['layers']} on {ctx.props.arch.decode()} "
           f"({ctx.props.compute_units} CUs)", file=sys.stderr, flush=True)
 
