@@ -243,6 +243,37 @@ def test_vit_cls_pruning_is_bitwise(ctx):
     assert np.array_equal(out[0].view(np.uint32), out[2].view(np.uint32))
 
 
+def test_vit_and_whisper_lane_clones_are_bitwise_their_parent(ctx):
+    """A lane clone (mx_encoder_clone) of a ViT or a Whisper encoder, run on a
+    stream of its own, gives its parent's logits / hidden state bit for bit:
+    the clone borrows the parent's weights and front-end tensors and has its
+    own workspace."""
+    lane_ctx = mxenc.Context(0)
+    for name, B in (("vit_base", 4), ("whisper_enc", 1)):
+        m = synth.make_model(name, layers=2, ln_random=True)
+        enc = mxenc.Encoder(ctx, m)
+        lane = enc.clone(lane_ctx)
+        if name == "vit_base":
+            x = synth.make_pixels(m, batch=B)
+            shape = (B, m["labels"])
+        else:
+            x = synth.make_mel(m, batch=B)
+            shape = (B * m["seq"], m["hidden"])
+        got = []
+        for e, c in ((enc, ctx), (lane, lane_ctx)):
+            out = c.empty(shape, np.float32)
+            if name == "vit_base":
+                e.vit(c.put(x), B, out)
+            else:
+                e.whisper(c.put(x), B, out)
+            got.append(out.host())
+        lane.close()
+        enc.close()
+        assert np.all(np.isfinite(got[0])), name
+        assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32)), name
+    lane_ctx.close()
+
+
 def test_vit_full_config(ctx, orc):
     """ViT-B/16 at 224x224, the configuration's batch of 256 images: patch
     embedding, CLS + positions, 12 pre-LN layers over 197 tokens, final LN and
