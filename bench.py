@@ -42,9 +42,10 @@ INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
 HBM_PEAK_GBS = 8000.0
 
 
-# The lane count each BERT config runs fastest at on one MI355X (bench.py --lanes 2, 3, 4):
+# The lane count each config runs fastest at on one MI355X (bench.py --lanes 2, 3, 4):
 # bge-base 15.8k / 15.3k / 14.9k seq/s; MiniLM's small batches, whose GEMMs fill a fraction
-# of the chip, 129k / 172k / 135k sustained.
+# of the chip, 129k / 172k / 135k sustained; ViT-B/16 (lanes 1 / 2 / 3) 19.8k / 22.3k /
+# 22.0k images/s, the Whisper encoder 370 / 396 / 389 samples/s.
 LANES_DEFAULT = {"minilm": 3}
 
 
@@ -394,7 +395,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="bge_base")
     ap.add_argument("--lanes", type=int, default=None,
-                    help="BERT configs: concurrent lanes (the reference's --pipeline), each "
+                    help="concurrent lanes (the reference's --pipeline), each "
                          "an encoder clone on its own stream and host thread with its own "
                          "copy of the batch in HBM; the timed steps are split over them. "
                          "Default: the fastest count measured for the config (MiniLM's "
