@@ -61,6 +61,20 @@ __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
   return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
 }
 
+// 16-byte streaming accesses: global loads and stores with the nontemporal
+// hint, for data a kernel touches once and that no cache holds from an earlier
+// kernel (the bf16 softmax rows, the narrowings, GELU over fp32 input). Where
+// each is used, its kernel states what it measured against cached accesses.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const void *p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_stream16(void *p, uint4 w) {
+  const u32x4_t v = {w.x, w.y, w.z, w.w};
+  __builtin_nontemporal_store(v, (u32x4_t *)p);
+}
+
 // The rows a launch runs over: `rows` (the launch's bound, what its buffers
 // hold), or fewer when rows_dev is given -- a count an earlier kernel on the
 // stream wrote on the device (token packing's packed row total), read here so
