@@ -226,15 +226,32 @@ __global__ __launch_bounds__(256) void layernorm_wave_k(
 
 // The same with four consecutive values per lane per access (16-byte fp32 /
 // 8-byte bf16 loads and stores): NQ quads of 256 columns.
+//
+// ST: the residual LayerNorm of a post-LN layer, x <- LN(x + y) in place. x's
+// old value and y (the GEMM result) are dead once read, and the new x is next
+// read by the following residual LayerNorm, a GEMM and attention later. Their
+// accesses stream (nontemporal), so the 160 MB this kernel moves at 17,455
+// rows x 768 does not evict the GEMMs' operands from the caches: the kernel
+// itself takes 1-2 us longer, but the GEMMs and attention around it gain more
+// (bge-base b64 x s512, two lanes: 15,950-16,013 -> 16,561-16,629 seq/s). The
+// bf16 copy, the next GEMM's A operand, stays on cached stores (streaming it
+// gave 16,111-16,230).
+template <bool ST>
 __device__ __forceinline__ float4 ld4(const void *p, int bf, int64_t off) {
   if (bf) {
-    const uint2 u = *(const uint2 *)((const uint16_t *)p + off);
+    const uint2 u = ST ? ld_stream8((const uint16_t *)p + off)
+                       : *(const uint2 *)((const uint16_t *)p + off);
     return make_float4(bf2f(u.x & 0xFFFFu), bf2f(u.x >> 16), bf2f(u.y & 0xFFFFu), bf2f(u.y >> 16));
+  }
+  if (ST) {
+    const uint4 u = ld_stream16((const float *)p + off);
+    return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                       __uint_as_float(u.w));
   }
   return *(const float4 *)((const float *)p + off);
 }
 
-template <int NQ>
+template <int NQ, bool ST>
 __global__ __launch_bounds__(256) void layernorm_wave4_k(
     const void *__restrict__ x, int x_bf, const void *__restrict__ y, int y_bf,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps,
@@ -255,9 +272,9 @@ __global__ __launch_bounds__(256) void layernorm_wave4_k(
 #pragma unroll
   for (int i = 0; i < NQ; ++i) {
     const int64_t off = row * cols + i * 256 + lane * 4;
-    v[i] = ld4(x, x_bf, off);
+    v[i] = ld4<ST>(x, x_bf, off);
     if (y) {
-      const float4 w = ld4(y, y_bf, off);
+      const float4 w = ld4<ST>(y, y_bf, off);
       v[i].x += w.x;
       v[i].y += w.y;
       v[i].z += w.z;
@@ -288,7 +305,13 @@ __global__ __launch_bounds__(256) void layernorm_wave4_k(
     r.z = __builtin_fmaf((v[i].z - mean) * is, gm[i].z, bt[i].z);
     r.w = __builtin_fmaf((v[i].w - mean) * is, gm[i].w, bt[i].w);
     const int64_t off = row * cols + c;
-    if (out_f32) *(float4 *)(out_f32 + off) = r;
+    if (out_f32) {
+      if (ST)
+        st_stream16(out_f32 + off, make_uint4(__float_as_uint(r.x), __float_as_uint(r.y),
+                                              __float_as_uint(r.z), __float_as_uint(r.w)));
+      else
+        *(float4 *)(out_f32 + off) = r;
+    }
     if (out_bf16) *(uint2 *)(out_bf16 + off) = make_uint2(pack_bf2(r.x, r.y), pack_bf2(r.z, r.w));
   }
 }
@@ -928,11 +951,17 @@ hipError_t layernorm(const void *x, int x_bf, const void *y, int y_bf, const flo
                          ((uintptr_t)gamma % 16 == 0) && ((uintptr_t)beta % 16 == 0) &&
                          (!out_f32 || (uintptr_t)out_f32 % 16 == 0) &&
                          (!out_bf16 || (uintptr_t)out_bf16 % 8 == 0);
+  // The post-LN residual form (x <- LN(x + y) in place) streams its accesses.
+  const bool st = y && out_f32 && (const void *)out_f32 == x;
   if (aligned16 && cols % 256 == 0) {
 #define MX_LN4_CASE(nq)                                                                   \
   case nq:                                                                                \
-    layernorm_wave4_k<nq><<<g, 256, 0, s>>>(x, x_bf, y, y_bf, gamma, beta, eps, rows,     \
-                                            out_f32, out_bf16, rows_dev);                 \
+    if (st)                                                                               \
+      layernorm_wave4_k<nq, true><<<g, 256, 0, s>>>(x, x_bf, y, y_bf, gamma, beta, eps,   \
+                                                    rows, out_f32, out_bf16, rows_dev);   \
+    else                                                                                  \
+      layernorm_wave4_k<nq, false><<<g, 256, 0, s>>>(x, x_bf, y, y_bf, gamma, beta, eps,  \
+                                                     rows, out_f32, out_bf16, rows_dev);  \
     return hipGetLastError();
     switch (cols / 256) {
       MX_LN4_CASE(1)

@@ -63,8 +63,9 @@ __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
 
 // 16-byte streaming accesses: global loads and stores with the nontemporal
 // hint, for data a kernel touches once and that no cache holds from an earlier
-// kernel (the bf16 softmax rows, the narrowings, GELU over fp32 input). Where
-// each is used, its kernel states what it measured against cached accesses.
+// kernel (the bf16 softmax rows, the narrowings, GELU over fp32 input, the
+// residual LayerNorm's inputs and fp32 output). Where each is used, its kernel
+// states what it measured against cached accesses.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_stream16(const void *p) {
   const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
@@ -73,6 +74,11 @@ __device__ __forceinline__ uint4 ld_stream16(const void *p) {
 __device__ __forceinline__ void st_stream16(void *p, uint4 w) {
   const u32x4_t v = {w.x, w.y, w.z, w.w};
   __builtin_nontemporal_store(v, (u32x4_t *)p);
+}
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 ld_stream8(const void *p) {
+  const u32x2_t v = __builtin_nontemporal_load((const u32x2_t *)p);
+  return make_uint2(v.x, v.y);
 }
 
 // The rows a launch runs over: `rows` (the launch's bound, what its buffers
