@@ -21,10 +21,18 @@ using namespace mxd;
 
 namespace {
 
+// ST: streaming (nontemporal) loads, for data dead once read.
+template <bool ST = false>
 __device__ __forceinline__ float4 load4(const void *p, bool bf, int64_t off) {
   if (bf) {
-    const uint2 u = *(const uint2 *)((const uint16_t *)p + off);
+    const uint2 u = ST ? ld_stream8((const uint16_t *)p + off)
+                       : *(const uint2 *)((const uint16_t *)p + off);
     return make_float4(bf2f(u.x & 0xFFFFu), bf2f(u.x >> 16), bf2f(u.y & 0xFFFFu), bf2f(u.y >> 16));
+  }
+  if (ST) {
+    const uint4 u = ld_stream16((const float *)p + off);
+    return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                       __uint_as_float(u.w));
   }
   return *(const float4 *)((const float *)p + off);
 }
@@ -93,7 +101,9 @@ __global__ __launch_bounds__(256) void quantise_rows_k(const void *__restrict__ 
 // add_norm_quant: z = x (+ y); x_out = (z - mean) / sqrt(var + eps) * gamma +
 // beta (fp32 statistics, the LayerNorm of k_elem.hip), then the quantisation
 // of x_out * ias. x_out is written to out_f32 (nullable; may alias x).
-template <int NQ>
+// ST: the in-place residual form (out_f32 == x, y given) streams x, y and the
+// new x, as the bf16 datapath's residual LayerNorm does (k_elem.hip).
+template <int NQ, bool ST>
 __global__ __launch_bounds__(256) void layernorm_quant_k(
     const float *__restrict__ x, const void *__restrict__ y, int y_bf,
     const float *__restrict__ gamma, const float *__restrict__ beta, float eps, int64_t rows,
@@ -122,9 +132,9 @@ __global__ __launch_bounds__(256) void layernorm_quant_k(
     v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (c < cols) {
       const int64_t off = row * cols + c;
-      v[i] = *(const float4 *)(x + off);
+      v[i] = load4<ST>(x, false, off);
       if (y) {
-        const float4 w = load4(y, y_bf, off);
+        const float4 w = load4<ST>(y, y_bf, off);
         v[i].x += w.x;
         v[i].y += w.y;
         v[i].z += w.z;
@@ -157,7 +167,14 @@ __global__ __launch_bounds__(256) void layernorm_quant_k(
       r.y = __builtin_fmaf((v[i].y - mean) * is, gm[i].y, bt[i].y);
       r.z = __builtin_fmaf((v[i].z - mean) * is, gm[i].z, bt[i].z);
       r.w = __builtin_fmaf((v[i].w - mean) * is, gm[i].w, bt[i].w);
-      if (out_f32) *(float4 *)(out_f32 + row * cols + c) = r;
+      if (out_f32) {
+        if (ST)
+          st_stream16(out_f32 + row * cols + c,
+                      make_uint4(__float_as_uint(r.x), __float_as_uint(r.y),
+                                 __float_as_uint(r.z), __float_as_uint(r.w)));
+        else
+          *(float4 *)(out_f32 + row * cols + c) = r;
+      }
       v[i] = mul4(r, ia[i]);
       mx = absmax4(mx, v[i]);
     }
@@ -214,10 +231,17 @@ hipError_t layernorm_quant(const float *x, const void *y, int y_bf, const float 
                            float *out_f32, const float *ias, int8_t *q, float *a_scale,
                            hipStream_t s, const int32_t *rows_dev) {
   const int g = (int)((rows + 3) / 4);
+  const bool st = y && out_f32 && out_f32 == x;
 #define MX_LQ_CASE(nq)                                                                    \
   case nq:                                                                                \
-    layernorm_quant_k<nq><<<g, 256, 0, s>>>(x, y, y_bf, gamma, beta, eps, rows, (int)cols, \
-                                            out_f32, ias, q, a_scale, rows_dev);          \
+    if (st)                                                                               \
+      layernorm_quant_k<nq, true><<<g, 256, 0, s>>>(x, y, y_bf, gamma, beta, eps, rows,   \
+                                                    (int)cols, out_f32, ias, q, a_scale,  \
+                                                    rows_dev);                            \
+    else                                                                                  \
+      layernorm_quant_k<nq, false><<<g, 256, 0, s>>>(x, y, y_bf, gamma, beta, eps, rows,  \
+                                                     (int)cols, out_f32, ias, q, a_scale, \
+                                                     rows_dev);                           \
     return hipGetLastError();
   switch (quant_groups(cols)) {
     MX_LQ_CASE(1)
