@@ -43,7 +43,8 @@ HBM_PEAK_GBS = 8000.0
 
 
 # The lane count each config runs fastest at on one MI355X (bench.py --lanes 2, 3, 4):
-# bge-base 15.8k / 15.3k / 14.9k seq/s; MiniLM's small batches, whose GEMMs fill a fraction
+# bge-base 15.8k / 15.3k / 14.9k seq/s (later, with the residual LayerNorm streaming, 16.9k /
+# 16.6k for two / three); MiniLM's small batches, whose GEMMs fill a fraction
 # of the chip, 129k / 172k / 135k sustained; ViT-B/16 (lanes 1 / 2 / 3) 19.8k / 22.3k /
 # 22.0k images/s, the Whisper encoder 370 / 396 / 389 samples/s.
 LANES_DEFAULT = {"minilm": 3}
@@ -361,6 +362,112 @@ def gemm_vs_library(mxenc, np):
               f"({row['hipblaslt_tflops']:5.0f} TF/s)", file=sys.stderr, flush=True)
         del ta, tw, tb
     print(json.dumps({"gemm_vs_library": res}))
+
+
+def attention_vs_library(mxenc, np):
+    """The bge-base attention shape (64 sequences x 512, 12 heads of 64) on
+    mx_attention beside torch's scaled_dot_product_attention on the same bf16
+    q, k, v: dense (every key of every sequence), and padded to 512 with the
+    bench's valid lengths, where this library skips the keys and queries past
+    each kv_len and torch applies the additive mask. Medians of 7 runs of 20
+    launches with HIP events on each side's stream; the largest output
+    difference over the valid rows. A reference point, not a product path."""
+    import ctypes
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from mxenc import synth
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    ctx = mxenc.Context(0)
+    stream = vp(mxenc.lib().mx_stream_handle(ctx.stream))
+    e0, e1 = vp(), vp()
+    assert hip.hipEventCreate(ctypes.byref(e0)) == 0 and hip.hipEventCreate(ctypes.byref(e1)) == 0
+    B, S, H, D = 64, 512, 12, 64
+    rng = np.random.default_rng(0)
+    qkv32 = rng.standard_normal((B * S, 3 * H * D), dtype=np.float32) * 0.5
+    bits = mxenc.to_bf16_bits(qkv32)
+    d_qkv = ctx.put(bits)
+    d_out = ctx.empty((B * S, H * D), np.uint16)
+    _, am, lens = synth.make_text_inputs(synth.CONFIGS["bge_base"])
+    lens = np.asarray(lens, dtype=np.int64)
+    # the additive mask the encoder builds (0 / -1e30, mask_k)
+    add = np.where(am > 0, 0.0, -1.0e30).astype(np.float32)
+    d_mask = ctx.put(add)
+    d_kvl = ctx.put(lens.astype(np.int32))
+    dev = torch.device("cuda:0")
+    t_qkv = torch.from_numpy(bits.view(np.int16)).to(dev).view(torch.bfloat16)
+    q, k, v = (t_qkv[:, i * H * D:(i + 1) * H * D].view(B, S, H, D).transpose(1, 2).contiguous()
+               for i in range(3))
+    t_mask = torch.from_numpy(add).to(dev).to(torch.bfloat16).view(B, 1, 1, S)
+
+    def ours(masked):
+        def fn():
+            mxenc.attention(ctx, d_qkv, 3 * H * D, B, S, H, D, 0.125,
+                            d_mask if masked else None, d_kvl if masked else None, d_out, H * D)
+        fn()
+        fn()
+        ctx.sync()
+        ts = []
+        for _ in range(7):
+            assert hip.hipEventRecord(e0, stream) == 0
+            for _ in range(20):
+                fn()
+            assert hip.hipEventRecord(e1, stream) == 0
+            assert hip.hipEventSynchronize(e1) == 0
+            ms = ctypes.c_float()
+            assert hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1) == 0
+            ts.append(ms.value * 1e3 / 20)
+        out = d_out.host().view(np.int16)
+        return float(np.median(ts)), torch.from_numpy(out).view(torch.bfloat16).float()
+
+    def torch_side(fn):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(7):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(20):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3 / 20)
+        return float(np.median(ts)), fn().float()
+
+    def rows(o):  # [B*S, H*D] -> [B, H, S, D]
+        return o.view(B, S, H, D).transpose(1, 2)
+
+    valid = torch.from_numpy(np.arange(S)[None, :] < lens[:, None]).to(dev).view(B, 1, S, 1)
+    res = []
+    for case, masked in (("dense", False), ("padded_masked", True)):
+        flop = 4.0 * H * D * (B * S * S if not masked else float((lens ** 2).sum()))
+        us, o_ours = ours(masked)
+        row = {"case": case, "B": B, "S": S, "H": H, "head_dim": D, "useful_flop": flop,
+               "ours_us": us, "ours_tflops": flop / (us * 1e-6) / 1e12}
+        o_ours = rows(o_ours.to(dev))
+        for name, be in (("flash", SDPBackend.FLASH_ATTENTION),
+                         ("efficient", SDPBackend.EFFICIENT_ATTENTION),
+                         ("math", SDPBackend.MATH)):
+            if name == "math" and not masked:
+                continue
+            try:
+                with sdpa_kernel(be):
+                    tus, o_t = torch_side(lambda: F.scaled_dot_product_attention(
+                        q, k, v, attn_mask=t_mask if masked else None, scale=0.125))
+            except RuntimeError as ex:
+                row[f"torch_{name}"] = f"unavailable: {str(ex).splitlines()[0][:100]}"
+                continue
+            diff = ((o_ours - o_t).abs() * (valid if masked else 1.0)).max().item()
+            row[f"torch_{name}_us"] = tus
+            row[f"torch_{name}_max_abs_diff"] = diff
+            print(f"bench --attention-vs-library: {case:13s} ours {us:6.1f} us "
+                  f"({row['ours_tflops']:4.0f} TF/s useful)  torch {name:9s} {tus:6.1f} us "
+                  f"({flop / (tus * 1e-6) / 1e12:4.0f} TF/s)  max |diff| {diff:.2e}",
+                  file=sys.stderr, flush=True)
+        res.append(row)
+    print(json.dumps({"attention_vs_library": res}))
+    ctx.close()
     ctx.close()
 
 
@@ -425,6 +532,10 @@ def main():
     ap.add_argument("--gemm-vs-library", action="store_true",
                     help="only time the four bge-base GEMM sites on this library's kernel "
                          "and on torch.addmm (hipBLASLt) over the same bf16 operands")
+    ap.add_argument("--attention-vs-library", action="store_true",
+                    help="only time the bge-base attention shape (64 x 512, 12 heads of 64) on "
+                         "mx_attention and on torch's scaled_dot_product_attention, dense and "
+                         "padded with the bench's valid lengths")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run narrow_f32_bf16 over 64 Mi fp32 values, 5 times: a "
                          "streaming kernel of known bytes (256 MiB read, 128 MiB written "
@@ -447,6 +558,10 @@ def main():
 
     if args.gemm_vs_library:
         gemm_vs_library(mxenc, np)
+        return
+
+    if args.attention_vs_library:
+        attention_vs_library(mxenc, np)
         return
 
     if args.calibrate:
