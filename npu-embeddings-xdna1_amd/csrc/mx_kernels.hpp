@@ -118,6 +118,19 @@ inline int persistent_grid(int ntiles, int grid) {
   if (g >= 16 && (g & 7)) g = (g + 7) & ~7;
   return g;
 }
+// The fewest resident blocks (a multiple of 8, at most `grid`) that walk
+// `ntiles` tiles in as many rounds as `grid` blocks would: ceil(ntiles /
+// rounds). The makespan in tiles is the same. At the packed bge-base rows the
+// QKV (621 tiles), FFN-up (828) and N = 768 (207) GEMMs then run on 208 blocks
+// instead of 256, and one lane's step is 1.5 % faster with the same bits (each
+// tile's arithmetic does not depend on the block that runs it).
+inline int balanced_grid(int ntiles, int grid) {
+  if (ntiles <= 0 || grid <= 0) return grid;
+  const int rounds = (ntiles + grid - 1) / grid;
+  int g = (ntiles + rounds - 1) / rounds;
+  if (g >= 16 && (g & 7)) g = (g + 7) & ~7;
+  return g < grid ? g : grid;
+}
 // The LDS-pipelined kernel addresses a lane's operand row within a tile as a
 // 32-bit byte offset from the tile origin: row r (< 256) of A at r * lda * esz
 // and of Wt at r * K * esz, plus at most 128 bytes of K. Both must stay below
