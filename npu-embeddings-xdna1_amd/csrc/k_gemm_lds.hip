@@ -37,10 +37,7 @@ hipError_t gemm_lds_launch_t(const GemmArgs &a, int grid, hipStream_t s) {
   }
   const int tiles_m = (int)((a.M + BM - 1) / BM), tiles_n = (int)((a.N + BN - 1) / BN);
   const int ntiles = tiles_m * tiles_n;
-  // Blocks for the rows the tile was chosen for (the packed rows' hint when
-  // the launch is sized for a row bound), balanced over the rounds.
-  const int tiles_eff = (int)((mxk::gemm_pick_rows(a.M, a.m_hint) + BM - 1) / BM) * tiles_n;
-  const int g = mxk::persistent_grid(ntiles, mxk::balanced_grid(tiles_eff, grid));
+  const int g = mxk::persistent_grid(ntiles, grid);
   kern<<<g, Cfg::NT, Cfg::LDS, s>>>((const uint16_t *)a.A, a.lda, (const uint16_t *)a.Wt,
                                     (int)a.M, (int)a.N, (int)a.K, a.bias, a.residual, a.C, a.ldc,
                                     tiles_m, tiles_n, a.rows_dev);

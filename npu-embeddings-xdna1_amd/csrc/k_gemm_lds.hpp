@@ -277,9 +277,11 @@ __device__ __forceinline__ void gemm_lds_body(
   }
   // This block's tiles: t(i) = first + i * stride, i < my_tiles. With a grid
   // that is a multiple of 8, XCD x owns tiles [x*chunk, (x+1)*chunk) and its
-  // G/8 blocks interleave over them.
+  // G/8 blocks interleave over them. G: the launched blocks balanced over the
+  // live tiles (mxk::balanced_grid); the blocks past it exit here.
   const int ntiles = tiles_m * tiles_n;
-  const int G = gridDim.x;
+  const int G = mxk::balanced_grid(ntiles, (int)gridDim.x);
+  if ((int)blockIdx.x >= G) return;
   int first = (int)blockIdx.x, stride = G, end = ntiles;
   if ((G & 7) == 0 && G >= 16) {
     const int chunk = (ntiles + 7) >> 3, x = (int)(blockIdx.x & 7);

@@ -118,13 +118,15 @@ inline int persistent_grid(int ntiles, int grid) {
   if (g >= 16 && (g & 7)) g = (g + 7) & ~7;
   return g;
 }
-// The fewest resident blocks (a multiple of 8, at most `grid`) that walk
-// `ntiles` tiles in as many rounds as `grid` blocks would: ceil(ntiles /
-// rounds). The makespan in tiles is the same. At the packed bge-base rows the
-// QKV (621 tiles), FFN-up (828) and N = 768 (207) GEMMs then run on 208 blocks
-// instead of 256, and one lane's step is 1.5 % faster with the same bits (each
-// tile's arithmetic does not depend on the block that runs it).
-inline int balanced_grid(int ntiles, int grid) {
+// The fewest blocks (a multiple of 8, at most `grid`) that walk `ntiles` tiles
+// in as many rounds as `grid` blocks would: ceil(ntiles / rounds). The
+// makespan in tiles is the same. The persistent kernels apply it on the device
+// to the live tile count (the packed row count is known only there): at the
+// packed bge-base rows the QKV (621 tiles), FFN-up (828) and N = 768 (207)
+// GEMMs run on 208 of the 256 launched blocks, the rest exit at once, and one
+// lane's step is 1.5 % faster with the same bits (each tile's arithmetic does
+// not depend on the block that runs it).
+__host__ __device__ inline int balanced_grid(int ntiles, int grid) {
   if (ntiles <= 0 || grid <= 0) return grid;
   const int rounds = (ntiles + grid - 1) / grid;
   int g = (ntiles + rounds - 1) / rounds;
