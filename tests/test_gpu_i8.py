@@ -232,10 +232,18 @@ def test_layernorm_quant(ctx, orc, cols, ybf):
     ias = (1.0 / rng.uniform(0.5, 2.0, cols)).astype(np.float32)
     dx = ctx.put(x)
     dy = ctx.put(mxenc.to_bf16_bits(y) if ybf else y)
+    dg, dbt, dias = ctx.put(g), ctx.put(bt), ctx.put(ias)
+    # out of place first (cached accesses), then in place over x as the stack
+    # calls it (streaming accesses): the same bits
+    of = ctx.empty((rows, cols), np.float32)
+    q0, s0 = ctx.empty((rows, cols), np.int8), ctx.empty((rows,), np.float32)
+    mxenc.layernorm_i8(ctx, dx, dy, dg, dbt, 1e-12, rows, cols, of, dias, q0, s0)
     q, s = ctx.empty((rows, cols), np.int8), ctx.empty((rows,), np.float32)
-    mxenc.layernorm_i8(ctx, dx, dy, ctx.put(g), ctx.put(bt), 1e-12, rows, cols, dx,
-                       ctx.put(ias), q, s)
+    mxenc.layernorm_i8(ctx, dx, dy, dg, dbt, 1e-12, rows, cols, dx, dias, q, s)
     ln = dx.host()
+    assert np.array_equal(ln.view(np.uint32), of.host().view(np.uint32))
+    assert np.array_equal(q.host(), q0.host())
+    assert np.array_equal(s.host().view(np.uint32), s0.host().view(np.uint32))
     want = x + y
     orc.orc_layer_norm_rows(P(want), rows, cols, P(g), P(bt), np.float32(1e-12))
     assert np.abs(ln - want).max() <= 2e-5 * max(1.0, float(np.abs(want).max()))

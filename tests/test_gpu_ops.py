@@ -159,9 +159,12 @@ def test_layernorm_residual_fused(ctx, orc, cols):
     assert np.max(np.abs(got - want)) < 2e-5
     # the bf16 copy is the fp32 result narrowed by to_bf16, bit for bit
     assert np.array_equal(ob.host(), to_bf16_bits(got))
-    # in place over the residual stream
-    mxenc.layernorm(ctx, dx, dy, dg, db, 1e-12, rows, cols, out_f32=dx)
+    # in place over the residual stream, with the bf16 copy as the stack writes
+    # it (the form whose accesses stream, nontemporal): the same bits
+    ob2 = ctx.empty(x.shape, np.uint16)
+    mxenc.layernorm(ctx, dx, dy, dg, db, 1e-12, rows, cols, out_f32=dx, out_bf16=ob2)
     assert np.array_equal(dx.host(), got)
+    assert np.array_equal(ob2.host(), ob.host())
 
 
 def test_layernorm_bf16_input(ctx, orc):
