@@ -125,7 +125,9 @@ inline int persistent_grid(int ntiles, int grid) {
 // packed bge-base rows the QKV (621 tiles), FFN-up (828) and N = 768 (207)
 // GEMMs run on 208 of the 256 launched blocks, the rest exit at once, and one
 // lane's step is 1.5 % faster with the same bits (each tile's arithmetic does
-// not depend on the block that runs it).
+// not depend on the block that runs it). tests/cpu_checks/balanced_grid.cpp
+// checks the rounds, the XCD multiple and the minimality for every tile count
+// up to 20,000.
 __host__ __device__ inline int balanced_grid(int ntiles, int grid) {
   if (ntiles <= 0 || grid <= 0) return grid;
   const int rounds = (ntiles + grid - 1) / grid;
